@@ -1,0 +1,141 @@
+/* treesa_hip.h -- C ABI of the MI355X TreeSA sweep library (libtreesa_hip.so).
+ *
+ * The reference ships one CUDA binary whose host class Runner<W> drives the sweep kernels directly
+ * (csrc/treesa_gpu.cu:1415-2062).  Here that device-facing half of Runner is a C ABI: the CLI host
+ * (treesa_gpu_amd/bin/treesa_gpu, the drop-in for TREESA_GPU_BINARY, treesa_gpu/driver.py:45) and the
+ * Python tests call these entry points with plain pointers and sizes.  Every call returns TSA_OK (0)
+ * or a negative status; tsa_last_error() then holds a message.  No C++ exception crosses the ABI.
+ * A context owns its device buffers and one HIP stream; calls on one context are synchronous with
+ * respect to the host buffers passed in and must come from one host thread at a time.
+ *
+ * Chain record (what tsa_upload / tsa_download exchange), in 64-bit words, one record per chain,
+ * records back to back (the layout is returned by tsa_layout):
+ *   [0, nint*W)              labels of internal node m+i at i*W: the unsliced output-label set, bit l%64
+ *                            of word l/64 for label l (W = words per set)
+ *   [ch_off, ch_off+ceil(nint/2))  children, uint32 per internal node i: left | right << 16
+ *                            (node ids: leaves 0..m-1, internal m..2m-2, root 2m-2)
+ *   [s_off, s_off+W)         slice set S (sliced labels have log2 size 0 in every cost)
+ *   padding up to chain_words (a multiple of 2, so records are 16-byte aligned)
+ * Reference layout with 32-bit words: csrc/treesa_gpu.cu:15-20, 1439-1448.
+ */
+#ifndef TREESA_HIP_H
+#define TREESA_HIP_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TSA_OK 0
+#define TSA_ERR_ARG (-1)     /* invalid argument or size */
+#define TSA_ERR_HIP (-2)     /* HIP runtime error (message names the call) */
+#define TSA_ERR_FIT (-3)     /* node arrays do not fit in LDS */
+#define TSA_ERR_LIBM (-4)    /* the host libm disagrees with the restated expf/exp2f/log2f */
+
+#define TSA_ORDER_PAR 0      /* random-priority independent-set phases (csrc/common.h:240-272) */
+#define TSA_ORDER_PREORDER 1 /* the Julia pre-order sweep (csrc/cpu_ref.h:87-126) */
+
+#define TSA_MODE_TC 0        /* tc + sc penalty (Julia tcscrw) */
+#define TSA_MODE_GPU 1       /* modeled GPU time, roofline model v1 */
+#define TSA_MODE_H100 2      /* modeled time, measured H100 model */
+
+/* Kernel selection flags for tsa_create (results never depend on them). */
+#define TSA_KERNEL_AUTO 0
+#define TSA_KERNEL_LDS 1     /* chain staged in LDS (fails with TSA_ERR_FIT if it does not fit) */
+#define TSA_KERNEL_GLOBAL 2  /* chain worked on in HBM, node arrays in LDS */
+
+typedef struct tsa_layout_t {
+  int32_t m, nint, nlab;
+  int32_t W;            /* 64-bit words per label set (1, 2, 4, 8 on the register path, else ceil(nlab/64)) */
+  int32_t runtime_width;/* 1: kernels loop over W words at run time (wide path); 0: W is a register width */
+  int32_t ch_off;       /* word offset of the children array */
+  int32_t s_off;        /* word offset of S */
+  int32_t chain_words;  /* words per chain record */
+} tsa_layout_t;
+
+/* Energy model and run parameters; the reference's Params (csrc/common.h:60-94) minus the layout. */
+typedef struct tsa_config_t {
+  int32_t mode;                 /* TSA_MODE_* */
+  float sc_target, sc_weight;
+  uint32_t key0, key1;          /* Philox key: low / high half of splitmix64(seed) (csrc/treesa_gpu.cu:1457-1459) */
+  int32_t slicing;              /* 1: every cost uses label sets masked by ~S */
+  int32_t slice_moves;          /* slice proposals after every slice_every-th global sweep (0: none) */
+  int32_t slice_every;
+  int32_t max_slices;           /* cap on |S| */
+  int32_t par_follow;           /* par order: an accepted visit re-arms an already visited pivot */
+  int32_t par_band;             /* par order: 0, or 2..16 = top-down priorities within bands of L levels */
+  int32_t kernel;               /* TSA_KERNEL_* */
+  /* GPU roofline model v1, log2 units (csrc/treesa_gpu.cu:1460-1465) */
+  float lpeak, lbw, llaunch;
+  int32_t m0, n0, k0;
+  /* measured H100 model, log2 of the constants (csrc/treesa_gpu.cu:1466-1474) */
+  float v2_l3launch, v2_lperm2, v2_lcc_bit, v2_lcc_cell, v2_ltc_bit, v2_ltc_pad, v2_ltc_out, v2_lsmall_cell;
+  int32_t v2_small_rank;
+} tsa_config_t;
+
+typedef struct tsa_ctx tsa_ctx;
+
+/* Record layout for an instance with m tensors and nlab labels.  wide != 0 forces the runtime-width
+ * path (the reference's --wide).  Pure host function: needs no GPU.
+ * Replaces the layout set-up of Runner<W>::Runner, csrc/treesa_gpu.cu:1439-1448, 2078-2085. */
+int tsa_layout(int32_t m, int32_t nlab, int32_t wide, tsa_layout_t* out);
+
+/* Create a context for nchains chains on the current HIP device.  leaf: m*W words, the label sets of
+ * the input tensors in the layout's word format; leaf_sc = largest leaf tensor (log2).
+ * Replaces Runner<W>::Runner + alloc, csrc/treesa_gpu.cu:1435-1548, 1564-1578. */
+int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t leaf_sc, const tsa_config_t* cfg,
+               int32_t nchains, tsa_ctx** out);
+
+/* Upload the whole population (nchains * chain_words words).  Replaces the H2D copy of init_chains,
+ * csrc/treesa_gpu.cu:1629. */
+int tsa_upload(tsa_ctx* ctx, const uint64_t* population);
+
+/* Download count chain records starting at chain c0.  Replaces the best-chain and --check copies,
+ * csrc/treesa_gpu.cu:1823, 1948-1949. */
+int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* out);
+
+/* Enqueue nsweeps sweeps of every chain at inverse temperature beta, global sweep counter sweep0
+ * (the RNG counter), in TSA_ORDER_*; slice moves follow every sweep s with (sweep0+s+1) % slice_every
+ * == 0 when slice_moves > 0.  Asynchronous; event-timed.  Replaces Runner::sweeps / sweeps_mode,
+ * csrc/treesa_gpu.cu:1659-1716. */
+int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0, int32_t nsweeps);
+
+/* Wait for the last tsa_sweeps and return its event-timed kernel time in ms (0 if none pending).
+ * Replaces the cudaEventElapsedTime bookkeeping of run_anneal, csrc/treesa_gpu.cu:1799-1809, 1870-1876. */
+int tsa_sweeps_ms(tsa_ctx* ctx, double* ms);
+
+/* Per-chain energy: lc = log2 of the per-slice cost (lse fold of node costs), sc = largest tensor
+ * (masked by S, leaves included), ns = |S|.  Synchronous.  Replaces Runner::energy + k_energy,
+ * csrc/treesa_gpu.cu:999-1014, 1717-1729. */
+int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns);
+
+/* Population step: chain c <- chain anc[c] for every c.  Replaces Runner::resample + k_copy,
+ * csrc/treesa_gpu.cu:1016-1022, 1925-1933. */
+int tsa_resample(tsa_ctx* ctx, const int32_t* anc);
+
+/* Switch the energy mode (stage 2 of a two-stage run, csrc/treesa_gpu.cu:1790-1798). */
+int tsa_set_mode(tsa_ctx* ctx, int32_t mode);
+
+/* Counters since creation: proposals, accepts, phases (par) or frontier steps (preorder), node
+ * visits, slice proposals, slice accepts, busy lanes.  Replaces the d_stats copy,
+ * csrc/treesa_gpu.cu:1880-1881. */
+int tsa_stats(tsa_ctx* ctx, uint64_t out[7]);
+
+/* Human-readable description of the kernels this context launches (name, lanes, LDS bytes). */
+int tsa_describe(tsa_ctx* ctx, char* buf, int32_t len);
+
+/* Release everything.  Replaces Runner::release, csrc/treesa_gpu.cu:1579-1582. */
+int tsa_destroy(tsa_ctx* ctx);
+
+/* Message of the last failed call on ctx (or of the last failed tsa_create / tsa_layout when ctx is
+ * NULL).  Never NULL. */
+const char* tsa_last_error(const tsa_ctx* ctx);
+
+/* Single-float math shared with the kernels (host side), for tests: expf, exp2f and log2f on [1, 2]
+ * exactly as the device computes them.  which: 0 expf, 1 exp2f, 2 log2f.  Returns the float. */
+float tsa_host_math(int32_t which, float x);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TREESA_HIP_H */

@@ -1,0 +1,178 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so) -- the checker of every parity test.
+
+The oracle restates the reference's CPU port (csrc/cpu_ref.h) with its own vector-label data structures;
+see oracle/tsa_oracle.cpp.  Only tests/, __graft_entry__.smoke() and bench.py's CPU-baseline leg use it.
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "oracle", "liboracle.so")
+REF_BIN = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
+
+_lib = None
+
+
+class OParams(ctypes.Structure):
+    _fields_ = [("mode", ctypes.c_int32), ("sc_target", ctypes.c_float), ("sc_weight", ctypes.c_float),
+                ("key0", ctypes.c_uint32), ("key1", ctypes.c_uint32), ("slicing", ctypes.c_int32),
+                ("slice_moves", ctypes.c_int32), ("slice_every", ctypes.c_int32), ("max_slices", ctypes.c_int32),
+                ("par_follow", ctypes.c_int32), ("par_band", ctypes.c_int32),
+                ("lpeak", ctypes.c_float), ("lbw", ctypes.c_float), ("llaunch", ctypes.c_float),
+                ("m0", ctypes.c_int32), ("n0", ctypes.c_int32), ("k0", ctypes.c_int32),
+                ("v2_l3launch", ctypes.c_float), ("v2_lperm2", ctypes.c_float), ("v2_lcc_bit", ctypes.c_float),
+                ("v2_lcc_cell", ctypes.c_float), ("v2_ltc_bit", ctypes.c_float), ("v2_ltc_pad", ctypes.c_float),
+                ("v2_ltc_out", ctypes.c_float), ("v2_lsmall_cell", ctypes.c_float), ("v2_small_rank", ctypes.c_int32),
+                ("leaf_sc", ctypes.c_int32)]
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
+
+
+def load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB):
+        build()
+    lib = ctypes.CDLL(LIB)
+    P, I, U32, U64, F = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint32, ctypes.c_uint64, ctypes.c_float
+    lib.oracle_new.argtypes = [I, I, P, P, I, P]
+    lib.oracle_new.restype = P
+    lib.oracle_free.argtypes = [P]
+    lib.oracle_splitmix64.argtypes = [U64]
+    lib.oracle_splitmix64.restype = U64
+    lib.oracle_philox.argtypes = [P, U32, U32, P]
+    lib.oracle_par_pri.argtypes = [U32, U32, U32, U32]
+    lib.oracle_par_pri.restype = U32
+    lib.oracle_lse_table.argtypes = [P]
+    lib.oracle_random_tree.argtypes = [I, U64, P]
+    lib.oracle_labels.argtypes = [P, P, I, P]
+    lib.oracle_random_slices.argtypes = [I, U64, I, I, I, P]
+    lib.oracle_sweeps.argtypes = [P, ctypes.POINTER(OParams), I, I, I, I, P, I, I, I, F, U32, I, P]
+    lib.oracle_energy.argtypes = [P, ctypes.POINTER(OParams), I, I, I, I, P, I, P, P, P]
+    lib.oracle_host_energy.argtypes = [P, P, P, I, I, I, I, P, I, P]
+    _lib = lib
+    return lib
+
+
+def params_from_config(cfg, leaf_sc, nlab):
+    """OParams with the same values as a treesa_gpu_amd.capi.Config."""
+    p = OParams()
+    for name, _ in OParams._fields_:
+        if name == "leaf_sc":
+            continue
+        setattr(p, name, getattr(cfg, name))
+    if p.max_slices <= 0:
+        p.max_slices = nlab
+    if not p.slicing:
+        p.slice_moves = 0
+    p.leaf_sc = leaf_sc
+    return p
+
+
+class Oracle:
+    def __init__(self, m, nlab, ixs, iy=()):
+        self.lib = load()
+        offs = np.zeros(m + 1, np.int32)
+        for i, ix in enumerate(ixs):
+            offs[i + 1] = offs[i] + len(ix)
+        labs = np.array([l for ix in ixs for l in ix] or [0], np.int32)
+        iya = np.array(list(iy) or [0], np.int32)
+        self.h = self.lib.oracle_new(m, nlab, offs.ctypes.data, labs.ctypes.data, len(iy), iya.ctypes.data)
+        self.m, self.nlab = m, nlab
+
+    def labels(self, ch, W):
+        ch = np.ascontiguousarray(ch, np.uint32)
+        lab = np.zeros((self.m - 1, W), np.uint64)
+        if self.lib.oracle_labels(self.h, ch.ctypes.data, W, lab.ctypes.data) != 0:
+            return None
+        return lab
+
+    def sweeps(self, params, lay, pop, order, beta, sweep0, nsweeps, c0=0):
+        """In-place sweeps of a (n, chain_words) population whose row k is chain c0 + k; returns stats."""
+        assert pop.dtype == np.uint64 and pop.flags.c_contiguous
+        st = np.zeros(6, np.int64)
+        self.lib.oracle_sweeps(self.h, ctypes.byref(params), lay.W, lay.ch_off, lay.s_off, lay.chain_words,
+                               pop.ctypes.data, c0, pop.shape[0], order, beta, sweep0, nsweeps, st.ctypes.data)
+        return [int(x) for x in st]
+
+    def energy(self, params, lay, pop):
+        n = pop.shape[0]
+        lc = np.zeros(n, np.float32)
+        sc = np.zeros(n, np.int32)
+        ns = np.zeros(n, np.int32)
+        pop = np.ascontiguousarray(pop, np.uint64)
+        self.lib.oracle_energy(self.h, ctypes.byref(params), lay.W, lay.ch_off, lay.s_off, lay.chain_words,
+                               pop.ctypes.data, n, lc.ctypes.data, sc.ctypes.data, ns.ctypes.data)
+        return lc, sc, ns
+
+    def host_energy(self, lay, rec, slicing, gm, h100):
+        rec = np.ascontiguousarray(rec, np.uint64)
+        g = np.array(gm, np.float64)
+        h = np.array(h100, np.float64)
+        out = np.zeros(5, np.float64)
+        self.lib.oracle_host_energy(self.h, g.ctypes.data, h.ctypes.data, lay.W, lay.ch_off, lay.s_off,
+                                    lay.chain_words, rec.ctypes.data, 1 if slicing else 0, out.ctypes.data)
+        return float(out[0]), int(out[1]), float(out[2]), float(out[3]), int(out[4])
+
+    def __del__(self):
+        try:
+            self.lib.oracle_free(self.h)
+        except Exception:
+            pass
+
+
+def philox(ctr, k0, k1):
+    lib = load()
+    c = np.array(ctr, np.uint32)
+    out = np.zeros(4, np.uint32)
+    lib.oracle_philox(c.ctypes.data, k0, k1, out.ctypes.data)
+    return [int(x) for x in out]
+
+
+def random_tree(m, seed):
+    out = np.zeros(m - 1, np.uint32)
+    load().oracle_random_tree(m, seed, out.ctypes.data)
+    return out
+
+
+def lse_table():
+    out = np.zeros(64, np.float32)
+    load().oracle_lse_table(out.ctypes.data)
+    return out
+
+
+def read_instance_py(path):
+    """Plain-Python reader of the instance format (m nlab / k l.. / ny y..), independent of the host layer."""
+    with open(path) as f:
+        tok = f.read().split()
+    it = iter(tok)
+    m, nlab = int(next(it)), int(next(it))
+    ixs = []
+    for _ in range(m):
+        k = int(next(it))
+        ixs.append(sorted(int(next(it)) for _ in range(k)))
+    iy = []
+    try:
+        ny = int(next(it))
+        iy = [int(next(it)) for _ in range(ny)]
+    except StopIteration:
+        pass
+    return m, nlab, ixs, iy
+
+
+def read_trees_py(path, m):
+    with open(path) as f:
+        vals = [int(x) for x in f.read().split()]
+    per = 2 * (m - 1)
+    assert len(vals) % per == 0
+    out = []
+    for k in range(len(vals) // per):
+        v = vals[k * per:(k + 1) * per]
+        out.append(np.array([v[2 * i] | (v[2 * i + 1] << 16) for i in range(m - 1)], np.uint32))
+    return np.array(out, np.uint32)

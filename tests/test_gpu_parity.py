@@ -1,0 +1,141 @@
+"""GPU parity: the HIP kernels (through the C ABI) against the oracle, bit for bit.
+
+Every golden case of the reference's validation matrix (tests/run_checks.sh parameters, 48 chains) runs on
+the GPU and in the oracle from the same initial records; the final records (children, label sets, slice
+sets) and the proposal / accept counts must be identical, the first four chains must also match the
+reference CPU port's hashes (tests/golden/ref_sweeps.json), and the energy kernel must return exactly the
+oracle's 32-lane fold.  Slice moves (no reference CPU twin) are compared with the oracle's mirror.
+"""
+import numpy as np
+import pytest
+
+import common
+import oracle as orc
+from treesa_gpu_amd import capi
+
+pytestmark = pytest.mark.gpu
+
+NCHAINS = 48
+
+
+def leaf_sets(m, ixs, W):
+    leaf = np.zeros((m, W), np.uint64)
+    for i, ix in enumerate(ixs):
+        for l in ix:
+            leaf[i, l >> 6] |= np.uint64(1) << np.uint64(l & 63)
+    return leaf
+
+
+class Case:
+    def __init__(self, inst, order, mode, init="greedy", random_slices=0, par_follow=False, par_band=0, slicing=False,
+                 slice_moves=1, slice_every=1, nchains=NCHAINS, kernel=capi.KERNEL_AUTO, wide=False, seed=None,
+                 sc_target=None):
+        self.inst, self.order = inst, order
+        m, nlab, ixs, iy = common.load_instance(inst)
+        self.m, self.nlab, self.ixs = m, nlab, ixs
+        self.O = orc.Oracle(m, nlab, ixs, iy)
+        self.lay = capi.layout(m, nlab, wide)
+        seed = common.CHECK_SEED if seed is None else seed
+        tf = common.tree_file(inst, init)
+        trees = orc.read_trees_py(tf, m) if tf else None
+        self.pop0 = common.oracle_population(self.O, self.lay, m, nchains, seed, trees, random_slices)
+        sl = slicing or random_slices > 0
+        self.cfg = capi.make_config(mode=mode, sc_target=common.CHECK_SC_TARGET if sc_target is None else sc_target,
+                                    seed=seed, slicing=sl, slice_moves=slice_moves if slicing else 0,
+                                    slice_every=slice_every, par_follow=par_follow, par_band=par_band, kernel=kernel)
+        self.leaf_sc = max(len(x) for x in ixs)
+        self.P = orc.params_from_config(self.cfg, self.leaf_sc, nlab)
+        self.leaf = leaf_sets(m, ixs, self.lay.W)
+        self.nchains = nchains
+        self.ord = capi.ORDER_PAR if order == "par" else capi.ORDER_PREORDER
+
+    def run_gpu(self, betas=common.CHECK_BETAS, niters=common.CHECK_NITERS):
+        print(f"[gpu] {self.inst} {self.order} mode={self.cfg.mode} slicing={self.cfg.slicing} "
+              f"kernel={self.cfg.kernel} W={self.lay.W} chains={self.nchains}", flush=True)
+        with capi.Context(self.lay, self.leaf, self.leaf_sc, self.cfg, self.nchains) as ctx:
+            ctx.upload(self.pop0)
+            for lev, b in enumerate(betas):
+                ctx.sweeps(self.ord, b, lev * niters, niters)
+            ctx.sweeps_ms()
+            pop = ctx.download()
+            st = ctx.stats()
+            en = ctx.energy()
+            desc = ctx.describe()
+        return pop, st, en, desc
+
+    def run_oracle(self, betas=common.CHECK_BETAS, niters=common.CHECK_NITERS):
+        pop = self.pop0.copy()
+        tot = [0] * 6
+        for lev, b in enumerate(betas):
+            st = self.O.sweeps(self.P, self.lay, pop, self.ord, b, lev * niters, niters)
+            tot = [a + x for a, x in zip(tot, st)]
+        return pop, tot, self.O.energy(self.P, self.lay, pop)
+
+
+def compare(case, gpu, ora):
+    gpop, gst, gen, desc = gpu
+    opop, ost, oen = ora
+    bad = [c for c in range(case.nchains) if not np.array_equal(gpop[c], opop[c])]
+    assert not bad, f"{len(bad)}/{case.nchains} chains differ from the oracle (first {bad[:5]}) [{desc}]"
+    assert gst[0] == ost[0] and gst[1] == ost[1], f"proposals/accepts gpu {gst[:2]} oracle {ost[:2]}"
+    assert gst[3] == ost[3], "node visits"
+    assert gst[4] == ost[4] and gst[5] == ost[5], "slice proposals/accepts"
+    glc, gsc, gns = gen
+    olc, osc, ons = oen
+    assert np.array_equal(glc.view(np.uint32), olc.view(np.uint32)), "energy kernel lcost differs from the oracle"
+    assert np.array_equal(gsc, osc) and np.array_equal(gns, ons)
+
+
+@pytest.mark.parametrize("golden", common.golden_cases(), ids=common.case_id)
+def test_sweeps_match_oracle_and_reference(golden):
+    rs, pf, pb = common.case_options(golden)
+    case = Case(golden["inst"], golden["order"], golden["mode"], golden["init"], random_slices=rs, par_follow=pf,
+                par_band=pb)
+    gpu = case.run_gpu()
+    compare(case, gpu, case.run_oracle())
+    for c, want in enumerate(golden["chains"]):
+        chf, labf = common.record_hashes(gpu[0][c], case.lay, case.nlab)
+        assert (chf, labf) == (want["children_fnv"], want["labels_fnv"]), f"chain {c} vs the reference CPU port"
+
+
+@pytest.mark.parametrize("inst,order,mode", [("sat100", "par", "tc"), ("sat100", "preorder", "h100"),
+                                             ("lat14", "par", "gpu"), ("reg3_250", "preorder", "tc")])
+def test_lds_and_global_kernels_agree(inst, order, mode):
+    a = Case(inst, order, mode, kernel=capi.KERNEL_LDS)
+    b = Case(inst, order, mode, kernel=capi.KERNEL_GLOBAL)
+    ga, gb = a.run_gpu(), b.run_gpu()
+    assert ga[3].startswith("lds") and gb[3].startswith("global")
+    assert np.array_equal(ga[0], gb[0])
+    compare(a, ga, a.run_oracle())
+
+
+@pytest.mark.parametrize("inst,order,mode,moves,every", [("sat100", "par", "tc", 1, 1), ("sat100", "preorder", "tc", 2, 1),
+                                                         ("grid24", "par", "h100", 1, 2), ("sat60", "par", "tc", 3, 1),
+                                                         ("reg3_250", "par", "gpu", 1, 1)])
+def test_slice_moves_match_oracle_mirror(inst, order, mode, moves, every):
+    case = Case(inst, order, mode, slicing=True, slice_moves=moves, slice_every=every, sc_target=20)
+    gpu = case.run_gpu()
+    assert gpu[1][4] > 0, "no slice proposals"
+    compare(case, gpu, case.run_oracle())
+
+
+def test_resample_copies_ancestors():
+    case = Case("sat40", "par", "tc")
+    rng = np.random.default_rng(3)
+    anc = rng.integers(0, case.nchains, case.nchains).astype(np.int32)
+    with capi.Context(case.lay, case.leaf, case.leaf_sc, case.cfg, case.nchains) as ctx:
+        ctx.upload(case.pop0)
+        ctx.sweeps(case.ord, 1.0, 0, 2)
+        before = ctx.download()
+        ctx.resample(anc)
+        after = ctx.download()
+    assert np.array_equal(after, before[anc])
+
+
+def test_upload_rejects_invalid_tree():
+    case = Case("sat40", "par", "tc", nchains=4)
+    bad = case.pop0.copy()
+    bad[2, case.lay.ch_off:].view(np.uint32)[5] = 0xFFFF  # node id out of range
+    with capi.Context(case.lay, case.leaf, case.leaf_sc, case.cfg, case.nchains) as ctx:
+        with pytest.raises(capi.TsaError, match="not a valid tree"):
+            ctx.upload(bad)

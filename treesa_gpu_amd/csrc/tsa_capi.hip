@@ -1,0 +1,460 @@
+// tsa_capi.hip -- host side of libtreesa_hip.so: the C ABI declared in include/treesa_hip.h.
+//
+// Owns device memory and one HIP stream per context, validates everything a kernel will index with
+// before it reaches the GPU (tree structure of uploaded chains, ancestor indices), and prepares the
+// host-built tables the kernels read: the lse table (csrc/treesa_gpu.cu:2075) and the log2f correction
+// table of tsa_math.h, which is filled by comparing the restated log2f with this process's libm.
+#include <hip/hip_runtime.h>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "treesa_hip.h"
+#include "tsa_kernels.h"
+
+struct tsa_ctx {
+  tsa_layout_t lay;
+  tsa_config_t cfg;
+  TsaKParams P;
+  int mode = 0;
+  int nchains = 0;
+  int Wt = 0;  // kernel template width (0 = runtime width)
+  TsaLaunch L{};
+  std::string kname;
+  hipStream_t st = nullptr;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  bool pending = false;
+  uint64_t* d_rec = nullptr;
+  uint64_t* d_rec2 = nullptr;
+  uint64_t* d_leaf = nullptr;
+  uint32_t* d_fix = nullptr;
+  unsigned long long* d_stats = nullptr;
+  float* d_lc = nullptr;
+  int* d_sc = nullptr;
+  int* d_ns = nullptr;
+  int* d_anc = nullptr;
+  std::string err;
+};
+
+static thread_local std::string g_err;
+
+static int fail(tsa_ctx* ctx, int code, const std::string& msg) {
+  if (ctx) ctx->err = msg;
+  else g_err = msg;
+  return code;
+}
+
+#define TSA_HIP(ctx, call)                                                                          \
+  do {                                                                                             \
+    hipError_t e_ = (call);                                                                        \
+    if (e_ != hipSuccess)                                                                          \
+      return fail((ctx), TSA_ERR_HIP, std::string(#call) + ": " + hipGetErrorString(e_));          \
+  } while (0)
+
+// ---------------------------------------------------------------------------------------------------
+// Host-built tables
+// ---------------------------------------------------------------------------------------------------
+static std::once_flag g_fix_once;
+static std::vector<uint32_t> g_fix;  // TSA_LOG2FIX_WORDS words
+static long long g_fix_far = 0;      // inputs where the restated log2f is more than 1 ulp from libm
+
+static void build_log2_fix() {
+  g_fix.assign(TSA_LOG2FIX_WORDS, 0u);
+  unsigned nt = std::thread::hardware_concurrency();
+  nt = nt == 0 ? 4 : (nt > 16 ? 16 : nt);
+  std::vector<std::thread> th;
+  std::vector<long long> far(nt, 0);
+  const uint32_t nw = TSA_LOG2FIX_WORDS;
+  for (unsigned t = 0; t < nt; t++) {
+    th.emplace_back([&, t]() {
+      for (uint32_t w = t; w < nw; w += nt) {  // word w covers mantissas 16w .. 16w+15
+        uint32_t word = 0;
+        for (uint32_t j = 0; j < 16; j++) {
+          const uint32_t mant = w * 16 + j;
+          const float y = tsa_ffrom(0x3f800000u + mant);
+          const int32_t d = (int32_t)(tsa_fbits(log2f(y)) - tsa_fbits(tsa_log2f_core(y)));
+          uint32_t code = 0;
+          if (d == 1) code = 1;
+          else if (d == -1) code = 2;
+          else if (d != 0) far[t]++;
+          word |= code << (2 * j);
+        }
+        g_fix[w] = word;
+      }
+    });
+  }
+  for (auto& x : th) x.join();
+  for (long long f : far) g_fix_far += f;
+  if (tsa_fbits(log2f(2.0f)) != tsa_fbits(tsa_log2f_core(2.0f))) g_fix_far++;
+}
+
+// Sampled comparison of the restated expf / exp2f with this process's libm (the exhaustive comparison
+// is a test); any disagreement means the host libm is not the one the restatement was checked against.
+static long long libm_selftest() {
+  long long bad = 0;
+  uint32_t s = 0x12345678u;
+  for (int i = 0; i < (1 << 18); i++) {
+    s = s * 1664525u + 1013904223u;
+    const float x = tsa_ffrom(s);
+    const float a = expf(x), b = tsa_expf(x), c = exp2f(x), d = tsa_exp2f(x);
+    if (tsa_fbits(a) != tsa_fbits(b) && !(std::isnan(a) && std::isnan(b))) bad++;
+    if (tsa_fbits(c) != tsa_fbits(d) && !(std::isnan(c) && std::isnan(d))) bad++;
+  }
+  // the Metropolis range: -beta*dE in [-20, 0] on a fine grid
+  for (int i = 0; i < (1 << 18); i++) {
+    const float x = -20.0f * (float)i / (float)(1 << 18);
+    if (tsa_fbits(expf(x)) != tsa_fbits(tsa_expf(x))) bad++;
+  }
+  return bad;
+}
+
+static void build_lse(float* lse) {
+  for (int d = 0; d < 64; d++) lse[d] = (float)std::log2(1.0 + std::exp2(-(double)d));
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Layout and validation
+// ---------------------------------------------------------------------------------------------------
+extern "C" int tsa_layout(int32_t m, int32_t nlab, int32_t wide, tsa_layout_t* out) {
+  if (!out) return fail(nullptr, TSA_ERR_ARG, "tsa_layout: null output");
+  if (m < 3) return fail(nullptr, TSA_ERR_ARG, "need at least 3 tensors");
+  if (2 * m - 1 > 65535) return fail(nullptr, TSA_ERR_ARG, "too many tensors (node ids are 16-bit)");
+  if (nlab < 1) return fail(nullptr, TSA_ERR_ARG, "need at least one label");
+  tsa_layout_t L;
+  memset(&L, 0, sizeof L);
+  L.m = m;
+  L.nint = m - 1;
+  L.nlab = nlab;
+  const int w64 = (nlab + 63) / 64;
+  if (!wide && w64 <= 8) {
+    L.W = w64 <= 1 ? 1 : w64 <= 2 ? 2 : w64 <= 4 ? 4 : 8;
+    L.runtime_width = 0;
+  } else {
+    L.W = w64;
+    L.runtime_width = 1;
+  }
+  L.ch_off = L.nint * L.W;
+  L.s_off = L.ch_off + (L.nint + 1) / 2;
+  L.chain_words = (L.s_off + L.W + 1) & ~1;
+  *out = L;
+  return TSA_OK;
+}
+
+// Every chain must be a binary tree over all 2m-1 nodes rooted at 2m-2 (ids < 2m-1, each node reached
+// once); the kernels index label sets with these ids.  Reference check: csrc/treesa_gpu.cu:1127-1145.
+static bool valid_tree(const uint32_t* ch, int m, std::vector<char>& seen, std::vector<int>& st) {
+  const int n = 2 * m - 1;
+  seen.assign(n, 0);
+  st.clear();
+  st.push_back(n - 1);
+  int cnt = 0;
+  while (!st.empty()) {
+    const int v = st.back();
+    st.pop_back();
+    if (v < 0 || v >= n || seen[v]) return false;
+    seen[v] = 1;
+    cnt++;
+    if (v >= m) {
+      st.push_back((int)(ch[v - m] >> 16));
+      st.push_back((int)(ch[v - m] & 0xFFFFu));
+    }
+  }
+  return cnt == n;
+}
+
+// ---------------------------------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------------------------------
+static void free_ctx(tsa_ctx* c) {
+  if (!c) return;
+  if (c->d_rec) (void)hipFree(c->d_rec);
+  if (c->d_rec2) (void)hipFree(c->d_rec2);
+  if (c->d_leaf) (void)hipFree(c->d_leaf);
+  if (c->d_fix) (void)hipFree(c->d_fix);
+  if (c->d_stats) (void)hipFree(c->d_stats);
+  if (c->d_lc) (void)hipFree(c->d_lc);
+  if (c->d_sc) (void)hipFree(c->d_sc);
+  if (c->d_ns) (void)hipFree(c->d_ns);
+  if (c->d_anc) (void)hipFree(c->d_anc);
+  if (c->e0) (void)hipEventDestroy(c->e0);
+  if (c->e1) (void)hipEventDestroy(c->e1);
+  if (c->st) (void)hipStreamDestroy(c->st);
+  delete c;
+}
+
+static void fill_params(tsa_ctx* c, int32_t leaf_sc) {
+  TsaKParams& P = c->P;
+  memset(&P, 0, sizeof P);
+  P.m = c->lay.m;
+  P.nint = c->lay.nint;
+  P.W = c->lay.W;
+  P.ch_off = c->lay.ch_off;
+  P.s_off = c->lay.s_off;
+  P.chain_words = c->lay.chain_words;
+  P.leaf_sc = leaf_sc;
+  const tsa_config_t& C = c->cfg;
+  P.slicing = C.slicing ? 1 : 0;
+  P.slice_moves = C.slicing ? C.slice_moves : 0;
+  P.slice_every = C.slice_every > 0 ? C.slice_every : 1;
+  P.max_slices = C.max_slices > 0 ? C.max_slices : c->lay.nlab;
+  P.par_follow = C.par_follow;
+  P.par_band = C.par_band;
+  P.key0 = C.key0;
+  P.key1 = C.key1;
+  TsaModel& M = P.model;
+  M.sc_target = C.sc_target;
+  M.sc_weight = C.sc_weight;
+  M.lpeak = C.lpeak;
+  M.lbw = C.lbw;
+  M.llaunch = C.llaunch;
+  M.m0 = C.m0;
+  M.n0 = C.n0;
+  M.k0 = C.k0;
+  M.v2_l3launch = C.v2_l3launch;
+  M.v2_lperm2 = C.v2_lperm2;
+  M.v2_lcc_bit = C.v2_lcc_bit;
+  M.v2_lcc_cell = C.v2_lcc_cell;
+  M.v2_ltc_bit = C.v2_ltc_bit;
+  M.v2_ltc_pad = C.v2_ltc_pad;
+  M.v2_ltc_out = C.v2_ltc_out;
+  M.v2_lsmall_cell = C.v2_lsmall_cell;
+  M.v2_small_rank = C.v2_small_rank;
+  build_lse(P.lse);
+}
+
+extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t leaf_sc, const tsa_config_t* cfg,
+                          int32_t nchains, tsa_ctx** out) {
+  if (!lay || !leaf || !cfg || !out) return fail(nullptr, TSA_ERR_ARG, "tsa_create: null argument");
+  *out = nullptr;
+  tsa_layout_t chk;
+  if (tsa_layout(lay->m, lay->nlab, lay->runtime_width, &chk) != TSA_OK) return TSA_ERR_ARG;
+  if (memcmp(&chk, lay, sizeof chk) != 0) return fail(nullptr, TSA_ERR_ARG, "tsa_create: layout not from tsa_layout");
+  if (nchains < 1 || nchains > (1 << 24)) return fail(nullptr, TSA_ERR_ARG, "tsa_create: nchains out of range");
+  if (cfg->mode < 0 || cfg->mode > 2) return fail(nullptr, TSA_ERR_ARG, "tsa_create: mode must be 0, 1 or 2");
+  if (cfg->par_band == 1 || cfg->par_band < 0 || cfg->par_band > 16)
+    return fail(nullptr, TSA_ERR_ARG, "--par-band L: 0 (off) or 2..16");
+  if (cfg->slicing && cfg->slice_moves < 0) return fail(nullptr, TSA_ERR_ARG, "tsa_create: slice_moves < 0");
+  for (size_t i = 0; i < (size_t)lay->m * lay->W; i++) {
+    const int used = lay->nlab - 64 * (int)(i % lay->W);  // labels that word i may hold
+    if (used <= 0 ? leaf[i] != 0 : (used < 64 && (leaf[i] >> used) != 0))
+      return fail(nullptr, TSA_ERR_ARG, "tsa_create: leaf label out of range");
+  }
+
+  std::call_once(g_fix_once, build_log2_fix);
+  if (g_fix_far != 0)
+    return fail(nullptr, TSA_ERR_LIBM, "host libm log2f is more than 1 ulp from the restated log2f on [1, 2]");
+  static long long selftest = -1;
+  static std::mutex mu;
+  {
+    std::lock_guard<std::mutex> g(mu);
+    if (selftest < 0) selftest = libm_selftest();
+  }
+  if (selftest != 0) return fail(nullptr, TSA_ERR_LIBM, "host libm expf/exp2f differ from the restated algorithm");
+
+  tsa_ctx* c = new tsa_ctx();
+  c->lay = *lay;
+  c->cfg = *cfg;
+  c->mode = cfg->mode;
+  c->nchains = nchains;
+  fill_params(c, leaf_sc);
+
+  int dev = 0;
+  int lds_max = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+  if (e != hipSuccess) {
+    free_ctx(c);
+    return fail(nullptr, TSA_ERR_HIP, std::string("no HIP device: ") + hipGetErrorString(e));
+  }
+
+  // kernel choice: chain + leaf table in LDS when it fits and the width is a register width
+  const int nodew = tsa_node_words(lay->nint) + (cfg->par_band > 0 ? ((lay->nint + 3) & ~3) / 2 : 0);
+  const int nodew2 = (nodew + 1) & ~1;
+  const int leafw = (lay->m * lay->W + 1) & ~1;
+  const int per_wave_lds = lay->chain_words + nodew2;
+  const int ldsw = lds_max / 8;
+  const bool reg = !lay->runtime_width;
+  const bool lds_fits = reg && leafw + per_wave_lds <= ldsw;
+  bool use_lds;
+  if (cfg->kernel == TSA_KERNEL_LDS) {
+    if (!lds_fits) {
+      free_ctx(c);
+      return fail(nullptr, TSA_ERR_FIT, "chain does not fit in LDS (or the label width is not a register width)");
+    }
+    use_lds = true;
+  } else if (cfg->kernel == TSA_KERNEL_GLOBAL) {
+    use_lds = false;
+  } else {
+    use_lds = lds_fits;
+  }
+  if (use_lds) {
+    c->Wt = lay->W;
+    c->L.W = lay->W;
+    c->L.lds = 1;
+    c->L.lds_words = per_wave_lds;
+    int wpb = (ldsw - leafw) / per_wave_lds;
+    c->L.wpb = wpb < 1 ? 1 : (wpb > 4 ? 4 : wpb);
+  } else {
+    if (nodew2 > ldsw) {
+      free_ctx(c);
+      return fail(nullptr, TSA_ERR_FIT, "par: node arrays do not fit in LDS");
+    }
+    c->Wt = 0;
+    c->L.W = 0;
+    c->L.lds = 0;
+    c->L.lds_words = nodew2;
+    int wpb = ldsw / nodew2;
+    c->L.wpb = wpb < 1 ? 1 : (wpb > 4 ? 4 : wpb);
+  }
+  char kb[160];
+  snprintf(kb, sizeof kb, "%s W=%d waves/block=%d lds_bytes/wave=%d", use_lds ? "lds" : "global",
+           use_lds ? c->Wt : lay->W, c->L.wpb, c->L.lds_words * 8);
+  c->kname = kb;
+
+  const size_t recb = (size_t)nchains * lay->chain_words * 8;
+#define TSA_CREATE_HIP(call)                                                                       \
+  do {                                                                                            \
+    hipError_t e2 = (call);                                                                       \
+    if (e2 != hipSuccess) {                                                                       \
+      std::string m_ = std::string(#call) + ": " + hipGetErrorString(e2);                         \
+      free_ctx(c);                                                                                \
+      return fail(nullptr, TSA_ERR_HIP, m_);                                                      \
+    }                                                                                             \
+  } while (0)
+  TSA_CREATE_HIP(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking));
+  TSA_CREATE_HIP(hipEventCreate(&c->e0));
+  TSA_CREATE_HIP(hipEventCreate(&c->e1));
+  TSA_CREATE_HIP(hipMalloc(&c->d_rec, recb));
+  TSA_CREATE_HIP(hipMemsetAsync(c->d_rec, 0, recb, c->st));
+  TSA_CREATE_HIP(hipMalloc(&c->d_leaf, (size_t)lay->m * lay->W * 8));
+  TSA_CREATE_HIP(hipMemcpyAsync(c->d_leaf, leaf, (size_t)lay->m * lay->W * 8, hipMemcpyHostToDevice, c->st));
+  TSA_CREATE_HIP(hipMalloc(&c->d_fix, (size_t)TSA_LOG2FIX_WORDS * 4));
+  TSA_CREATE_HIP(hipMemcpyAsync(c->d_fix, g_fix.data(), (size_t)TSA_LOG2FIX_WORDS * 4, hipMemcpyHostToDevice, c->st));
+  TSA_CREATE_HIP(hipMalloc(&c->d_stats, TSA_NSTAT * sizeof(unsigned long long)));
+  TSA_CREATE_HIP(hipMemsetAsync(c->d_stats, 0, TSA_NSTAT * sizeof(unsigned long long), c->st));
+  TSA_CREATE_HIP(hipMalloc(&c->d_lc, (size_t)nchains * 4));
+  TSA_CREATE_HIP(hipMalloc(&c->d_sc, (size_t)nchains * 4));
+  TSA_CREATE_HIP(hipMalloc(&c->d_ns, (size_t)nchains * 4));
+  TSA_CREATE_HIP(hipMalloc(&c->d_anc, (size_t)nchains * 4));
+  TSA_CREATE_HIP(hipStreamSynchronize(c->st));
+#undef TSA_CREATE_HIP
+  *out = c;
+  return TSA_OK;
+}
+
+extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
+  if (!ctx || !population) return fail(ctx, TSA_ERR_ARG, "tsa_upload: null argument");
+  const tsa_layout_t& L = ctx->lay;
+  std::vector<char> seen;
+  std::vector<int> st;
+  for (int c = 0; c < ctx->nchains; c++) {
+    const uint64_t* rec = population + (size_t)c * L.chain_words;
+    if (!valid_tree(reinterpret_cast<const uint32_t*>(rec + L.ch_off), L.m, seen, st))
+      return fail(ctx, TSA_ERR_ARG, "tsa_upload: chain " + std::to_string(c) + " is not a valid tree");
+  }
+  TSA_HIP(ctx, hipMemcpyAsync(ctx->d_rec, population, (size_t)ctx->nchains * L.chain_words * 8,
+                              hipMemcpyHostToDevice, ctx->st));
+  TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  return TSA_OK;
+}
+
+extern "C" int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* out) {
+  if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_download: null argument");
+  if (c0 < 0 || count < 0 || c0 + count > ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_download: range");
+  const size_t cw = ctx->lay.chain_words;
+  TSA_HIP(ctx, hipMemcpyAsync(out, ctx->d_rec + (size_t)c0 * cw, (size_t)count * cw * 8, hipMemcpyDeviceToHost,
+                              ctx->st));
+  TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  return TSA_OK;
+}
+
+extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0, int32_t nsweeps) {
+  if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps: null context");
+  if (order != TSA_ORDER_PAR && order != TSA_ORDER_PREORDER) return fail(ctx, TSA_ERR_ARG, "--order par|preorder");
+  if (nsweeps < 0) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps: nsweeps < 0");
+  if (nsweeps == 0) return TSA_OK;
+  TSA_HIP(ctx, hipEventRecord(ctx->e0, ctx->st));
+  TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains,
+                                 beta, sweep0, nsweeps, ctx->d_stats, ctx->st));
+  TSA_HIP(ctx, hipEventRecord(ctx->e1, ctx->st));
+  ctx->pending = true;
+  return TSA_OK;
+}
+
+extern "C" int tsa_sweeps_ms(tsa_ctx* ctx, double* ms) {
+  if (!ctx || !ms) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps_ms: null argument");
+  *ms = 0.0;
+  if (!ctx->pending) return TSA_OK;
+  TSA_HIP(ctx, hipEventSynchronize(ctx->e1));
+  float f = 0.f;
+  TSA_HIP(ctx, hipEventElapsedTime(&f, ctx->e0, ctx->e1));
+  ctx->pending = false;
+  *ms = (double)f;
+  return TSA_OK;
+}
+
+extern "C" int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns) {
+  if (!ctx || !lc || !sc || !ns) return fail(ctx, TSA_ERR_ARG, "tsa_energy: null argument");
+  TSA_HIP(ctx, tsa_launch_energy(ctx->Wt, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains,
+                                 ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->st));
+  const size_t b = (size_t)ctx->nchains * 4;
+  TSA_HIP(ctx, hipMemcpyAsync(lc, ctx->d_lc, b, hipMemcpyDeviceToHost, ctx->st));
+  TSA_HIP(ctx, hipMemcpyAsync(sc, ctx->d_sc, b, hipMemcpyDeviceToHost, ctx->st));
+  TSA_HIP(ctx, hipMemcpyAsync(ns, ctx->d_ns, b, hipMemcpyDeviceToHost, ctx->st));
+  TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  return TSA_OK;
+}
+
+extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
+  if (!ctx || !anc) return fail(ctx, TSA_ERR_ARG, "tsa_resample: null argument");
+  for (int c = 0; c < ctx->nchains; c++)
+    if (anc[c] < 0 || anc[c] >= ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_resample: ancestor out of range");
+  if (!ctx->d_rec2) TSA_HIP(ctx, hipMalloc(&ctx->d_rec2, (size_t)ctx->nchains * ctx->lay.chain_words * 8));
+  TSA_HIP(ctx, hipMemcpyAsync(ctx->d_anc, anc, (size_t)ctx->nchains * 4, hipMemcpyHostToDevice, ctx->st));
+  TSA_HIP(ctx, tsa_launch_copy(ctx->d_rec, ctx->d_rec2, ctx->d_anc, ctx->nchains, ctx->lay.chain_words, ctx->st));
+  TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  std::swap(ctx->d_rec, ctx->d_rec2);
+  return TSA_OK;
+}
+
+extern "C" int tsa_set_mode(tsa_ctx* ctx, int32_t mode) {
+  if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: null context");
+  if (mode < 0 || mode > 2) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: mode must be 0, 1 or 2");
+  ctx->mode = mode;
+  return TSA_OK;
+}
+
+extern "C" int tsa_stats(tsa_ctx* ctx, uint64_t out[7]) {
+  if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_stats: null argument");
+  unsigned long long s[TSA_NSTAT];
+  TSA_HIP(ctx, hipMemcpyAsync(s, ctx->d_stats, sizeof s, hipMemcpyDeviceToHost, ctx->st));
+  TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  for (int i = 0; i < TSA_NSTAT; i++) out[i] = s[i];
+  return TSA_OK;
+}
+
+extern "C" int tsa_describe(tsa_ctx* ctx, char* buf, int32_t len) {
+  if (!ctx || !buf || len < 1) return fail(ctx, TSA_ERR_ARG, "tsa_describe: null argument");
+  snprintf(buf, (size_t)len, "%s", ctx->kname.c_str());
+  return TSA_OK;
+}
+
+extern "C" int tsa_destroy(tsa_ctx* ctx) {
+  if (!ctx) return TSA_OK;
+  if (ctx->st) (void)hipStreamSynchronize(ctx->st);
+  free_ctx(ctx);
+  return TSA_OK;
+}
+
+extern "C" const char* tsa_last_error(const tsa_ctx* ctx) { return ctx ? ctx->err.c_str() : g_err.c_str(); }
+
+extern "C" float tsa_host_math(int32_t which, float x) {
+  if (which == 0) return tsa_expf(x);
+  if (which == 1) return tsa_exp2f(x);
+  std::call_once(g_fix_once, build_log2_fix);
+  return tsa_log2f_12(x, g_fix.data());
+}

@@ -1,0 +1,601 @@
+// tsa_kernels.hip -- TreeSA sweep kernels for gfx950 (MI355X).
+//
+// One wave64 owns one chain.  A workgroup holds several waves (chains) that never wait on each other
+// after the prologue.  When the chain record fits, it is staged in LDS together with the shared leaf
+// table (LDS variant: every label-set access is a ds_read); otherwise the record stays in HBM and only
+// the per-node arrays live in LDS (global variant, runtime label width).
+//
+// A sweep gives every internal node exactly one proposal.  Par order (the reference's k_par,
+// csrc/treesa_gpu.cu:829-997): random 16-bit priorities per node and sweep; each phase scans all
+// internal nodes, compacts the independent set (unvisited nodes whose (priority, id) key beats their
+// unvisited parent and internal children) into a work list with a 64-lane ballot, and visits it 64
+// nodes at a time, one node per lane.  Pre-order (the reference's k_warp, csrc/treesa_gpu.cu:585-722):
+// a work list of ready nodes (parent already visited), up to 64 visited per step, children pushed by
+// ballot prefix.  Every visit draws Philox((node, sweep, chain)), so both mappings reproduce the CPU
+// recursion and the CPU phase-by-phase sweep bit for bit.
+//
+// Wave-local ordering: lanes of one wave exchange data only through LDS/global words that a later
+// instruction of the same wave reads; tsa_wave_sync() (wavefront-scope release/acquire fences around
+// a wave barrier) keeps the compiler from moving those accesses across the exchange points.
+#include "tsa_kernels.h"
+
+struct TsaEvalOut {
+  float lcost;
+  int sc, sc_int, ncand, ns;
+};
+
+__device__ __forceinline__ void tsa_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ uint64_t tsa_lt_mask(int lane) { return (1ull << lane) - 1ull; }
+
+// position of the n-th (0-based) set bit of x, n < popc(x)
+__device__ __forceinline__ int tsa_nth_bit(uint64_t x, int n) {
+  for (int k = 0; k < n; k++) x &= x - 1;
+  return __ffsll((unsigned long long)x) - 1;
+}
+
+// n-th label (set bit) of A & ~S over NW words; S may be null (csrc/treesa_gpu.cu:125-133)
+__device__ __forceinline__ int tsa_nth_label(const uint64_t* A, const uint64_t* S, int NW, int n) {
+  for (int w = 0; w < NW; w++) {
+    const uint64_t a = A[w] & (S ? ~S[w] : ~0ull);
+    const int c = __popcll(a);
+    if (n < c) return w * 64 + tsa_nth_bit(a, n);
+    n -= c;
+  }
+  return -1;
+}
+
+struct TsaVisit {
+  uint32_t cw;  // the visited node's children word after the visit
+  int Pn, On, Mn;
+  bool prop, acc;
+};
+
+// One proposal at internal node v by one lane (csrc/treesa_gpu.cu:156-235; CPU twin
+// csrc/cpu_ref.h:87-126).  lf: leaf sets (m*NW words), lab: internal sets, ch: children words, Sm: slice
+// set or null.  With P the pivot child, O the other child, M the grandchild under P that moves up and K
+// the one that stays, every rule swaps M and O, and P gets X = (K|O)&(M|d).
+template <int W, int MODE>
+__device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab, uint32_t* ch, const uint64_t* Sm,
+                                              const uint64_t* lf, const uint32_t* __restrict__ fix, int v, float beta,
+                                              uint32_t sw, uint32_t chain) {
+  const int m = P.m;
+  const int NW = W > 0 ? W : P.W;
+  TsaVisit o;
+  o.prop = false;
+  o.acc = false;
+  o.Pn = o.On = o.Mn = 0;
+  const uint32_t chv = ch[v - m];
+  o.cw = chv;
+  const int l = (int)(chv & 0xFFFFu), r = (int)(chv >> 16);
+  const bool li = l >= m, ri = r >= m;
+  if (!li && !ri) return o;
+  const TsaU4 rnd = tsa_philox(TsaU4{(uint32_t)v, sw, chain, 0u}, P.key0, P.key1);
+  const int rule = tsa_pick_rule(li, ri, rnd.x);
+  const int slotP = tsa_slot_p(rule), slotM = tsa_slot_m(rule);
+  const int Pn = slotP ? r : l, On = slotP ? l : r;
+  const uint32_t chp = ch[Pn - m];
+  const int Mn = slotM ? (int)(chp >> 16) : (int)(chp & 0xFFFFu);
+  const int Kn = slotM ? (int)(chp & 0xFFFFu) : (int)(chp >> 16);
+  uint64_t* pP = lab + (size_t)(Pn - m) * NW;
+  const uint64_t* pD = lab + (size_t)(v - m) * NW;
+  const uint64_t* pO = On >= m ? lab + (size_t)(On - m) * NW : lf + (size_t)On * NW;
+  const uint64_t* pK = Kn >= m ? lab + (size_t)(Kn - m) * NW : lf + (size_t)Kn * NW;
+  const uint64_t* pM = Mn >= m ? lab + (size_t)(Mn - m) * NW : lf + (size_t)Mn * NW;
+  TsaCounts cnt;
+  tsa_counts_zero(cnt);
+  bool acc;
+  if constexpr (W > 0) {
+    uint64_t X[W];
+#pragma unroll
+    for (int i = 0; i < W; i++) {
+      const uint64_t d = pD[i], p = pP[i], oo = pO[i], k = pK[i], mm = pM[i];
+      const uint64_t x = (k | oo) & (mm | d);
+      X[i] = x;
+      const uint64_t nm = Sm ? ~Sm[i] : ~0ull;
+      tsa_acc<MODE>(cnt, k & nm, mm & nm, p & nm, oo & nm, d & nm, x & nm);
+    }
+    const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, P.lse, fix);
+    acc = tsa_metropolis(rnd.y, beta, dE);
+    if (acc) {
+#pragma unroll
+      for (int i = 0; i < W; i++) pP[i] = X[i];
+    }
+  } else {
+    for (int i = 0; i < NW; i++) {
+      const uint64_t d = pD[i], p = pP[i], oo = pO[i], k = pK[i], mm = pM[i];
+      const uint64_t x = (k | oo) & (mm | d);
+      const uint64_t nm = Sm ? ~Sm[i] : ~0ull;
+      tsa_acc<MODE>(cnt, k & nm, mm & nm, p & nm, oo & nm, d & nm, x & nm);
+    }
+    const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, P.lse, fix);
+    acc = tsa_metropolis(rnd.y, beta, dE);
+    if (acc)
+      for (int i = 0; i < NW; i++) pP[i] = (pK[i] | pO[i]) & (pM[i] | pD[i]);
+  }
+  o.prop = true;
+  if (acc) {
+    const uint32_t nchp = slotM ? ((chp & 0xFFFFu) | ((uint32_t)On << 16)) : ((chp & 0xFFFF0000u) | (uint32_t)On);
+    const uint32_t nchv = slotP ? ((chv & 0xFFFF0000u) | (uint32_t)Mn) : ((chv & 0xFFFFu) | ((uint32_t)Mn << 16));
+    ch[Pn - m] = nchp;
+    ch[v - m] = nchv;
+    o.cw = nchv;
+  }
+  o.acc = acc;
+  o.Pn = Pn;
+  o.On = On;
+  o.Mn = Mn;
+  return o;
+}
+
+// Whole-chain evaluation by a 32-lane group (l32 = lane within the group), in the reference's fold
+// order (csrc/treesa_gpu.cu:386-434): lane t folds nodes t, t+32, ... with lse_f starting from -inf,
+// then an xor butterfly 16, 8, 4, 2, 1 combines the lanes; sc, the number of internal nodes of maximal
+// masked size and |S| are integer reductions.  Costs use label sets masked by ~S (S may be null).
+template <int W, int MODE>
+__device__ TsaEvalOut tsa_eval32(const TsaKParams& P, const uint64_t* lab, const uint32_t* ch, const uint64_t* S,
+                                 const uint64_t* lf, const uint32_t* __restrict__ fix, int l32) {
+  const int NW = W > 0 ? W : P.W, m = P.m;
+  float acc = -INFINITY;
+  int scl = 0, cntl = 0;
+  for (int i = l32; i < P.nint; i += 32) {
+    const uint32_t cw = ch[i];
+    const int l = (int)(cw & 0xFFFFu), r = (int)(cw >> 16);
+    const uint64_t* x = l >= m ? lab + (size_t)(l - m) * NW : lf + (size_t)l * NW;
+    const uint64_t* y = r >= m ? lab + (size_t)(r - m) * NW : lf + (size_t)r * NW;
+    const uint64_t* z = lab + (size_t)i * NW;
+    int B = 0, M = 0, N = 0, K = 0, Z = 0;
+    for (int w = 0; w < NW; w++) {
+      const uint64_t nm = S ? ~S[w] : ~0ull;
+      const uint64_t zz = z[w] & nm;
+      tsa_count3(x[w] & nm, y[w] & nm, zz, B, M, N, K);
+      Z += __popcll(zz);
+    }
+    acc = tsa_lse_f(acc, tsa_node_cost<MODE>(B, M, N, K, Z, P.model, fix), fix);
+    if (Z > scl) {
+      scl = Z;
+      cntl = 1;
+    } else if (Z == scl) {
+      cntl++;
+    }
+  }
+  int scmax = scl;
+  for (int o = 16; o > 0; o >>= 1) {
+    acc = tsa_lse_f(acc, __shfl_xor(acc, o, 32), fix);
+    const int t = __shfl_xor(scmax, o, 32);
+    scmax = scmax > t ? scmax : t;
+  }
+  int cnt = (scl == scmax) ? cntl : 0, ns = 0;
+  if (S)
+    for (int w = l32; w < NW; w += 32) ns += __popcll(S[w]);
+  for (int o = 16; o > 0; o >>= 1) {
+    cnt += __shfl_xor(cnt, o, 32);
+    ns += __shfl_xor(ns, o, 32);
+  }
+  int sc = scmax > P.leaf_sc ? scmax : P.leaf_sc;
+  if (S && P.leaf_sc > scmax) {  // a leaf may be the largest tensor: masked leaf sizes
+    int ll = 0;
+    for (int i = l32; i < m; i += 32) {
+      int Z = 0;
+      for (int w = 0; w < NW; w++) Z += __popcll(lf[(size_t)i * NW + w] & ~S[w]);
+      ll = ll > Z ? ll : Z;
+    }
+    for (int o = 16; o > 0; o >>= 1) {
+      const int t = __shfl_xor(ll, o, 32);
+      ll = ll > t ? ll : t;
+    }
+    sc = scmax > ll ? scmax : ll;
+  }
+  TsaEvalOut e;
+  e.lcost = acc;
+  e.sc = sc;
+  e.sc_int = scmax;
+  e.ncand = cnt;
+  e.ns = ns;
+  return e;
+}
+
+// E = |S| + log2(per-slice cost) + sc_weight * max(0, sc - sc_target), in float
+// (csrc/treesa_gpu.cu:436-439).
+__device__ __forceinline__ float tsa_slice_energy(const TsaEvalOut& e, const TsaKParams& P) {
+  const float pen = (float)e.sc > P.model.sc_target ? P.model.sc_weight * ((float)e.sc - P.model.sc_target) : 0.0f;
+  return (float)e.ns + e.lcost + pen;
+}
+
+// Slice moves of one chain by one wave (csrc/treesa_gpu.cu:445-502).  Both 32-lane halves run the
+// reference's 32-lane algorithm on the same data; lane 0 alone writes S.
+template <int W, int MODE>
+__device__ void tsa_slice_step(const TsaKParams& P, const uint64_t* lab, const uint32_t* ch, uint64_t* S,
+                               const uint64_t* lf, const uint32_t* __restrict__ fix, float beta, uint32_t sw,
+                               uint32_t chain, int lane, int& nsp, int& nsa) {
+  const int NW = W > 0 ? W : P.W;
+  const int l32 = lane & 31;
+  TsaEvalOut cur = tsa_eval32<W, MODE>(P, lab, ch, S, lf, fix, l32);
+  float Ecur = tsa_slice_energy(cur, P);
+  for (int j = 0; j < P.slice_moves; j++) {
+    const TsaU4 r1 = tsa_philox(TsaU4{0x10000u + 2u * (uint32_t)j, sw, chain, 0u}, P.key0, P.key1);
+    const TsaU4 r2 = tsa_philox(TsaU4{0x10001u + 2u * (uint32_t)j, sw, chain, 0u}, P.key0, P.key1);
+    int type;  // 0 add, 1 remove, 2 swap
+    if (cur.ns == 0) type = 0;
+    else if (cur.ns >= P.max_slices) type = (r1.x >> 31) ? 1 : 2;
+    else type = r1.x < 0x80000000u ? 0 : (r1.x < 0xC0000000u ? 1 : 2);
+    int ladd = -1, lrem = -1;
+    if (type != 1 && cur.ncand > 0 && cur.sc_int > 0) {
+      // the (r1.y % ncand)-th internal node of maximal masked size, in node-id order
+      int rr = (int)(r1.y % (uint32_t)cur.ncand), node = -1;
+      for (int base = 0; base < P.nint && node < 0; base += 32) {
+        const int i = base + l32;
+        int Z = -1;
+        if (i < P.nint) {
+          Z = 0;
+          const uint64_t* z = lab + (size_t)i * NW;
+          for (int w = 0; w < NW; w++) Z += __popcll(z[w] & ~S[w]);
+        }
+        const uint32_t b = (uint32_t)(__ballot(Z == cur.sc_int) >> (lane & 32));
+        const int c = __popc(b);
+        if (rr < c) node = base + tsa_nth_bit(b, rr);
+        else rr -= c;
+      }
+      if (node >= 0) ladd = tsa_nth_label(lab + (size_t)node * NW, S, NW, (int)(r1.z % (uint32_t)cur.sc_int));
+    }
+    if (type != 0) lrem = tsa_nth_label(S, nullptr, NW, (int)(r1.w % (uint32_t)cur.ns));
+    if (type == 2 && ladd < 0) type = 1;
+    if (type == 0 && ladd < 0) continue;
+    tsa_wave_sync();
+    if (lane == 0) {
+      if (type != 1) S[ladd >> 6] |= 1ull << (ladd & 63);
+      if (type != 0) S[lrem >> 6] &= ~(1ull << (lrem & 63));
+    }
+    tsa_wave_sync();
+    const TsaEvalOut nxt = tsa_eval32<W, MODE>(P, lab, ch, S, lf, fix, l32);
+    const float Enew = tsa_slice_energy(nxt, P);
+    nsp++;
+    if (tsa_metropolis(r2.x, beta, Enew - Ecur)) {
+      nsa++;
+      cur = nxt;
+      Ecur = Enew;
+    } else {
+      tsa_wave_sync();
+      if (lane == 0) {
+        if (type != 1) S[ladd >> 6] &= ~(1ull << (ladd & 63));
+        if (type != 0) S[lrem >> 6] |= 1ull << (lrem & 63);
+      }
+      tsa_wave_sync();
+    }
+  }
+}
+
+__device__ __forceinline__ long long tsa_wave_sum(long long x) {
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+// Sweep kernel.  ORDER 0: par, 1: pre-order.  LDS: chain and leaf table staged in LDS.
+// LDS layout (words): [leaf table (LDS variant only), rounded to even] then per wave lds_words:
+// [chain record (LDS variant only)][pri u16 x nint4][par u16 x nint4][work list u16 x nint4]
+// [band words u32 x nint4 when par_band > 0].
+template <int W, int MODE, int ORDER, bool LDS>
+__global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restrict__ rec,
+                                               const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
+                                               int nchains, int lds_words, float beta, uint32_t sweep0, int nsweeps,
+                                               unsigned long long* __restrict__ stats) {
+  extern __shared__ uint64_t tsa_smem[];
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, wpb = blockDim.x >> 6;
+  const int NW = W > 0 ? W : P.W;
+  const int m = P.m, nint = P.nint, nint4 = (nint + 3) & ~3;
+  const uint64_t* lf = leaf;
+  int leafw = 0;
+  if constexpr (LDS) {
+    leafw = (m * NW + 1) & ~1;
+    for (int i = threadIdx.x; i < m * NW; i += blockDim.x) tsa_smem[i] = leaf[i];
+    __syncthreads();
+    lf = tsa_smem;
+  }
+  const int c = blockIdx.x * wpb + wv;
+  if (c >= nchains) return;  // whole waves; no workgroup barrier below this point
+  uint64_t* const g = rec + (size_t)c * P.chain_words;
+  uint64_t* const wbase = tsa_smem + leafw + (size_t)wv * lds_words;
+  uint64_t* base;
+  uint16_t* nodes;
+  if constexpr (LDS) {
+    base = wbase;
+    const uint4* src = reinterpret_cast<const uint4*>(g);
+    uint4* dst = reinterpret_cast<uint4*>(base);
+    for (int i = lane; i < P.chain_words / 2; i += 64) dst[i] = src[i];
+    nodes = reinterpret_cast<uint16_t*>(base + P.chain_words);
+  } else {
+    base = g;
+    nodes = reinterpret_cast<uint16_t*>(wbase);
+  }
+  uint64_t* const lab = base;
+  uint32_t* const ch = reinterpret_cast<uint32_t*>(base + P.ch_off);
+  uint64_t* const S = base + P.s_off;
+  const uint64_t* const Sm = P.slicing ? S : nullptr;
+  uint16_t* const pri = nodes;
+  uint16_t* const par = nodes + nint4;
+  uint16_t* const wl = par + nint4;
+  uint32_t* const dw = reinterpret_cast<uint32_t*>(wl + nint4);
+  int np = 0, na = 0, nst = 0, nv = 0, nsp = 0, nsa = 0, nbusy = 0;
+  tsa_wave_sync();
+
+  if constexpr (ORDER == 0) {
+    for (int i = lane; i < nint; i += 64) {
+      const uint32_t cw = ch[i];
+      const int l = (int)(cw & 0xFFFFu), r = (int)(cw >> 16);
+      if (l >= m) par[l - m] = (uint16_t)(m + i);
+      if (r >= m) par[r - m] = (uint16_t)(m + i);
+    }
+    if (lane == 0) par[nint - 1] = 0xFFFFu;
+    tsa_wave_sync();
+    for (int s = 0; s < nsweeps; s++) {
+      const uint32_t sw = sweep0 + (uint32_t)s;
+      const uint32_t hs = tsa_sweep_hash(sw, (uint32_t)c, P.key0);
+      for (int i = lane; i < nint; i += 64) pri[i] = (uint16_t)tsa_par_pri((uint32_t)(m + i), hs);
+      if (P.par_band > 0) {
+        // depth at sweep start by pointer jumping on (depth << 16 | ancestor) words; an update that reads
+        // an already advanced ancestor word still keeps depth(v) = d + depth(ancestor)
+        for (int i = lane; i < nint; i += 64) dw[i] = par[i] == 0xFFFFu ? 0xFFFFu : (0x10000u | par[i]);
+        tsa_wave_sync();
+        for (;;) {
+          bool any = false;
+          for (int i = lane; i < nint; i += 64) {
+            const uint32_t w = dw[i], a = w & 0xFFFFu;
+            if (a != 0xFFFFu) {
+              const uint32_t w2 = dw[a - m];
+              dw[i] = ((w & 0xFFFF0000u) + (w2 & 0xFFFF0000u)) | (w2 & 0xFFFFu);
+              any = true;
+            }
+          }
+          tsa_wave_sync();
+          if (__ballot(any) == 0ull) break;
+        }
+        const int L = P.par_band;
+        for (int i = lane; i < nint; i += 64)
+          pri[i] = (uint16_t)((((uint32_t)((L - 1 - (int)(dw[i] >> 16) % L) & 15)) << 12) | (pri[i] & 0x0FFEu) | 1u);
+      }
+      tsa_wave_sync();
+      for (;;) {
+        // scan: the phase's independent set into the work list
+        int cnt = 0;
+        for (int i0 = 0; i0 < nint; i0 += 64) {
+          const int i = i0 + lane;
+          bool act = false;
+          if (i < nint) {
+            const uint32_t pv = pri[i];
+            if (pv) {
+              const uint32_t key = (pv << 16) | (uint32_t)(m + i);
+              act = true;
+              const uint32_t p = par[i];
+              if (p != 0xFFFFu) {
+                const uint32_t pp = pri[p - m];
+                if (pp && ((pp << 16) | p) > key) act = false;
+              }
+              const uint32_t cw = ch[i];
+              const uint32_t l = cw & 0xFFFFu, r = cw >> 16;
+              if (act && l >= (uint32_t)m) {
+                const uint32_t pl = pri[l - m];
+                if (pl && ((pl << 16) | l) > key) act = false;
+              }
+              if (act && r >= (uint32_t)m) {
+                const uint32_t pr = pri[r - m];
+                if (pr && ((pr << 16) | r) > key) act = false;
+              }
+            }
+          }
+          const uint64_t b = __ballot(act);
+          if (act) wl[cnt + __popcll(b & tsa_lt_mask(lane))] = (uint16_t)(m + i);
+          cnt += __popcll(b);
+        }
+        if (cnt == 0) break;
+        nst++;
+        tsa_wave_sync();
+        for (int b0 = 0; b0 < cnt; b0 += 64) {
+          const int j = b0 + lane;
+          if (j < cnt) {
+            const int v = wl[j];
+            const bool rev = (pri[v - m] & 1u) == 0;  // a follow-up visit draws its own numbers
+            const uint32_t swv = sw | (rev ? 0x80000000u : 0u);
+            const TsaVisit o = tsa_visit<W, MODE>(P, lab, ch, Sm, lf, fix, v, beta, swv, (uint32_t)c);
+            nv++;
+            nbusy++;
+            np += o.prop;
+            if (o.acc) {
+              na++;
+              if (o.On >= m) par[o.On - m] = (uint16_t)o.Pn;
+              if (o.Mn >= m) par[o.Mn - m] = (uint16_t)v;
+              if (P.par_follow && !rev && pri[o.Pn - m] == 0)
+                pri[o.Pn - m] = (uint16_t)tsa_follow_pri((uint32_t)o.Pn, hs);
+            }
+            pri[v - m] = 0;
+          }
+        }
+        tsa_wave_sync();
+      }
+      if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
+        tsa_slice_step<W, MODE>(P, lab, ch, S, lf, fix, beta, sw, (uint32_t)c, lane, nsp, nsa);
+        tsa_wave_sync();
+      }
+    }
+  } else {
+    const int root = 2 * m - 2;
+    for (int s = 0; s < nsweeps; s++) {
+      const uint32_t sw = sweep0 + (uint32_t)s;
+      if (lane == 0) wl[0] = (uint16_t)root;
+      int sp = 1;
+      tsa_wave_sync();
+      while (sp > 0) {
+        const int k = sp < 64 ? sp : 64, b0 = sp - k;
+        const int v = lane < k ? (int)wl[b0 + lane] : 0;
+        tsa_wave_sync();  // every lane has read its node before pushes overwrite the list
+        uint32_t cw = 0;
+        if (lane < k) {
+          const TsaVisit o = tsa_visit<W, MODE>(P, lab, ch, Sm, lf, fix, v, beta, sw, (uint32_t)c);
+          cw = o.cw;
+          nv++;
+          nbusy++;
+          np += o.prop;
+          na += o.acc;
+        }
+        nst++;
+        const bool c1 = lane < k && (int)(cw & 0xFFFFu) >= m;
+        const bool c2 = lane < k && (int)(cw >> 16) >= m;
+        const uint64_t b1 = __ballot(c1), b2 = __ballot(c2);
+        int pos = b0 + __popcll(b1 & tsa_lt_mask(lane)) + __popcll(b2 & tsa_lt_mask(lane));
+        if (c2) wl[pos++] = (uint16_t)(cw >> 16);
+        if (c1) wl[pos] = (uint16_t)(cw & 0xFFFFu);
+        sp = b0 + __popcll(b1) + __popcll(b2);
+        tsa_wave_sync();
+      }
+      if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
+        tsa_slice_step<W, MODE>(P, lab, ch, S, lf, fix, beta, sw, (uint32_t)c, lane, nsp, nsa);
+        tsa_wave_sync();
+      }
+    }
+  }
+
+  if constexpr (LDS) {
+    tsa_wave_sync();
+    const uint4* src = reinterpret_cast<const uint4*>(base);
+    uint4* dst = reinterpret_cast<uint4*>(g);
+    for (int i = lane; i < P.chain_words / 2; i += 64) dst[i] = src[i];
+  }
+  const long long sp_ = tsa_wave_sum(np), sa_ = tsa_wave_sum(na), sv_ = tsa_wave_sum(nv), sb_ = tsa_wave_sum(nbusy);
+  if (lane == 0) {
+    atomicAdd(&stats[TSA_ST_PROP], (unsigned long long)sp_);
+    atomicAdd(&stats[TSA_ST_ACC], (unsigned long long)sa_);
+    atomicAdd(&stats[TSA_ST_STEPS], (unsigned long long)nst);
+    atomicAdd(&stats[TSA_ST_VISITS], (unsigned long long)sv_);
+    atomicAdd(&stats[TSA_ST_SPROP], (unsigned long long)nsp);
+    atomicAdd(&stats[TSA_ST_SACC], (unsigned long long)nsa);
+    atomicAdd(&stats[TSA_ST_BUSY], (unsigned long long)sb_);
+  }
+}
+
+// Per-chain energy, one 32-lane half-wave per chain (csrc/treesa_gpu.cu:999-1014).
+template <int W, int MODE>
+__global__ void __launch_bounds__(256) k_energy(TsaKParams P, const uint64_t* __restrict__ rec,
+                                                const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
+                                                int nchains, float* __restrict__ lc, int* __restrict__ sc,
+                                                int* __restrict__ ns) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int c = t >> 5, l32 = threadIdx.x & 31;
+  const int cc = c < nchains ? c : nchains - 1;  // a half-wave past the end duplicates the last chain
+  const uint64_t* lab = rec + (size_t)cc * P.chain_words;
+  const uint32_t* ch = reinterpret_cast<const uint32_t*>(lab + P.ch_off);
+  const uint64_t* S = P.slicing ? lab + P.s_off : nullptr;
+  const TsaEvalOut e = tsa_eval32<W, MODE>(P, lab, ch, S, leaf, fix, l32);
+  if (l32 == 0 && c < nchains) {
+    lc[c] = e.lcost;
+    sc[c] = e.sc;
+    ns[c] = e.ns;
+  }
+}
+
+// Population resampling: dst chain c <- src chain anc[c] (csrc/treesa_gpu.cu:1016-1022).
+__global__ void __launch_bounds__(256) k_copy(const uint4* __restrict__ src, uint4* __restrict__ dst,
+                                              const int* __restrict__ anc, int n4) {
+  const uint4* s = src + (size_t)anc[blockIdx.x] * n4;
+  uint4* d = dst + (size_t)blockIdx.x * n4;
+  for (int i = threadIdx.x; i < n4; i += blockDim.x) d[i] = s[i];
+}
+
+// ---------------------------------------------------------------------------------------------------
+// Host-side launchers
+// ---------------------------------------------------------------------------------------------------
+template <int W, int MODE, int ORDER, bool LDS>
+static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
+                                 const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
+                                 unsigned long long* stats, hipStream_t st) {
+  const int NW = W > 0 ? W : P.W;
+  const size_t leafw = LDS ? (size_t)((P.m * NW + 1) & ~1) : 0;
+  const size_t smem = (leafw + (size_t)L.wpb * L.lds_words) * 8;
+  static size_t attr_set = 0;
+  if (smem > 65536 && smem > attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_sweep<W, MODE, ORDER, LDS>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (e != hipSuccess) return e;
+    attr_set = smem;
+  }
+  const int grid = (nchains + L.wpb - 1) / L.wpb;
+  hipLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS>), dim3(grid), dim3(64 * L.wpb), smem, st, P, rec, leaf, fix,
+                     nchains, L.lds_words, beta, sweep0, nsweeps, stats);
+  return hipGetLastError();
+}
+
+template <int W, int MODE>
+static hipError_t launch_sweep_wm(const TsaLaunch& L, int order, const TsaKParams& P, uint64_t* rec,
+                                  const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
+                                  int nsweeps, unsigned long long* stats, hipStream_t st) {
+  if constexpr (W > 0) {
+    if (L.lds) {
+      if (order == 0) return launch_sweep_t<W, MODE, 0, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+      return launch_sweep_t<W, MODE, 1, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+    }
+    return hipErrorInvalidValue;  // the register-width kernels exist only in the LDS variant
+  } else {
+    if (L.lds) return hipErrorInvalidValue;
+    if (order == 0) return launch_sweep_t<0, MODE, 0, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+    return launch_sweep_t<0, MODE, 1, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+  }
+}
+
+template <int W>
+static hipError_t launch_sweep_w(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
+                                 const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
+                                 int nsweeps, unsigned long long* stats, hipStream_t st) {
+  if (mode == 0) return launch_sweep_wm<W, 0>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+  if (mode == 1) return launch_sweep_wm<W, 1>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+  return launch_sweep_wm<W, 2>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+}
+
+hipError_t tsa_launch_sweeps(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
+                             const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
+                             int nsweeps, unsigned long long* stats, hipStream_t st) {
+  switch (L.W) {
+    case 1: return launch_sweep_w<1>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+    case 2: return launch_sweep_w<2>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+    case 4: return launch_sweep_w<4>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+    case 8: return launch_sweep_w<8>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+    case 0: return launch_sweep_w<0>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+template <int W, int MODE>
+static hipError_t launch_energy_t(const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf, const uint32_t* fix,
+                                  int nchains, float* lc, int* sc, int* ns, hipStream_t st) {
+  const int threads = 256, grid = (nchains * 32 + threads - 1) / threads;
+  hipLaunchKernelGGL((k_energy<W, MODE>), dim3(grid), dim3(threads), 0, st, P, rec, leaf, fix, nchains, lc, sc, ns);
+  return hipGetLastError();
+}
+
+template <int W>
+static hipError_t launch_energy_w(int mode, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
+                                  const uint32_t* fix, int nchains, float* lc, int* sc, int* ns, hipStream_t st) {
+  if (mode == 0) return launch_energy_t<W, 0>(P, rec, leaf, fix, nchains, lc, sc, ns, st);
+  if (mode == 1) return launch_energy_t<W, 1>(P, rec, leaf, fix, nchains, lc, sc, ns, st);
+  return launch_energy_t<W, 2>(P, rec, leaf, fix, nchains, lc, sc, ns, st);
+}
+
+hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
+                             const uint32_t* fix, int nchains, float* lc, int* sc, int* ns, hipStream_t st) {
+  switch (Wt) {
+    case 1: return launch_energy_w<1>(mode, P, rec, leaf, fix, nchains, lc, sc, ns, st);
+    case 2: return launch_energy_w<2>(mode, P, rec, leaf, fix, nchains, lc, sc, ns, st);
+    case 4: return launch_energy_w<4>(mode, P, rec, leaf, fix, nchains, lc, sc, ns, st);
+    case 8: return launch_energy_w<8>(mode, P, rec, leaf, fix, nchains, lc, sc, ns, st);
+    case 0: return launch_energy_w<0>(mode, P, rec, leaf, fix, nchains, lc, sc, ns, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t tsa_launch_copy(const uint64_t* src, uint64_t* dst, const int* anc, int nchains, int chain_words,
+                           hipStream_t st) {
+  hipLaunchKernelGGL(k_copy, dim3(nchains), dim3(256), 0, st, reinterpret_cast<const uint4*>(src),
+                     reinterpret_cast<uint4*>(dst), anc, chain_words / 2);
+  return hipGetLastError();
+}

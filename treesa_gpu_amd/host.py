@@ -1,0 +1,150 @@
+"""ctypes binding of libtreesa_hip's host layer (lib/libtreesa_host.so): instance / tree / betas files,
+topology labels, Julia random trees, the initial population and the double-precision energy.
+
+These are the same C++ functions bin/treesa_gpu uses (treesa_gpu_amd/host/tsa_host.cpp); the reference's
+host code they follow is csrc/treesa_gpu.cu:1027-1274, 1300-1328, 1585-1630.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+from . import capi
+
+_lib = None
+
+
+def load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(capi.HOST_LIB_PATH):
+        raise FileNotFoundError(f"{capi.HOST_LIB_PATH} is missing: build it with `make -C treesa_gpu_amd`")
+    lib = ctypes.CDLL(capi.HOST_LIB_PATH)
+    P, I, U64, D = ctypes.c_void_p, ctypes.c_int, ctypes.c_uint64, ctypes.c_double
+    C = ctypes.c_char_p
+    lib.tsh_instance_load.argtypes = [C, ctypes.c_char_p, I]
+    lib.tsh_instance_load.restype = P
+    lib.tsh_instance_make.argtypes = [I, I, P, P, I, P, ctypes.c_char_p, I]
+    lib.tsh_instance_make.restype = P
+    lib.tsh_instance_free.argtypes = [P]
+    lib.tsh_instance_info.argtypes = [P, P, P, P]
+    lib.tsh_instance_leaf.argtypes = [P, I, P]
+    lib.tsh_read_trees.argtypes = [C, I, P, I, ctypes.c_char_p, I]
+    lib.tsh_parse_betas.argtypes = [C, P, I, ctypes.c_char_p, I]
+    lib.tsh_splitmix64.argtypes = [U64]
+    lib.tsh_splitmix64.restype = U64
+    lib.tsh_random_tree.argtypes = [I, U64, P]
+    lib.tsh_labels.argtypes = [P, I, P, P]
+    lib.tsh_build_population.argtypes = [P, I, I, I, I, P, I, I, U64, P, I, P, ctypes.c_char_p, I]
+    lib.tsh_host_energy.argtypes = [P, I, P, P, P, P, P, P]
+    lib.tsh_greedy_repair.argtypes = [P, I, P, P, D]
+    _lib = lib
+    return lib
+
+
+class HostError(RuntimeError):
+    pass
+
+
+class Instance:
+    """A tensor network read from the reference's instance format (or built from ixs / iy)."""
+
+    def __init__(self, path=None, m=None, nlab=None, ixs=None, iy=()):
+        self.lib = load()
+        err = ctypes.create_string_buffer(512)
+        if path is not None:
+            h = self.lib.tsh_instance_load(path.encode(), err, 512)
+        else:
+            offs = np.zeros(m + 1, np.int32)
+            for i, ix in enumerate(ixs):
+                offs[i + 1] = offs[i] + len(ix)
+            labs = np.array([l for ix in ixs for l in ix] or [0], np.int32)
+            iya = np.array(list(iy) or [0], np.int32)
+            h = self.lib.tsh_instance_make(m, nlab, offs.ctypes.data, labs.ctypes.data, len(iy), iya.ctypes.data, err,
+                                           512)
+        if not h:
+            raise HostError(err.value.decode())
+        self.h = h
+        m_, n_, s_ = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+        self.lib.tsh_instance_info(h, ctypes.byref(m_), ctypes.byref(n_), ctypes.byref(s_))
+        self.m, self.nlab, self.leaf_sc = m_.value, n_.value, s_.value
+        self.nint = self.m - 1
+
+    def leaf(self, W):
+        out = np.zeros((self.m, W), np.uint64)
+        self.lib.tsh_instance_leaf(self.h, W, out.ctypes.data)
+        return out
+
+    def read_trees(self, path, maxk=64):
+        out = np.zeros((maxk, self.nint), np.uint32)
+        err = ctypes.create_string_buffer(512)
+        k = self.lib.tsh_read_trees(path.encode(), self.m, out.ctypes.data, maxk, err, 512)
+        if k < 0:
+            raise HostError(err.value.decode())
+        return out[:min(k, maxk)].copy()
+
+    def labels(self, ch, W):
+        ch = np.ascontiguousarray(ch, np.uint32)
+        lab = np.zeros((self.nint, W), np.uint64)
+        if self.lib.tsh_labels(self.h, W, ch.ctypes.data, lab.ctypes.data) != 0:
+            return None
+        return lab
+
+    def population(self, lay, trees, nchains, seed=1, S0=None, random_slices=0):
+        """Initial population in the C ABI record format (nchains x chain_words)."""
+        trees = np.ascontiguousarray(trees if trees is not None and len(trees) else np.zeros((0, self.nint)),
+                                     np.uint32)
+        pop = np.zeros((nchains, lay.chain_words), np.uint64)
+        s0 = None if S0 is None else np.ascontiguousarray(S0, np.uint64)
+        err = ctypes.create_string_buffer(512)
+        rc = self.lib.tsh_build_population(self.h, lay.W, lay.ch_off, lay.s_off, lay.chain_words, trees.ctypes.data,
+                                           len(trees), nchains, seed, None if s0 is None else s0.ctypes.data,
+                                           random_slices, pop.ctypes.data, err, 512)
+        if rc != 0:
+            raise HostError(err.value.decode())
+        return pop
+
+    def host_energy(self, lay, rec, slicing=False, gm=capi.DEFAULT_GM, h100=capi.DEFAULT_H100):
+        """(tc, sc, gpu_time, h100_time, |S|) of one chain record, in double."""
+        rec = np.ascontiguousarray(rec, np.uint64)
+        g = np.array(gm, np.float64)
+        h = np.array(h100, np.float64)
+        out = np.zeros(5, np.float64)
+        ch = rec[lay.ch_off:].view(np.uint32)
+        S = rec[lay.s_off:lay.s_off + lay.W]
+        self.lib.tsh_host_energy(self.h, lay.W, g.ctypes.data, h.ctypes.data, rec.ctypes.data, ch.ctypes.data,
+                                 S.ctypes.data if slicing else None, out.ctypes.data)
+        return float(out[0]), int(out[1]), float(out[2]), float(out[3]), int(out[4])
+
+    def close(self):
+        if self.h:
+            self.lib.tsh_instance_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def parse_betas(spec):
+    lib = load()
+    n = 1 << 16
+    out = np.zeros(n, np.float32)
+    err = ctypes.create_string_buffer(512)
+    k = lib.tsh_parse_betas(spec.encode(), out.ctypes.data, n, err, 512)
+    if k < 0:
+        raise HostError(err.value.decode())
+    return out[:k].copy()
+
+
+def random_tree(m, seed):
+    out = np.zeros(m - 1, np.uint32)
+    load().tsh_random_tree(m, seed, out.ctypes.data)
+    return out
+
+
+def splitmix64(x):
+    return int(load().tsh_splitmix64(x))
