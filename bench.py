@@ -1,0 +1,195 @@
+#!/usr/bin/env python3
+"""Throughput of the TreeSA sweep path on one MI355X (node visits/s), with its roofline and a CPU baseline.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu]
+
+Workload (default c2, the headline): random 3-SAT n=100 (m=426 clause tensors, 100 labels,
+tests/golden/data/sat100.txt), par-order sweeps of 8192 independent chains starting from the reference's three
+spectral path trees (tests/golden/data/sat100_multi.tree, trees 1-3, chain c from tree c % 3), beta linear
+1.0 -> 15 over 200 levels of one sweep each, tc energy with sc_target 20, best-of-N selection.  One step is one
+level exactly as the drop-in binary runs it: one sweep kernel over all chains, the energy kernel, the host
+score loop, and a download of the best chain when it improves.  The population is uploaded before the timed
+region; K steps run levels 0..K-1 of the schedule (wrapping after 200).
+
+The timed region is the drop-in binary's own level loop (bin/treesa_gpu, t_anneal: after the population is
+resident in HBM, until the last level's energies are back), after --bench-warmup W untimed levels.
+value = K * nchains * (m - 1) / that wall time (whole job).
+kernel_visits_per_s = the reference's own definition (bench/throughput.py:64-70): node visits over the
+event-timed sweep kernels only.  roofline: algorithmic bytes of the sweep kernel per launch (5 label sets of
+W words + 8 B of children per proposal, W words + 8 B written per accept, 4 B per visit without a rule, from
+the kernel's own counters) over its average event-timed launch duration, against the 8 TB/s HBM peak.
+cpu_baseline: the reference's own CPU port (csrc/cpu_ref.h, oracle/_ref/ref_harness) on one core, over a
+bounded sample of the same workload (a subset of the chains, every level).
+"""
+import argparse
+import json
+import os
+import subprocess
+import sys
+import tempfile
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from treesa_gpu_amd import capi, host  # noqa: E402
+
+DATA = os.path.join(ROOT, "tests", "golden", "data")
+METRIC = "node visits/sec on 1 MI355X, random 3-SAT n=100; best log2 tc at fixed wall time"
+HBM_PEAK_GBS = 8000.0
+
+
+def linear_betas(a, b, n):
+    return [float(np.float32(a + i * (b - a) / (n - 1))) for i in range(n)]
+
+
+CONFIGS = {
+    # the reference's CPU-runnable check case: greedy start, pre-order, 256 chains x 100 sweeps
+    "c1": dict(inst="sat100", trees=("sat100.tree", None), order="preorder", nchains=256, levels=100,
+               betas=(0.01, 15.0), sc_target=20.0, desc="random 3-SAT n=100 (m=426), greedy start, pre-order, "
+                                                        "256 chains x 100 sweeps, beta 0.01->15"),
+    "c2": dict(inst="sat100", trees=("sat100_multi.tree", (1, 2, 3)), order="par", nchains=8192, levels=200,
+               betas=(1.0, 15.0), sc_target=20.0, desc="random 3-SAT n=100 (m=426), spectral path starts, par order, "
+                                                        "8192 chains x 200 sweeps, beta 1->15, best-of-N"),
+}
+
+
+def score_tc(lc, sc, sc_target, sc_weight=1.0):
+    """Selection score of the reference in tc mode (csrc/treesa_gpu.cu:1740-1746), vectorised."""
+    lc = lc.astype(np.float64)
+    sc = sc.astype(np.float64)
+    out = lc.copy()
+    over = (sc > sc_target) & (sc_weight > 0)
+    if over.any():
+        pen = np.log2(sc_weight) + sc[over] + np.log2(1.0 - np.exp2(sc_target - sc[over]))
+        mx = np.maximum(lc[over], pen)
+        mn = np.minimum(lc[over], pen)
+        out[over] = mx + np.log2(1.0 + np.exp2(mn - mx))
+    return out
+
+
+def setup(cfgname):
+    C = CONFIGS[cfgname]
+    inst = host.Instance(os.path.join(DATA, C["inst"] + ".txt"))
+    lay = capi.layout(inst.m, inst.nlab)
+    tf, pick = C["trees"]
+    trees = inst.read_trees(os.path.join(DATA, tf))
+    if pick is not None:
+        trees = trees[list(pick)]
+    pop = inst.population(lay, trees, C["nchains"], seed=1)
+    cfg = capi.make_config(mode="tc", sc_target=C["sc_target"], seed=1)
+    betas = linear_betas(C["betas"][0], C["betas"][1], C["levels"])
+    order = capi.ORDER_PAR if C["order"] == "par" else capi.ORDER_PREORDER
+    return C, inst, lay, trees, pop, cfg, betas, order
+
+
+def algorithmic_bytes(st, W):
+    """Per the sweep-kernel counters: proposals read 5 sets + 8 B children, accepts write a set + 8 B,
+    visits without a rule read 4 B."""
+    prop, acc, visits = st[0], st[1], st[3]
+    return prop * (40 * W + 8) + acc * (8 * W + 8) + (visits - prop) * 4
+
+
+def cpu_baseline(C, inst, trees, betas, nsample):
+    ref = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
+    with tempfile.TemporaryDirectory() as td:
+        tf = os.path.join(td, "trees.txt")
+        with open(tf, "w") as f:
+            for t in trees:
+                for w in t:
+                    f.write(f"{int(w) & 0xFFFF} {int(w) >> 16}\n")
+        bs = ",".join(repr(b) for b in betas)
+        if os.path.exists(ref):
+            args = [ref, "-i", os.path.join(DATA, C["inst"] + ".txt"), "--tree", tf, "--chains", str(nsample),
+                    "--niters", "1", "--betas", bs, "--order", C["order"], "--mode", "tc", "--sc-target",
+                    str(C["sc_target"]), "--seed", "1", "--timing"]
+            out = json.loads(subprocess.run(args, check=True, capture_output=True, text=True).stdout)
+            secs, kind = out["seconds"], "reference"
+        else:  # the oracle restatement, one thread
+            sys.path.insert(0, os.path.join(ROOT, "tests"))
+            import oracle as orc
+            from common import oracle_population
+            m, nlab, ixs, iy = orc.read_instance_py(os.path.join(DATA, C["inst"] + ".txt"))
+            O = orc.Oracle(m, nlab, ixs, iy)
+            lay = capi.layout(m, nlab)
+            pop = oracle_population(O, lay, m, nsample, 1, trees)
+            P = orc.params_from_config(capi.make_config(mode="tc", sc_target=C["sc_target"], seed=1), 3, nlab)
+            os.environ["OMP_NUM_THREADS"] = "1"
+            t0 = time.perf_counter()
+            for lev, b in enumerate(betas):
+                O.sweeps(P, lay, pop, 0 if C["order"] == "par" else 1, b, lev, 1)
+            secs, kind = time.perf_counter() - t0, "port"
+    visits = nsample * len(betas) * (inst.m - 1)
+    return dict(value=visits / secs, unit="node visits/s", cores=1, kind=kind,
+                sample=f"{nsample} of {C['nchains']} chains x {len(betas)} sweeps ({visits:.3e} visits, {secs:.1f} s)")
+
+
+def run_binary(C, trees, betas, steps, warmup):
+    """The drop-in binary's level loop on the workload; returns its JSON result."""
+    with tempfile.TemporaryDirectory() as td:
+        tf = os.path.join(td, "trees.txt")
+        with open(tf, "w") as f:
+            for t in trees:
+                for w in t:
+                    f.write(f"{int(w) & 0xFFFF} {int(w) >> 16}\n")
+        bf = os.path.join(td, "betas.txt")
+        with open(bf, "w") as f:
+            f.write("\n".join(repr(betas[k % len(betas)]) for k in range(steps)) + "\n")
+        out = os.path.join(td, "out.json")
+        args = [capi.BIN_PATH, "-i", os.path.join(DATA, C["inst"] + ".txt"), "--tree", tf, "--betas", "file:" + bf,
+                "--nchains", str(C["nchains"]), "--niters", "1", "--sc-target", str(C["sc_target"]), "--mode", "tc",
+                "--order", C["order"], "--kernel", "auto", "--scheme", "indep", "--seed", "1", "--eval-every", "1",
+                "--bench-warmup", str(warmup), "--out", out, "--quiet"]
+        p = subprocess.run(args, capture_output=True, text=True)
+        if p.returncode != 0:
+            raise RuntimeError(f"treesa_gpu failed ({p.returncode}): {p.stderr[-2000:]}")
+        with open(out) as f:
+            return json.load(f)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None, help="levels timed (default: the workload's schedule)")
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-chains", type=int, default=128)
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        sys.exit("bench.py measures one GPU: chains are independent, and a multi-GPU run would shard them across "
+                 "processes (see DESIGN.md); run with --gpus 1")
+    C, inst, lay, trees, pop, cfg, betas, order = setup(a.config)
+    steps = a.steps or C["levels"]
+    nchains = C["nchains"]
+    r = run_binary(C, trees, betas, steps, a.warmup)
+    visits = steps * nchains * (inst.m - 1)
+    assert r["node_visits"] == visits, (r["node_visits"], visits)
+    st = [r["proposals"], r["accepts"], r["warp_steps"], r["node_visits"]]
+    B = algorithmic_bytes(st, lay.W) / steps
+    dur = r["kernel_s"] / steps
+    wall = r["t_anneal"]
+    res = {
+        "metric": METRIC, "value": visits / wall, "unit": "node visits/s", "n_gpus": 1, "steps": steps,
+        "warmup": a.warmup, "ms_per_step": wall * 1e3 / steps, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u64",
+        "data": "synthetic: the reference's committed instance and start-tree fixtures, seed 1",
+        "config": {"workload": C["desc"], "config": a.config, "nchains": nchains, "levels_timed": steps,
+                   "sweeps_per_level": 1, "label_words64": lay.W, "kernel": r.get("hip_kernel")},
+        "kernel_visits_per_s": visits / r["kernel_s"], "sweeps_per_s_per_chain": steps / r["kernel_s"],
+        "proposals": r["proposals"], "accepts": r["accepts"], "phases": r["warp_steps"],
+        "best_tc": r["tc"], "best_sc": r["sc"], "wall_s": wall,
+        "roofline": {"bound": "hbm", "achieved": B / dur / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": B / dur / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                     "kernel": "k_sweep " + ("par" if order == capi.ORDER_PAR else "pre-order") + ", chain in LDS",
+                     "bytes_per_launch": B, "avg_launch_ms": dur * 1e3},
+    }
+    if not a.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(C, inst, trees, betas, min(a.cpu_chains, nchains))
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

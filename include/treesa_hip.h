@@ -100,7 +100,8 @@ int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* out);
  * csrc/treesa_gpu.cu:1659-1716. */
 int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0, int32_t nsweeps);
 
-/* Wait for the last tsa_sweeps and return its event-timed kernel time in ms (0 if none pending).
+/* Wait for every tsa_sweeps since the previous call and return their summed event-timed kernel time in
+ * ms (0 if none pending).
  * Replaces the cudaEventElapsedTime bookkeeping of run_anneal, csrc/treesa_gpu.cu:1799-1809, 1870-1876. */
 int tsa_sweeps_ms(tsa_ctx* ctx, double* ms);
 
@@ -120,6 +121,37 @@ int tsa_set_mode(tsa_ctx* ctx, int32_t mode);
  * visits, slice proposals, slice accepts, busy lanes.  Replaces the d_stats copy,
  * csrc/treesa_gpu.cu:1880-1881. */
 int tsa_stats(tsa_ctx* ctx, uint64_t out[7]);
+
+/* Device-side best tracking for runs without population steps (scheme indep): after a level's sweeps,
+ * tsa_track enqueues the energy kernel and a selection kernel that scores every chain (lower is better,
+ * the reference's score, csrc/treesa_gpu.cu:1737-1748, evaluated with the restated double log2 / exp2 of
+ * tsa_select.h), keeps the lowest score over all tracked levels (first chain and first level on ties, as
+ * the reference's loop at csrc/treesa_gpu.cu:1810-1824) and snapshots that chain's record on the device,
+ * and writes one trace row per tracked level.  Nothing synchronizes until tsa_track_end. */
+typedef struct tsa_select_t {
+  int32_t mode, slicing, select_sc;
+  double sc_target, sc_weight;
+} tsa_select_t;
+
+typedef struct tsa_trace_row_t {
+  float lc;             /* lcost of the level's best chain */
+  int32_t sc, ns;       /* its sc and |S| */
+  int32_t chain;        /* its index (-1: no finite score) */
+  double score;         /* its score */
+  double meanE, meanNs; /* population means of the energy and of |S| */
+  uint64_t ticks;       /* device wall clock when the row was written */
+} tsa_trace_row_t;
+
+/* Start tracking: best score +inf, room for max_levels rows.  Replaces the best-tracking state of
+ * run_anneal, csrc/treesa_gpu.cu:1777-1779. */
+int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t max_levels);
+/* Enqueue energy + selection for level (0 <= level < max_levels).  Asynchronous. */
+int tsa_track(tsa_ctx* ctx, int32_t level);
+/* Wait and return the best over the tracked levels (best_chain -1 if none), its record (chain_words words),
+ * max_levels trace rows (rows of untracked levels are zero) and the device wall-clock rate in Hz;
+ * ticks0 = device wall clock at tsa_track_begin. */
+int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_level, double* best_score, uint64_t* best_record,
+                  tsa_trace_row_t* rows, uint64_t* ticks0, double* tick_hz);
 
 /* Human-readable description of the kernels this context launches (name, lanes, LDS bytes). */
 int tsa_describe(tsa_ctx* ctx, char* buf, int32_t len);

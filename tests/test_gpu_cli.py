@@ -1,0 +1,77 @@
+"""The drop-in binary (bin/treesa_gpu) end to end on the GPU.
+
+* Device-side selection (scheme indep: energies, scores and the best-chain snapshot stay on the GPU) returns
+  exactly what the host-side level loop returns (--host-select), for both orders.
+* --check passes: valid trees, maintained labels equal the topology's, the energy kernel agrees with the host
+  double computation, and the LDS and global kernel mappings are bit-identical
+  (the reference's validation matrix parameters, tests/run_checks.sh:13).
+* Every result is valid (exit code 0, valid, labels_ok) and its tc / sc equal the host double recomputation.
+"""
+import json
+import os
+import subprocess
+
+import pytest
+
+import common
+from treesa_gpu_amd import capi, host
+
+pytestmark = pytest.mark.gpu
+
+CHECK_ARGS = ["--check", "--nchains", "48", "--niters", "4", "--betas", "0.2:0.7:7", "--sc-target", "24",
+              "--ref-chains", "4", "--seed", "7"]
+
+
+def run(args, tmp_path, name="out.json"):
+    out = str(tmp_path / name)
+    print("[cli]", " ".join(args), flush=True)
+    p = subprocess.run([capi.BIN_PATH] + args + ["--out", out, "--quiet"], capture_output=True, text=True,
+                       timeout=600)
+    assert p.returncode == 0, p.stderr[-2000:]
+    with open(out) as f:
+        return json.load(f)
+
+
+@pytest.mark.parametrize("order", ["par", "preorder"])
+@pytest.mark.parametrize("inst", ["sat60", "lat14"])
+def test_device_selection_equals_host_selection(inst, order, tmp_path):
+    args = ["-i", common.inst_path(inst), "--nchains", "96", "--niters", "2", "--betas", "0.01:0.05:15",
+            "--sc-target", "30", "--order", order, "--seed", "3"]
+    a = run(args, tmp_path, "a.json")
+    b = run(args + ["--host-select"], tmp_path, "b.json")
+    for k in ("tc", "sc", "best_chain", "tree", "proposals", "accepts", "node_visits", "valid", "labels_ok"):
+        assert a[k] == b[k], k
+    assert a["valid"] and a["labels_ok"]
+    ta = json.loads("[" + json.dumps(a["trace"])[1:-1] + "]")
+    tb = json.loads("[" + json.dumps(b["trace"])[1:-1] + "]")
+    assert [r[1:5] + r[6:] for r in ta] == [r[1:5] + r[6:] for r in tb]  # all columns but t and meanE
+    assert max(abs(x[5] - y[5]) for x, y in zip(ta, tb)) < 1e-9
+
+
+@pytest.mark.parametrize("inst,extra", [("sat100", ["--kernel", "par"]), ("sat100", ["--order", "preorder"]),
+                                        ("reg3_250", ["--mode", "h100"]), ("grid24", ["--mode", "gpu"]),
+                                        ("sat60", ["--random-slices", "8"]),
+                                        ("grid28", ["--slicing", "--sc-target", "20", "--mode", "h100"])])
+def test_check_mode_passes(inst, extra, tmp_path):
+    args = [capi.BIN_PATH, "-i", common.inst_path(inst), "--tree", common.tree_file(inst, "greedy")] + CHECK_ARGS + extra
+    print("[cli]", " ".join(args), flush=True)
+    p = subprocess.run(args, capture_output=True, text=True, timeout=600)
+    assert p.returncode == 0 and "CHECK PASSED" in p.stdout, p.stdout + p.stderr
+
+
+@pytest.mark.parametrize("scheme", ["indep", "pa", "trunc"])
+def test_result_is_valid_and_consistent(scheme, tmp_path):
+    r = run(["-i", common.inst_path("sat40"), "--nchains", "64", "--niters", "2", "--betas", "0.1:0.5:10",
+             "--scheme", scheme, "--slicing", "--sc-target", "24"], tmp_path)
+    assert r["valid"] and r["labels_ok"]
+    inst = host.Instance(common.inst_path("sat40"))
+    lay = capi.layout(inst.m, inst.nlab)
+    import numpy as np
+    rec = np.zeros(lay.chain_words, np.uint64)
+    ch = np.array([a | (b << 16) for a, b in r["tree"]], np.uint32)
+    rec[lay.ch_off:].view(np.uint32)[:lay.nint] = ch
+    rec[:lay.nint * lay.W] = inst.labels(ch, lay.W).reshape(-1)
+    for l in r["sliced"]:
+        rec[lay.s_off + (l >> 6)] |= np.uint64(1) << np.uint64(l & 63)
+    tc, sc, _, _, ns = inst.host_energy(lay, rec, slicing=True)
+    assert abs(tc - r["tc"]) < 1e-6 and sc == r["sc"] and ns == r["nsliced"] and sc <= 24

@@ -97,37 +97,37 @@ TSA_HD float tsa_lse_i(int a, int b, const float* lse) {
 }
 
 // log2 of the modeled time of one contraction, GPU roofline model (common.h:129-135).
-TSA_HD float tsa_gpu_lt(int B, int M, int N, int K, const TsaModel& P, const uint32_t* fix) {
+TSA_HD float tsa_gpu_lt(int B, int M, int N, int K, const TsaModel& P, const TsaMathTabs& T) {
   const int Me = M > P.m0 ? M : P.m0, Ne = N > P.n0 ? N : P.n0, Ke = K > P.k0 ? K : P.k0;
   const float lops = (float)(1 + B + Me + Ne + Ke) - P.lpeak;
-  const float lbits = tsa_lse_f(tsa_lse_f((float)(B + M + K), (float)(B + N + K), fix), (float)(B + M + N), fix) - P.lbw;
+  const float lbits = tsa_lse_f(tsa_lse_f((float)(B + M + K), (float)(B + N + K), T), (float)(B + M + N), T) - P.lbw;
   const float lt = lops > lbits ? lops : lbits;
-  return tsa_lse_f(lt, P.llaunch, fix);
+  return tsa_lse_f(lt, P.llaunch, T);
 }
 
 // log2 of the modeled time of one contraction, measured H100 model (common.h:138-151).
-TSA_HD float tsa_h100_lt(int B, int M, int N, int K, const TsaModel& P, const uint32_t* fix) {
+TSA_HD float tsa_h100_lt(int B, int M, int N, int K, const TsaModel& P, const TsaMathTabs& T) {
   if (B + M + N <= P.v2_small_rank) return P.v2_lsmall_cell + (float)(B + M + N + K);
   const float la = (float)(B + M + K), lb = (float)(B + N + K), lc = (float)(B + M + N);
-  const float lab = tsa_lse_f(la, lb, fix), lmoved = tsa_lse_f(lab, lc, fix);
+  const float lab = tsa_lse_f(la, lb, T), lmoved = tsa_lse_f(lab, lc, T);
   const float perm = P.v2_lperm2 + lab;
-  float best = tsa_lse_f(P.v2_lcc_bit + lmoved, P.v2_lcc_cell + (float)(B + M + N + K), fix);
+  float best = tsa_lse_f(P.v2_lcc_bit + lmoved, P.v2_lcc_cell + (float)(B + M + N + K), T);
   const int MN = M > N ? M : N;
   if (K >= 7 && MN >= 5) {
     const int Me = M > 6 ? M : 6, Ne = N > 6 ? N : 6, Ke = K > 8 ? K : 8;
     const float tc =
-        tsa_lse_f(tsa_lse_f(P.v2_ltc_bit + lmoved, P.v2_ltc_pad + (float)(B + Me + Ne + Ke), fix), P.v2_ltc_out + lc, fix);
+        tsa_lse_f(tsa_lse_f(P.v2_ltc_bit + lmoved, P.v2_ltc_pad + (float)(B + Me + Ne + Ke), T), P.v2_ltc_out + lc, T);
     best = tc < best ? tc : best;
   }
-  return tsa_lse_f(tsa_lse_f(P.v2_l3launch, perm, fix), best, fix);
+  return tsa_lse_f(tsa_lse_f(P.v2_l3launch, perm, T), best, T);
 }
 
 // Cost (log2) of contraction (x, y) -> z with counts B=|xyz|, M=|x~yz|, N=|~xyz|, K=|xy~z|, Z=|z|.
 // Mode 0 is tc = |z| + |x & y & ~z| (common.h:159-163).
 template <int MODE>
-TSA_HD float tsa_node_cost(int B, int M, int N, int K, int Z, const TsaModel& P, const uint32_t* fix) {
+TSA_HD float tsa_node_cost(int B, int M, int N, int K, int Z, const TsaModel& P, const TsaMathTabs& T) {
   if (MODE == 0) return (float)(Z + K);
-  return MODE == 1 ? tsa_gpu_lt(B, M, N, K, P, fix) : tsa_h100_lt(B, M, N, K, P, fix);
+  return MODE == 1 ? tsa_gpu_lt(B, M, N, K, P, T) : tsa_h100_lt(B, M, N, K, P, T);
 }
 
 // Counters of one proposal: sizes of d (the visited node), P (pivot child) and X (P's new label set),
@@ -173,17 +173,17 @@ TSA_HD void tsa_acc(TsaCounts& c, uint64_t k, uint64_t m, uint64_t p, uint64_t o
 //   dtc = log2(2^c2 + 2^c3) - log2(2^c0 + 2^c1); dE = w*(sc1 - sc0) + dtc with sc0 = max(|P|,|d|),
 //   sc1 = max(|X|,|d|) and w = sc_weight if max(sc0, sc1) > sc_target else 0.
 template <int MODE>
-TSA_HD float tsa_energy_from_counts(const TsaCounts& c, const TsaModel& P, const float* lse, const uint32_t* fix) {
+TSA_HD float tsa_energy_from_counts(const TsaCounts& c, const TsaModel& P, const float* lse, const TsaMathTabs& T) {
   float dtc;
   if (MODE == 0) {
     const float tc0 = tsa_lse_i(c.sp + c.K[0], c.sd + c.K[1], lse);
     const float tc1 = tsa_lse_i(c.sx + c.K[2], c.sd + c.K[3], lse);
     dtc = tc1 - tc0;
   } else {
-    const float t0 = tsa_lse_f(tsa_node_cost<MODE>(c.B[0], c.M[0], c.N[0], c.K[0], c.sp, P, fix),
-                               tsa_node_cost<MODE>(c.B[1], c.M[1], c.N[1], c.K[1], c.sd, P, fix), fix);
-    const float t1 = tsa_lse_f(tsa_node_cost<MODE>(c.B[2], c.M[2], c.N[2], c.K[2], c.sx, P, fix),
-                               tsa_node_cost<MODE>(c.B[3], c.M[3], c.N[3], c.K[3], c.sd, P, fix), fix);
+    const float t0 = tsa_lse_f(tsa_node_cost<MODE>(c.B[0], c.M[0], c.N[0], c.K[0], c.sp, P, T),
+                               tsa_node_cost<MODE>(c.B[1], c.M[1], c.N[1], c.K[1], c.sd, P, T), T);
+    const float t1 = tsa_lse_f(tsa_node_cost<MODE>(c.B[2], c.M[2], c.N[2], c.K[2], c.sx, P, T),
+                               tsa_node_cost<MODE>(c.B[3], c.M[3], c.N[3], c.K[3], c.sd, P, T), T);
     dtc = t1 - t0;
   }
   const int sc0 = c.sp > c.sd ? c.sp : c.sd;
@@ -194,9 +194,9 @@ TSA_HD float tsa_energy_from_counts(const TsaCounts& c, const TsaModel& P, const
 }
 
 // Metropolis: u = (r >> 8) * 2^-24 < expf(-beta * dE).  common.h:226-229.
-TSA_HD bool tsa_metropolis(uint32_t r, float beta, float dE) {
+TSA_HD bool tsa_metropolis(uint32_t r, float beta, float dE, const uint64_t* exp2tab) {
   const float u = (float)(r >> 8) * (1.0f / 16777216.0f);
-  return u < tsa_expf(-beta * dE);
+  return u < tsa_expf_t(-beta * dE, exp2tab);
 }
 
 // Slots of rule r (reference comment csrc/treesa_gpu.cu:137-144): the pivot P is the left child

@@ -26,16 +26,23 @@ struct tsa_ctx {
   TsaLaunch L{};
   std::string kname;
   hipStream_t st = nullptr;
-  hipEvent_t e0 = nullptr, e1 = nullptr;
-  bool pending = false;
+  std::vector<hipEvent_t> ev;  // start / stop event pairs of the sweep launches since the last tsa_sweeps_ms
+  int npending = 0;            // pairs in use
+  TsaSelect sel{};
+  int track_levels = 0;
+  TsaTrackState* d_track = nullptr;
+  TsaTraceRowD* d_trace = nullptr;
+  uint64_t* d_best = nullptr;
+  unsigned long long* d_ticks0 = nullptr;
   uint64_t* d_rec = nullptr;
   uint64_t* d_rec2 = nullptr;
   uint64_t* d_leaf = nullptr;
   uint32_t* d_fix = nullptr;
   unsigned long long* d_stats = nullptr;
-  float* d_lc = nullptr;
+  float* d_lc = nullptr;  // d_lc, d_sc, d_ns: one allocation of 3 * nchains words, copied back at once
   int* d_sc = nullptr;
   int* d_ns = nullptr;
+  uint32_t* h_en = nullptr;  // pinned host copy of the three energy arrays
   int* d_anc = nullptr;
   std::string err;
 };
@@ -177,11 +184,13 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_fix) (void)hipFree(c->d_fix);
   if (c->d_stats) (void)hipFree(c->d_stats);
   if (c->d_lc) (void)hipFree(c->d_lc);
-  if (c->d_sc) (void)hipFree(c->d_sc);
-  if (c->d_ns) (void)hipFree(c->d_ns);
+  if (c->h_en) (void)hipHostFree(c->h_en);
   if (c->d_anc) (void)hipFree(c->d_anc);
-  if (c->e0) (void)hipEventDestroy(c->e0);
-  if (c->e1) (void)hipEventDestroy(c->e1);
+  for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
+  if (c->d_track) (void)hipFree(c->d_track);
+  if (c->d_trace) (void)hipFree(c->d_trace);
+  if (c->d_best) (void)hipFree(c->d_best);
+  if (c->d_ticks0) (void)hipFree(c->d_ticks0);
   if (c->st) (void)hipStreamDestroy(c->st);
   delete c;
 }
@@ -326,19 +335,18 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
     }                                                                                             \
   } while (0)
   TSA_CREATE_HIP(hipStreamCreateWithFlags(&c->st, hipStreamNonBlocking));
-  TSA_CREATE_HIP(hipEventCreate(&c->e0));
-  TSA_CREATE_HIP(hipEventCreate(&c->e1));
   TSA_CREATE_HIP(hipMalloc(&c->d_rec, recb));
   TSA_CREATE_HIP(hipMemsetAsync(c->d_rec, 0, recb, c->st));
   TSA_CREATE_HIP(hipMalloc(&c->d_leaf, (size_t)lay->m * lay->W * 8));
   TSA_CREATE_HIP(hipMemcpyAsync(c->d_leaf, leaf, (size_t)lay->m * lay->W * 8, hipMemcpyHostToDevice, c->st));
   TSA_CREATE_HIP(hipMalloc(&c->d_fix, (size_t)TSA_LOG2FIX_WORDS * 4));
   TSA_CREATE_HIP(hipMemcpyAsync(c->d_fix, g_fix.data(), (size_t)TSA_LOG2FIX_WORDS * 4, hipMemcpyHostToDevice, c->st));
-  TSA_CREATE_HIP(hipMalloc(&c->d_stats, TSA_NSTAT * sizeof(unsigned long long)));
-  TSA_CREATE_HIP(hipMemsetAsync(c->d_stats, 0, TSA_NSTAT * sizeof(unsigned long long), c->st));
-  TSA_CREATE_HIP(hipMalloc(&c->d_lc, (size_t)nchains * 4));
-  TSA_CREATE_HIP(hipMalloc(&c->d_sc, (size_t)nchains * 4));
-  TSA_CREATE_HIP(hipMalloc(&c->d_ns, (size_t)nchains * 4));
+  TSA_CREATE_HIP(hipMalloc(&c->d_stats, TSA_NSTAT * TSA_STAT_SLOTS * sizeof(unsigned long long)));
+  TSA_CREATE_HIP(hipMemsetAsync(c->d_stats, 0, TSA_NSTAT * TSA_STAT_SLOTS * sizeof(unsigned long long), c->st));
+  TSA_CREATE_HIP(hipMalloc(&c->d_lc, (size_t)nchains * 12));
+  c->d_sc = reinterpret_cast<int*>(c->d_lc) + nchains;
+  c->d_ns = reinterpret_cast<int*>(c->d_lc) + 2 * (size_t)nchains;
+  TSA_CREATE_HIP(hipHostMalloc(&c->h_en, (size_t)nchains * 12, hipHostMallocDefault));
   TSA_CREATE_HIP(hipMalloc(&c->d_anc, (size_t)nchains * 4));
   TSA_CREATE_HIP(hipStreamSynchronize(c->st));
 #undef TSA_CREATE_HIP
@@ -377,23 +385,95 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
   if (order != TSA_ORDER_PAR && order != TSA_ORDER_PREORDER) return fail(ctx, TSA_ERR_ARG, "--order par|preorder");
   if (nsweeps < 0) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps: nsweeps < 0");
   if (nsweeps == 0) return TSA_OK;
-  TSA_HIP(ctx, hipEventRecord(ctx->e0, ctx->st));
+  while ((int)ctx->ev.size() < 2 * (ctx->npending + 1)) {
+    hipEvent_t e;
+    TSA_HIP(ctx, hipEventCreate(&e));
+    ctx->ev.push_back(e);
+  }
+  hipEvent_t e0 = ctx->ev[2 * ctx->npending], e1 = ctx->ev[2 * ctx->npending + 1];
+  TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
   TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains,
                                  beta, sweep0, nsweeps, ctx->d_stats, ctx->st));
-  TSA_HIP(ctx, hipEventRecord(ctx->e1, ctx->st));
-  ctx->pending = true;
+  TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
+  ctx->npending++;
   return TSA_OK;
 }
 
 extern "C" int tsa_sweeps_ms(tsa_ctx* ctx, double* ms) {
   if (!ctx || !ms) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps_ms: null argument");
   *ms = 0.0;
-  if (!ctx->pending) return TSA_OK;
-  TSA_HIP(ctx, hipEventSynchronize(ctx->e1));
-  float f = 0.f;
-  TSA_HIP(ctx, hipEventElapsedTime(&f, ctx->e0, ctx->e1));
-  ctx->pending = false;
-  *ms = (double)f;
+  if (ctx->npending == 0) return TSA_OK;
+  TSA_HIP(ctx, hipEventSynchronize(ctx->ev[2 * ctx->npending - 1]));
+  double sum = 0.0;
+  for (int k = 0; k < ctx->npending; k++) {
+    float f = 0.f;
+    TSA_HIP(ctx, hipEventElapsedTime(&f, ctx->ev[2 * k], ctx->ev[2 * k + 1]));
+    sum += (double)f;
+  }
+  ctx->npending = 0;
+  *ms = sum;
+  return TSA_OK;
+}
+
+extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t max_levels) {
+  if (!ctx || !sel) return fail(ctx, TSA_ERR_ARG, "tsa_track_begin: null argument");
+  if (max_levels < 1) return fail(ctx, TSA_ERR_ARG, "tsa_track_begin: max_levels < 1");
+  ctx->sel.mode = sel->mode;
+  ctx->sel.slicing = sel->slicing;
+  ctx->sel.select_sc = sel->select_sc;
+  ctx->sel.sc_target = sel->sc_target;
+  ctx->sel.sc_weight = sel->sc_weight;
+  if (!ctx->d_track) TSA_HIP(ctx, hipMalloc(&ctx->d_track, sizeof(TsaTrackState)));
+  if (!ctx->d_ticks0) TSA_HIP(ctx, hipMalloc(&ctx->d_ticks0, sizeof(unsigned long long)));
+  if (!ctx->d_best) TSA_HIP(ctx, hipMalloc(&ctx->d_best, (size_t)ctx->lay.chain_words * 8));
+  if (max_levels > ctx->track_levels) {
+    if (ctx->d_trace) TSA_HIP(ctx, hipFree(ctx->d_trace));
+    ctx->d_trace = nullptr;
+    TSA_HIP(ctx, hipMalloc(&ctx->d_trace, (size_t)max_levels * sizeof(TsaTraceRowD)));
+  }
+  ctx->track_levels = max_levels;
+  TSA_HIP(ctx, hipMemsetAsync(ctx->d_trace, 0, (size_t)max_levels * sizeof(TsaTraceRowD), ctx->st));
+  TSA_HIP(ctx, hipMemsetAsync(ctx->d_best, 0, (size_t)ctx->lay.chain_words * 8, ctx->st));
+  TSA_HIP(ctx, tsa_launch_track_init(ctx->d_track, ctx->d_ticks0, ctx->st));
+  return TSA_OK;
+}
+
+extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
+  if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_track: null context");
+  if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_track: no tsa_track_begin");
+  if (level < 0 || level >= ctx->track_levels) return fail(ctx, TSA_ERR_ARG, "tsa_track: level out of range");
+  TSA_HIP(ctx, tsa_launch_energy(ctx->Wt, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains,
+                                 ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->st));
+  TsaSelect S = ctx->sel;
+  S.mode = ctx->mode;
+  TSA_HIP(ctx, tsa_launch_track(ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->nchains, S, level, ctx->d_rec,
+                                ctx->lay.chain_words, ctx->d_track, ctx->d_trace, ctx->d_best, ctx->st));
+  return TSA_OK;
+}
+
+extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_level, double* best_score,
+                             uint64_t* best_record, tsa_trace_row_t* rows, uint64_t* ticks0, double* tick_hz) {
+  if (!ctx || !best_chain || !best_level || !best_score || !best_record || !rows || !ticks0 || !tick_hz)
+    return fail(ctx, TSA_ERR_ARG, "tsa_track_end: null argument");
+  if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_track_end: no tsa_track_begin");
+  static_assert(sizeof(TsaTraceRowD) == sizeof(tsa_trace_row_t), "trace row layout");
+  TsaTrackState h;
+  unsigned long long t0 = 0;
+  TSA_HIP(ctx, hipMemcpyAsync(&h, ctx->d_track, sizeof h, hipMemcpyDeviceToHost, ctx->st));
+  TSA_HIP(ctx, hipMemcpyAsync(&t0, ctx->d_ticks0, sizeof t0, hipMemcpyDeviceToHost, ctx->st));
+  TSA_HIP(ctx, hipMemcpyAsync(best_record, ctx->d_best, (size_t)ctx->lay.chain_words * 8, hipMemcpyDeviceToHost,
+                              ctx->st));
+  TSA_HIP(ctx, hipMemcpyAsync(rows, ctx->d_trace, (size_t)ctx->track_levels * sizeof(TsaTraceRowD),
+                              hipMemcpyDeviceToHost, ctx->st));
+  TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  int dev = 0, khz = 0;
+  TSA_HIP(ctx, hipGetDevice(&dev));
+  TSA_HIP(ctx, hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+  *best_chain = h.best_chain;
+  *best_level = h.best_level;
+  *best_score = h.best_score;
+  *ticks0 = t0;
+  *tick_hz = (double)khz * 1e3;
   return TSA_OK;
 }
 
@@ -402,10 +482,11 @@ extern "C" int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns) {
   TSA_HIP(ctx, tsa_launch_energy(ctx->Wt, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains,
                                  ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->st));
   const size_t b = (size_t)ctx->nchains * 4;
-  TSA_HIP(ctx, hipMemcpyAsync(lc, ctx->d_lc, b, hipMemcpyDeviceToHost, ctx->st));
-  TSA_HIP(ctx, hipMemcpyAsync(sc, ctx->d_sc, b, hipMemcpyDeviceToHost, ctx->st));
-  TSA_HIP(ctx, hipMemcpyAsync(ns, ctx->d_ns, b, hipMemcpyDeviceToHost, ctx->st));
+  TSA_HIP(ctx, hipMemcpyAsync(ctx->h_en, ctx->d_lc, 3 * b, hipMemcpyDeviceToHost, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  memcpy(lc, ctx->h_en, b);
+  memcpy(sc, ctx->h_en + ctx->nchains, b);
+  memcpy(ns, ctx->h_en + 2 * (size_t)ctx->nchains, b);
   return TSA_OK;
 }
 
@@ -430,10 +511,13 @@ extern "C" int tsa_set_mode(tsa_ctx* ctx, int32_t mode) {
 
 extern "C" int tsa_stats(tsa_ctx* ctx, uint64_t out[7]) {
   if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_stats: null argument");
-  unsigned long long s[TSA_NSTAT];
+  unsigned long long s[TSA_NSTAT * TSA_STAT_SLOTS];
   TSA_HIP(ctx, hipMemcpyAsync(s, ctx->d_stats, sizeof s, hipMemcpyDeviceToHost, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
-  for (int i = 0; i < TSA_NSTAT; i++) out[i] = s[i];
+  for (int i = 0; i < TSA_NSTAT; i++) {
+    out[i] = 0;
+    for (int k = 0; k < TSA_STAT_SLOTS; k++) out[i] += s[i * TSA_STAT_SLOTS + k];
+  }
   return TSA_OK;
 }
 

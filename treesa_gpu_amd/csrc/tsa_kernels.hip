@@ -61,8 +61,8 @@ struct TsaVisit {
 // the one that stays, every rule swaps M and O, and P gets X = (K|O)&(M|d).
 template <int W, int MODE>
 __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab, uint32_t* ch, const uint64_t* Sm,
-                                              const uint64_t* lf, const uint32_t* __restrict__ fix, int v, float beta,
-                                              uint32_t sw, uint32_t chain) {
+                                              const uint64_t* lf, const float* lse, const TsaMathTabs& T, int v,
+                                              float beta, uint32_t sw, uint32_t chain) {
   const int m = P.m;
   const int NW = W > 0 ? W : P.W;
   TsaVisit o;
@@ -99,8 +99,8 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
       const uint64_t nm = Sm ? ~Sm[i] : ~0ull;
       tsa_acc<MODE>(cnt, k & nm, mm & nm, p & nm, oo & nm, d & nm, x & nm);
     }
-    const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, P.lse, fix);
-    acc = tsa_metropolis(rnd.y, beta, dE);
+    const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, lse, T);
+    acc = tsa_metropolis(rnd.y, beta, dE, T.exp2);
     if (acc) {
 #pragma unroll
       for (int i = 0; i < W; i++) pP[i] = X[i];
@@ -112,8 +112,8 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
       const uint64_t nm = Sm ? ~Sm[i] : ~0ull;
       tsa_acc<MODE>(cnt, k & nm, mm & nm, p & nm, oo & nm, d & nm, x & nm);
     }
-    const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, P.lse, fix);
-    acc = tsa_metropolis(rnd.y, beta, dE);
+    const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, lse, T);
+    acc = tsa_metropolis(rnd.y, beta, dE, T.exp2);
     if (acc)
       for (int i = 0; i < NW; i++) pP[i] = (pK[i] | pO[i]) & (pM[i] | pD[i]);
   }
@@ -138,7 +138,7 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
 // masked size and |S| are integer reductions.  Costs use label sets masked by ~S (S may be null).
 template <int W, int MODE>
 __device__ TsaEvalOut tsa_eval32(const TsaKParams& P, const uint64_t* lab, const uint32_t* ch, const uint64_t* S,
-                                 const uint64_t* lf, const uint32_t* __restrict__ fix, int l32) {
+                                 const uint64_t* lf, const TsaMathTabs& T, int l32) {
   const int NW = W > 0 ? W : P.W, m = P.m;
   float acc = -INFINITY;
   int scl = 0, cntl = 0;
@@ -155,7 +155,7 @@ __device__ TsaEvalOut tsa_eval32(const TsaKParams& P, const uint64_t* lab, const
       tsa_count3(x[w] & nm, y[w] & nm, zz, B, M, N, K);
       Z += __popcll(zz);
     }
-    acc = tsa_lse_f(acc, tsa_node_cost<MODE>(B, M, N, K, Z, P.model, fix), fix);
+    acc = tsa_lse_f(acc, tsa_node_cost<MODE>(B, M, N, K, Z, P.model, T), T);
     if (Z > scl) {
       scl = Z;
       cntl = 1;
@@ -165,7 +165,7 @@ __device__ TsaEvalOut tsa_eval32(const TsaKParams& P, const uint64_t* lab, const
   }
   int scmax = scl;
   for (int o = 16; o > 0; o >>= 1) {
-    acc = tsa_lse_f(acc, __shfl_xor(acc, o, 32), fix);
+    acc = tsa_lse_f(acc, __shfl_xor(acc, o, 32), T);
     const int t = __shfl_xor(scmax, o, 32);
     scmax = scmax > t ? scmax : t;
   }
@@ -210,11 +210,11 @@ __device__ __forceinline__ float tsa_slice_energy(const TsaEvalOut& e, const Tsa
 // reference's 32-lane algorithm on the same data; lane 0 alone writes S.
 template <int W, int MODE>
 __device__ void tsa_slice_step(const TsaKParams& P, const uint64_t* lab, const uint32_t* ch, uint64_t* S,
-                               const uint64_t* lf, const uint32_t* __restrict__ fix, float beta, uint32_t sw,
-                               uint32_t chain, int lane, int& nsp, int& nsa) {
+                               const uint64_t* lf, const TsaMathTabs& T, float beta, uint32_t sw, uint32_t chain,
+                               int lane, int& nsp, int& nsa) {
   const int NW = W > 0 ? W : P.W;
   const int l32 = lane & 31;
-  TsaEvalOut cur = tsa_eval32<W, MODE>(P, lab, ch, S, lf, fix, l32);
+  TsaEvalOut cur = tsa_eval32<W, MODE>(P, lab, ch, S, lf, T, l32);
   float Ecur = tsa_slice_energy(cur, P);
   for (int j = 0; j < P.slice_moves; j++) {
     const TsaU4 r1 = tsa_philox(TsaU4{0x10000u + 2u * (uint32_t)j, sw, chain, 0u}, P.key0, P.key1);
@@ -251,10 +251,10 @@ __device__ void tsa_slice_step(const TsaKParams& P, const uint64_t* lab, const u
       if (type != 0) S[lrem >> 6] &= ~(1ull << (lrem & 63));
     }
     tsa_wave_sync();
-    const TsaEvalOut nxt = tsa_eval32<W, MODE>(P, lab, ch, S, lf, fix, l32);
+    const TsaEvalOut nxt = tsa_eval32<W, MODE>(P, lab, ch, S, lf, T, l32);
     const float Enew = tsa_slice_energy(nxt, P);
     nsp++;
-    if (tsa_metropolis(r2.x, beta, Enew - Ecur)) {
+    if (tsa_metropolis(r2.x, beta, Enew - Ecur, T.exp2)) {
       nsa++;
       cur = nxt;
       Ecur = Enew;
@@ -284,17 +284,23 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
                                                int nchains, int lds_words, float beta, uint32_t sweep0, int nsweeps,
                                                unsigned long long* __restrict__ stats) {
   extern __shared__ uint64_t tsa_smem[];
+  __shared__ float s_lse[64];
+  __shared__ uint64_t s_exp2[32];
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, wpb = blockDim.x >> 6;
   const int NW = W > 0 ? W : P.W;
   const int m = P.m, nint = P.nint, nint4 = (nint + 3) & ~3;
+  // the small tables every proposal indexes per lane live in LDS
+  if (threadIdx.x < 64) s_lse[threadIdx.x] = P.lse[threadIdx.x];
+  if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
+  const TsaMathTabs T{s_exp2, fix};
   const uint64_t* lf = leaf;
   int leafw = 0;
   if constexpr (LDS) {
     leafw = (m * NW + 1) & ~1;
     for (int i = threadIdx.x; i < m * NW; i += blockDim.x) tsa_smem[i] = leaf[i];
-    __syncthreads();
     lf = tsa_smem;
   }
+  __syncthreads();
   const int c = blockIdx.x * wpb + wv;
   if (c >= nchains) return;  // whole waves; no workgroup barrier below this point
   uint64_t* const g = rec + (size_t)c * P.chain_words;
@@ -399,7 +405,7 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
             const int v = wl[j];
             const bool rev = (pri[v - m] & 1u) == 0;  // a follow-up visit draws its own numbers
             const uint32_t swv = sw | (rev ? 0x80000000u : 0u);
-            const TsaVisit o = tsa_visit<W, MODE>(P, lab, ch, Sm, lf, fix, v, beta, swv, (uint32_t)c);
+            const TsaVisit o = tsa_visit<W, MODE>(P, lab, ch, Sm, lf, s_lse, T, v, beta, swv, (uint32_t)c);
             nv++;
             nbusy++;
             np += o.prop;
@@ -416,7 +422,7 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
         tsa_wave_sync();
       }
       if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
-        tsa_slice_step<W, MODE>(P, lab, ch, S, lf, fix, beta, sw, (uint32_t)c, lane, nsp, nsa);
+        tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
         tsa_wave_sync();
       }
     }
@@ -433,7 +439,7 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
         tsa_wave_sync();  // every lane has read its node before pushes overwrite the list
         uint32_t cw = 0;
         if (lane < k) {
-          const TsaVisit o = tsa_visit<W, MODE>(P, lab, ch, Sm, lf, fix, v, beta, sw, (uint32_t)c);
+          const TsaVisit o = tsa_visit<W, MODE>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c);
           cw = o.cw;
           nv++;
           nbusy++;
@@ -451,7 +457,7 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
         tsa_wave_sync();
       }
       if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
-        tsa_slice_step<W, MODE>(P, lab, ch, S, lf, fix, beta, sw, (uint32_t)c, lane, nsp, nsa);
+        tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
         tsa_wave_sync();
       }
     }
@@ -464,14 +470,15 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
     for (int i = lane; i < P.chain_words / 2; i += 64) dst[i] = src[i];
   }
   const long long sp_ = tsa_wave_sum(np), sa_ = tsa_wave_sum(na), sv_ = tsa_wave_sum(nv), sb_ = tsa_wave_sum(nbusy);
-  if (lane == 0) {
-    atomicAdd(&stats[TSA_ST_PROP], (unsigned long long)sp_);
-    atomicAdd(&stats[TSA_ST_ACC], (unsigned long long)sa_);
-    atomicAdd(&stats[TSA_ST_STEPS], (unsigned long long)nst);
-    atomicAdd(&stats[TSA_ST_VISITS], (unsigned long long)sv_);
-    atomicAdd(&stats[TSA_ST_SPROP], (unsigned long long)nsp);
-    atomicAdd(&stats[TSA_ST_SACC], (unsigned long long)nsa);
-    atomicAdd(&stats[TSA_ST_BUSY], (unsigned long long)sb_);
+  if (lane == 0) {  // counters spread over TSA_STAT_SLOTS addresses each, summed by the host
+    unsigned long long* st = stats + (c & (TSA_STAT_SLOTS - 1));
+    atomicAdd(&st[TSA_ST_PROP * TSA_STAT_SLOTS], (unsigned long long)sp_);
+    atomicAdd(&st[TSA_ST_ACC * TSA_STAT_SLOTS], (unsigned long long)sa_);
+    atomicAdd(&st[TSA_ST_STEPS * TSA_STAT_SLOTS], (unsigned long long)nst);
+    atomicAdd(&st[TSA_ST_VISITS * TSA_STAT_SLOTS], (unsigned long long)sv_);
+    atomicAdd(&st[TSA_ST_SPROP * TSA_STAT_SLOTS], (unsigned long long)nsp);
+    atomicAdd(&st[TSA_ST_SACC * TSA_STAT_SLOTS], (unsigned long long)nsa);
+    atomicAdd(&st[TSA_ST_BUSY * TSA_STAT_SLOTS], (unsigned long long)sb_);
   }
 }
 
@@ -481,13 +488,17 @@ __global__ void __launch_bounds__(256) k_energy(TsaKParams P, const uint64_t* __
                                                 const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
                                                 int nchains, float* __restrict__ lc, int* __restrict__ sc,
                                                 int* __restrict__ ns) {
+  __shared__ uint64_t s_exp2[32];
+  if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
+  __syncthreads();
+  const TsaMathTabs T{s_exp2, fix};
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   const int c = t >> 5, l32 = threadIdx.x & 31;
   const int cc = c < nchains ? c : nchains - 1;  // a half-wave past the end duplicates the last chain
   const uint64_t* lab = rec + (size_t)cc * P.chain_words;
   const uint32_t* ch = reinterpret_cast<const uint32_t*>(lab + P.ch_off);
   const uint64_t* S = P.slicing ? lab + P.s_off : nullptr;
-  const TsaEvalOut e = tsa_eval32<W, MODE>(P, lab, ch, S, leaf, fix, l32);
+  const TsaEvalOut e = tsa_eval32<W, MODE>(P, lab, ch, S, leaf, T, l32);
   if (l32 == 0 && c < nchains) {
     lc[c] = e.lcost;
     sc[c] = e.sc;
@@ -501,6 +512,82 @@ __global__ void __launch_bounds__(256) k_copy(const uint4* __restrict__ src, uin
   const uint4* s = src + (size_t)anc[blockIdx.x] * n4;
   uint4* d = dst + (size_t)blockIdx.x * n4;
   for (int i = threadIdx.x; i < n4; i += blockDim.x) d[i] = s[i];
+}
+
+// Best tracking of one level (one workgroup of 1024 threads): score every chain, argmin with the lowest
+// index on ties, population means, and a snapshot of the best chain when it beats the best so far
+// (csrc/treesa_gpu.cu:1810-1832).  Sums are reduced in a fixed tree order, so they are deterministic.
+__global__ void __launch_bounds__(1024) k_track(const float* __restrict__ lc, const int* __restrict__ sc,
+                                                const int* __restrict__ ns, int n, TsaSelect S, int level,
+                                                const uint64_t* __restrict__ rec, int chain_words,
+                                                TsaTrackState* __restrict__ st, TsaTraceRowD* __restrict__ trace,
+                                                uint64_t* __restrict__ best_rec) {
+  __shared__ double s_s[1024], s_e[1024], s_n[1024];
+  __shared__ int s_i[1024];
+  __shared__ int s_copy, s_bi;
+  const int t = threadIdx.x;
+  double bs = INFINITY, se = 0.0, sn = 0.0;
+  int bi = n;
+  for (int c = t; c < n; c += 1024) {
+    const double s = tsa_score(lc[c], sc[c], ns[c], S);
+    if (s < bs) {
+      bs = s;
+      bi = c;
+    }
+    se += tsa_energyE(lc[c], sc[c], ns[c], S);
+    sn += (double)ns[c];
+  }
+  s_s[t] = bs;
+  s_i[t] = bi;
+  s_e[t] = se;
+  s_n[t] = sn;
+  __syncthreads();
+  for (int o = 512; o > 0; o >>= 1) {
+    if (t < o) {
+      const double a = s_s[t], b = s_s[t + o];
+      const int ia = s_i[t], ib = s_i[t + o];
+      if (b < a || (b == a && ib < ia)) {
+        s_s[t] = b;
+        s_i[t] = ib;
+      }
+      s_e[t] += s_e[t + o];
+      s_n[t] += s_n[t + o];
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    const int b = s_i[0];
+    TsaTraceRowD row;
+    row.chain = b < n ? b : -1;
+    row.lc = b < n ? lc[b] : 0.0f;
+    row.sc = b < n ? sc[b] : 0;
+    row.ns = b < n ? ns[b] : 0;
+    row.score = s_s[0];
+    row.meanE = s_e[0] / n;
+    row.meanNs = s_n[0] / n;
+    row.ticks = wall_clock64();
+    trace[level] = row;
+    const bool better = b < n && s_s[0] < st->best_score;
+    if (better) {
+      st->best_score = s_s[0];
+      st->best_chain = b;
+      st->best_level = level;
+    }
+    s_copy = better ? 1 : 0;
+    s_bi = b;
+  }
+  __syncthreads();
+  if (s_copy) {
+    const uint64_t* src = rec + (size_t)s_bi * chain_words;
+    for (int w = t; w < chain_words; w += 1024) best_rec[w] = src[w];
+  }
+}
+
+__global__ void k_track_init(TsaTrackState* st, unsigned long long* ticks0) {
+  st->best_score = INFINITY;
+  st->best_chain = -1;
+  st->best_level = -1;
+  *ticks0 = wall_clock64();
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -591,6 +678,19 @@ hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64
     case 0: return launch_energy_w<0>(mode, P, rec, leaf, fix, nchains, lc, sc, ns, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int nchains, const TsaSelect& S, int level,
+                            const uint64_t* rec, int chain_words, TsaTrackState* stt, TsaTraceRowD* trace,
+                            uint64_t* best_rec, hipStream_t stream) {
+  hipLaunchKernelGGL(k_track, dim3(1), dim3(1024), 0, stream, lc, sc, ns, nchains, S, level, rec, chain_words, stt, trace,
+                     best_rec);
+  return hipGetLastError();
+}
+
+hipError_t tsa_launch_track_init(TsaTrackState* stt, unsigned long long* ticks0, hipStream_t stream) {
+  hipLaunchKernelGGL(k_track_init, dim3(1), dim3(1), 0, stream, stt, ticks0);
+  return hipGetLastError();
 }
 
 hipError_t tsa_launch_copy(const uint64_t* src, uint64_t* dst, const int* anc, int nchains, int chain_words,

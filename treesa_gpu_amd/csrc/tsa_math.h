@@ -49,8 +49,10 @@ TSA_MATH_FN float tsa_ffrom(uint32_t u) { float x; memcpy(&x, &u, 4); return x; 
    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,       \
    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull}
 
-#if defined(__HIP_DEVICE_COMPILE__)
+#if defined(__HIPCC__)
 __constant__ static const uint64_t tsa_exp2_tab_d[32] = TSA_EXP2_TAB;
+#endif
+#if defined(__HIP_DEVICE_COMPILE__)
 #define TSA_EXP2_TABLE tsa_exp2_tab_d
 #else
 static const uint64_t tsa_exp2_tab_h[32] = TSA_EXP2_TAB;
@@ -65,7 +67,9 @@ static const uint64_t tsa_exp2_tab_h[32] = TSA_EXP2_TAB;
 #define TSA_EXP_INVLN2N (0x1.71547652b82fep+0 * 32)
 #define TSA_EXPF_RAISE31 30ull
 
-TSA_MATH_FN float tsa_expf(float x) {
+// expf with the 2^(i/32) table passed in (kernels pass a copy staged in LDS: a per-lane index into a
+// constant or kernel-argument array would be a vector memory load on every call).
+TSA_MATH_FN float tsa_expf_t(float x, const uint64_t* tab) {
   const uint32_t abstop = (tsa_fbits(x) >> 20) & 0x7ff;
   if (abstop >= 0x42b) {  // |x| >= 88: infinities, NaN, overflow and underflow
     if (tsa_fbits(x) == 0xff800000u) return 0.0f;
@@ -80,7 +84,7 @@ TSA_MATH_FN float tsa_expf(float x) {
   kd -= TSA_EXP_SHIFT;
   const double r = z - kd;
   const uint32_t i = (uint32_t)(ki & 31u);
-  const uint64_t t = TSA_EXP2_TABLE[i] + (i == 31u ? TSA_EXPF_RAISE31 : 0ull) + (ki << 47);
+  const uint64_t t = tab[i] + (i == 31u ? TSA_EXPF_RAISE31 : 0ull) + (ki << 47);
   const double s = tsa_dfrom(t);
   const double c0 = TSA_EXP2_C0 / 32 / 32 / 32, c1 = TSA_EXP2_C1 / 32 / 32, c2 = TSA_EXP2_C2 / 32;
   const double zz = fma(c0, r, c1);
@@ -90,7 +94,7 @@ TSA_MATH_FN float tsa_expf(float x) {
   return (float)(y * s);
 }
 
-TSA_MATH_FN float tsa_exp2f(float x) {
+TSA_MATH_FN float tsa_exp2f_t(float x, const uint64_t* tab) {
   const uint32_t abstop = (tsa_fbits(x) >> 20) & 0x7ff;
   if (abstop >= 0x430) {  // |x| >= 128
     if (tsa_fbits(x) == 0xff800000u) return 0.0f;
@@ -103,7 +107,7 @@ TSA_MATH_FN float tsa_exp2f(float x) {
   const uint64_t ki = tsa_dbits(kd);
   kd -= TSA_EXP_SHIFT / 32;
   const double r = xd - kd;
-  const uint64_t t = TSA_EXP2_TABLE[ki & 31u] + (ki << 47);
+  const uint64_t t = tab[ki & 31u] + (ki << 47);
   const double s = tsa_dfrom(t);
   const double zz = fma(TSA_EXP2_C0, r, TSA_EXP2_C1);
   const double r2 = r * r;
@@ -111,6 +115,9 @@ TSA_MATH_FN float tsa_exp2f(float x) {
   y = fma(zz, r2, y);
   return (float)(y * s);
 }
+
+TSA_MATH_FN float tsa_expf(float x) { return tsa_expf_t(x, TSA_EXP2_TABLE); }
+TSA_MATH_FN float tsa_exp2f(float x) { return tsa_exp2f_t(x, TSA_EXP2_TABLE); }
 
 // log2(y) in double for y in [1, 2] (float input): halve above sqrt(2), then
 // log(v) = 2 atanh(s), s = (v - 1) / (v + 1), |s| <= 0.1716, series to s^23 (error < 1e-17 relative).
@@ -151,10 +158,16 @@ TSA_MATH_FN float tsa_log2f_12(float y, const uint32_t* fix) {
   return tsa_ffrom(tsa_fbits(r) + (code == 1u ? 1u : 0xffffffffu));
 }
 
+// Tables the float math reads: the 2^(i/32) table and the log2f correction table.
+struct TsaMathTabs {
+  const uint64_t* exp2;
+  const uint32_t* fix;
+};
+
 // log2(2^a + 2^b) for floats (a or b may be -inf), the fold of modeled node costs.
-TSA_MATH_FN float tsa_lse_f(float a, float b, const uint32_t* fix) {
+TSA_MATH_FN float tsa_lse_f(float a, float b, const TsaMathTabs& T) {
   const float mx = a > b ? a : b;
   const float mn = a > b ? b : a;
   if (mx == -INFINITY) return mx;
-  return mx + tsa_log2f_12(1.0f + tsa_exp2f(mn - mx), fix);
+  return mx + tsa_log2f_12(1.0f + tsa_exp2f_t(mn - mx, T.exp2), T.fix);
 }

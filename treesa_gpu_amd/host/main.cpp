@@ -18,6 +18,7 @@
 
 #include "treesa_hip.h"
 #include "tsa_host.h"
+#include "tsa_select.h"
 
 using namespace tsa;
 
@@ -37,6 +38,8 @@ struct Opts {
   ModelConsts mc;
   int mode2 = 1;
   int max_levels = -1;
+  int bench_warmup = 0;  // untimed levels before the level loop (then the population is re-uploaded)
+  bool host_select = false;  // select on the host every level even for indep runs
 };
 
 double now_s() { return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count(); }
@@ -57,7 +60,9 @@ std::string jnum(double x) {
           "  [--sc-target x] [--sc-weight y] [--scheme indep|pa|trunc] [--trunc-frac f]\n"
           "  [--slicing [--slice-moves k] [--slice-every s] [--max-slices n] [--init-slices l1,l2,..]]\n"
           "  [--order par|preorder] [--kernel auto|seq|seqsm|warp|warpsm|block|par [--wpc n]] [--lpc 32|16|8] [--coop-max G] [--coop-min G0] [--coop-full G1] [--par-follow] [--par-band L] [--coop-min-units u] [--wide] [--sums|--no-sum] [--select-sc] [--block B] [--wpb W] [--seed s]\n"
-          "  [--eval-every k] [--out result.json] [--check [--ref-chains R] [--random-slices k]] [--quiet]\n");
+          "  [--eval-every k] [--out result.json] [--check [--ref-chains R] [--random-slices k]] [--quiet]\n"
+          "  [--bench-warmup W]  (W untimed levels first, then the initial population again)\n"
+          "  [--host-select]  (select the best chain on the host at every level, also for --scheme indep)\n");
   exit(1);
 }
 
@@ -108,6 +113,8 @@ Opts parse(int argc, char** argv) {
       else if (a == "--eval-every") o.eval_every = std::stoi(nx());
       else if (a == "--ref-chains") o.ref_chains = std::stoi(nx());
       else if (a == "--max-levels") o.max_levels = std::stoi(nx());
+      else if (a == "--bench-warmup") o.bench_warmup = std::stoi(nx());
+      else if (a == "--host-select") o.host_select = true;
       else if (a == "--slicing") o.slicing = true;
       else if (a == "--slice-moves") o.slice_moves = std::stoi(nx());
       else if (a == "--slice-every") o.slice_every = std::stoi(nx());
@@ -259,23 +266,21 @@ class Runner {
   const uint64_t* chS(const uint64_t* base) const { return O.slicing ? base + lay.s_off : nullptr; }
   const uint32_t* chCh(const uint64_t* base) const { return reinterpret_cast<const uint32_t*>(base + lay.ch_off); }
 
-  // Selection score, lower is better, log2 domain (csrc/treesa_gpu.cu:1737-1748).
-  double score(float lc, int sc, int ns) const {
-    if (O.slicing) return (double)ns + (double)lc + 1000.0 * std::max(0.0, (double)sc - O.sc_target);
-    if (O.select_sc) return 4096.0 * (double)std::max(0.0, (double)sc - O.sc_target) + (double)lc;
-    if (mode == 0) {
-      const double tc = (double)lc;
-      if ((double)sc <= O.sc_target || O.sc_weight <= 0) return tc;
-      const double pen = std::log2(O.sc_weight) + (double)sc + std::log2(1.0 - std::exp2(O.sc_target - (double)sc));
-      const double mx = std::max(tc, pen), mn = std::min(tc, pen);
-      return mx + std::log2(1.0 + std::exp2(mn - mx));
-    }
-    return energyE(lc, sc, ns);
+  // Selection score and population energy (tsa_select.h, the same functions the device-side tracking
+  // evaluates).
+  TsaSelect select_params() const {
+    TsaSelect S;
+    S.mode = mode;
+    S.slicing = O.slicing ? 1 : 0;
+    S.select_sc = O.select_sc ? 1 : 0;
+    S.sc_target = O.sc_target;
+    S.sc_weight = O.sc_weight;
+    return S;
   }
-  // Population energy: |S| + lcost + sc_weight * max(0, sc - sc_target) (csrc/treesa_gpu.cu:1751-1753).
-  double energyE(float lc, int sc, int ns) const {
-    return (double)ns + (double)lc + O.sc_weight * std::max(0.0, (double)sc - O.sc_target);
-  }
+  double score(float lc, int sc, int ns) const { return tsa_score(lc, sc, ns, select_params()); }
+  double energyE(float lc, int sc, int ns) const { return tsa_energyE(lc, sc, ns, select_params()); }
+  int run_levels_tracked(const std::vector<float>& betas, const std::vector<int>& lniters, uint32_t& sweep_ctr,
+                         std::vector<uint64_t>& best, std::string& trace, double t0);
   void resample(const std::vector<int>& anc, std::vector<int>& family) {
     ck(tsa_resample(ctx, anc.data()));
     std::vector<int> nfm(O.nchains);
@@ -289,6 +294,57 @@ class Runner {
     return strncmp(b, "lds", 3) == 0 ? "warpsm" : "warp";
   }
 };
+
+// The level loop of an indep run with device-side selection: every level enqueues its sweeps and, at
+// evaluated levels, the energy and selection kernels; the host waits once at the end.  The selected chain,
+// the trace rows and the kernel time are those of the synchronous loop below (same score function, same
+// first-chain / first-level tie rule); only the trace's time column comes from the device clock.
+int Runner::run_levels_tracked(const std::vector<float>& betas, const std::vector<int>& lniters, uint32_t& sweep_ctr,
+                               std::vector<uint64_t>& best, std::string& trace, double t0) {
+  const TsaSelect S = select_params();
+  tsa_select_t sel;
+  sel.mode = S.mode;
+  sel.slicing = S.slicing;
+  sel.select_sc = S.select_sc;
+  sel.sc_target = S.sc_target;
+  sel.sc_weight = S.sc_weight;
+  const int nlev = (int)betas.size();
+  ck(tsa_track_begin(ctx, &sel, nlev));
+  std::vector<char> evaluated(nlev, 0);
+  for (int lev = 0; lev < nlev; lev++) {
+    ck(tsa_sweeps(ctx, order, betas[lev], sweep_ctr, lniters[lev]));
+    sweep_ctr += (uint32_t)lniters[lev];
+    const bool last = lev + 1 == nlev;
+    if (lev % O.eval_every == O.eval_every - 1 || last) {
+      ck(tsa_track(ctx, lev));
+      evaluated[lev] = 1;
+    }
+  }
+  double ms = 0;
+  ck(tsa_sweeps_ms(ctx, &ms));
+  kernel_ms += ms;
+  std::vector<tsa_trace_row_t> rows(nlev);
+  int32_t bc = -1, bl = -1;
+  double bs = 0, hz = 1;
+  uint64_t tk0 = 0;
+  ck(tsa_track_end(ctx, &bc, &bl, &bs, best.data(), rows.data(), &tk0, &hz));
+  const double t_dev0 = now_s() - t0;  // the level loop has finished; device times are scaled to it
+  const double span = std::max(1.0, (double)(rows[nlev - 1].ticks - tk0));
+  for (int lev = 0; lev < nlev; lev++) {
+    if (!evaluated[lev]) continue;
+    const tsa_trace_row_t& r = rows[lev];
+    const double t = t_dev0 * (double)(r.ticks - tk0) / span;
+    char buf[320];
+    snprintf(buf, sizeof buf, "%s[%.4f,%d,%.4f,%.6f,%d,%.6f,%d,%d,%d,%.3f]", trace.empty() ? "" : ",", t, lev,
+             betas[lev], (double)r.lc, r.sc, r.meanE, O.nchains, mode, r.ns, r.meanNs);
+    trace += buf;
+    if (!O.quiet && (lev % 25 == 0 || lev + 1 == nlev))
+      fprintf(stderr, "lev %4d beta %7.3f  best(l2cost/slice %.3f sc %d |S| %d)  meanE %.3f  mean|S| %.2f  families %d  t=%.2fs\n",
+              lev, betas[lev], (double)r.lc, r.sc, r.ns, r.meanE, r.meanNs, O.nchains, t);
+  }
+  (void)hz;
+  return bc;
+}
 
 int Runner::run_anneal() {
   std::vector<float> betas = parse_betas(O.betas);
@@ -306,9 +362,23 @@ int Runner::run_anneal() {
   uint32_t sweep_ctr = 0;
   const double t_start = now_s();
   create(&ctx, cfg.kernel);
+  uint64_t stats0[7] = {0, 0, 0, 0, 0, 0, 0};
   {
     const std::vector<uint64_t> pop = init_population();
     ck(tsa_upload(ctx, pop.data()));
+    if (O.bench_warmup > 0 && !betas.empty()) {
+      // untimed warm-up levels (clocks, code objects), then the same initial population again
+      std::vector<float> l(O.nchains);
+      std::vector<int> s(O.nchains), n(O.nchains);
+      for (int k = 0; k < O.bench_warmup; k++) {
+        ck(tsa_sweeps(ctx, order, betas[k % betas.size()], (uint32_t)k, lniters[k % betas.size()]));
+        ck(tsa_energy(ctx, l.data(), s.data(), n.data()));
+      }
+      double ms = 0;
+      ck(tsa_sweeps_ms(ctx, &ms));
+      ck(tsa_upload(ctx, pop.data()));
+      ck(tsa_stats(ctx, stats0));
+    }
   }
   const double t_init = now_s() - t_start;
   const double t0 = now_s();
@@ -324,7 +394,10 @@ int Runner::run_anneal() {
   std::mt19937_64 hrng(splitmix64(O.seed + 777));
   float beta_last_resample = betas.empty() ? 0.f : betas[0];
   int nresample = 0;
-  for (size_t lev = 0; lev < betas.size(); lev++) {
+  // independent chains in one energy mode: selection runs on the device, no host round trip per level
+  const bool tracked = O.scheme == "indep" && O.betas2.empty() && !betas.empty() && !O.host_select;
+  if (tracked) best_chain = run_levels_tracked(betas, lniters, sweep_ctr, best, trace, t0);
+  for (size_t lev = 0; lev < (tracked ? 0 : betas.size()); lev++) {
     if (lmode[lev] != mode) {
       // stage switch: the stage-1 best stays the incumbent, scored in the new energy
       H1 = host_energy(I, lay.W, ML, best.data(), chCh(best.data()), leaf, chS(best.data()));
@@ -417,6 +490,7 @@ int Runner::run_anneal() {
   const double t_anneal = now_s() - t0;
   uint64_t stats[7];
   ck(tsa_stats(ctx, stats));
+  for (int k = 0; k < 7; k++) stats[k] -= stats0[k];
 
   // final best tree: verified from scratch; with slicing, sc > sc_target is repaired greedily
   const uint32_t* bch = chCh(best.data());
