@@ -92,6 +92,21 @@ def algorithmic_bytes(st, W):
     return prop * (40 * W + 8) + acc * (8 * W + 8) + (visits - prop) * 4
 
 
+PROFILES = {"c2": "k_sweep_c2_sat100_par.md"}
+
+
+def measured_traffic(cfgname):
+    """HBM bytes per sweep-kernel dispatch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary."""
+    f = PROFILES.get(cfgname)
+    if not f or not os.path.exists(os.path.join(ROOT, "profiles", f)):
+        return None
+    with open(os.path.join(ROOT, "profiles", f)) as fh:
+        for line in fh:
+            if line.strip().startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":")[1])
+    return None
+
+
 def cpu_baseline(C, inst, trees, betas, nsample):
     ref = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
     with tempfile.TemporaryDirectory() as td:
@@ -126,7 +141,7 @@ def cpu_baseline(C, inst, trees, betas, nsample):
                 sample=f"{nsample} of {C['nchains']} chains x {len(betas)} sweeps ({visits:.3e} visits, {secs:.1f} s)")
 
 
-def run_binary(C, trees, betas, steps, warmup):
+def run_binary(C, trees, betas, steps, warmup, scheme="indep"):
     """The drop-in binary's level loop on the workload; returns its JSON result."""
     with tempfile.TemporaryDirectory() as td:
         tf = os.path.join(td, "trees.txt")
@@ -140,7 +155,7 @@ def run_binary(C, trees, betas, steps, warmup):
         out = os.path.join(td, "out.json")
         args = [capi.BIN_PATH, "-i", os.path.join(DATA, C["inst"] + ".txt"), "--tree", tf, "--betas", "file:" + bf,
                 "--nchains", str(C["nchains"]), "--niters", "1", "--sc-target", str(C["sc_target"]), "--mode", "tc",
-                "--order", C["order"], "--kernel", "auto", "--scheme", "indep", "--seed", "1", "--eval-every", "1",
+                "--order", C["order"], "--kernel", "auto", "--scheme", scheme, "--seed", "1", "--eval-every", "1",
                 "--bench-warmup", str(warmup), "--out", out, "--quiet"]
         p = subprocess.run(args, capture_output=True, text=True)
         if p.returncode != 0:
@@ -156,7 +171,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-chains", type=int, default=128)
+    ap.add_argument("--cpu-chains", type=int, default=256)
+    ap.add_argument("--scheme", default="indep", choices=("indep", "pa", "trunc"),
+                    help="population scheme (pa resamples every level: its copy kernel moves a known number of "
+                         "bytes, which calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.exit("bench.py measures one GPU: chains are independent, and a multi-GPU run would shard them across "
@@ -164,7 +182,7 @@ def main():
     C, inst, lay, trees, pop, cfg, betas, order = setup(a.config)
     steps = a.steps or C["levels"]
     nchains = C["nchains"]
-    r = run_binary(C, trees, betas, steps, a.warmup)
+    r = run_binary(C, trees, betas, steps, a.warmup, a.scheme)
     visits = steps * nchains * (inst.m - 1)
     assert r["node_visits"] == visits, (r["node_visits"], visits)
     st = [r["proposals"], r["accepts"], r["warp_steps"], r["node_visits"]]
@@ -182,7 +200,7 @@ def main():
         "proposals": r["proposals"], "accepts": r["accepts"], "phases": r["warp_steps"],
         "best_tc": r["tc"], "best_sc": r["sc"], "wall_s": wall,
         "roofline": {"bound": "hbm", "achieved": B / dur / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": B / dur / 1e9 / HBM_PEAK_GBS, "traffic": None,
+                     "frac": B / dur / 1e9 / HBM_PEAK_GBS, "traffic": measured_traffic(a.config),
                      "kernel": "k_sweep " + ("par" if order == capi.ORDER_PAR else "pre-order") + ", chain in LDS",
                      "bytes_per_launch": B, "avg_launch_ms": dur * 1e3},
     }

@@ -361,10 +361,10 @@ int Runner::run_anneal() {
   bool staged = false;
   uint32_t sweep_ctr = 0;
   const double t_start = now_s();
-  create(&ctx, cfg.kernel);
   uint64_t stats0[7] = {0, 0, 0, 0, 0, 0, 0};
   {
-    const std::vector<uint64_t> pop = init_population();
+    const std::vector<uint64_t> pop = init_population();  // input errors surface before the device is touched
+    create(&ctx, cfg.kernel);
     ck(tsa_upload(ctx, pop.data()));
     if (O.bench_warmup > 0 && !betas.empty()) {
       // untimed warm-up levels (clocks, code objects), then the same initial population again
@@ -551,8 +551,8 @@ int Runner::run_anneal() {
 int Runner::run_check() {
   std::vector<float> betas = parse_betas(O.betas);
   if (O.max_levels > 0 && (int)betas.size() > O.max_levels) betas.resize(O.max_levels);
-  create(&ctx, cfg.kernel);
   const std::vector<uint64_t> init = init_population();
+  create(&ctx, cfg.kernel);
   ck(tsa_upload(ctx, init.data()));
   for (size_t lev = 0; lev < betas.size(); lev++)
     ck(tsa_sweeps(ctx, order, betas[lev], (uint32_t)(lev * O.niters), O.niters));
