@@ -47,12 +47,25 @@ def linear_betas(a, b, n):
 
 CONFIGS = {
     # the reference's CPU-runnable check case: greedy start, pre-order, 256 chains x 100 sweeps
-    "c1": dict(inst="sat100", trees=("sat100.tree", None), order="preorder", nchains=256, levels=100,
-               betas=(0.01, 15.0), sc_target=20.0, desc="random 3-SAT n=100 (m=426), greedy start, pre-order, "
-                                                        "256 chains x 100 sweeps, beta 0.01->15"),
-    "c2": dict(inst="sat100", trees=("sat100_multi.tree", (1, 2, 3)), order="par", nchains=8192, levels=200,
-               betas=(1.0, 15.0), sc_target=20.0, desc="random 3-SAT n=100 (m=426), spectral path starts, par order, "
-                                                        "8192 chains x 200 sweeps, beta 1->15, best-of-N"),
+    "c1": dict(cpu_chains=256, inst="sat100", trees=("sat100.tree", None), order="preorder", nchains=256, levels=100, niters=1,
+               betas=(0.01, 15.0), sc_target=20.0, scheme="indep", slicing=False,
+               desc="random 3-SAT n=100 (m=426), greedy start, pre-order, 256 chains x 100 sweeps, beta 0.01->15"),
+    "c2": dict(cpu_chains=256, inst="sat100", trees=("sat100_multi.tree", (1, 2, 3)), order="par", nchains=8192, levels=200, niters=1,
+               betas=(1.0, 15.0), sc_target=20.0, scheme="indep", slicing=False,
+               desc="random 3-SAT n=100 (m=426), spectral path starts, par order, 8192 chains x 200 sweeps, "
+                    "beta 1->15, best-of-N"),
+    "c3": dict(cpu_chains=64, inst="sat70", trees=("sat70_greedy.tree", None), order="par", nchains=2048, levels=20, niters=10,
+               betas=(0.01, 15.0), sc_target=24.0, scheme="pa", slicing=True,
+               desc="random 3-SAT n=70 (m=298), greedy start, par order, slicing (1 slice move per sweep), "
+                    "2048 chains x 200 sweeps, population annealing every 10 sweeps, beta 0.01->15"),
+    "c4": dict(cpu_chains=8, inst="reg3_2000", trees=("reg3_2000_spectral.tree", None), order="par", nchains=512, levels=100,
+               niters=1, betas=(1.0, 15.0), sc_target=40.0, scheme="indep", slicing=False,
+               desc="random 3-regular graph n=2000 (3000 labels, 47 words), spectral path starts, par order, "
+                    "512 chains x 100 sweeps, beta 1->15"),
+    "c5": dict(cpu_chains=72, inst="sq64", trees=("sq64_row.tree", None), order="par", nchains=72, levels=20, niters=1,
+               betas=(0.01, 15.0), sc_target=70.0, scheme="indep", slicing=False,
+               desc="64x64 open lattice (4096 tensors, 8064 labels, 126 words), row-major path start, par order, "
+                    "72 chains x 20 sweeps, beta 0.01->15"),
 }
 
 
@@ -85,11 +98,16 @@ def setup(cfgname):
     return C, inst, lay, trees, pop, cfg, betas, order
 
 
-def algorithmic_bytes(st, W):
-    """Per the sweep-kernel counters: proposals read 5 sets + 8 B children, accepts write a set + 8 B,
-    visits without a rule read 4 B."""
-    prop, acc, visits = st[0], st[1], st[3]
-    return prop * (40 * W + 8) + acc * (8 * W + 8) + (visits - prop) * 4
+def algorithmic_bytes(st, W, nint, slicing=False, slice_steps=0):
+    """From the sweep kernel's counters: a proposal reads 5 label sets (+ S when slicing) and 8 B of children,
+    an accept writes one set and 8 B, a visit without a rule reads 4 B; a slice step evaluates the whole chain
+    once plus once per slice proposal (3 sets + 4 B per node, + S) and scans the internal sets once per slice
+    proposal."""
+    prop, acc, visits, sprop = st[0], st[1], st[3], st[4]
+    b = prop * (40 * W + 8 + (8 * W if slicing else 0)) + acc * (8 * W + 8) + (visits - prop) * 4
+    evals = slice_steps + sprop
+    b += evals * (24 * W * nint + 4 * nint + 8 * W) + sprop * 8 * W * nint
+    return b
 
 
 PROFILES = {"c2": "k_sweep_c2_sat100_par.md"}
@@ -107,41 +125,52 @@ def measured_traffic(cfgname):
     return None
 
 
-def cpu_baseline(C, inst, trees, betas, nsample):
+def cpu_port_worker(cfgname, nsample):
+    """One-thread timing of the oracle port (slice moves included) on nsample chains; prints seconds."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle as orc
+    from common import oracle_population
+    C, inst, lay, trees, pop, cfg, betas, order = setup(cfgname)
+    m, nlab, ixs, iy = orc.read_instance_py(os.path.join(DATA, C["inst"] + ".txt"))
+    O = orc.Oracle(m, nlab, ixs, iy)
+    p0 = oracle_population(O, lay, m, nsample, 1, trees)
+    ocfg = capi.make_config(mode="tc", sc_target=C["sc_target"], seed=1, slicing=C["slicing"], slice_moves=1)
+    P = orc.params_from_config(ocfg, inst.leaf_sc, nlab)
+    t0 = time.perf_counter()
+    for lev, b in enumerate(betas):
+        O.sweeps(P, lay, p0, order, b, lev * C["niters"], C["niters"])
+    print(time.perf_counter() - t0)
+
+
+def cpu_baseline(cfgname, C, inst, trees, betas, nsample):
+    """The reference's own CPU port (oracle/_ref, csrc/cpu_ref.h) on one core over nsample chains and every
+    level; configurations with slice moves (which the reference's CPU port lacks) time the oracle port."""
     ref = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
-    with tempfile.TemporaryDirectory() as td:
-        tf = os.path.join(td, "trees.txt")
-        with open(tf, "w") as f:
-            for t in trees:
-                for w in t:
-                    f.write(f"{int(w) & 0xFFFF} {int(w) >> 16}\n")
-        bs = ",".join(repr(b) for b in betas)
-        if os.path.exists(ref):
+    if os.path.exists(ref) and not C["slicing"]:
+        with tempfile.TemporaryDirectory() as td:
+            tf = os.path.join(td, "trees.txt")
+            with open(tf, "w") as f:
+                for t in trees:
+                    for w in t:
+                        f.write(f"{int(w) & 0xFFFF} {int(w) >> 16}\n")
+            bs = ",".join(repr(b) for b in betas)
             args = [ref, "-i", os.path.join(DATA, C["inst"] + ".txt"), "--tree", tf, "--chains", str(nsample),
-                    "--niters", "1", "--betas", bs, "--order", C["order"], "--mode", "tc", "--sc-target",
-                    str(C["sc_target"]), "--seed", "1", "--timing"]
+                    "--niters", str(C["niters"]), "--betas", bs, "--order", C["order"], "--mode", "tc",
+                    "--sc-target", str(C["sc_target"]), "--seed", "1", "--timing"]
             out = json.loads(subprocess.run(args, check=True, capture_output=True, text=True).stdout)
             secs, kind = out["seconds"], "reference"
-        else:  # the oracle restatement, one thread
-            sys.path.insert(0, os.path.join(ROOT, "tests"))
-            import oracle as orc
-            from common import oracle_population
-            m, nlab, ixs, iy = orc.read_instance_py(os.path.join(DATA, C["inst"] + ".txt"))
-            O = orc.Oracle(m, nlab, ixs, iy)
-            lay = capi.layout(m, nlab)
-            pop = oracle_population(O, lay, m, nsample, 1, trees)
-            P = orc.params_from_config(capi.make_config(mode="tc", sc_target=C["sc_target"], seed=1), 3, nlab)
-            os.environ["OMP_NUM_THREADS"] = "1"
-            t0 = time.perf_counter()
-            for lev, b in enumerate(betas):
-                O.sweeps(P, lay, pop, 0 if C["order"] == "par" else 1, b, lev, 1)
-            secs, kind = time.perf_counter() - t0, "port"
-    visits = nsample * len(betas) * (inst.m - 1)
+    else:
+        env = dict(os.environ, OMP_NUM_THREADS="1")
+        p = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-port-worker", cfgname, "--cpu-chains",
+                            str(nsample)], check=True, capture_output=True, text=True, env=env)
+        secs, kind = float(p.stdout.strip().splitlines()[-1]), "port"
+    visits = nsample * len(betas) * C["niters"] * (inst.m - 1)
     return dict(value=visits / secs, unit="node visits/s", cores=1, kind=kind,
-                sample=f"{nsample} of {C['nchains']} chains x {len(betas)} sweeps ({visits:.3e} visits, {secs:.1f} s)")
+                sample=f"{nsample} of {C['nchains']} chains x {len(betas) * C['niters']} sweeps "
+                       f"({visits:.3e} visits, {secs:.1f} s)")
 
 
-def run_binary(C, trees, betas, steps, warmup, scheme="indep"):
+def run_binary(C, trees, betas, steps, warmup, scheme=None):
     """The drop-in binary's level loop on the workload; returns its JSON result."""
     with tempfile.TemporaryDirectory() as td:
         tf = os.path.join(td, "trees.txt")
@@ -154,9 +183,11 @@ def run_binary(C, trees, betas, steps, warmup, scheme="indep"):
             f.write("\n".join(repr(betas[k % len(betas)]) for k in range(steps)) + "\n")
         out = os.path.join(td, "out.json")
         args = [capi.BIN_PATH, "-i", os.path.join(DATA, C["inst"] + ".txt"), "--tree", tf, "--betas", "file:" + bf,
-                "--nchains", str(C["nchains"]), "--niters", "1", "--sc-target", str(C["sc_target"]), "--mode", "tc",
-                "--order", C["order"], "--kernel", "auto", "--scheme", scheme, "--seed", "1", "--eval-every", "1",
-                "--bench-warmup", str(warmup), "--out", out, "--quiet"]
+                "--nchains", str(C["nchains"]), "--niters", str(C["niters"]), "--sc-target", str(C["sc_target"]),
+                "--mode", "tc", "--order", C["order"], "--kernel", "auto", "--scheme", scheme or C["scheme"],
+                "--seed", "1", "--eval-every", "1", "--bench-warmup", str(warmup), "--out", out, "--quiet"]
+        if C["slicing"]:
+            args += ["--slicing", "--slice-moves", "1", "--slice-every", "1"]
         p = subprocess.run(args, capture_output=True, text=True)
         if p.returncode != 0:
             raise RuntimeError(f"treesa_gpu failed ({p.returncode}): {p.stderr[-2000:]}")
@@ -171,11 +202,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-chains", type=int, default=256)
-    ap.add_argument("--scheme", default="indep", choices=("indep", "pa", "trunc"),
+    ap.add_argument("--cpu-chains", type=int, default=None, help="chains in the CPU sample (default per workload)")
+    ap.add_argument("--cpu-port-worker", default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--scheme", default=None, choices=("indep", "pa", "trunc"),
                     help="population scheme (pa resamples every level: its copy kernel moves a known number of "
                          "bytes, which calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     a = ap.parse_args()
+    if a.cpu_port_worker:
+        cpu_port_worker(a.cpu_port_worker, a.cpu_chains or 1)
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.exit("bench.py measures one GPU: chains are independent, and a multi-GPU run would shard them across "
                  "processes (see DESIGN.md); run with --gpus 1")
@@ -183,10 +218,11 @@ def main():
     steps = a.steps or C["levels"]
     nchains = C["nchains"]
     r = run_binary(C, trees, betas, steps, a.warmup, a.scheme)
-    visits = steps * nchains * (inst.m - 1)
+    visits = steps * C["niters"] * nchains * (inst.m - 1)
     assert r["node_visits"] == visits, (r["node_visits"], visits)
-    st = [r["proposals"], r["accepts"], r["warp_steps"], r["node_visits"]]
-    B = algorithmic_bytes(st, lay.W) / steps
+    st = [r["proposals"], r["accepts"], r["warp_steps"], r["node_visits"], r["slice_proposals"]]
+    slice_steps = steps * C["niters"] * nchains if C["slicing"] else 0
+    B = algorithmic_bytes(st, lay.W, inst.m - 1, C["slicing"], slice_steps) / steps
     dur = r["kernel_s"] / steps
     wall = r["t_anneal"]
     res = {
@@ -195,17 +231,20 @@ def main():
         "vs_baseline": None, "dtype": "u64",
         "data": "synthetic: the reference's committed instance and start-tree fixtures, seed 1",
         "config": {"workload": C["desc"], "config": a.config, "nchains": nchains, "levels_timed": steps,
-                   "sweeps_per_level": 1, "label_words64": lay.W, "kernel": r.get("hip_kernel")},
-        "kernel_visits_per_s": visits / r["kernel_s"], "sweeps_per_s_per_chain": steps / r["kernel_s"],
+                   "sweeps_per_level": C["niters"], "label_words64": lay.W, "kernel": r.get("hip_kernel"),
+                   "scheme": a.scheme or C["scheme"]},
+        "kernel_visits_per_s": visits / r["kernel_s"], "sweeps_per_s_per_chain": steps * C["niters"] / r["kernel_s"],
+        "slice_proposals": r["slice_proposals"], "slice_accepts": r["slice_accepts"], "nsliced": r["nsliced"],
         "proposals": r["proposals"], "accepts": r["accepts"], "phases": r["warp_steps"],
         "best_tc": r["tc"], "best_sc": r["sc"], "wall_s": wall,
         "roofline": {"bound": "hbm", "achieved": B / dur / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": B / dur / 1e9 / HBM_PEAK_GBS, "traffic": measured_traffic(a.config),
-                     "kernel": "k_sweep " + ("par" if order == capi.ORDER_PAR else "pre-order") + ", chain in LDS",
+                     "kernel": "k_sweep " + ("par" if order == capi.ORDER_PAR else "pre-order") + ", "
+                               + ("chain in LDS" if "lds" in (r.get("hip_kernel") or "") else "chain in HBM"),
                      "bytes_per_launch": B, "avg_launch_ms": dur * 1e3},
     }
     if not a.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(C, inst, trees, betas, min(a.cpu_chains, nchains))
+        res["cpu_baseline"] = cpu_baseline(a.config, C, inst, trees, betas, min(a.cpu_chains or C["cpu_chains"], nchains))
     print(json.dumps(res))
 
 
