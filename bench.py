@@ -170,7 +170,15 @@ def cpu_baseline(cfgname, C, inst, trees, betas, nsample):
                        f"({visits:.3e} visits, {secs:.1f} s)")
 
 
-def run_binary(C, trees, betas, steps, warmup, scheme=None):
+def kernel_label(desc, order):
+    """Name of the sweep kernel the binary ran, from its hip_kernel description."""
+    o = "par" if order == capi.ORDER_PAR else "pre-order"
+    if desc.startswith("wide") and order == capi.ORDER_PAR:
+        return "k_wide par, label sets in HBM, " + desc.split(" ", 1)[1]
+    return f"k_sweep {o}, " + ("chain in LDS" if desc.startswith("lds") else "chain in HBM")
+
+
+def run_binary(C, trees, betas, steps, warmup, scheme=None, extra=()):
     """The drop-in binary's level loop on the workload; returns its JSON result."""
     with tempfile.TemporaryDirectory() as td:
         tf = os.path.join(td, "trees.txt")
@@ -188,6 +196,7 @@ def run_binary(C, trees, betas, steps, warmup, scheme=None):
                 "--seed", "1", "--eval-every", "1", "--bench-warmup", str(warmup), "--out", out, "--quiet"]
         if C["slicing"]:
             args += ["--slicing", "--slice-moves", "1", "--slice-every", "1"]
+        args += list(extra)
         p = subprocess.run(args, capture_output=True, text=True)
         if p.returncode != 0:
             raise RuntimeError(f"treesa_gpu failed ({p.returncode}): {p.stderr[-2000:]}")
@@ -207,6 +216,8 @@ def main():
     ap.add_argument("--scheme", default=None, choices=("indep", "pa", "trunc"),
                     help="population scheme (pa resamples every level: its copy kernel moves a known number of "
                          "bytes, which calibrates the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--wide-waves", type=int, default=0, help="wide kernel: waves per workgroup (0: automatic)")
+    ap.add_argument("--wide-wgs", type=int, default=0, help="wide kernel: workgroups per chain (0: automatic)")
     a = ap.parse_args()
     if a.cpu_port_worker:
         cpu_port_worker(a.cpu_port_worker, a.cpu_chains or 1)
@@ -217,7 +228,9 @@ def main():
     C, inst, lay, trees, pop, cfg, betas, order = setup(a.config)
     steps = a.steps or C["levels"]
     nchains = C["nchains"]
-    r = run_binary(C, trees, betas, steps, a.warmup, a.scheme)
+    extra = (["--wpc", str(2 * a.wide_waves)] if a.wide_waves else []) + \
+        (["--wide-wgs", str(a.wide_wgs)] if a.wide_wgs else [])
+    r = run_binary(C, trees, betas, steps, a.warmup, a.scheme, extra)
     visits = steps * C["niters"] * nchains * (inst.m - 1)
     assert r["node_visits"] == visits, (r["node_visits"], visits)
     st = [r["proposals"], r["accepts"], r["warp_steps"], r["node_visits"], r["slice_proposals"]]
@@ -239,8 +252,7 @@ def main():
         "best_tc": r["tc"], "best_sc": r["sc"], "wall_s": wall,
         "roofline": {"bound": "hbm", "achieved": B / dur / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": B / dur / 1e9 / HBM_PEAK_GBS, "traffic": measured_traffic(a.config),
-                     "kernel": "k_sweep " + ("par" if order == capi.ORDER_PAR else "pre-order") + ", "
-                               + ("chain in LDS" if "lds" in (r.get("hip_kernel") or "") else "chain in HBM"),
+                     "kernel": kernel_label(r.get("hip_kernel") or "", order),
                      "bytes_per_launch": B, "avg_launch_ms": dur * 1e3},
     }
     if not a.no_cpu:

@@ -42,11 +42,15 @@ extern "C" {
 /* Kernel selection flags for tsa_create (results never depend on them). */
 #define TSA_KERNEL_AUTO 0
 #define TSA_KERNEL_LDS 1     /* chain staged in LDS (fails with TSA_ERR_FIT if it does not fit) */
-#define TSA_KERNEL_GLOBAL 2  /* chain worked on in HBM, node arrays in LDS */
+#define TSA_KERNEL_GLOBAL 2  /* chain worked on in HBM, node arrays in LDS, one wave per chain */
+#define TSA_KERNEL_WIDE 3    /* runtime-width chains, par order: G lanes per proposal, K workgroups per chain
+                                (fails with TSA_ERR_FIT if the chain does not qualify); AUTO picks it for
+                                runtime-width chains without slice moves */
 
 typedef struct tsa_layout_t {
   int32_t m, nint, nlab;
-  int32_t W;            /* 64-bit words per label set (1, 2, 4, 8 on the register path, else ceil(nlab/64)) */
+  int32_t W;            /* 64-bit words per label set (1, 2, 4, 8 on the register path, else ceil(nlab/64)
+                           rounded up to even, so that label sets and S are 16-byte aligned) */
   int32_t runtime_width;/* 1: kernels loop over W words at run time (wide path); 0: W is a register width */
   int32_t ch_off;       /* word offset of the children array */
   int32_t s_off;        /* word offset of S */
@@ -71,6 +75,8 @@ typedef struct tsa_config_t {
   /* measured H100 model, log2 of the constants (csrc/treesa_gpu.cu:1466-1474) */
   float v2_l3launch, v2_lperm2, v2_lcc_bit, v2_lcc_cell, v2_ltc_bit, v2_ltc_pad, v2_ltc_out, v2_lsmall_cell;
   int32_t v2_small_rank;
+  /* wide kernel plan (0 = automatic): waves per workgroup (1..16), workgroups per chain (1..16) */
+  int32_t wide_waves, wide_wgs;
 } tsa_config_t;
 
 typedef struct tsa_ctx tsa_ctx;

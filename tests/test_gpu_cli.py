@@ -33,7 +33,7 @@ def run(args, tmp_path, name="out.json"):
 
 
 @pytest.mark.parametrize("order", ["par", "preorder"])
-@pytest.mark.parametrize("inst", ["sat60", "lat14"])
+@pytest.mark.parametrize("inst", ["sat60", "lat14", "sq46"])  # sq46: the wide path and the many-block snapshot
 def test_device_selection_equals_host_selection(inst, order, tmp_path):
     args = ["-i", common.inst_path(inst), "--nchains", "96", "--niters", "2", "--betas", "0.01:0.05:15",
             "--sc-target", "30", "--order", order, "--seed", "3"]
@@ -50,7 +50,8 @@ def test_device_selection_equals_host_selection(inst, order, tmp_path):
 
 @pytest.mark.parametrize("inst,extra", [("sat100", ["--kernel", "par"]), ("sat100", ["--order", "preorder"]),
                                         ("reg3_250", ["--mode", "h100"]), ("grid24", ["--mode", "gpu"]),
-                                        ("sat60", ["--random-slices", "8"]),
+                                        ("sat60", ["--random-slices", "8"]), ("sq46", ["--kernel", "par"]),
+                                        ("grid45", ["--kernel", "par", "--mode", "h100"]),
                                         ("grid28", ["--slicing", "--sc-target", "20", "--mode", "h100"])])
 def test_check_mode_passes(inst, extra, tmp_path):
     args = [capi.BIN_PATH, "-i", common.inst_path(inst), "--tree", common.tree_file(inst, "greedy")] + CHECK_ARGS + extra

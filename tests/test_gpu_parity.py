@@ -29,7 +29,7 @@ def leaf_sets(m, ixs, W):
 class Case:
     def __init__(self, inst, order, mode, init="greedy", random_slices=0, par_follow=False, par_band=0, slicing=False,
                  slice_moves=1, slice_every=1, nchains=NCHAINS, kernel=capi.KERNEL_AUTO, wide=False, seed=None,
-                 sc_target=None):
+                 sc_target=None, wide_waves=0, wide_wgs=0):
         self.inst, self.order = inst, order
         m, nlab, ixs, iy = common.load_instance(inst)
         self.m, self.nlab, self.ixs = m, nlab, ixs
@@ -42,7 +42,8 @@ class Case:
         sl = slicing or random_slices > 0
         self.cfg = capi.make_config(mode=mode, sc_target=common.CHECK_SC_TARGET if sc_target is None else sc_target,
                                     seed=seed, slicing=sl, slice_moves=slice_moves if slicing else 0,
-                                    slice_every=slice_every, par_follow=par_follow, par_band=par_band, kernel=kernel)
+                                    slice_every=slice_every, par_follow=par_follow, par_band=par_band, kernel=kernel,
+                                    wide_waves=wide_waves, wide_wgs=wide_wgs)
         self.leaf_sc = max(len(x) for x in ixs)
         self.P = orc.params_from_config(self.cfg, self.leaf_sc, nlab)
         self.leaf = leaf_sets(m, ixs, self.lay.W)
@@ -51,7 +52,8 @@ class Case:
 
     def run_gpu(self, betas=common.CHECK_BETAS, niters=common.CHECK_NITERS):
         print(f"[gpu] {self.inst} {self.order} mode={self.cfg.mode} slicing={self.cfg.slicing} "
-              f"kernel={self.cfg.kernel} W={self.lay.W} chains={self.nchains}", flush=True)
+              f"kernel={self.cfg.kernel} W={self.lay.W} chains={self.nchains} wide_waves={self.cfg.wide_waves} "
+              f"wide_wgs={self.cfg.wide_wgs}", flush=True)
         with capi.Context(self.lay, self.leaf, self.leaf_sc, self.cfg, self.nchains) as ctx:
             ctx.upload(self.pop0)
             for lev, b in enumerate(betas):
@@ -117,6 +119,61 @@ def test_slice_moves_match_oracle_mirror(inst, order, mode, moves, every):
     gpu = case.run_gpu()
     assert gpu[1][4] > 0, "no slice proposals"
     compare(case, gpu, case.run_oracle())
+
+
+# The wide kernel (runtime-width chains, par order): every plan -- one workgroup per chain, or K co-resident
+# workgroups per chain with chain barriers -- gives the oracle's phase-by-phase sweep bit for bit, and so does
+# its two-step energy kernel.
+@pytest.mark.parametrize("inst,mode,waves,wgs,follow,band", [
+    ("sq46", "tc", 0, 0, False, 0), ("sq46", "tc", 16, 1, False, 0), ("sq46", "tc", 4, 1, True, 0),
+    ("sq46", "gpu", 8, 3, False, 3), ("sq46", "h100", 16, 5, True, 0), ("grid24", "tc", 8, 2, False, 0),
+    ("grid24", "gpu", 4, 1, True, 4), ("grid45", "tc", 16, 4, False, 0), ("lat14", "tc", 2, 2, False, 0)])
+def test_wide_kernel_matches_oracle(inst, mode, waves, wgs, follow, band):
+    case = Case(inst, "par", mode, wide=True, kernel=capi.KERNEL_WIDE, wide_waves=waves, wide_wgs=wgs,
+                par_follow=follow, par_band=band)
+    gpu = case.run_gpu()
+    assert gpu[3].startswith("wide"), gpu[3]
+    if wgs:
+        assert f"blocks/chain={wgs}" in gpu[3], gpu[3]
+    compare(case, gpu, case.run_oracle())
+
+
+@pytest.mark.parametrize("inst,init,nchains", [("reg3_2000", None, 6), ("sq64", None, 4)])
+def test_wide_kernel_at_benchmark_widths(inst, init, nchains):
+    # the 3-regular n=2000 graph (48 words) and the 64 x 64 lattice (126 words) from random trees,
+    # three levels of one sweep
+    case = Case(inst, "par", "tc", init=init, nchains=nchains, kernel=capi.KERNEL_WIDE, sc_target=40)
+    betas = [0.5, 2.0, 8.0]
+    gpu = case.run_gpu(betas=betas, niters=1)
+    assert gpu[3].startswith("wide"), gpu[3]
+    compare(case, gpu, case.run_oracle(betas=betas, niters=1))
+
+
+# Energies from the node-cost cache the wide sweep kernel keeps: after every level the fold of the cached
+# costs equals the oracle's evaluation of the same population, in every energy mode, also with a GPU model
+# whose m0 != n0 (node costs that depend on the order of the two children).
+@pytest.mark.parametrize("mode,gm", [("tc", capi.DEFAULT_GM), ("h100", capi.DEFAULT_GM),
+                                     ("gpu", (11.9e15, 1.6e13, 3, 9, 8, 4e-6))])
+def test_wide_cached_energies_every_level(mode, gm):
+    case = Case("sq46", "par", mode, kernel=capi.KERNEL_WIDE, nchains=24)
+    if gm is not capi.DEFAULT_GM:
+        case.cfg = capi.make_config(mode=mode, sc_target=common.CHECK_SC_TARGET, seed=common.CHECK_SEED,
+                                    kernel=capi.KERNEL_WIDE, gm=gm)
+        case.P = orc.params_from_config(case.cfg, case.leaf_sc, case.nlab)
+    opop = case.pop0.copy()
+    print(f"[gpu] cached energies sq46 mode={mode} gm={gm}", flush=True)
+    with capi.Context(case.lay, case.leaf, case.leaf_sc, case.cfg, case.nchains) as ctx:
+        ctx.upload(case.pop0)
+        for lev, b in enumerate([0.3, 1.0, 3.0, 10.0]):
+            if lev != 1:  # level 1 runs two launches between energies
+                ctx.energy()
+            ctx.sweeps(case.ord, b, 2 * lev, 2)
+            case.O.sweeps(case.P, case.lay, opop, case.ord, b, 2 * lev, 2)
+            glc, gsc, gns = ctx.energy()
+            olc, osc, ons = case.O.energy(case.P, case.lay, opop)
+            assert np.array_equal(glc.view(np.uint32), olc.view(np.uint32)), f"level {lev}: lcost"
+            assert np.array_equal(gsc, osc) and np.array_equal(gns, ons), f"level {lev}: sc / ns"
+        assert np.array_equal(ctx.download(), opop)
 
 
 def test_resample_copies_ancestors():

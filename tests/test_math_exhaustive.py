@@ -23,8 +23,8 @@ def test_restated_expf_exp2f_log2_core_exhaustive(tmp_path):
     subprocess.run(["g++", "-O2", "-fopenmp", "-ffp-contract=off", "-I", os.path.join(ROOT, "treesa_gpu_amd", "csrc"),
                     os.path.join(HERE, "math_check.cpp"), "-o", exe], check=True)
     r = subprocess.run([exe], capture_output=True, text=True, timeout=600)
-    bad_e, bad_2, far, fixed = map(int, r.stdout.split())
-    assert (bad_e, bad_2, far) == (0, 0, 0), r.stdout
+    bad_e, bad_2, far, fixed, bad_lse = map(int, r.stdout.split())
+    assert (bad_e, bad_2, far, bad_lse) == (0, 0, 0, 0), r.stdout
     assert 0 < fixed < (1 << 23) // 20  # the correction table is sparse: about 1 % of [1, 2)
 
 

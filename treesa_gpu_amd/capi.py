@@ -17,7 +17,7 @@ HOST_LIB_PATH = os.path.join(HERE, "lib", "libtreesa_host.so")
 
 ORDER_PAR, ORDER_PREORDER = 0, 1
 MODES = {"tc": 0, "gpu": 1, "h100": 2}
-KERNEL_AUTO, KERNEL_LDS, KERNEL_GLOBAL = 0, 1, 2
+KERNEL_AUTO, KERNEL_LDS, KERNEL_GLOBAL, KERNEL_WIDE = 0, 1, 2, 3
 
 # Default model constants of the reference's CLI (csrc/treesa_gpu.cu:1292-1295).
 DEFAULT_GM = (11.9e15, 1.6e13, 6, 6, 8, 4e-6)
@@ -43,7 +43,8 @@ class Config(ctypes.Structure):
                 ("m0", ctypes.c_int32), ("n0", ctypes.c_int32), ("k0", ctypes.c_int32),
                 ("v2_l3launch", ctypes.c_float), ("v2_lperm2", ctypes.c_float), ("v2_lcc_bit", ctypes.c_float),
                 ("v2_lcc_cell", ctypes.c_float), ("v2_ltc_bit", ctypes.c_float), ("v2_ltc_pad", ctypes.c_float),
-                ("v2_ltc_out", ctypes.c_float), ("v2_lsmall_cell", ctypes.c_float), ("v2_small_rank", ctypes.c_int32)]
+                ("v2_ltc_out", ctypes.c_float), ("v2_lsmall_cell", ctypes.c_float), ("v2_small_rank", ctypes.c_int32),
+                ("wide_waves", ctypes.c_int32), ("wide_wgs", ctypes.c_int32)]
 
 
 _lib = None
@@ -108,7 +109,8 @@ def layout(m, nlab, wide=False):
 
 
 def make_config(mode="tc", sc_target=20.0, sc_weight=1.0, seed=1, slicing=False, slice_moves=1, slice_every=1,
-                max_slices=0, par_follow=False, par_band=0, kernel=KERNEL_AUTO, gm=DEFAULT_GM, h100=DEFAULT_H100):
+                max_slices=0, par_follow=False, par_band=0, kernel=KERNEL_AUTO, gm=DEFAULT_GM, h100=DEFAULT_H100,
+                wide_waves=0, wide_wgs=0):
     """Config with the fields the reference's Runner derives from its options (csrc/treesa_gpu.cu:1449-1474)."""
     k = splitmix64(seed)
     c = Config()
@@ -130,6 +132,7 @@ def make_config(mode="tc", sc_target=20.0, sc_weight=1.0, seed=1, slicing=False,
     c.v2_lcc_bit, c.v2_lcc_cell = f32_log2(h[2]), f32_log2(h[3])
     c.v2_ltc_bit, c.v2_ltc_pad, c.v2_ltc_out = f32_log2(h[4]), f32_log2(h[5]), f32_log2(h[6])
     c.v2_small_rank, c.v2_lsmall_cell = int(h[7]), f32_log2(h[8])
+    c.wide_waves, c.wide_wgs = wide_waves, wide_wgs
     return c
 
 

@@ -44,6 +44,14 @@ struct tsa_ctx {
   int* d_ns = nullptr;
   uint32_t* h_en = nullptr;  // pinned host copy of the three energy arrays
   int* d_anc = nullptr;
+  TsaWide wide{};              // wide path plan (wide.on: par sweeps and energies run tsa_wide.hip)
+  TsaWideSync wsync{};         // chain barrier words (one allocation) and visit outcomes
+  unsigned* d_wsync = nullptr;
+  float* d_ncost = nullptr;    // per-node costs of the wide energy kernel, nchains * nint4
+  uint16_t* d_nz = nullptr;    // per-node masked sizes, nchains * nint4
+  unsigned* d_fcnt = nullptr;  // per-chain workgroup counters of the wide energy kernel
+  bool costs_valid = false;    // d_ncost / d_nz hold every node's cost (full pass since the last upload,
+                               // resample or mode switch, and every sweep since ran the wide kernel)
   std::string err;
 };
 
@@ -66,7 +74,7 @@ static int fail(tsa_ctx* ctx, int code, const std::string& msg) {
 // Host-built tables
 // ---------------------------------------------------------------------------------------------------
 static std::once_flag g_fix_once;
-static std::vector<uint32_t> g_fix;  // TSA_LOG2FIX_WORDS words
+static std::vector<uint32_t> g_fix;  // TSA_LOG2FIX_WORDS words, then TSA_LOG2MAP_WORDS words of summary bitmap
 static long long g_fix_far = 0;      // inputs where the restated log2f is more than 1 ulp from libm
 
 static void build_log2_fix() {
@@ -95,6 +103,9 @@ static void build_log2_fix() {
     });
   }
   for (auto& x : th) x.join();
+  g_fix.resize(TSA_LOG2FIX_WORDS + TSA_LOG2MAP_WORDS, 0u);
+  for (uint32_t w = 0; w < nw; w++)
+    if (g_fix[w]) g_fix[nw + (w >> 5)] |= 1u << (w & 31u);
   for (long long f : far) g_fix_far += f;
   if (tsa_fbits(log2f(2.0f)) != tsa_fbits(tsa_log2f_core(2.0f))) g_fix_far++;
 }
@@ -141,11 +152,13 @@ extern "C" int tsa_layout(int32_t m, int32_t nlab, int32_t wide, tsa_layout_t* o
     L.W = w64 <= 1 ? 1 : w64 <= 2 ? 2 : w64 <= 4 ? 4 : 8;
     L.runtime_width = 0;
   } else {
-    L.W = w64;
+    // an even number of words: every label set (and S) is a run of 16-byte chunks, 16-byte aligned
+    L.W = (w64 + 1) & ~1;
     L.runtime_width = 1;
   }
   L.ch_off = L.nint * L.W;
   L.s_off = L.ch_off + (L.nint + 1) / 2;
+  if (L.runtime_width) L.s_off = (L.s_off + 1) & ~1;
   L.chain_words = (L.s_off + L.W + 1) & ~1;
   *out = L;
   return TSA_OK;
@@ -186,6 +199,11 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_lc) (void)hipFree(c->d_lc);
   if (c->h_en) (void)hipHostFree(c->h_en);
   if (c->d_anc) (void)hipFree(c->d_anc);
+  if (c->d_wsync) (void)hipFree(c->d_wsync);
+  if (c->wsync.out) (void)hipFree(c->wsync.out);
+  if (c->d_ncost) (void)hipFree(c->d_ncost);
+  if (c->d_nz) (void)hipFree(c->d_nz);
+  if (c->d_fcnt) (void)hipFree(c->d_fcnt);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   if (c->d_track) (void)hipFree(c->d_track);
   if (c->d_trace) (void)hipFree(c->d_trace);
@@ -319,9 +337,29 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
     int wpb = ldsw / nodew2;
     c->L.wpb = wpb < 1 ? 1 : (wpb > 4 ? 4 : wpb);
   }
-  char kb[160];
-  snprintf(kb, sizeof kb, "%s W=%d waves/block=%d lds_bytes/wave=%d", use_lds ? "lds" : "global",
-           use_lds ? c->Wt : lay->W, c->L.wpb, c->L.lds_words * 8);
+  // wide path: runtime-width chains without slice moves run par sweeps and energies in tsa_wide.hip
+  const bool want_wide = cfg->kernel == TSA_KERNEL_WIDE || (cfg->kernel == TSA_KERNEL_AUTO && !use_lds);
+  if (want_wide) {
+    hipError_t we = hipErrorInvalidValue;
+    if (lay->runtime_width && !cfg->slicing) we = tsa_wide_plan(c->P, nchains, cfg->wide_waves, cfg->wide_wgs, &c->wide);
+    if (we != hipSuccess) {
+      c->wide = TsaWide{};
+      if (cfg->kernel == TSA_KERNEL_WIDE || cfg->wide_waves > 0 || cfg->wide_wgs > 0) {
+        free_ctx(c);
+        return fail(nullptr, TSA_ERR_FIT,
+                    std::string("wide kernel: no plan (it needs runtime width, no slicing, W <= 256 words, the node "
+                                "arrays in LDS, and nchains x workgroups per chain co-resident): ") +
+                        hipGetErrorString(we));
+      }
+    }
+  }
+  char kb[200];
+  if (c->wide.on)
+    snprintf(kb, sizeof kb, "wide W=%d G=%d waves/block=%d blocks/chain=%d lds_bytes/block=%d energy_blocks/chain=%d",
+             lay->W, c->wide.G, c->wide.nt / 64, c->wide.K, c->wide.smem, c->wide.eK);
+  else
+    snprintf(kb, sizeof kb, "%s W=%d waves/block=%d lds_bytes/wave=%d", use_lds ? "lds" : "global",
+             use_lds ? c->Wt : lay->W, c->L.wpb, c->L.lds_words * 8);
   c->kname = kb;
 
   const size_t recb = (size_t)nchains * lay->chain_words * 8;
@@ -339,19 +377,57 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   TSA_CREATE_HIP(hipMemsetAsync(c->d_rec, 0, recb, c->st));
   TSA_CREATE_HIP(hipMalloc(&c->d_leaf, (size_t)lay->m * lay->W * 8));
   TSA_CREATE_HIP(hipMemcpyAsync(c->d_leaf, leaf, (size_t)lay->m * lay->W * 8, hipMemcpyHostToDevice, c->st));
-  TSA_CREATE_HIP(hipMalloc(&c->d_fix, (size_t)TSA_LOG2FIX_WORDS * 4));
-  TSA_CREATE_HIP(hipMemcpyAsync(c->d_fix, g_fix.data(), (size_t)TSA_LOG2FIX_WORDS * 4, hipMemcpyHostToDevice, c->st));
+  TSA_CREATE_HIP(hipMalloc(&c->d_fix, g_fix.size() * 4));
+  TSA_CREATE_HIP(hipMemcpyAsync(c->d_fix, g_fix.data(), g_fix.size() * 4, hipMemcpyHostToDevice, c->st));
   TSA_CREATE_HIP(hipMalloc(&c->d_stats, TSA_NSTAT * TSA_STAT_SLOTS * sizeof(unsigned long long)));
   TSA_CREATE_HIP(hipMemsetAsync(c->d_stats, 0, TSA_NSTAT * TSA_STAT_SLOTS * sizeof(unsigned long long), c->st));
-  TSA_CREATE_HIP(hipMalloc(&c->d_lc, (size_t)nchains * 12));
+  TSA_CREATE_HIP(hipMalloc(&c->d_lc, (size_t)nchains * 12 + 16));  // + the wide path's error word
+  TSA_CREATE_HIP(hipMemsetAsync(c->d_lc, 0, (size_t)nchains * 12 + 16, c->st));
   c->d_sc = reinterpret_cast<int*>(c->d_lc) + nchains;
   c->d_ns = reinterpret_cast<int*>(c->d_lc) + 2 * (size_t)nchains;
-  TSA_CREATE_HIP(hipHostMalloc(&c->h_en, (size_t)nchains * 12, hipHostMallocDefault));
+  TSA_CREATE_HIP(hipHostMalloc(&c->h_en, (size_t)nchains * 12 + 16, hipHostMallocDefault));
+  if (c->wide.on) {
+    const size_t nint4 = (size_t)((lay->nint + 3) & ~3);
+    TSA_CREATE_HIP(hipMalloc(&c->d_wsync, (size_t)nchains * 8));
+    TSA_CREATE_HIP(hipMemsetAsync(c->d_wsync, 0, (size_t)nchains * 8, c->st));
+    c->wsync.bar = c->d_wsync;
+    c->wsync.done = c->d_wsync + nchains;
+    c->wsync.err = reinterpret_cast<unsigned*>(c->d_lc) + 3 * (size_t)nchains;
+    if (c->wide.K > 1) TSA_CREATE_HIP(hipMalloc(&c->wsync.out, (size_t)nchains * 2 * nint4));
+    TSA_CREATE_HIP(hipMalloc(&c->d_ncost, (size_t)nchains * nint4 * 4));
+    TSA_CREATE_HIP(hipMalloc(&c->d_nz, (size_t)nchains * nint4 * 2));
+    c->wsync.ncost = c->d_ncost;
+    c->wsync.nz = c->d_nz;
+    TSA_CREATE_HIP(hipMalloc(&c->d_fcnt, (size_t)nchains * 4));
+    TSA_CREATE_HIP(hipMemsetAsync(c->d_fcnt, 0, (size_t)nchains * 4, c->st));
+  }
   TSA_CREATE_HIP(hipMalloc(&c->d_anc, (size_t)nchains * 4));
   TSA_CREATE_HIP(hipStreamSynchronize(c->st));
 #undef TSA_CREATE_HIP
   *out = c;
   return TSA_OK;
+}
+
+static hipError_t launch_energy(tsa_ctx* c) {
+  if (c->wide.on) {
+    const hipError_t e = tsa_launch_wide_energy(c->wide, c->mode, c->P, c->d_rec, c->d_leaf, c->d_fix, c->nchains,
+                                                c->d_ncost, c->d_nz, c->d_fcnt, c->d_lc, c->d_sc, c->d_ns,
+                                                c->costs_valid ? 0 : 1, c->st);
+    c->costs_valid = e == hipSuccess;
+    return e;
+  }
+  return tsa_launch_energy(c->Wt, c->mode, c->P, c->d_rec, c->d_leaf, c->d_fix, c->nchains, c->d_lc, c->d_sc,
+                           c->d_ns, c->st);
+}
+
+// The wide path's error word (set when a chain barrier gave up, leaving the population undefined):
+// reported once by the next synchronizing call, then cleared.
+static int wide_error(tsa_ctx* c, uint32_t word) {
+  if (word == 0) return TSA_OK;
+  c->costs_valid = false;
+  (void)hipMemsetAsync(c->wsync.err, 0, 4, c->st);
+  (void)hipStreamSynchronize(c->st);
+  return fail(c, TSA_ERR_HIP, "wide sweep kernel: a chain barrier timed out; the population is undefined");
 }
 
 extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
@@ -364,6 +440,7 @@ extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
     if (!valid_tree(reinterpret_cast<const uint32_t*>(rec + L.ch_off), L.m, seen, st))
       return fail(ctx, TSA_ERR_ARG, "tsa_upload: chain " + std::to_string(c) + " is not a valid tree");
   }
+  ctx->costs_valid = false;
   TSA_HIP(ctx, hipMemcpyAsync(ctx->d_rec, population, (size_t)ctx->nchains * L.chain_words * 8,
                               hipMemcpyHostToDevice, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
@@ -392,8 +469,14 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
   }
   hipEvent_t e0 = ctx->ev[2 * ctx->npending], e1 = ctx->ev[2 * ctx->npending + 1];
   TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
-  TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains,
-                                 beta, sweep0, nsweeps, ctx->d_stats, ctx->st));
+  if (ctx->wide.on && order == TSA_ORDER_PAR) {
+    TSA_HIP(ctx, tsa_launch_wide(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains, beta,
+                                 sweep0, nsweeps, ctx->d_stats, ctx->wsync, ctx->st));
+  } else {
+    ctx->costs_valid = false;
+    TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
+                                   ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, ctx->st));
+  }
   TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
   ctx->npending++;
   return TSA_OK;
@@ -442,8 +525,7 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_track: null context");
   if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_track: no tsa_track_begin");
   if (level < 0 || level >= ctx->track_levels) return fail(ctx, TSA_ERR_ARG, "tsa_track: level out of range");
-  TSA_HIP(ctx, tsa_launch_energy(ctx->Wt, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains,
-                                 ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->st));
+  TSA_HIP(ctx, launch_energy(ctx));
   TsaSelect S = ctx->sel;
   S.mode = ctx->mode;
   TSA_HIP(ctx, tsa_launch_track(ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->nchains, S, level, ctx->d_rec,
@@ -465,7 +547,11 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
                               ctx->st));
   TSA_HIP(ctx, hipMemcpyAsync(rows, ctx->d_trace, (size_t)ctx->track_levels * sizeof(TsaTraceRowD),
                               hipMemcpyDeviceToHost, ctx->st));
+  uint32_t werr = 0;
+  if (ctx->wide.on)
+    TSA_HIP(ctx, hipMemcpyAsync(&werr, ctx->wsync.err, 4, hipMemcpyDeviceToHost, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  if (wide_error(ctx, werr) != TSA_OK) return TSA_ERR_HIP;
   int dev = 0, khz = 0;
   TSA_HIP(ctx, hipGetDevice(&dev));
   TSA_HIP(ctx, hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
@@ -479,11 +565,11 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
 
 extern "C" int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns) {
   if (!ctx || !lc || !sc || !ns) return fail(ctx, TSA_ERR_ARG, "tsa_energy: null argument");
-  TSA_HIP(ctx, tsa_launch_energy(ctx->Wt, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains,
-                                 ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->st));
+  TSA_HIP(ctx, launch_energy(ctx));
   const size_t b = (size_t)ctx->nchains * 4;
-  TSA_HIP(ctx, hipMemcpyAsync(ctx->h_en, ctx->d_lc, 3 * b, hipMemcpyDeviceToHost, ctx->st));
+  TSA_HIP(ctx, hipMemcpyAsync(ctx->h_en, ctx->d_lc, 3 * b + 4, hipMemcpyDeviceToHost, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  if (ctx->wide.on && wide_error(ctx, ctx->h_en[3 * (size_t)ctx->nchains]) != TSA_OK) return TSA_ERR_HIP;
   memcpy(lc, ctx->h_en, b);
   memcpy(sc, ctx->h_en + ctx->nchains, b);
   memcpy(ns, ctx->h_en + 2 * (size_t)ctx->nchains, b);
@@ -496,6 +582,7 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
     if (anc[c] < 0 || anc[c] >= ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_resample: ancestor out of range");
   if (!ctx->d_rec2) TSA_HIP(ctx, hipMalloc(&ctx->d_rec2, (size_t)ctx->nchains * ctx->lay.chain_words * 8));
   TSA_HIP(ctx, hipMemcpyAsync(ctx->d_anc, anc, (size_t)ctx->nchains * 4, hipMemcpyHostToDevice, ctx->st));
+  ctx->costs_valid = false;
   TSA_HIP(ctx, tsa_launch_copy(ctx->d_rec, ctx->d_rec2, ctx->d_anc, ctx->nchains, ctx->lay.chain_words, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
   std::swap(ctx->d_rec, ctx->d_rec2);
@@ -505,6 +592,7 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
 extern "C" int tsa_set_mode(tsa_ctx* ctx, int32_t mode) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: null context");
   if (mode < 0 || mode > 2) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: mode must be 0, 1 or 2");
+  if (mode != ctx->mode) ctx->costs_valid = false;
   ctx->mode = mode;
   return TSA_OK;
 }
@@ -540,5 +628,5 @@ extern "C" float tsa_host_math(int32_t which, float x) {
   if (which == 0) return tsa_expf(x);
   if (which == 1) return tsa_exp2f(x);
   std::call_once(g_fix_once, build_log2_fix);
-  return tsa_log2f_12(x, g_fix.data());
+  return tsa_log2f_12(x, g_fix.data(), g_fix.data() + TSA_LOG2FIX_WORDS);
 }

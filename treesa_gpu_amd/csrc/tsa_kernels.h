@@ -43,6 +43,7 @@ hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64
 struct TsaTrackState {
   double best_score;
   int best_chain, best_level;
+  int snap;  // chain whose record the last tracked level snapshots, -1 if none
 };
 struct TsaTraceRowD {  // same layout as tsa_trace_row_t
   float lc;
@@ -50,9 +51,79 @@ struct TsaTraceRowD {  // same layout as tsa_trace_row_t
   double score, meanE, meanNs;
   unsigned long long ticks;
 };
+// Chains above TSA_TRACK_INLINE_WORDS words are snapshot by a separate many-workgroup copy kernel.
+#define TSA_TRACK_INLINE_WORDS 16384
 hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int nchains, const TsaSelect& S, int level,
                             const uint64_t* rec, int chain_words, TsaTrackState* st, TsaTraceRowD* trace,
                             uint64_t* best_rec, hipStream_t stream);
 hipError_t tsa_launch_track_init(TsaTrackState* st, unsigned long long* ticks0, hipStream_t stream);
 hipError_t tsa_launch_copy(const uint64_t* src, uint64_t* dst, const int* anc, int nchains, int chain_words,
                            hipStream_t st);
+
+// ---------------------------------------------------------------------------------------------------
+// Wide path (tsa_wide.hip): par-order sweeps and energies of runtime-width chains, label sets streamed
+// from HBM in 16-byte chunks by groups of G lanes per proposal, node arrays in LDS, K workgroups per chain.
+// ---------------------------------------------------------------------------------------------------
+#define TSA_WIDE_CPL 2        // 16-byte chunks per lane and label set (so W <= 2 * TSA_WIDE_CPL * 64 = 256)
+#define TSA_WIDE_MAX_K 16     // workgroups per chain
+#define TSA_WIDE_SPIN (1u << 22)  // polls of a chain barrier before the launch gives up (seconds)
+
+struct TsaWide {
+  int on;     // 1: par-order sweeps of this context run k_wide
+  int G;      // lanes per proposal (4..64)
+  int K;      // workgroups per chain (K > 1: cooperative launch with chain barriers)
+  int nt;     // threads per workgroup
+  int smem;   // dynamic LDS bytes per workgroup
+  int eG, eK; // energy: lanes per node, workgroups per chain
+  int fold_stage;     // energy fold: 0 reads node costs from HBM, 1 stages them in LDS, 2 also the log2f bitmap
+  int fold_smem;      // LDS bytes of stage 1 (0: the costs do not fit)
+  int fold_smem_map;  // LDS bytes of stage 2
+};
+
+// Device state of the wide sweep kernel: the chain barrier words bar[nchains], done[nchains], err[1] (all
+// zero between launches); outcome bytes of the visits of the last two phases, out[nchains][2][nint4]
+// (K > 1 only); the per-node cost cache ncost / nz [nchains][nint4] (cost and masked size of every internal
+// node), which the sweep kernel keeps current on every accepted rotation and the energy kernel folds.
+struct TsaWideSync {
+  unsigned* bar;
+  unsigned* done;
+  unsigned* err;
+  uint8_t* out;
+  float* ncost;
+  uint16_t* nz;
+};
+
+// LDS byte offsets of k_wide (same function on host and device).
+struct TsaWideLds {
+  int masks, ch, dw, offs, pri, par, wl, out, bytes;
+};
+__host__ __device__ static inline TsaWideLds tsa_wide_lds(int nint, int band, int coop) {
+  const int nint4 = (nint + 3) & ~3, ngrp = (nint + 63) / 64;
+  TsaWideLds L;
+  int b = 0;
+  L.masks = b;  b += ngrp * 8;
+  L.ch = b;     b += nint4 * 4;
+  L.dw = b;     b += band ? nint4 * 4 : 0;
+  L.offs = b;   b += ((ngrp + 1) & ~1) * 4;
+  L.pri = b;    b += nint4 * 2;
+  L.par = b;    b += nint4 * 2;
+  L.wl = b;     b += nint4 * 2;
+  L.out = b;    b += coop ? 0 : nint4;
+  L.bytes = (b + 15) & ~15;
+  return L;
+}
+
+// Plan a wide launch for nchains chains on the current device: G from W, threads per workgroup (want_waves
+// waves, 0 = by chain count), workgroups per chain (want_k, 0 = as many as stay co-resident).  Returns
+// hipErrorInvalidValue when the chain does not qualify (W > 2 * TSA_WIDE_CPL * 64 or LDS too small).
+hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int want_k, TsaWide* out);
+hipError_t tsa_launch_wide(const TsaWide& X, int mode, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
+                           const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
+                           unsigned long long* stats, const TsaWideSync& sy, hipStream_t st);
+// Energies through per-node costs: ncost / nz hold nchains * nint4 node costs and masked sizes, fcnt
+// nchains zeroed counters.  nodes = 1: recompute every node cost from the label sets first; nodes = 0: fold
+// the cached costs only.
+hipError_t tsa_launch_wide_energy(const TsaWide& X, int mode, const TsaKParams& P, const uint64_t* rec,
+                                  const uint64_t* leaf, const uint32_t* fix, int nchains, float* ncost,
+                                  uint16_t* nz, unsigned* fcnt, float* lc, int* sc, int* ns, int nodes,
+                                  hipStream_t st);

@@ -292,7 +292,7 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
   // the small tables every proposal indexes per lane live in LDS
   if (threadIdx.x < 64) s_lse[threadIdx.x] = P.lse[threadIdx.x];
   if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
-  const TsaMathTabs T{s_exp2, fix};
+  const TsaMathTabs T{s_exp2, fix, nullptr};
   const uint64_t* lf = leaf;
   int leafw = 0;
   if constexpr (LDS) {
@@ -491,7 +491,7 @@ __global__ void __launch_bounds__(256) k_energy(TsaKParams P, const uint64_t* __
   __shared__ uint64_t s_exp2[32];
   if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
   __syncthreads();
-  const TsaMathTabs T{s_exp2, fix};
+  const TsaMathTabs T{s_exp2, fix, nullptr};
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   const int c = t >> 5, l32 = threadIdx.x & 31;
   const int cc = c < nchains ? c : nchains - 1;  // a half-wave past the end duplicates the last chain
@@ -573,20 +573,31 @@ __global__ void __launch_bounds__(1024) k_track(const float* __restrict__ lc, co
       st->best_chain = b;
       st->best_level = level;
     }
+    st->snap = better ? b : -1;
     s_copy = better ? 1 : 0;
     s_bi = b;
   }
   __syncthreads();
-  if (s_copy) {
+  if (s_copy && chain_words <= TSA_TRACK_INLINE_WORDS) {
     const uint64_t* src = rec + (size_t)s_bi * chain_words;
     for (int w = t; w < chain_words; w += 1024) best_rec[w] = src[w];
   }
+}
+
+// Snapshot of a large best chain (after k_track, which names it in st->snap), by many workgroups.
+__global__ void __launch_bounds__(256) k_snap(const TsaTrackState* __restrict__ st, const uint4* __restrict__ rec,
+                                              int n4, uint4* __restrict__ best_rec) {
+  const int b = st->snap;
+  if (b < 0) return;
+  const uint4* src = rec + (size_t)b * n4;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) best_rec[i] = src[i];
 }
 
 __global__ void k_track_init(TsaTrackState* st, unsigned long long* ticks0) {
   st->best_score = INFINITY;
   st->best_chain = -1;
   st->best_level = -1;
+  st->snap = -1;
   *ticks0 = wall_clock64();
 }
 
@@ -685,6 +696,11 @@ hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int n
                             uint64_t* best_rec, hipStream_t stream) {
   hipLaunchKernelGGL(k_track, dim3(1), dim3(1024), 0, stream, lc, sc, ns, nchains, S, level, rec, chain_words, stt, trace,
                      best_rec);
+  if (chain_words > TSA_TRACK_INLINE_WORDS) {
+    const int n4 = chain_words / 2, nb = (n4 + 1023) / 1024;
+    hipLaunchKernelGGL(k_snap, dim3(nb < 512 ? nb : 512), dim3(256), 0, stream, stt,
+                       reinterpret_cast<const uint4*>(rec), n4, reinterpret_cast<uint4*>(best_rec));
+  }
   return hipGetLastError();
 }
 

@@ -146,28 +146,41 @@ TSA_MATH_FN float tsa_log2f_core(float y) {
 // 16 per word, so word mant >> 4 holds mantissa mant.
 #define TSA_LOG2FIX_WORDS (1u << 19)
 
-// log2f on [1, 2] with the host-libm correction table fix (2 bits per input: 0 keep, 1 +1 ulp, 2 -1 ulp).
-// Inputs outside [1, 2] only arise from NaN operands and return NaN.
-TSA_MATH_FN float tsa_log2f_12(float y, const uint32_t* fix) {
+// Words of the summary bitmap of the correction table: bit w is set iff fix word w is nonzero (about one
+// word in ten is), so a reader holding the 64 KB bitmap close by skips most reads of the 2 MB table.
+#define TSA_LOG2MAP_WORDS (TSA_LOG2FIX_WORDS / 32u)
+
+// log2f on [1, 2] with the host-libm correction table fix (2 bits per input: 0 keep, 1 +1 ulp, 2 -1 ulp)
+// and, when map is not null, its summary bitmap.  Inputs outside [1, 2] only arise from NaN operands and
+// return NaN.
+TSA_MATH_FN float tsa_log2f_12(float y, const uint32_t* fix, const uint32_t* map = nullptr) {
   if (!(y >= 1.0f && y <= 2.0f)) return y - y + NAN;
   const float r = tsa_log2f_core(y);
   if (y == 2.0f) return r;
   const uint32_t mant = tsa_fbits(y) & 0x7fffffu;
-  const uint32_t code = (fix[mant >> 4] >> ((mant & 15u) * 2u)) & 3u;
+  const uint32_t w = mant >> 4;
+  if (map && ((map[w >> 5] >> (w & 31u)) & 1u) == 0u) return r;
+  const uint32_t code = (fix[w] >> ((mant & 15u) * 2u)) & 3u;
   if (code == 0u) return r;
   return tsa_ffrom(tsa_fbits(r) + (code == 1u ? 1u : 0xffffffffu));
 }
 
-// Tables the float math reads: the 2^(i/32) table and the log2f correction table.
+// Tables the float math reads: the 2^(i/32) table, the log2f correction table and optionally its summary
+// bitmap.
 struct TsaMathTabs {
   const uint64_t* exp2;
   const uint32_t* fix;
+  const uint32_t* map;
 };
 
-// log2(2^a + 2^b) for floats (a or b may be -inf), the fold of modeled node costs.
+// log2(2^a + 2^b) for floats (a or b may be -inf), the fold of modeled node costs.  For min - max <= -24,
+// exp2f gives at most 2^-24, 1 + that rounds to 1.0f (2^-24 is half an ulp of 1: ties to even) and
+// log2f(1) = +0, so the result is max + 0.0f without evaluating either function.
 TSA_MATH_FN float tsa_lse_f(float a, float b, const TsaMathTabs& T) {
   const float mx = a > b ? a : b;
   const float mn = a > b ? b : a;
   if (mx == -INFINITY) return mx;
-  return mx + tsa_log2f_12(1.0f + tsa_exp2f_t(mn - mx, T.exp2), T.fix);
+  const float d = mn - mx;
+  if (d <= -24.0f) return mx + 0.0f;
+  return mx + tsa_log2f_12(1.0f + tsa_exp2f_t(d, T.exp2), T.fix, T.map);
 }

@@ -1,0 +1,739 @@
+// tsa_wide.hip -- par-order sweeps and chain energies for wide label sets (runtime width W, an even number
+// of 64-bit words, so every label set is a run of W/2 16-byte chunks, 16-byte aligned in HBM).
+//
+// Sweep kernel k_wide (the reference's k_par with cooperative visits, csrc/treesa_gpu.cu:829-997 and
+// 237-373, re-planned for gfx950).  K workgroups own one chain.  Every workgroup keeps a private copy of the
+// chain's node arrays in LDS (children words, priorities, parents, work list) and works the label sets in
+// HBM.  A phase:
+//   1. scan (every workgroup, redundantly): the independent set of the phase -- unvisited nodes whose
+//      (priority, id) key beats their unvisited parent and internal children -- compacted in node order
+//      into the work list with wave ballots and a prefix over the 64-node groups;
+//   2. visits: work-list entry j goes to lane group j mod (K * groups per workgroup); the G lanes of a
+//      group load the five label sets D, P, O, K, M in 16-byte chunks (chunk t, t+G, ...), count with
+//      popcounts, sum the counters (packed two per 32-bit word) with xor shuffles inside the group, all
+//      lanes evaluate the same dE and Metropolis test, and on accept each lane stores its chunks of
+//      X = (K|O)&(M|D) into P's set.  The group leader publishes one outcome byte (accepted, pivot slot,
+//      moved-grandchild slot);
+//   3. chain barrier (K > 1) or workgroup barrier (K = 1);
+//   4. replay (every workgroup): apply every published outcome to the LDS copies -- the two children
+//      words of an accepted rotation, the parents of the two moved subtrees, priority 0 for the visited
+//      node and the follow-up priority of a re-armed pivot.
+// Visits of one phase touch disjoint words (a visit at v writes P's set and the words of v, P, O and M;
+// an active node is never the parent, child or grandchild of another active node's pivot), so the visits,
+// and the replays, of one phase commute.  Every proposal draws Philox((v, sweep, chain)), so the result is
+// the CPU phase-by-phase sweep bit for bit, whatever K and G.
+//
+// Chain barrier: cooperative launch (all workgroups co-resident).  Thread 0 of each workgroup releases at
+// agent scope, adds 1 to the chain's counter and polls it until K * (barriers so far) with a bounded number
+// of polls; a workgroup that runs out of polls sets the error word, and every workgroup that sees the error
+// word stops, so every wave reaches the end of the kernel.  The last workgroup of a chain to finish resets
+// the chain's counters to zero for the next launch.
+#include "tsa_kernels.h"
+
+namespace {
+
+struct alignas(16) TsaW2 {
+  uint64_t a, b;
+};
+
+__device__ __forceinline__ uint64_t wide_lt_mask(int lane) { return (1ull << lane) - 1ull; }
+
+// Counters of one proposal as a flat list: |d|, |P|, |X|, then K0..K3 (mode 0) or B0..3, M0..3, N0..3,
+// K0..3 (modes 1, 2).
+template <int MODE>
+struct TsaFlat {
+  static constexpr int N = MODE == 0 ? 7 : 19;
+  static constexpr int NP = (N + 1) / 2;
+};
+
+template <int MODE>
+__device__ __forceinline__ void counts_pack(const TsaCounts& c, uint32_t (&a)[TsaFlat<MODE>::NP]) {
+  int f[TsaFlat<MODE>::NP * 2];
+  f[0] = c.sd;
+  f[1] = c.sp;
+  f[2] = c.sx;
+  if (MODE == 0) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) f[3 + q] = c.K[q];
+    f[7] = 0;
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      f[3 + q] = c.B[q];
+      f[7 + q] = c.M[q];
+      f[11 + q] = c.N[q];
+      f[15 + q] = c.K[q];
+    }
+    f[19] = 0;
+  }
+#pragma unroll
+  for (int i = 0; i < TsaFlat<MODE>::NP; i++) a[i] = (uint32_t)f[2 * i] | ((uint32_t)f[2 * i + 1] << 16);
+}
+
+template <int MODE>
+__device__ __forceinline__ void counts_unpack(const uint32_t (&a)[TsaFlat<MODE>::NP], TsaCounts& c) {
+  int f[TsaFlat<MODE>::NP * 2];
+#pragma unroll
+  for (int i = 0; i < TsaFlat<MODE>::NP; i++) {
+    f[2 * i] = (int)(a[i] & 0xFFFFu);
+    f[2 * i + 1] = (int)(a[i] >> 16);
+  }
+  c.sd = f[0];
+  c.sp = f[1];
+  c.sx = f[2];
+  if (MODE == 0) {
+#pragma unroll
+    for (int q = 0; q < 4; q++) c.K[q] = f[3 + q];
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      c.B[q] = f[3 + q];
+      c.M[q] = f[7 + q];
+      c.N[q] = f[11 + q];
+      c.K[q] = f[15 + q];
+    }
+  }
+}
+
+// Sum over the G lanes of a group (xor butterfly: every lane ends with the total).  Each packed half
+// stays below 2^16: a label set has at most 2 * TSA_WIDE_CPL * 64 * 64 = 16384 labels.
+template <int G, int N>
+__device__ __forceinline__ void group_sum(uint32_t (&a)[N]) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) {
+#pragma unroll
+    for (int i = 0; i < N; i++) a[i] += (uint32_t)__shfl_xor((int)a[i], o, G);
+  }
+}
+
+// Chain barrier (see the file comment).  Block-uniform result: false when the launch gave up.
+__device__ bool chain_barrier(const TsaWideSync& sy, int c, unsigned target, int* s_ok) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int ok = 1;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    __hip_atomic_fetch_add(sy.bar + c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    unsigned polls = 0;
+    for (;;) {
+      if (__hip_atomic_load(sy.bar + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
+      if (__hip_atomic_load(sy.err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+        ok = 0;
+        break;
+      }
+      if (++polls >= TSA_WIDE_SPIN) {
+        __hip_atomic_store(sy.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ok = 0;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    *s_ok = ok;
+  }
+  __syncthreads();
+  return *s_ok != 0;
+}
+
+__device__ __forceinline__ long long wide_wave_sum(long long x) {
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, 64);
+  return x;
+}
+
+template <int G, int MODE, bool COOP>
+__global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restrict__ rec,
+                                               const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
+                                               int nchains, int K, float beta, uint32_t sweep0, int nsweeps,
+                                               unsigned long long* __restrict__ stats, TsaWideSync sy) {
+  extern __shared__ __align__(16) unsigned char tsa_wsm[];
+  __shared__ float s_lse[64];
+  __shared__ uint64_t s_exp2[32];
+  __shared__ int s_cnt, s_ok;
+  const int NT = blockDim.x, nwv = NT >> 6, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  const int m = P.m, nint = P.nint, nint4 = (nint + 3) & ~3, ngrp = (nint + 63) >> 6;
+  const int NW = P.W, nch = NW >> 1;
+  const int c = blockIdx.x / K, k = blockIdx.x - c * K;
+  if (c >= nchains) return;  // whole workgroups; the grid is nchains * K
+  const TsaWideLds Lo = tsa_wide_lds(nint, P.par_band > 0, COOP ? 1 : 0);
+  uint64_t* const masks = reinterpret_cast<uint64_t*>(tsa_wsm + Lo.masks);
+  uint32_t* const ch = reinterpret_cast<uint32_t*>(tsa_wsm + Lo.ch);
+  uint32_t* const dw = reinterpret_cast<uint32_t*>(tsa_wsm + Lo.dw);
+  uint32_t* const offs = reinterpret_cast<uint32_t*>(tsa_wsm + Lo.offs);
+  uint16_t* const pri = reinterpret_cast<uint16_t*>(tsa_wsm + Lo.pri);
+  uint16_t* const par = reinterpret_cast<uint16_t*>(tsa_wsm + Lo.par);
+  uint16_t* const wl = reinterpret_cast<uint16_t*>(tsa_wsm + Lo.wl);
+  uint8_t* const outl = tsa_wsm + Lo.out;
+  if (threadIdx.x < 64) s_lse[threadIdx.x] = P.lse[threadIdx.x];
+  if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
+  const TsaMathTabs T{s_exp2, fix, fix + TSA_LOG2FIX_WORDS};
+  uint64_t* const lab = rec + (size_t)c * P.chain_words;
+  uint32_t* const gch = reinterpret_cast<uint32_t*>(lab + P.ch_off);
+  for (int i = threadIdx.x; i < nint; i += NT) ch[i] = gch[i];
+  __syncthreads();
+  for (int i = threadIdx.x; i < nint; i += NT) {
+    const uint32_t cw = ch[i];
+    const int l = (int)(cw & 0xFFFFu), r = (int)(cw >> 16);
+    if (l >= m) par[l - m] = (uint16_t)(m + i);
+    if (r >= m) par[r - m] = (uint16_t)(m + i);
+  }
+  if (threadIdx.x == 0) par[nint - 1] = 0xFFFFu;
+  __syncthreads();
+
+  constexpr int gpw = 64 / G;
+  const int ngr = nwv * gpw;
+  const int t = lane & (G - 1);
+  const int gid = k * ngr + wv * gpw + lane / G;
+  const int stride = K * ngr;
+  int np = 0, na = 0, nv = 0, nst = 0;
+  unsigned nb = 0;
+  bool ok = true;
+
+  for (int s = 0; s < nsweeps && ok; s++) {
+    const uint32_t sw = sweep0 + (uint32_t)s;
+    const uint32_t hs = tsa_sweep_hash(sw, (uint32_t)c, P.key0);
+    for (int i = threadIdx.x; i < nint; i += NT) pri[i] = (uint16_t)tsa_par_pri((uint32_t)(m + i), hs);
+    if (P.par_band > 0) {
+      // depth at sweep start by pointer jumping on (depth << 16 | ancestor) words; an update that reads an
+      // already advanced ancestor word still keeps depth(v) = d + depth(ancestor)
+      for (int i = threadIdx.x; i < nint; i += NT) dw[i] = par[i] == 0xFFFFu ? 0xFFFFu : (0x10000u | par[i]);
+      __syncthreads();
+      for (;;) {
+        int any = 0;
+        for (int i = threadIdx.x; i < nint; i += NT) {
+          const uint32_t w = dw[i], a = w & 0xFFFFu;
+          if (a != 0xFFFFu) {
+            const uint32_t w2 = dw[a - m];
+            dw[i] = ((w & 0xFFFF0000u) + (w2 & 0xFFFF0000u)) | (w2 & 0xFFFFu);
+            any = 1;
+          }
+        }
+        if (!__syncthreads_or(any)) break;
+      }
+      const int L = P.par_band;
+      for (int i = threadIdx.x; i < nint; i += NT)
+        pri[i] = (uint16_t)((((uint32_t)((L - 1 - (int)(dw[i] >> 16) % L) & 15)) << 12) | (pri[i] & 0x0FFEu) | 1u);
+    }
+    __syncthreads();
+    for (;;) {
+      // 1. scan
+      for (int gi = wv; gi < ngrp; gi += nwv) {
+        const int i = gi * 64 + lane;
+        bool act = false;
+        if (i < nint) {
+          const uint32_t pv = pri[i];
+          if (pv) {
+            const uint32_t key = (pv << 16) | (uint32_t)(m + i);
+            act = true;
+            const uint32_t p = par[i];
+            if (p != 0xFFFFu) {
+              const uint32_t pp = pri[p - m];
+              if (pp && ((pp << 16) | p) > key) act = false;
+            }
+            const uint32_t cw = ch[i];
+            const uint32_t l = cw & 0xFFFFu, r = cw >> 16;
+            if (act && l >= (uint32_t)m) {
+              const uint32_t pl = pri[l - m];
+              if (pl && ((pl << 16) | l) > key) act = false;
+            }
+            if (act && r >= (uint32_t)m) {
+              const uint32_t pr = pri[r - m];
+              if (pr && ((pr << 16) | r) > key) act = false;
+            }
+          }
+        }
+        const uint64_t b = __ballot(act);
+        if (lane == 0) masks[gi] = b;
+      }
+      __syncthreads();
+      if (wv == 0) {
+        int base = 0;
+        for (int g0 = 0; g0 < ngrp; g0 += 64) {
+          const int gi = g0 + lane;
+          const int x = gi < ngrp ? __popcll(masks[gi]) : 0;
+          int y = x;
+          for (int o = 1; o < 64; o <<= 1) {
+            const int u = __shfl_up(y, o, 64);
+            if (lane >= o) y += u;
+          }
+          if (gi < ngrp) offs[gi] = (uint32_t)(base + y - x);
+          base += __shfl(y, 63, 64);
+        }
+        if (lane == 0) s_cnt = base;
+      }
+      __syncthreads();
+      for (int gi = wv; gi < ngrp; gi += nwv) {
+        const uint64_t b = masks[gi];
+        if ((b >> lane) & 1ull) wl[offs[gi] + __popcll(b & wide_lt_mask(lane))] = (uint16_t)(m + gi * 64 + lane);
+      }
+      __syncthreads();
+      const int cnt = s_cnt;
+      if (cnt == 0) break;
+      nst++;
+      uint8_t* const out = COOP ? sy.out + ((size_t)c * 2 + (nb & 1u)) * (size_t)nint4 : outl;
+
+      // 2. visits
+      for (int j0 = 0; j0 < cnt; j0 += stride) {
+        const int j = j0 + gid;
+        if (j < cnt) {  // uniform within a lane group
+          const int v = wl[j];
+          const uint32_t chv = ch[v - m];
+          const int l = (int)(chv & 0xFFFFu), r = (int)(chv >> 16);
+          const bool li = l >= m, ri = r >= m;
+          uint32_t o = 0;
+          if (li || ri) {
+            const bool rev = (pri[v - m] & 1u) == 0;  // a follow-up visit draws its own numbers
+            const uint32_t swv = sw | (rev ? 0x80000000u : 0u);
+            const TsaU4 rnd = tsa_philox(TsaU4{(uint32_t)v, swv, (uint32_t)c, 0u}, P.key0, P.key1);
+            const int rule = tsa_pick_rule(li, ri, rnd.x);
+            const int slotP = tsa_slot_p(rule), slotM = tsa_slot_m(rule);
+            const int Pn = slotP ? r : l, On = slotP ? l : r;
+            const uint32_t chp = ch[Pn - m];
+            const int Mn = slotM ? (int)(chp >> 16) : (int)(chp & 0xFFFFu);
+            const int Kn = slotM ? (int)(chp & 0xFFFFu) : (int)(chp >> 16);
+            const TsaW2* qD = reinterpret_cast<const TsaW2*>(lab + (size_t)(v - m) * NW);
+            TsaW2* qP = reinterpret_cast<TsaW2*>(lab + (size_t)(Pn - m) * NW);
+            const TsaW2* qO = reinterpret_cast<const TsaW2*>(On >= m ? lab + (size_t)(On - m) * NW : leaf + (size_t)On * NW);
+            const TsaW2* qK = reinterpret_cast<const TsaW2*>(Kn >= m ? lab + (size_t)(Kn - m) * NW : leaf + (size_t)Kn * NW);
+            const TsaW2* qM = reinterpret_cast<const TsaW2*>(Mn >= m ? lab + (size_t)(Mn - m) * NW : leaf + (size_t)Mn * NW);
+            TsaW2 dd[TSA_WIDE_CPL], pp[TSA_WIDE_CPL], oo[TSA_WIDE_CPL], kk[TSA_WIDE_CPL], mm[TSA_WIDE_CPL];
+#pragma unroll
+            for (int q = 0; q < TSA_WIDE_CPL; q++) {
+              const int cc = t + q * G;
+              if (cc < nch) {
+                dd[q] = qD[cc];
+                pp[q] = qP[cc];
+                oo[q] = qO[cc];
+                kk[q] = qK[cc];
+                mm[q] = qM[cc];
+              } else {
+                dd[q] = pp[q] = oo[q] = kk[q] = mm[q] = TsaW2{0ull, 0ull};
+              }
+            }
+            TsaCounts cn;
+            tsa_counts_zero(cn);
+            TsaW2 xx[TSA_WIDE_CPL];  // only X stays live across the energy evaluation
+#pragma unroll
+            for (int q = 0; q < TSA_WIDE_CPL; q++) {
+              xx[q].a = (kk[q].a | oo[q].a) & (mm[q].a | dd[q].a);
+              xx[q].b = (kk[q].b | oo[q].b) & (mm[q].b | dd[q].b);
+              tsa_acc<MODE>(cn, kk[q].a, mm[q].a, pp[q].a, oo[q].a, dd[q].a, xx[q].a);
+              tsa_acc<MODE>(cn, kk[q].b, mm[q].b, pp[q].b, oo[q].b, dd[q].b, xx[q].b);
+            }
+            uint32_t pk[TsaFlat<MODE>::NP];
+            counts_pack<MODE>(cn, pk);
+            group_sum<G, TsaFlat<MODE>::NP>(pk);
+            counts_unpack<MODE>(pk, cn);
+            const float dE = tsa_energy_from_counts<MODE>(cn, P.model, s_lse, T);
+            const bool acc = tsa_metropolis(rnd.y, beta, dE, T.exp2);
+            if (acc) {
+#pragma unroll
+              for (int q = 0; q < TSA_WIDE_CPL; q++) {
+                const int cc = t + q * G;
+                if (cc < nch) qP[cc] = xx[q];
+              }
+            }
+            o = 8u | (acc ? 1u : 0u) | ((uint32_t)slotP << 1) | ((uint32_t)slotM << 2);
+            if (t == 0) {
+              np++;
+              na += acc ? 1 : 0;
+              if (acc) {
+                // the two node costs the rotation changes: P with children K and O (O in M's slot) and v with
+                // children P and M (M in O's slot); count3 order is (left child, right child, node)
+                const size_t cb = (size_t)c * nint4;
+                sy.ncost[cb + (Pn - m)] = tsa_node_cost<MODE>(cn.B[2], slotM ? cn.M[2] : cn.N[2],
+                                                              slotM ? cn.N[2] : cn.M[2], cn.K[2], cn.sx, P.model, T);
+                sy.nz[cb + (Pn - m)] = (uint16_t)cn.sx;
+                sy.ncost[cb + (v - m)] = tsa_node_cost<MODE>(cn.B[3], slotP ? cn.N[3] : cn.M[3],
+                                                             slotP ? cn.M[3] : cn.N[3], cn.K[3], cn.sd, P.model, T);
+              }
+            }
+          }
+          if (t == 0) {
+            out[j] = (uint8_t)o;
+            nv++;
+          }
+        }
+      }
+
+      // 3. barrier
+      if constexpr (COOP) {
+        nb++;
+        if (!chain_barrier(sy, c, nb * (unsigned)K, &s_ok)) {
+          ok = false;
+          break;
+        }
+      } else {
+        __syncthreads();
+      }
+
+      // 4. replay
+      for (int j = threadIdx.x; j < cnt; j += NT) {
+        const int v = wl[j];
+        const uint32_t o = out[j];
+        const uint32_t pv = pri[v - m];
+        if (o & 1u) {
+          const uint32_t chv = ch[v - m];
+          const int slotP = (int)((o >> 1) & 1u), slotM = (int)((o >> 2) & 1u);
+          const int l = (int)(chv & 0xFFFFu), r = (int)(chv >> 16);
+          const int Pn = slotP ? r : l, On = slotP ? l : r;
+          const uint32_t chp = ch[Pn - m];
+          const int Mn = slotM ? (int)(chp >> 16) : (int)(chp & 0xFFFFu);
+          ch[Pn - m] = slotM ? ((chp & 0xFFFFu) | ((uint32_t)On << 16)) : ((chp & 0xFFFF0000u) | (uint32_t)On);
+          ch[v - m] = slotP ? ((chv & 0xFFFF0000u) | (uint32_t)Mn) : ((chv & 0xFFFFu) | ((uint32_t)Mn << 16));
+          if (On >= m) par[On - m] = (uint16_t)Pn;
+          if (Mn >= m) par[Mn - m] = (uint16_t)v;
+          if (P.par_follow && (pv & 1u) && pri[Pn - m] == 0) pri[Pn - m] = (uint16_t)tsa_follow_pri((uint32_t)Pn, hs);
+        }
+        pri[v - m] = 0;
+      }
+      __syncthreads();
+    }
+  }
+
+  if (ok && k == 0)
+    for (int i = threadIdx.x; i < nint; i += NT) gch[i] = ch[i];
+  const long long sp_ = wide_wave_sum(np), sa_ = wide_wave_sum(na), sv_ = wide_wave_sum(nv);
+  if (lane == 0) {  // counters spread over TSA_STAT_SLOTS addresses each, summed by the host
+    unsigned long long* st = stats + ((c * 16 + wv) & (TSA_STAT_SLOTS - 1));
+    atomicAdd(&st[TSA_ST_PROP * TSA_STAT_SLOTS], (unsigned long long)sp_);
+    atomicAdd(&st[TSA_ST_ACC * TSA_STAT_SLOTS], (unsigned long long)sa_);
+    atomicAdd(&st[TSA_ST_VISITS * TSA_STAT_SLOTS], (unsigned long long)sv_);
+    atomicAdd(&st[TSA_ST_BUSY * TSA_STAT_SLOTS], (unsigned long long)sv_);
+    if (k == 0 && wv == 0) atomicAdd(&st[TSA_ST_STEPS * TSA_STAT_SLOTS], (unsigned long long)nst);
+  }
+  if constexpr (COOP) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      const unsigned old = __hip_atomic_fetch_add(sy.done + c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == (unsigned)(K - 1)) {  // every workgroup of the chain has left its last barrier
+        __hip_atomic_store(sy.bar + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(sy.done + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+}
+
+// Chain energies in two steps (csrc/treesa_gpu.cu:999-1014 computes both in one 32-lane loop):
+// node costs -- G lanes per internal node count B, M, N, K, Z of (left, right) -> node with label sets
+// masked by ~S, and the group leader stores tsa_node_cost and Z -- by eK workgroups per chain (skipped when
+// nodes = 0: the sweep kernel has kept the cached costs current); then the last workgroup of the chain to
+// finish folds them in the reference's 32-lane order (lane t folds nodes t, t+32, ... from -inf with
+// lse_f, then an xor butterfly 16, 8, 4, 2, 1), so lcost is bit-identical to the one-loop evaluation.
+template <int G, int MODE>
+__global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __restrict__ rec,
+                                               const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
+                                               int nchains, int K2, int nodes, int stage, float* __restrict__ ncost,
+                                               uint16_t* __restrict__ nz, unsigned* __restrict__ fcnt,
+                                               float* __restrict__ lc, int* __restrict__ sc, int* __restrict__ ns) {
+  // LDS (stage != 0): the chain's node costs f32[nint4] and sizes u16[nint4], then (stage == 2) the log2f
+  // summary bitmap at the next 16-byte boundary
+  extern __shared__ __align__(16) unsigned char s_dyn[];
+  __shared__ uint64_t s_exp2[32];
+  __shared__ int s_last;
+  if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
+  __syncthreads();
+  const uint32_t* const gmap = fix + TSA_LOG2FIX_WORDS;
+  const int c = blockIdx.x / K2, k = blockIdx.x - c * K2;
+  if (c >= nchains) return;
+  const int m = P.m, nint = P.nint, nint4 = (nint + 3) & ~3, NW = P.W, nch = NW >> 1;
+  const uint64_t* const lab = rec + (size_t)c * P.chain_words;
+  const uint64_t* const S = P.slicing ? lab + P.s_off : nullptr;
+  float* const cst = ncost + (size_t)c * nint4;
+  uint16_t* const zz = nz + (size_t)c * nint4;
+
+  if (nodes) {
+    const TsaMathTabs T{s_exp2, fix, gmap};
+    const uint32_t* const ch = reinterpret_cast<const uint32_t*>(lab + P.ch_off);
+    const int gpb = (int)blockDim.x / G, grp = (int)threadIdx.x / G, t = (int)threadIdx.x & (G - 1);
+    const int npb = (nint + K2 - 1) / K2, i0 = k * npb, i1 = (i0 + npb < nint) ? i0 + npb : nint;
+    TsaW2 sm[TSA_WIDE_CPL];
+#pragma unroll
+    for (int q = 0; q < TSA_WIDE_CPL; q++) {
+      const int cc = t + q * G;
+      if (S && cc < nch) {
+        const TsaW2 sv = reinterpret_cast<const TsaW2*>(S)[cc];
+        sm[q] = TsaW2{~sv.a, ~sv.b};
+      } else {
+        sm[q] = TsaW2{~0ull, ~0ull};
+      }
+    }
+    for (int b = i0; b < i1; b += gpb) {
+      const int i = b + grp;
+      if (i < i1) {  // uniform within a lane group
+        const uint32_t cw = ch[i];
+        const int l = (int)(cw & 0xFFFFu), r = (int)(cw >> 16);
+        const TsaW2* qx = reinterpret_cast<const TsaW2*>(l >= m ? lab + (size_t)(l - m) * NW : leaf + (size_t)l * NW);
+        const TsaW2* qy = reinterpret_cast<const TsaW2*>(r >= m ? lab + (size_t)(r - m) * NW : leaf + (size_t)r * NW);
+        const TsaW2* qz = reinterpret_cast<const TsaW2*>(lab + (size_t)i * NW);
+        TsaW2 xx[TSA_WIDE_CPL], yy[TSA_WIDE_CPL], zv[TSA_WIDE_CPL];
+#pragma unroll
+        for (int q = 0; q < TSA_WIDE_CPL; q++) {
+          const int cc = t + q * G;
+          if (cc < nch) {
+            xx[q] = qx[cc];
+            yy[q] = qy[cc];
+            zv[q] = qz[cc];
+          } else {
+            xx[q] = yy[q] = zv[q] = TsaW2{0ull, 0ull};
+          }
+        }
+        int B = 0, M = 0, N = 0, Kc = 0, Z = 0;
+#pragma unroll
+        for (int q = 0; q < TSA_WIDE_CPL; q++) {
+          const uint64_t za = zv[q].a & sm[q].a, zb = zv[q].b & sm[q].b;
+          tsa_count3(xx[q].a & sm[q].a, yy[q].a & sm[q].a, za, B, M, N, Kc);
+          tsa_count3(xx[q].b & sm[q].b, yy[q].b & sm[q].b, zb, B, M, N, Kc);
+          Z += __popcll(za) + __popcll(zb);
+        }
+        uint32_t a[3] = {(uint32_t)B | ((uint32_t)M << 16), (uint32_t)N | ((uint32_t)Kc << 16), (uint32_t)Z};
+        group_sum<G, 3>(a);
+        if (t == 0) {
+          B = (int)(a[0] & 0xFFFFu);
+          M = (int)(a[0] >> 16);
+          N = (int)(a[1] & 0xFFFFu);
+          Kc = (int)(a[1] >> 16);
+          Z = (int)a[2];
+          cst[i] = tsa_node_cost<MODE>(B, M, N, Kc, Z, P.model, T);
+          zz[i] = (uint16_t)Z;
+        }
+      }
+    }
+    // the last workgroup of the chain to finish folds
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+      const unsigned old = __hip_atomic_fetch_add(fcnt + c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int last = old == (unsigned)(K2 - 1);
+      if (last) {
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        __hip_atomic_store(fcnt + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+  }
+
+  // fold: the costs are read in a serial chain per lane, so they are first staged in LDS
+  const float* fc = cst;
+  const uint16_t* fz = zz;
+  const uint32_t* map = gmap;
+  if (stage) {
+    // vector copies, unrolled so that every thread has all its loads in flight at once
+    float* const scst = reinterpret_cast<float*>(s_dyn);
+    uint16_t* const szz = reinterpret_cast<uint16_t*>(s_dyn + (size_t)nint4 * 4);
+    const int n4 = nint4 / 4;
+#pragma unroll 4
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+      const float4 cv = reinterpret_cast<const float4*>(cst)[i];
+      const uint2 zv = reinterpret_cast<const uint2*>(zz)[i];
+      reinterpret_cast<float4*>(scst)[i] = cv;
+      reinterpret_cast<uint2*>(szz)[i] = zv;
+    }
+    if (stage == 2) {
+      uint4* const smap = reinterpret_cast<uint4*>(s_dyn + (((size_t)nint4 * 6 + 15) & ~(size_t)15));
+      const uint4* src = reinterpret_cast<const uint4*>(gmap);
+#pragma unroll 16
+      for (int i = threadIdx.x; i < (int)(TSA_LOG2MAP_WORDS / 4); i += blockDim.x) smap[i] = src[i];
+      map = reinterpret_cast<const uint32_t*>(smap);
+    }
+    __syncthreads();
+    fc = scst;
+    fz = szz;
+  }
+  if (threadIdx.x >= 32) return;
+  const TsaMathTabs T{s_exp2, fix, map};
+  const int l32 = (int)threadIdx.x;
+  float acc = -INFINITY;
+  int scl = 0;
+  for (int i = l32; i < nint; i += 32) {
+    acc = tsa_lse_f(acc, fc[i], T);
+    const int Z = fz[i];
+    scl = Z > scl ? Z : scl;
+  }
+  int scmax = scl;
+  for (int o = 16; o > 0; o >>= 1) {
+    acc = tsa_lse_f(acc, __shfl_xor(acc, o, 32), T);
+    const int u = __shfl_xor(scmax, o, 32);
+    scmax = scmax > u ? scmax : u;
+  }
+  int nsv = 0;
+  if (S)
+    for (int w = l32; w < NW; w += 32) nsv += __popcll(S[w]);
+  for (int o = 16; o > 0; o >>= 1) nsv += __shfl_xor(nsv, o, 32);
+  int scv = scmax > P.leaf_sc ? scmax : P.leaf_sc;
+  if (S && P.leaf_sc > scmax) {  // a leaf may be the largest tensor: masked leaf sizes
+    int ll = 0;
+    for (int i = l32; i < m; i += 32) {
+      int Z = 0;
+      for (int w = 0; w < NW; w++) Z += __popcll(leaf[(size_t)i * NW + w] & ~S[w]);
+      ll = ll > Z ? ll : Z;
+    }
+    for (int o = 16; o > 0; o >>= 1) {
+      const int u = __shfl_xor(ll, o, 32);
+      ll = ll > u ? ll : u;
+    }
+    scv = scmax > ll ? scmax : ll;
+  }
+  if (l32 == 0) {
+    lc[c] = acc;
+    sc[c] = scv;
+    ns[c] = nsv;
+  }
+}
+
+template <int G, int MODE>
+hipError_t launch_wide_gm(const TsaWide& X, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
+                          const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
+                          unsigned long long* stats, const TsaWideSync& sy, hipStream_t st) {
+  if (X.K > 1) {
+    TsaKParams p = P;
+    int K = X.K;
+    TsaWideSync s = sy;
+    void* args[] = {&p, &rec, &leaf, &fix, &nchains, &K, &beta, &sweep0, &nsweeps, &stats, &s};
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&k_wide<G, MODE, true>), dim3(nchains * X.K),
+                                      dim3(X.nt), args, (unsigned)X.smem, st);
+  }
+  hipLaunchKernelGGL((k_wide<G, MODE, false>), dim3(nchains), dim3(X.nt), (size_t)X.smem, st, P, rec, leaf, fix,
+                     nchains, 1, beta, sweep0, nsweeps, stats, sy);
+  return hipGetLastError();
+}
+
+template <int G>
+hipError_t launch_wide_g(const TsaWide& X, int mode, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
+                         const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
+                         unsigned long long* stats, const TsaWideSync& sy, hipStream_t st) {
+  if (mode == 0) return launch_wide_gm<G, 0>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+  if (mode == 1) return launch_wide_gm<G, 1>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+  return launch_wide_gm<G, 2>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+}
+
+template <int G, int MODE>
+hipError_t launch_wcost_gm(const TsaWide& X, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
+                           const uint32_t* fix, int nchains, float* ncost, uint16_t* nz, unsigned* fcnt, float* lc,
+                           int* sc, int* ns, int nodes, hipStream_t st) {
+  const int K2 = nodes ? X.eK : 1;
+  const int stage = nodes ? (X.fold_smem > 0 ? 1 : 0) : X.fold_stage;
+  const size_t smem = stage == 2 ? (size_t)X.fold_smem_map : stage == 1 ? (size_t)X.fold_smem : 0;
+  hipLaunchKernelGGL((k_wcost<G, MODE>), dim3(nchains * K2), dim3(256), smem, st, P, rec, leaf, fix, nchains, K2, nodes,
+                     stage, ncost, nz, fcnt, lc, sc, ns);
+  return hipGetLastError();
+}
+
+template <int G>
+hipError_t launch_wcost_g(const TsaWide& X, int mode, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
+                          const uint32_t* fix, int nchains, float* ncost, uint16_t* nz, unsigned* fcnt, float* lc,
+                          int* sc, int* ns, int nodes, hipStream_t st) {
+  if (mode == 0) return launch_wcost_gm<G, 0>(X, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
+  if (mode == 1) return launch_wcost_gm<G, 1>(X, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
+  return launch_wcost_gm<G, 2>(X, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
+}
+
+// Largest number of co-resident workgroups per CU of the cooperative sweep kernel over the three modes.
+template <int G>
+hipError_t wide_occupancy(int nt, int smem, int fold_smem, int* per_cu) {
+  const void* fns[3] = {reinterpret_cast<const void*>(&k_wide<G, 0, true>),
+                        reinterpret_cast<const void*>(&k_wide<G, 1, true>),
+                        reinterpret_cast<const void*>(&k_wide<G, 2, true>)};
+  const void* fns1[3] = {reinterpret_cast<const void*>(&k_wide<G, 0, false>),
+                         reinterpret_cast<const void*>(&k_wide<G, 1, false>),
+                         reinterpret_cast<const void*>(&k_wide<G, 2, false>)};
+  const void* fold[3] = {reinterpret_cast<const void*>(&k_wcost<G, 0>), reinterpret_cast<const void*>(&k_wcost<G, 1>),
+                         reinterpret_cast<const void*>(&k_wcost<G, 2>)};
+  int best = 1 << 30;
+  for (int i = 0; i < 3; i++) {
+    hipError_t ef = hipFuncSetAttribute(fold[i], hipFuncAttributeMaxDynamicSharedMemorySize, fold_smem);
+    if (ef != hipSuccess) return ef;
+    if (smem > 65536) {
+      hipError_t e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+      if (e != hipSuccess) return e;
+      e = hipFuncSetAttribute(fns1[i], hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+      if (e != hipSuccess) return e;
+    }
+    int nb = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fns[i], nt, (size_t)smem);
+    if (e != hipSuccess) return e;
+    best = nb < best ? nb : best;
+  }
+  *per_cu = best;
+  return hipSuccess;
+}
+
+}  // namespace
+
+hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int want_k, TsaWide* out) {
+  TsaWide X{};
+  const int nch = P.W / 2;
+  if ((P.W & 1) || nch < 1 || nch > TSA_WIDE_CPL * 64) return hipErrorInvalidValue;
+  int G = 4;
+  while (G < 64 && (nch + G - 1) / G > TSA_WIDE_CPL) G *= 2;
+  X.G = G;
+  int dev = 0, ncu = 0, lds_max = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+  if (e != hipSuccess) return e;
+  // measured on MI355X: with at least one chain per CU, one 8-wave workgroup per chain streams best; with
+  // fewer chains, 16-wave workgroups, as many per chain as stay co-resident
+  int waves = want_waves > 0 ? want_waves : (nchains >= ncu ? 8 : 16);
+  waves = waves < 1 ? 1 : (waves > 16 ? 16 : waves);
+  X.nt = 64 * waves;
+  const int band = P.par_band > 0 ? 1 : 0;
+  const TsaWideLds L1 = tsa_wide_lds(P.nint, band, 0), Lc = tsa_wide_lds(P.nint, band, 1);
+  if (L1.bytes > lds_max) return hipErrorInvalidValue;
+  int per_cu = 0;
+  // the fold stages a chain's node costs (6 B per node) and, when it also fits, the log2f summary bitmap
+  const int nint4 = (P.nint + 3) & ~3, fold_budget = lds_max - 1024;
+  X.fold_smem = nint4 * 6 <= fold_budget ? nint4 * 6 : 0;
+  X.fold_smem_map = ((nint4 * 6 + 15) & ~15) + (int)TSA_LOG2MAP_WORDS * 4;
+  X.fold_stage = X.fold_smem == 0 ? 0 : (X.fold_smem_map <= fold_budget ? 2 : 1);
+  switch (G) {  // the fold's LDS cap is set to the largest any context may ask for
+    case 4: e = wide_occupancy<4>(X.nt, L1.bytes, fold_budget, &per_cu); break;
+    case 8: e = wide_occupancy<8>(X.nt, L1.bytes, fold_budget, &per_cu); break;
+    case 16: e = wide_occupancy<16>(X.nt, L1.bytes, fold_budget, &per_cu); break;
+    case 32: e = wide_occupancy<32>(X.nt, L1.bytes, fold_budget, &per_cu); break;
+    default: e = wide_occupancy<64>(X.nt, L1.bytes, fold_budget, &per_cu); break;
+  }
+  if (e != hipSuccess) return e;
+  if (per_cu < 1) return hipErrorInvalidValue;
+  const int cap = per_cu * ncu;
+  int K = want_k > 0 ? want_k : cap / nchains;
+  K = K < 1 ? 1 : (K > TSA_WIDE_MAX_K ? TSA_WIDE_MAX_K : K);
+  if (K > 1 && K * nchains > cap) return hipErrorCooperativeLaunchTooLarge;
+  X.K = K;
+  X.smem = K > 1 ? Lc.bytes : L1.bytes;
+  X.eG = G;
+  const int gpb = 256 / G, maxk = (P.nint + gpb - 1) / gpb;
+  int eK = (4 * ncu + nchains - 1) / nchains;
+  X.eK = eK < 1 ? 1 : (eK > maxk ? maxk : eK);
+  X.on = 1;
+  *out = X;
+  return hipSuccess;
+}
+
+hipError_t tsa_launch_wide(const TsaWide& X, int mode, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
+                           const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
+                           unsigned long long* stats, const TsaWideSync& sy, hipStream_t st) {
+  switch (X.G) {
+    case 4: return launch_wide_g<4>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    case 8: return launch_wide_g<8>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    case 16: return launch_wide_g<16>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    case 32: return launch_wide_g<32>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    case 64: return launch_wide_g<64>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t tsa_launch_wide_energy(const TsaWide& X, int mode, const TsaKParams& P, const uint64_t* rec,
+                                  const uint64_t* leaf, const uint32_t* fix, int nchains, float* ncost,
+                                  uint16_t* nz, unsigned* fcnt, float* lc, int* sc, int* ns, int nodes,
+                                  hipStream_t st) {
+  switch (X.eG) {
+    case 4: return launch_wcost_g<4>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
+    case 8: return launch_wcost_g<8>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
+    case 16: return launch_wcost_g<16>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
+    case 32: return launch_wcost_g<32>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
+    case 64: return launch_wcost_g<64>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
+    default: return hipErrorInvalidValue;
+  }
+}

@@ -32,7 +32,7 @@ struct Opts {
   bool check = false, quiet = false, cross = true, wide = false, slicing = false, no_sum = false, force_sum = false;
   bool select_sc = false;
   int slice_moves = 1, slice_every = 1, max_slices = 0, random_slices = 0;
-  int coop_max = 0, coop_min_units = -1, coop_min = 1, coop_full = 0, coop_cpl = 2, par_follow = 0, par_band = 0, wpc = 0;
+  int coop_max = 0, coop_min_units = -1, coop_min = 1, coop_full = 0, coop_cpl = 2, par_follow = 0, par_band = 0, wpc = 0, wide_wgs = 0;
   double sc_target = 20.0, sc_weight = 1.0, trunc_frac = 0.25;
   uint64_t seed = 1;
   ModelConsts mc;
@@ -59,7 +59,7 @@ std::string jnum(double x) {
           "  [--stage2-betas SPEC [--stage2-niters K] [--stage2-mode gpu|h100]]  (continue the population)\n"
           "  [--sc-target x] [--sc-weight y] [--scheme indep|pa|trunc] [--trunc-frac f]\n"
           "  [--slicing [--slice-moves k] [--slice-every s] [--max-slices n] [--init-slices l1,l2,..]]\n"
-          "  [--order par|preorder] [--kernel auto|seq|seqsm|warp|warpsm|block|par [--wpc n]] [--lpc 32|16|8] [--coop-max G] [--coop-min G0] [--coop-full G1] [--par-follow] [--par-band L] [--coop-min-units u] [--wide] [--sums|--no-sum] [--select-sc] [--block B] [--wpb W] [--seed s]\n"
+          "  [--order par|preorder] [--kernel auto|seq|seqsm|warp|warpsm|block|par [--wpc n]] [--lpc 32|16|8] [--coop-max G] [--coop-min G0] [--coop-full G1] [--par-follow] [--par-band L] [--coop-min-units u] [--wide] [--sums|--no-sum] [--select-sc] [--block B] [--wpb W] [--seed s] [--wide-wgs K]\n"
           "  [--eval-every k] [--out result.json] [--check [--ref-chains R] [--random-slices k]] [--quiet]\n"
           "  [--bench-warmup W]  (W untimed levels first, then the initial population again)\n"
           "  [--host-select]  (select the best chain on the host at every level, also for --scheme indep)\n");
@@ -133,6 +133,7 @@ Opts parse(int argc, char** argv) {
       else if (a == "--par-follow") o.par_follow = 1;
       else if (a == "--par-band") o.par_band = std::stoi(nx());
       else if (a == "--wpc") o.wpc = std::stoi(nx());
+      else if (a == "--wide-wgs") o.wide_wgs = std::stoi(nx());
       else if (a == "--wide") o.wide = true;
       else if (a == "--no-sum") o.no_sum = true;
       else if (a == "--select-sc") o.select_sc = true;
@@ -207,6 +208,8 @@ class Runner {
     cfg.v2_ltc_out = ML.v2_ltc_out;
     cfg.v2_lsmall_cell = ML.v2_lsmall_cell;
     cfg.v2_small_rank = ML.v2_small_rank;
+    cfg.wide_waves = O.wpc > 0 ? (O.wpc + 1) / 2 : 0;  // --wpc counts 32-lane warps
+    cfg.wide_wgs = O.wide_wgs;
   }
   ~Runner() {
     if (ctx) tsa_destroy(ctx);
@@ -367,11 +370,24 @@ int Runner::run_anneal() {
     create(&ctx, cfg.kernel);
     ck(tsa_upload(ctx, pop.data()));
     if (O.bench_warmup > 0 && !betas.empty()) {
-      // untimed warm-up levels (clocks, code objects), then the same initial population again
+      // untimed warm-up levels (clocks, code objects, the tracking buffers of the level loop), then the same
+      // initial population again
       std::vector<float> l(O.nchains);
       std::vector<int> s(O.nchains), n(O.nchains);
+      const bool track = O.scheme == "indep" && O.betas2.empty() && !O.host_select;
+      tsa_select_t sel{};
+      if (track) {
+        const TsaSelect S = select_params();
+        sel.mode = S.mode;
+        sel.slicing = S.slicing;
+        sel.select_sc = S.select_sc;
+        sel.sc_target = S.sc_target;
+        sel.sc_weight = S.sc_weight;
+        ck(tsa_track_begin(ctx, &sel, (int)betas.size()));
+      }
       for (int k = 0; k < O.bench_warmup; k++) {
         ck(tsa_sweeps(ctx, order, betas[k % betas.size()], (uint32_t)k, lniters[k % betas.size()]));
+        if (track) ck(tsa_track(ctx, k % (int)betas.size()));
         ck(tsa_energy(ctx, l.data(), s.data(), n.data()));
       }
       double ms = 0;
@@ -597,8 +613,8 @@ int Runner::run_check() {
   }
   printf("  [2] GPU energy kernel vs host double: max |dlog2cost| = %.3g, sc/|S| mismatches %d\n", maxd, scbad);
   int xdiff = -1;
-  const bool is_lds = strncmp(desc, "lds", 3) == 0;
-  if (O.cross && cfg.slice_moves == 0 && is_lds) {
+  const bool is_lds = strncmp(desc, "lds", 3) == 0, is_wide = strncmp(desc, "wide", 4) == 0;
+  if (O.cross && cfg.slice_moves == 0 && (is_lds || (is_wide && order == TSA_ORDER_PAR))) {
     tsa_ctx* c2 = nullptr;
     create(&c2, TSA_KERNEL_GLOBAL);
     ck(tsa_upload(c2, init.data()));
@@ -612,7 +628,7 @@ int Runner::run_check() {
       if (!std::equal(fin.begin() + (size_t)c * lay.chain_words, fin.begin() + (size_t)(c + 1) * lay.chain_words,
                       fin2.begin() + (size_t)c * lay.chain_words))
         xdiff++;
-    printf("  [3] kernel lds vs global: chains differing: %d/%d\n", xdiff, O.nchains);
+    printf("  [3] kernel %s vs global: chains differing: %d/%d\n", is_lds ? "lds" : "wide", xdiff, O.nchains);
   }
   printf("  [4] CPU reference: not linked into this binary\n");
   const bool ok = bad_tree == 0 && bad_lab == 0 && scbad == 0 && maxd < 1e-3 && xdiff <= 0;
