@@ -77,6 +77,10 @@ typedef struct tsa_config_t {
   int32_t v2_small_rank;
   /* wide kernel plan (0 = automatic): waves per workgroup (1..16), workgroups per chain (1..16) */
   int32_t wide_waves, wide_wgs;
+  /* 1: every tsa_sweeps also leaves the energies of the swept population ready (each chain is evaluated by
+   * the sweep kernel while it is still staged), so that tsa_energy / tsa_track launch no energy kernel;
+   * for callers that evaluate after every level */
+  int32_t fused_energy;
 } tsa_config_t;
 
 typedef struct tsa_ctx tsa_ctx;

@@ -44,7 +44,7 @@ class Config(ctypes.Structure):
                 ("v2_l3launch", ctypes.c_float), ("v2_lperm2", ctypes.c_float), ("v2_lcc_bit", ctypes.c_float),
                 ("v2_lcc_cell", ctypes.c_float), ("v2_ltc_bit", ctypes.c_float), ("v2_ltc_pad", ctypes.c_float),
                 ("v2_ltc_out", ctypes.c_float), ("v2_lsmall_cell", ctypes.c_float), ("v2_small_rank", ctypes.c_int32),
-                ("wide_waves", ctypes.c_int32), ("wide_wgs", ctypes.c_int32)]
+                ("wide_waves", ctypes.c_int32), ("wide_wgs", ctypes.c_int32), ("fused_energy", ctypes.c_int32)]
 
 
 _lib = None
@@ -110,7 +110,7 @@ def layout(m, nlab, wide=False):
 
 def make_config(mode="tc", sc_target=20.0, sc_weight=1.0, seed=1, slicing=False, slice_moves=1, slice_every=1,
                 max_slices=0, par_follow=False, par_band=0, kernel=KERNEL_AUTO, gm=DEFAULT_GM, h100=DEFAULT_H100,
-                wide_waves=0, wide_wgs=0):
+                wide_waves=0, wide_wgs=0, fused_energy=False):
     """Config with the fields the reference's Runner derives from its options (csrc/treesa_gpu.cu:1449-1474)."""
     k = splitmix64(seed)
     c = Config()
@@ -133,6 +133,7 @@ def make_config(mode="tc", sc_target=20.0, sc_weight=1.0, seed=1, slicing=False,
     c.v2_ltc_bit, c.v2_ltc_pad, c.v2_ltc_out = f32_log2(h[4]), f32_log2(h[5]), f32_log2(h[6])
     c.v2_small_rank, c.v2_lsmall_cell = int(h[7]), f32_log2(h[8])
     c.wide_waves, c.wide_wgs = wide_waves, wide_wgs
+    c.fused_energy = 1 if fused_energy else 0
     return c
 
 

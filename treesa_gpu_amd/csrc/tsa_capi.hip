@@ -52,6 +52,10 @@ struct tsa_ctx {
   unsigned* d_fcnt = nullptr;  // per-chain workgroup counters of the wide energy kernel
   bool costs_valid = false;    // d_ncost / d_nz hold every node's cost (full pass since the last upload,
                                // resample or mode switch, and every sweep since ran the wide kernel)
+  bool energy_fresh = false;   // d_lc / d_sc / d_ns hold the energies of the current population (written by
+                               // the last sweep launch, cfg.fused_energy)
+  TsaTrackPart* d_tpart = nullptr;  // selection kernel: per-workgroup results and its counter
+  unsigned* d_tdone = nullptr;
   std::string err;
 };
 
@@ -204,6 +208,8 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_ncost) (void)hipFree(c->d_ncost);
   if (c->d_nz) (void)hipFree(c->d_nz);
   if (c->d_fcnt) (void)hipFree(c->d_fcnt);
+  if (c->d_tpart) (void)hipFree(c->d_tpart);
+  if (c->d_tdone) (void)hipFree(c->d_tdone);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   if (c->d_track) (void)hipFree(c->d_track);
   if (c->d_trace) (void)hipFree(c->d_trace);
@@ -409,6 +415,7 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
 }
 
 static hipError_t launch_energy(tsa_ctx* c) {
+  if (c->energy_fresh) return hipSuccess;  // the last sweep launch left them in d_lc / d_sc / d_ns
   if (c->wide.on) {
     const hipError_t e = tsa_launch_wide_energy(c->wide, c->mode, c->P, c->d_rec, c->d_leaf, c->d_fix, c->nchains,
                                                 c->d_ncost, c->d_nz, c->d_fcnt, c->d_lc, c->d_sc, c->d_ns,
@@ -441,6 +448,7 @@ extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
       return fail(ctx, TSA_ERR_ARG, "tsa_upload: chain " + std::to_string(c) + " is not a valid tree");
   }
   ctx->costs_valid = false;
+  ctx->energy_fresh = false;
   TSA_HIP(ctx, hipMemcpyAsync(ctx->d_rec, population, (size_t)ctx->nchains * L.chain_words * 8,
                               hipMemcpyHostToDevice, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
@@ -469,13 +477,17 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
   }
   hipEvent_t e0 = ctx->ev[2 * ctx->npending], e1 = ctx->ev[2 * ctx->npending + 1];
   TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
+  ctx->energy_fresh = false;
   if (ctx->wide.on && order == TSA_ORDER_PAR) {
     TSA_HIP(ctx, tsa_launch_wide(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains, beta,
                                  sweep0, nsweeps, ctx->d_stats, ctx->wsync, ctx->st));
   } else {
     ctx->costs_valid = false;
+    const bool fuse = ctx->cfg.fused_energy != 0;
+    const TsaEnergyOut eo{fuse ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns};
     TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
-                                   ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, ctx->st));
+                                   ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st));
+    ctx->energy_fresh = fuse;
   }
   TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
   ctx->npending++;
@@ -509,6 +521,11 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   if (!ctx->d_track) TSA_HIP(ctx, hipMalloc(&ctx->d_track, sizeof(TsaTrackState)));
   if (!ctx->d_ticks0) TSA_HIP(ctx, hipMalloc(&ctx->d_ticks0, sizeof(unsigned long long)));
   if (!ctx->d_best) TSA_HIP(ctx, hipMalloc(&ctx->d_best, (size_t)ctx->lay.chain_words * 8));
+  if (!ctx->d_tpart) {
+    TSA_HIP(ctx, hipMalloc(&ctx->d_tpart, (size_t)((ctx->nchains + 255) / 256) * sizeof(TsaTrackPart)));
+    TSA_HIP(ctx, hipMalloc(&ctx->d_tdone, sizeof(unsigned)));
+    TSA_HIP(ctx, hipMemsetAsync(ctx->d_tdone, 0, sizeof(unsigned), ctx->st));
+  }
   if (max_levels > ctx->track_levels) {
     if (ctx->d_trace) TSA_HIP(ctx, hipFree(ctx->d_trace));
     ctx->d_trace = nullptr;
@@ -529,7 +546,8 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
   TsaSelect S = ctx->sel;
   S.mode = ctx->mode;
   TSA_HIP(ctx, tsa_launch_track(ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->nchains, S, level, ctx->d_rec,
-                                ctx->lay.chain_words, ctx->d_track, ctx->d_trace, ctx->d_best, ctx->st));
+                                ctx->lay.chain_words, ctx->d_track, ctx->d_trace, ctx->d_best, ctx->d_tpart,
+                                ctx->d_tdone, ctx->st));
   return TSA_OK;
 }
 
@@ -583,6 +601,7 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
   if (!ctx->d_rec2) TSA_HIP(ctx, hipMalloc(&ctx->d_rec2, (size_t)ctx->nchains * ctx->lay.chain_words * 8));
   TSA_HIP(ctx, hipMemcpyAsync(ctx->d_anc, anc, (size_t)ctx->nchains * 4, hipMemcpyHostToDevice, ctx->st));
   ctx->costs_valid = false;
+  ctx->energy_fresh = false;
   TSA_HIP(ctx, tsa_launch_copy(ctx->d_rec, ctx->d_rec2, ctx->d_anc, ctx->nchains, ctx->lay.chain_words, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
   std::swap(ctx->d_rec, ctx->d_rec2);
@@ -592,7 +611,7 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
 extern "C" int tsa_set_mode(tsa_ctx* ctx, int32_t mode) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: null context");
   if (mode < 0 || mode > 2) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: mode must be 0, 1 or 2");
-  if (mode != ctx->mode) ctx->costs_valid = false;
+  if (mode != ctx->mode) ctx->costs_valid = ctx->energy_fresh = false;
   ctx->mode = mode;
   return TSA_OK;
 }

@@ -34,10 +34,18 @@ struct TsaLaunch {
   int lds_words;     // LDS words per wave
 };
 
+// Per-chain energies a sweep launch also writes (lc == nullptr: none): the chain is evaluated by the sweep
+// kernel right after its last sweep, while it is still staged, exactly as the energy kernel would.
+struct TsaEnergyOut {
+  float* lc;
+  int* sc;
+  int* ns;
+};
+
 // Host-side launchers (tsa_kernels.hip).  All return hipError_t of the launch.
 hipError_t tsa_launch_sweeps(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
                              const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
-                             int nsweeps, unsigned long long* stats, hipStream_t st);
+                             int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st);
 hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
                              const uint32_t* fix, int nchains, float* lc, int* sc, int* ns, hipStream_t st);
 struct TsaTrackState {
@@ -53,9 +61,15 @@ struct TsaTraceRowD {  // same layout as tsa_trace_row_t
 };
 // Chains above TSA_TRACK_INLINE_WORDS words are snapshot by a separate many-workgroup copy kernel.
 #define TSA_TRACK_INLINE_WORDS 16384
+// Result of one selection workgroup (256 chains): best score and chain, sums of E and |S|.
+struct TsaTrackPart {
+  double score, sumE, sumNs;
+  int idx;
+};
+// part: ceil(nchains / 256) entries; done: one zeroed counter (left zero after every launch).
 hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int nchains, const TsaSelect& S, int level,
                             const uint64_t* rec, int chain_words, TsaTrackState* st, TsaTraceRowD* trace,
-                            uint64_t* best_rec, hipStream_t stream);
+                            uint64_t* best_rec, TsaTrackPart* part, unsigned* done, hipStream_t stream);
 hipError_t tsa_launch_track_init(TsaTrackState* st, unsigned long long* ticks0, hipStream_t stream);
 hipError_t tsa_launch_copy(const uint64_t* src, uint64_t* dst, const int* anc, int nchains, int chain_words,
                            hipStream_t st);

@@ -18,11 +18,7 @@
 // instruction of the same wave reads; tsa_wave_sync() (wavefront-scope release/acquire fences around
 // a wave barrier) keeps the compiler from moving those accesses across the exchange points.
 #include "tsa_kernels.h"
-
-struct TsaEvalOut {
-  float lcost;
-  int sc, sc_int, ncand, ns;
-};
+#include "tsa_fold.h"
 
 __device__ __forceinline__ void tsa_wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -282,7 +278,7 @@ template <int W, int MODE, int ORDER, bool LDS>
 __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restrict__ rec,
                                                const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
                                                int nchains, int lds_words, float beta, uint32_t sweep0, int nsweeps,
-                                               unsigned long long* __restrict__ stats) {
+                                               unsigned long long* __restrict__ stats, TsaEnergyOut eo) {
   extern __shared__ uint64_t tsa_smem[];
   __shared__ float s_lse[64];
   __shared__ uint64_t s_exp2[32];
@@ -463,6 +459,24 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
     }
   }
 
+  if (eo.lc) {
+    // the chain's energy, as k_energy computes it: node costs by all 64 lanes into the node arrays (free
+    // after the sweeps: pri and par hold nint4 floats, wl nint4 sizes), then the 32-lane fold
+    tsa_wave_sync();
+    float* const ncost = reinterpret_cast<float*>(pri);
+    for (int i = lane; i < nint; i += 64) {
+      int Z;
+      ncost[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
+      wl[i] = (uint16_t)Z;
+    }
+    tsa_wave_sync();
+    const TsaEvalOut e = tsa_fold32(P, ncost, wl, Sm, lf, NW, T, lane & 31);
+    if (lane == 0) {
+      eo.lc[c] = e.lcost;
+      eo.sc[c] = e.sc;
+      eo.ns[c] = e.ns;
+    }
+  }
   if constexpr (LDS) {
     tsa_wave_sync();
     const uint4* src = reinterpret_cast<const uint4*>(base);
@@ -514,35 +528,79 @@ __global__ void __launch_bounds__(256) k_copy(const uint4* __restrict__ src, uin
   for (int i = threadIdx.x; i < n4; i += blockDim.x) d[i] = s[i];
 }
 
-// Best tracking of one level (one workgroup of 1024 threads): score every chain, argmin with the lowest
-// index on ties, population means, and a snapshot of the best chain when it beats the best so far
-// (csrc/treesa_gpu.cu:1810-1832).  Sums are reduced in a fixed tree order, so they are deterministic.
-__global__ void __launch_bounds__(1024) k_track(const float* __restrict__ lc, const int* __restrict__ sc,
-                                                const int* __restrict__ ns, int n, TsaSelect S, int level,
-                                                const uint64_t* __restrict__ rec, int chain_words,
-                                                TsaTrackState* __restrict__ st, TsaTraceRowD* __restrict__ trace,
-                                                uint64_t* __restrict__ best_rec) {
-  __shared__ double s_s[1024], s_e[1024], s_n[1024];
-  __shared__ int s_i[1024];
-  __shared__ int s_copy, s_bi;
-  const int t = threadIdx.x;
+// Best tracking of one level (csrc/treesa_gpu.cu:1810-1832): every chain scored by its own thread, argmin
+// with the lowest index on ties and the population sums reduced per workgroup of 256 in a fixed tree order,
+// then the last workgroup to finish reduces the per-workgroup results in index order, writes the trace
+// row, keeps the best so far and snapshots it when it improves.  Sums are therefore deterministic.
+__global__ void __launch_bounds__(256) k_track(const float* __restrict__ lc, const int* __restrict__ sc,
+                                               const int* __restrict__ ns, int n, TsaSelect S, int level,
+                                               const uint64_t* __restrict__ rec, int chain_words,
+                                               TsaTrackState* __restrict__ st, TsaTraceRowD* __restrict__ trace,
+                                               uint64_t* __restrict__ best_rec, TsaTrackPart* __restrict__ part,
+                                               unsigned* __restrict__ done) {
+  __shared__ double s_s[256], s_e[256], s_n[256];
+  __shared__ int s_i[256];
+  __shared__ int s_last, s_copy, s_bi;
+  const int t = threadIdx.x, c = blockIdx.x * 256 + t;
   double bs = INFINITY, se = 0.0, sn = 0.0;
   int bi = n;
-  for (int c = t; c < n; c += 1024) {
-    const double s = tsa_score(lc[c], sc[c], ns[c], S);
-    if (s < bs) {
-      bs = s;
-      bi = c;
-    }
-    se += tsa_energyE(lc[c], sc[c], ns[c], S);
-    sn += (double)ns[c];
+  if (c < n) {
+    bs = tsa_score(lc[c], sc[c], ns[c], S);
+    bi = bs < INFINITY ? c : n;
+    se = tsa_energyE(lc[c], sc[c], ns[c], S);
+    sn = (double)ns[c];
   }
   s_s[t] = bs;
   s_i[t] = bi;
   s_e[t] = se;
   s_n[t] = sn;
   __syncthreads();
-  for (int o = 512; o > 0; o >>= 1) {
+  for (int o = 128; o > 0; o >>= 1) {
+    if (t < o) {
+      const double a = s_s[t], b = s_s[t + o];
+      const int ia = s_i[t], ib = s_i[t + o];
+      if (b < a || (b == a && ib < ia)) {
+        s_s[t] = b;
+        s_i[t] = ib;
+      }
+      s_e[t] += s_e[t + o];
+      s_n[t] += s_n[t + o];
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    part[blockIdx.x] = TsaTrackPart{s_s[0], s_e[0], s_n[0], s_i[0]};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const unsigned old = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int last = old == gridDim.x - 1;
+    if (last) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    s_last = last;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // the per-workgroup results, in workgroup order: thread t folds workgroups t, t+256, ... then a tree
+  bs = INFINITY;
+  bi = n;
+  se = 0.0;
+  sn = 0.0;
+  for (int k = t; k < (int)gridDim.x; k += 256) {
+    const TsaTrackPart q = part[k];
+    if (q.score < bs || (q.score == bs && q.idx < bi)) {
+      bs = q.score;
+      bi = q.idx;
+    }
+    se += q.sumE;
+    sn += q.sumNs;
+  }
+  s_s[t] = bs;
+  s_i[t] = bi;
+  s_e[t] = se;
+  s_n[t] = sn;
+  __syncthreads();
+  for (int o = 128; o > 0; o >>= 1) {
     if (t < o) {
       const double a = s_s[t], b = s_s[t + o];
       const int ia = s_i[t], ib = s_i[t + o];
@@ -580,7 +638,7 @@ __global__ void __launch_bounds__(1024) k_track(const float* __restrict__ lc, co
   __syncthreads();
   if (s_copy && chain_words <= TSA_TRACK_INLINE_WORDS) {
     const uint64_t* src = rec + (size_t)s_bi * chain_words;
-    for (int w = t; w < chain_words; w += 1024) best_rec[w] = src[w];
+    for (int w = t; w < chain_words; w += 256) best_rec[w] = src[w];
   }
 }
 
@@ -607,7 +665,7 @@ __global__ void k_track_init(TsaTrackState* st, unsigned long long* ticks0) {
 template <int W, int MODE, int ORDER, bool LDS>
 static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
                                  const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
-                                 unsigned long long* stats, hipStream_t st) {
+                                 unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st) {
   const int NW = W > 0 ? W : P.W;
   const size_t leafw = LDS ? (size_t)((P.m * NW + 1) & ~1) : 0;
   const size_t smem = (leafw + (size_t)L.wpb * L.lds_words) * 8;
@@ -620,45 +678,45 @@ static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64
   }
   const int grid = (nchains + L.wpb - 1) / L.wpb;
   hipLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS>), dim3(grid), dim3(64 * L.wpb), smem, st, P, rec, leaf, fix,
-                     nchains, L.lds_words, beta, sweep0, nsweeps, stats);
+                     nchains, L.lds_words, beta, sweep0, nsweeps, stats, eo);
   return hipGetLastError();
 }
 
 template <int W, int MODE>
 static hipError_t launch_sweep_wm(const TsaLaunch& L, int order, const TsaKParams& P, uint64_t* rec,
                                   const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
-                                  int nsweeps, unsigned long long* stats, hipStream_t st) {
+                                  int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st) {
   if constexpr (W > 0) {
     if (L.lds) {
-      if (order == 0) return launch_sweep_t<W, MODE, 0, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
-      return launch_sweep_t<W, MODE, 1, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+      if (order == 0) return launch_sweep_t<W, MODE, 0, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+      return launch_sweep_t<W, MODE, 1, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
     }
     return hipErrorInvalidValue;  // the register-width kernels exist only in the LDS variant
   } else {
     if (L.lds) return hipErrorInvalidValue;
-    if (order == 0) return launch_sweep_t<0, MODE, 0, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
-    return launch_sweep_t<0, MODE, 1, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+    if (order == 0) return launch_sweep_t<0, MODE, 0, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+    return launch_sweep_t<0, MODE, 1, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
   }
 }
 
 template <int W>
 static hipError_t launch_sweep_w(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
                                  const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
-                                 int nsweeps, unsigned long long* stats, hipStream_t st) {
-  if (mode == 0) return launch_sweep_wm<W, 0>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
-  if (mode == 1) return launch_sweep_wm<W, 1>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
-  return launch_sweep_wm<W, 2>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+                                 int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st) {
+  if (mode == 0) return launch_sweep_wm<W, 0>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+  if (mode == 1) return launch_sweep_wm<W, 1>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+  return launch_sweep_wm<W, 2>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
 }
 
 hipError_t tsa_launch_sweeps(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
                              const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
-                             int nsweeps, unsigned long long* stats, hipStream_t st) {
+                             int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st) {
   switch (L.W) {
-    case 1: return launch_sweep_w<1>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
-    case 2: return launch_sweep_w<2>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
-    case 4: return launch_sweep_w<4>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
-    case 8: return launch_sweep_w<8>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
-    case 0: return launch_sweep_w<0>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, st);
+    case 1: return launch_sweep_w<1>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+    case 2: return launch_sweep_w<2>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+    case 4: return launch_sweep_w<4>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+    case 8: return launch_sweep_w<8>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+    case 0: return launch_sweep_w<0>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
     default: return hipErrorInvalidValue;
   }
 }
@@ -693,9 +751,9 @@ hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64
 
 hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int nchains, const TsaSelect& S, int level,
                             const uint64_t* rec, int chain_words, TsaTrackState* stt, TsaTraceRowD* trace,
-                            uint64_t* best_rec, hipStream_t stream) {
-  hipLaunchKernelGGL(k_track, dim3(1), dim3(1024), 0, stream, lc, sc, ns, nchains, S, level, rec, chain_words, stt, trace,
-                     best_rec);
+                            uint64_t* best_rec, TsaTrackPart* part, unsigned* done, hipStream_t stream) {
+  hipLaunchKernelGGL(k_track, dim3((nchains + 255) / 256), dim3(256), 0, stream, lc, sc, ns, nchains, S, level, rec,
+                     chain_words, stt, trace, best_rec, part, done);
   if (chain_words > TSA_TRACK_INLINE_WORDS) {
     const int n4 = chain_words / 2, nb = (n4 + 1023) / 1024;
     hipLaunchKernelGGL(k_snap, dim3(nb < 512 ? nb : 512), dim3(256), 0, stream, stt,

@@ -29,6 +29,7 @@
 // word stops, so every wave reaches the end of the kernel.  The last workgroup of a chain to finish resets
 // the chain's counters to zero for the next launch.
 #include "tsa_kernels.h"
+#include "tsa_fold.h"
 
 namespace {
 
@@ -543,42 +544,11 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
   }
   if (threadIdx.x >= 32) return;
   const TsaMathTabs T{s_exp2, fix, map};
-  const int l32 = (int)threadIdx.x;
-  float acc = -INFINITY;
-  int scl = 0;
-  for (int i = l32; i < nint; i += 32) {
-    acc = tsa_lse_f(acc, fc[i], T);
-    const int Z = fz[i];
-    scl = Z > scl ? Z : scl;
-  }
-  int scmax = scl;
-  for (int o = 16; o > 0; o >>= 1) {
-    acc = tsa_lse_f(acc, __shfl_xor(acc, o, 32), T);
-    const int u = __shfl_xor(scmax, o, 32);
-    scmax = scmax > u ? scmax : u;
-  }
-  int nsv = 0;
-  if (S)
-    for (int w = l32; w < NW; w += 32) nsv += __popcll(S[w]);
-  for (int o = 16; o > 0; o >>= 1) nsv += __shfl_xor(nsv, o, 32);
-  int scv = scmax > P.leaf_sc ? scmax : P.leaf_sc;
-  if (S && P.leaf_sc > scmax) {  // a leaf may be the largest tensor: masked leaf sizes
-    int ll = 0;
-    for (int i = l32; i < m; i += 32) {
-      int Z = 0;
-      for (int w = 0; w < NW; w++) Z += __popcll(leaf[(size_t)i * NW + w] & ~S[w]);
-      ll = ll > Z ? ll : Z;
-    }
-    for (int o = 16; o > 0; o >>= 1) {
-      const int u = __shfl_xor(ll, o, 32);
-      ll = ll > u ? ll : u;
-    }
-    scv = scmax > ll ? scmax : ll;
-  }
-  if (l32 == 0) {
-    lc[c] = acc;
-    sc[c] = scv;
-    ns[c] = nsv;
+  const TsaEvalOut e = tsa_fold32(P, fc, fz, S, leaf, NW, T, (int)threadIdx.x);
+  if (threadIdx.x == 0) {
+    lc[c] = e.lcost;
+    sc[c] = e.sc;
+    ns[c] = e.ns;
   }
 }
 

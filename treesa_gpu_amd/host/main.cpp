@@ -210,6 +210,7 @@ class Runner {
     cfg.v2_small_rank = ML.v2_small_rank;
     cfg.wide_waves = O.wpc > 0 ? (O.wpc + 1) / 2 : 0;  // --wpc counts 32-lane warps
     cfg.wide_wgs = O.wide_wgs;
+    cfg.fused_energy = O.eval_every == 1 ? 1 : 0;  // every level is evaluated: the sweep kernel evaluates too
   }
   ~Runner() {
     if (ctx) tsa_destroy(ctx);
