@@ -8,7 +8,9 @@
 //   1. scan (every workgroup, redundantly): the independent set of the phase -- unvisited nodes whose
 //      (priority, id) key beats their unvisited parent and internal children -- compacted in node order
 //      into the work list with wave ballots and a prefix over the 64-node groups;
-//   2. visits: work-list entry j goes to lane group j mod (K * groups per workgroup); the G lanes of a
+//   2. visits: workgroup k takes the k-th of K contiguous shares of the work list, and its waves take
+//      entries from that share 64/G at a time through an LDS counter (one entry per lane group), so
+//      that faster waves take more; the G lanes of a
 //      group load the five label sets D, P, O, K, M in 16-byte chunks (chunk t, t+G, ...), count with
 //      popcounts, sum the counters (packed two per 32-bit word) with xor shuffles inside the group, all
 //      lanes evaluate the same dE and Metropolis test, and on accept each lane stores its chunks of
@@ -148,7 +150,7 @@ __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restric
   extern __shared__ __align__(16) unsigned char tsa_wsm[];
   __shared__ float s_lse[64];
   __shared__ uint64_t s_exp2[32];
-  __shared__ int s_cnt, s_ok;
+  __shared__ int s_cnt, s_ok, s_next;
   const int NT = blockDim.x, nwv = NT >> 6, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m = P.m, nint = P.nint, nint4 = (nint + 3) & ~3, ngrp = (nint + 63) >> 6;
   const int NW = P.W, nch = NW >> 1;
@@ -182,8 +184,7 @@ __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restric
   constexpr int gpw = 64 / G;
   const int ngr = nwv * gpw;
   const int t = lane & (G - 1);
-  const int gid = k * ngr + wv * gpw + lane / G;
-  const int stride = K * ngr;
+  const int gsub = lane / G;  // lane group within the wave
   int np = 0, na = 0, nv = 0, nst = 0;
   unsigned nb = 0;
   bool ok = true;
@@ -258,7 +259,10 @@ __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restric
           if (gi < ngrp) offs[gi] = (uint32_t)(base + y - x);
           base += __shfl(y, 63, 64);
         }
-        if (lane == 0) s_cnt = base;
+        if (lane == 0) {
+          s_cnt = base;
+          s_next = 0;
+        }
       }
       __syncthreads();
       for (int gi = wv; gi < ngrp; gi += nwv) {
@@ -271,10 +275,16 @@ __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restric
       nst++;
       uint8_t* const out = COOP ? sy.out + ((size_t)c * 2 + (nb & 1u)) * (size_t)nint4 : outl;
 
-      // 2. visits
-      for (int j0 = 0; j0 < cnt; j0 += stride) {
-        const int j = j0 + gid;
-        if (j < cnt) {  // uniform within a lane group
+      // 2. visits: this workgroup's contiguous share [lo, hi) of the work list, handed out gpw entries at a
+      // time to whichever wave asks next (an LDS counter), so that waves that run ahead take more
+      const int lo = (int)(((long long)cnt * k) / K), hi = (int)(((long long)cnt * (k + 1)) / K);
+      for (;;) {
+        int j0 = 0;
+        if (lane == 0) j0 = atomicAdd(&s_next, gpw);
+        j0 = lo + __shfl(j0, 0, 64);
+        if (j0 >= hi) break;  // uniform within the wave
+        const int j = j0 + gsub;
+        if (j < hi) {  // uniform within a lane group
           const int v = wl[j];
           const uint32_t chv = ch[v - m];
           const int l = (int)(chv & 0xFFFFu), r = (int)(chv >> 16);
