@@ -54,11 +54,11 @@ CONFIGS = {
                betas=(1.0, 15.0), sc_target=20.0, scheme="indep", slicing=False,
                desc="random 3-SAT n=100 (m=426), spectral path starts, par order, 8192 chains x 200 sweeps, "
                     "beta 1->15, best-of-N"),
-    "c3": dict(cpu_chains=64, inst="sat70", trees=("sat70_greedy.tree", None), order="par", nchains=2048, levels=20, niters=10,
+    "c3": dict(cpu_chains=128, inst="sat70", trees=("sat70_greedy.tree", None), order="par", nchains=2048, levels=20, niters=10,
                betas=(0.01, 15.0), sc_target=24.0, scheme="pa", slicing=True,
                desc="random 3-SAT n=70 (m=298), greedy start, par order, slicing (1 slice move per sweep), "
                     "2048 chains x 200 sweeps, population annealing every 10 sweeps, beta 0.01->15"),
-    "c4": dict(cpu_chains=8, inst="reg3_2000", trees=("reg3_2000_spectral.tree", None), order="par", nchains=512, levels=100,
+    "c4": dict(cpu_chains=24, inst="reg3_2000", trees=("reg3_2000_spectral.tree", None), order="par", nchains=512, levels=100,
                niters=1, betas=(1.0, 15.0), sc_target=40.0, scheme="indep", slicing=False,
                desc="random 3-regular graph n=2000 (3000 labels, 47 words), spectral path starts, par order, "
                     "512 chains x 100 sweeps, beta 1->15"),
@@ -110,7 +110,7 @@ def algorithmic_bytes(st, W, nint, slicing=False, slice_steps=0):
     return b
 
 
-PROFILES = {"c2": "k_sweep_c2_sat100_par.md"}
+PROFILES = {"c2": "k_sweep_c2_sat100_par.md", "c4": "k_wide_c4_reg3_2000_par.md", "c5": "k_wide_c5_sq64_par.md"}
 
 
 def measured_traffic(cfgname):
@@ -170,6 +170,21 @@ def cpu_baseline(cfgname, C, inst, trees, betas, nsample):
                        f"({visits:.3e} visits, {secs:.1f} s)")
 
 
+def copy_calibration(cfgname, reps=10):
+    """reps population copies with identity ancestors through the C ABI (tsa_resample, kernel k_copy): every
+    launch reads and writes exactly nchains * chain_words * 8 bytes once, the reference point for the
+    FETCH_SIZE / WRITE_SIZE counters."""
+    C, inst, lay, trees, pop, cfg, betas, order = setup(cfgname)
+    with capi.Context(lay, inst.leaf(lay.W), inst.leaf_sc, cfg, C["nchains"]) as ctx:
+        ctx.upload(pop)
+        anc = np.arange(C["nchains"], dtype=np.int32)
+        for _ in range(reps):
+            ctx.resample(anc)
+    print(json.dumps({"config": cfgname, "kernel": "k_copy", "launches": reps,
+                      "bytes_read_per_launch": C["nchains"] * lay.chain_words * 8,
+                      "bytes_written_per_launch": C["nchains"] * lay.chain_words * 8}))
+
+
 def kernel_label(desc, order):
     """Name of the sweep kernel the binary ran, from its hip_kernel description."""
     o = "par" if order == capi.ORDER_PAR else "pre-order"
@@ -218,7 +233,12 @@ def main():
                          "bytes, which calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--wide-waves", type=int, default=0, help="wide kernel: waves per workgroup (0: automatic)")
     ap.add_argument("--wide-wgs", type=int, default=0, help="wide kernel: workgroups per chain (0: automatic)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run identity population copies of the workload (counter calibration)")
     a = ap.parse_args()
+    if a.copy_calibration:
+        copy_calibration(a.config)
+        return
     if a.cpu_port_worker:
         cpu_port_worker(a.cpu_port_worker, a.cpu_chains or 1)
         return
