@@ -77,9 +77,10 @@ typedef struct tsa_config_t {
   int32_t v2_small_rank;
   /* wide kernel plan (0 = automatic): waves per workgroup (1..16), workgroups per chain (1..16) */
   int32_t wide_waves, wide_wgs;
-  /* 1: every tsa_sweeps also leaves the energies of the swept population ready (each chain is evaluated by
-   * the sweep kernel while it is still staged), so that tsa_energy / tsa_track launch no energy kernel;
-   * for callers that evaluate after every level */
+  /* 1: every tsa_sweeps on the register-width path also leaves the energies of the swept population ready
+   * (each chain is evaluated by the sweep kernel while it is still staged in LDS), so that tsa_energy /
+   * tsa_track launch no energy kernel; for callers that evaluate after every level.  The wide path keeps a
+   * node-cost cache instead and its energy call only folds it. */
   int32_t fused_energy;
 } tsa_config_t;
 

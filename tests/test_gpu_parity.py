@@ -176,6 +176,32 @@ def test_wide_cached_energies_every_level(mode, gm):
         assert np.array_equal(ctx.download(), opop)
 
 
+# Fused energies (every sweep launch also leaves the energies of the swept population): after every level
+# tsa_energy returns exactly the oracle's evaluation, on the LDS, HBM and wide kernels and both wide plans.
+@pytest.mark.parametrize("inst,kernel,wgs,mode", [("sat100", capi.KERNEL_LDS, 0, "tc"), ("sat60", capi.KERNEL_GLOBAL, 0, "h100"),
+                                                  ("sq46", capi.KERNEL_WIDE, 0, "tc"), ("sq46", capi.KERNEL_WIDE, 1, "gpu"),
+                                                  ("grid24", capi.KERNEL_WIDE, 3, "h100")])
+def test_fused_energies_every_level(inst, kernel, wgs, mode):
+    case = Case(inst, "par", mode, kernel=kernel, nchains=24, wide=kernel == capi.KERNEL_WIDE)
+    case.cfg = capi.make_config(mode=mode, sc_target=common.CHECK_SC_TARGET, seed=common.CHECK_SEED, kernel=kernel,
+                                wide_wgs=wgs, fused_energy=True)
+    opop = case.pop0.copy()
+    print(f"[gpu] fused energies {inst} kernel={kernel} wgs={wgs} mode={mode}", flush=True)
+    with capi.Context(case.lay, case.leaf, case.leaf_sc, case.cfg, case.nchains) as ctx:
+        ctx.upload(case.pop0)
+        for lev, b in enumerate([0.3, 1.0, 3.0, 10.0]):
+            ctx.sweeps(case.ord, b, 2 * lev, 2)
+            case.O.sweeps(case.P, case.lay, opop, case.ord, b, 2 * lev, 2)
+            glc, gsc, gns = ctx.energy()
+            olc, osc, ons = case.O.energy(case.P, case.lay, opop)
+            assert np.array_equal(glc.view(np.uint32), olc.view(np.uint32)), f"level {lev}: lcost"
+            assert np.array_equal(gsc, osc) and np.array_equal(gns, ons), f"level {lev}: sc / ns"
+        assert np.array_equal(ctx.download(), opop)
+        desc = ctx.describe()
+    if kernel == capi.KERNEL_WIDE:
+        assert desc.startswith("wide") and "fold_stage=" in desc, desc
+
+
 def test_resample_copies_ancestors():
     case = Case("sat40", "par", "tc")
     rng = np.random.default_rng(3)

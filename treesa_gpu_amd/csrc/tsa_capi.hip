@@ -361,8 +361,9 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   }
   char kb[200];
   if (c->wide.on)
-    snprintf(kb, sizeof kb, "wide W=%d G=%d waves/block=%d blocks/chain=%d lds_bytes/block=%d energy_blocks/chain=%d",
-             lay->W, c->wide.G, c->wide.nt / 64, c->wide.K, c->wide.smem, c->wide.eK);
+    snprintf(kb, sizeof kb,
+             "wide W=%d G=%d waves/block=%d blocks/chain=%d lds_bytes/block=%d energy_blocks/chain=%d fold_stage=%d",
+             lay->W, c->wide.G, c->wide.nt / 64, c->wide.K, c->wide.smem, c->wide.eK, c->wide.fold_stage);
   else
     snprintf(kb, sizeof kb, "%s W=%d waves/block=%d lds_bytes/wave=%d", use_lds ? "lds" : "global",
              use_lds ? c->Wt : lay->W, c->L.wpb, c->L.lds_words * 8);
@@ -479,6 +480,8 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
   TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
   ctx->energy_fresh = false;
   if (ctx->wide.on && order == TSA_ORDER_PAR) {
+    // energies stay a separate fold of the node-cost cache: every chain ends its sweep at about the same
+    // time, so folding inside the sweep kernel would only lengthen it
     TSA_HIP(ctx, tsa_launch_wide(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains, beta,
                                  sweep0, nsweeps, ctx->d_stats, ctx->wsync, ctx->st));
   } else {

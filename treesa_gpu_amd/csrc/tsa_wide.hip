@@ -142,6 +142,51 @@ __device__ __forceinline__ long long wide_wave_sum(long long x) {
   return x;
 }
 
+// The fold of one chain's cached node costs by the calling workgroup: with stage >= 1 the costs (and with
+// stage 2 the log2f summary bitmap) are first copied into the workgroup's LDS at lds (vector copies, all
+// loads in flight at once: the fold reads them in a serial chain per lane); lanes 0..31 then fold in the
+// reference's order and lane 0 writes lc / sc / ns of chain c.  Every thread of the workgroup calls it.
+__device__ void wide_fold(const TsaKParams& P, int c, const float* cst, const uint16_t* zz, const uint64_t* S,
+                          const uint64_t* leaf, const uint32_t* fix, const uint64_t* s_exp2, int stage,
+                          unsigned char* lds, float* lc, int* sc, int* ns) {
+  const int nint4 = (P.nint + 3) & ~3;
+  const uint32_t* const gmap = fix + TSA_LOG2FIX_WORDS;
+  const float* fc = cst;
+  const uint16_t* fz = zz;
+  const uint32_t* map = gmap;
+  if (stage) {
+    float* const scst = reinterpret_cast<float*>(lds);
+    uint16_t* const szz = reinterpret_cast<uint16_t*>(lds + (size_t)nint4 * 4);
+    const int n4 = nint4 / 4;
+#pragma unroll 4
+    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
+      const float4 cv = reinterpret_cast<const float4*>(cst)[i];
+      const uint2 zv = reinterpret_cast<const uint2*>(zz)[i];
+      reinterpret_cast<float4*>(scst)[i] = cv;
+      reinterpret_cast<uint2*>(szz)[i] = zv;
+    }
+    if (stage == 2) {
+      uint4* const smap = reinterpret_cast<uint4*>(lds + (((size_t)nint4 * 6 + 15) & ~(size_t)15));
+      const uint4* src = reinterpret_cast<const uint4*>(gmap);
+#pragma unroll 16
+      for (int i = threadIdx.x; i < (int)(TSA_LOG2MAP_WORDS / 4); i += blockDim.x) smap[i] = src[i];
+      map = reinterpret_cast<const uint32_t*>(smap);
+    }
+    __syncthreads();
+    fc = scst;
+    fz = szz;
+  }
+  if (threadIdx.x < 32) {
+    const TsaMathTabs T{s_exp2, fix, map};
+    const TsaEvalOut e = tsa_fold32(P, fc, fz, S, leaf, P.W, T, (int)threadIdx.x);
+    if (threadIdx.x == 0) {
+      lc[c] = e.lcost;
+      sc[c] = e.sc;
+      ns[c] = e.ns;
+    }
+  }
+}
+
 template <int G, int MODE, bool COOP>
 __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restrict__ rec,
                                                const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
@@ -525,41 +570,7 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
     if (!s_last) return;
   }
 
-  // fold: the costs are read in a serial chain per lane, so they are first staged in LDS
-  const float* fc = cst;
-  const uint16_t* fz = zz;
-  const uint32_t* map = gmap;
-  if (stage) {
-    // vector copies, unrolled so that every thread has all its loads in flight at once
-    float* const scst = reinterpret_cast<float*>(s_dyn);
-    uint16_t* const szz = reinterpret_cast<uint16_t*>(s_dyn + (size_t)nint4 * 4);
-    const int n4 = nint4 / 4;
-#pragma unroll 4
-    for (int i = threadIdx.x; i < n4; i += blockDim.x) {
-      const float4 cv = reinterpret_cast<const float4*>(cst)[i];
-      const uint2 zv = reinterpret_cast<const uint2*>(zz)[i];
-      reinterpret_cast<float4*>(scst)[i] = cv;
-      reinterpret_cast<uint2*>(szz)[i] = zv;
-    }
-    if (stage == 2) {
-      uint4* const smap = reinterpret_cast<uint4*>(s_dyn + (((size_t)nint4 * 6 + 15) & ~(size_t)15));
-      const uint4* src = reinterpret_cast<const uint4*>(gmap);
-#pragma unroll 16
-      for (int i = threadIdx.x; i < (int)(TSA_LOG2MAP_WORDS / 4); i += blockDim.x) smap[i] = src[i];
-      map = reinterpret_cast<const uint32_t*>(smap);
-    }
-    __syncthreads();
-    fc = scst;
-    fz = szz;
-  }
-  if (threadIdx.x >= 32) return;
-  const TsaMathTabs T{s_exp2, fix, map};
-  const TsaEvalOut e = tsa_fold32(P, fc, fz, S, leaf, NW, T, (int)threadIdx.x);
-  if (threadIdx.x == 0) {
-    lc[c] = e.lcost;
-    sc[c] = e.sc;
-    ns[c] = e.ns;
-  }
+  wide_fold(P, c, cst, zz, S, leaf, fix, s_exp2, stage, s_dyn, lc, sc, ns);
 }
 
 template <int G, int MODE>
@@ -609,34 +620,44 @@ hipError_t launch_wcost_g(const TsaWide& X, int mode, const TsaKParams& P, const
   return launch_wcost_gm<G, 2>(X, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
 }
 
-// Largest number of co-resident workgroups per CU of the cooperative sweep kernel over the three modes.
+// Largest number of co-resident workgroups per CU of the cooperative sweep kernel over the three modes, at
+// smem bytes of dynamic LDS.  Raises the dynamic-LDS cap of every sweep and energy instantiation of this G to
+// lds_cap first (the largest any context asks for).
 template <int G>
-hipError_t wide_occupancy(int nt, int smem, int fold_smem, int* per_cu) {
+hipError_t wide_occupancy(int nt, int smem, int lds_cap, int* per_cu) {
   const void* fns[3] = {reinterpret_cast<const void*>(&k_wide<G, 0, true>),
                         reinterpret_cast<const void*>(&k_wide<G, 1, true>),
                         reinterpret_cast<const void*>(&k_wide<G, 2, true>)};
-  const void* fns1[3] = {reinterpret_cast<const void*>(&k_wide<G, 0, false>),
-                         reinterpret_cast<const void*>(&k_wide<G, 1, false>),
-                         reinterpret_cast<const void*>(&k_wide<G, 2, false>)};
-  const void* fold[3] = {reinterpret_cast<const void*>(&k_wcost<G, 0>), reinterpret_cast<const void*>(&k_wcost<G, 1>),
-                         reinterpret_cast<const void*>(&k_wcost<G, 2>)};
+  const void* others[6] = {reinterpret_cast<const void*>(&k_wide<G, 0, false>),
+                           reinterpret_cast<const void*>(&k_wide<G, 1, false>),
+                           reinterpret_cast<const void*>(&k_wide<G, 2, false>),
+                           reinterpret_cast<const void*>(&k_wcost<G, 0>),
+                           reinterpret_cast<const void*>(&k_wcost<G, 1>),
+                           reinterpret_cast<const void*>(&k_wcost<G, 2>)};
+  for (int i = 0; i < 9; i++) {
+    const hipError_t e = hipFuncSetAttribute(i < 3 ? fns[i] : others[i - 3],
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds_cap);
+    if (e != hipSuccess) return e;
+  }
   int best = 1 << 30;
   for (int i = 0; i < 3; i++) {
-    hipError_t ef = hipFuncSetAttribute(fold[i], hipFuncAttributeMaxDynamicSharedMemorySize, fold_smem);
-    if (ef != hipSuccess) return ef;
-    if (smem > 65536) {
-      hipError_t e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-      if (e != hipSuccess) return e;
-      e = hipFuncSetAttribute(fns1[i], hipFuncAttributeMaxDynamicSharedMemorySize, smem);
-      if (e != hipSuccess) return e;
-    }
     int nb = 0;
-    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fns[i], nt, (size_t)smem);
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fns[i], nt, (size_t)smem);
     if (e != hipSuccess) return e;
     best = nb < best ? nb : best;
   }
   *per_cu = best;
   return hipSuccess;
+}
+
+hipError_t wide_occupancy_g(int G, int nt, int smem, int lds_cap, int* per_cu) {
+  switch (G) {
+    case 4: return wide_occupancy<4>(nt, smem, lds_cap, per_cu);
+    case 8: return wide_occupancy<8>(nt, smem, lds_cap, per_cu);
+    case 16: return wide_occupancy<16>(nt, smem, lds_cap, per_cu);
+    case 32: return wide_occupancy<32>(nt, smem, lds_cap, per_cu);
+    default: return wide_occupancy<64>(nt, smem, lds_cap, per_cu);
+  }
 }
 
 }  // namespace
@@ -667,13 +688,7 @@ hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int w
   X.fold_smem = nint4 * 6 <= fold_budget ? nint4 * 6 : 0;
   X.fold_smem_map = ((nint4 * 6 + 15) & ~15) + (int)TSA_LOG2MAP_WORDS * 4;
   X.fold_stage = X.fold_smem == 0 ? 0 : (X.fold_smem_map <= fold_budget ? 2 : 1);
-  switch (G) {  // the fold's LDS cap is set to the largest any context may ask for
-    case 4: e = wide_occupancy<4>(X.nt, L1.bytes, fold_budget, &per_cu); break;
-    case 8: e = wide_occupancy<8>(X.nt, L1.bytes, fold_budget, &per_cu); break;
-    case 16: e = wide_occupancy<16>(X.nt, L1.bytes, fold_budget, &per_cu); break;
-    case 32: e = wide_occupancy<32>(X.nt, L1.bytes, fold_budget, &per_cu); break;
-    default: e = wide_occupancy<64>(X.nt, L1.bytes, fold_budget, &per_cu); break;
-  }
+  e = wide_occupancy_g(G, X.nt, L1.bytes, fold_budget, &per_cu);
   if (e != hipSuccess) return e;
   if (per_cu < 1) return hipErrorInvalidValue;
   const int cap = per_cu * ncu;
