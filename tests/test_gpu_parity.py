@@ -202,6 +202,16 @@ def test_fused_energies_every_level(inst, kernel, wgs, mode):
         assert desc.startswith("wide") and "fold_stage=" in desc, desc
 
 
+@pytest.mark.parametrize("inst,nchains", [("sq46", 48), ("reg3_2000", 512), ("sq64", 72), ("grid45", 8)])
+def test_automatic_plan_takes_the_wide_kernel(inst, nchains):
+    # runtime-width chains without slicing must get the wide kernel from the automatic choice (a failed plan
+    # would fall back to the one-wave HBM kernel, correct but slow)
+    case = Case(inst, "par", "tc", init=None, nchains=nchains)
+    with capi.Context(case.lay, case.leaf, case.leaf_sc, case.cfg, case.nchains) as ctx:
+        desc = ctx.describe()
+    assert case.lay.runtime_width == 1 and desc.startswith("wide"), desc
+
+
 def test_resample_copies_ancestors():
     case = Case("sat40", "par", "tc")
     rng = np.random.default_rng(3)

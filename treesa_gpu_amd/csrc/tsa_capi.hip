@@ -349,6 +349,7 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
     hipError_t we = hipErrorInvalidValue;
     if (lay->runtime_width && !cfg->slicing) we = tsa_wide_plan(c->P, nchains, cfg->wide_waves, cfg->wide_wgs, &c->wide);
     if (we != hipSuccess) {
+      (void)hipGetLastError();  // clear the runtime's last error: the context goes on without the wide path
       c->wide = TsaWide{};
       if (cfg->kernel == TSA_KERNEL_WIDE || cfg->wide_waves > 0 || cfg->wide_wgs > 0) {
         free_ctx(c);

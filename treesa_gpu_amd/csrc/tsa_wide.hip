@@ -684,7 +684,8 @@ hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int w
   if (L1.bytes > lds_max) return hipErrorInvalidValue;
   int per_cu = 0;
   // the fold stages a chain's node costs (6 B per node) and, when it also fits, the log2f summary bitmap
-  const int nint4 = (P.nint + 3) & ~3, fold_budget = lds_max - 1024;
+  // dynamic LDS cap: the device maximum less room for the kernels' static LDS (under 1 KB today)
+  const int nint4 = (P.nint + 3) & ~3, fold_budget = lds_max - 4096;
   X.fold_smem = nint4 * 6 <= fold_budget ? nint4 * 6 : 0;
   X.fold_smem_map = ((nint4 * 6 + 15) & ~15) + (int)TSA_LOG2MAP_WORDS * 4;
   X.fold_stage = X.fold_smem == 0 ? 0 : (X.fold_smem_map <= fold_budget ? 2 : 1);
