@@ -98,24 +98,35 @@ def setup(cfgname):
     return C, inst, lay, trees, pop, cfg, betas, order
 
 
-def algorithmic_bytes(st, W, nint, slicing=False, slice_steps=0):
+def algorithmic_bytes(st, W, nint, slicing=False, slice_steps=0, chunks=None):
     """From the sweep kernel's counters: a proposal reads 5 label sets (+ S when slicing) and 8 B of children,
     an accept writes one set and 8 B, a visit without a rule reads 4 B; a slice step evaluates the whole chain
     once plus once per slice proposal (3 sets + 4 B per node, + S) and scans the internal sets once per slice
-    proposal."""
+    proposal.  With chunk summaries (chunks = the kernel's counts of 16-byte chunk positions loaded and
+    written) a proposal reads only its union's chunks of the 5 sets and an accept writes only those of P."""
     prop, acc, visits, sprop = st[0], st[1], st[3], st[4]
+    if chunks is not None and chunks[0] > 0:
+        return chunks[0] * 80 + prop * 8 + chunks[1] * 16 + acc * 8 + (visits - prop) * 4
     b = prop * (40 * W + 8 + (8 * W if slicing else 0)) + acc * (8 * W + 8) + (visits - prop) * 4
     evals = slice_steps + sprop
     b += evals * (24 * W * nint + 4 * nint + 8 * W) + sprop * 8 * W * nint
     return b
 
 
-PROFILES = {"c2": "k_sweep_c2_sat100_par.md", "c4": "k_wide_c4_reg3_2000_par.md", "c5": "k_wide_c5_sq64_par.md"}
+# committed rocprofv3 summaries by (workload, label-set path: "dense" streaming or chunk "sums")
+PROFILES = {("c2", "dense"): "k_sweep_c2_sat100_par.md", ("c4", "dense"): "k_wide_c4_reg3_2000_par.md",
+            ("c5", "dense"): "k_wide_c5_sq64_par.md", ("c5", "sums"): "k_wide_sums_c5_sq64_par.md"}
 
 
-def measured_traffic(cfgname):
-    """HBM bytes per sweep-kernel dispatch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary."""
-    f = PROFILES.get(cfgname)
+def label_path(desc):
+    """"sums" when the sweep kernel read label sets through chunk summaries, else "dense"."""
+    return "sums" if desc.startswith("wide") and " sums=0 " not in desc else "dense"
+
+
+def measured_traffic(cfgname, path="dense"):
+    """HBM bytes per sweep-kernel dispatch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of the
+    same workload and path (None when there is none)."""
+    f = PROFILES.get((cfgname, path))
     if not f or not os.path.exists(os.path.join(ROOT, "profiles", f)):
         return None
     with open(os.path.join(ROOT, "profiles", f)) as fh:
@@ -189,7 +200,8 @@ def kernel_label(desc, order):
     """Name of the sweep kernel the binary ran, from its hip_kernel description."""
     o = "par" if order == capi.ORDER_PAR else "pre-order"
     if desc.startswith("wide") and order == capi.ORDER_PAR:
-        return "k_wide par, label sets in HBM, " + desc.split(" ", 1)[1]
+        how = "nonzero 16-byte chunks only (chunk summaries)" if " sums=0 " not in desc else "dense streaming"
+        return f"k_wide par, label sets in HBM, {how}, " + desc.split(" ", 1)[1]
     return f"k_sweep {o}, " + ("chain in LDS" if desc.startswith("lds") else "chain in HBM")
 
 
@@ -233,6 +245,9 @@ def main():
                          "bytes, which calibrates the FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--wide-waves", type=int, default=0, help="wide kernel: waves per workgroup (0: automatic)")
     ap.add_argument("--wide-wgs", type=int, default=0, help="wide kernel: workgroups per chain (0: automatic)")
+    ap.add_argument("--wide-lanes", type=int, default=0, help="wide kernel: lanes per proposal (0: automatic)")
+    ap.add_argument("--sums", default="auto", choices=("auto", "on", "off"),
+                    help="wide kernel: chunk summaries (the binary's --sums / --no-sum; auto: on from 64 words)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run identity population copies of the workload (counter calibration)")
     a = ap.parse_args()
@@ -249,13 +264,16 @@ def main():
     steps = a.steps or C["levels"]
     nchains = C["nchains"]
     extra = (["--wpc", str(2 * a.wide_waves)] if a.wide_waves else []) + \
-        (["--wide-wgs", str(a.wide_wgs)] if a.wide_wgs else [])
+        (["--wide-wgs", str(a.wide_wgs)] if a.wide_wgs else []) + \
+        (["--wide-lanes", str(a.wide_lanes)] if a.wide_lanes else []) + \
+        {"auto": [], "on": ["--sums"], "off": ["--no-sum"]}[a.sums]
     r = run_binary(C, trees, betas, steps, a.warmup, a.scheme, extra)
     visits = steps * C["niters"] * nchains * (inst.m - 1)
     assert r["node_visits"] == visits, (r["node_visits"], visits)
     st = [r["proposals"], r["accepts"], r["warp_steps"], r["node_visits"], r["slice_proposals"]]
     slice_steps = steps * C["niters"] * nchains if C["slicing"] else 0
-    B = algorithmic_bytes(st, lay.W, inst.m - 1, C["slicing"], slice_steps) / steps
+    B = algorithmic_bytes(st, lay.W, inst.m - 1, C["slicing"], slice_steps,
+                          (r.get("sum_chunks", 0), r.get("sum_xchunks", 0))) / steps
     dur = r["kernel_s"] / steps
     wall = r["t_anneal"]
     res = {
@@ -271,7 +289,7 @@ def main():
         "proposals": r["proposals"], "accepts": r["accepts"], "phases": r["warp_steps"],
         "best_tc": r["tc"], "best_sc": r["sc"], "wall_s": wall,
         "roofline": {"bound": "hbm", "achieved": B / dur / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": B / dur / 1e9 / HBM_PEAK_GBS, "traffic": measured_traffic(a.config),
+                     "frac": B / dur / 1e9 / HBM_PEAK_GBS, "traffic": measured_traffic(a.config, label_path(r.get("hip_kernel") or "")),
                      "kernel": kernel_label(r.get("hip_kernel") or "", order),
                      "bytes_per_launch": B, "avg_launch_ms": dur * 1e3},
     }

@@ -82,6 +82,12 @@ typedef struct tsa_config_t {
    * tsa_track launch no energy kernel; for callers that evaluate after every level.  The wide path keeps a
    * node-cost cache instead and its energy call only folds it. */
   int32_t fused_energy;
+  /* chunk summaries of the wide kernel (the reference's --sums / --no-sum, csrc/treesa_gpu.cu:1444-1448):
+   * 0 = automatic (on from 64 words per label set, 4096 labels), 1 = on, -1 = off.  With summaries a
+   * visit loads only the 16-byte chunks that are nonzero in one of its label sets; results do not change */
+  int32_t sums;
+  /* wide kernel: lanes per proposal (4, 8, 16, 32 or 64; 0 = automatic) */
+  int32_t wide_lanes;
 } tsa_config_t;
 
 typedef struct tsa_ctx tsa_ctx;
@@ -132,6 +138,12 @@ int tsa_set_mode(tsa_ctx* ctx, int32_t mode);
  * visits, slice proposals, slice accepts, busy lanes.  Replaces the d_stats copy,
  * csrc/treesa_gpu.cu:1880-1881. */
 int tsa_stats(tsa_ctx* ctx, uint64_t out[7]);
+
+/* Counters of the wide kernel with chunk summaries since creation: out[0] = 16-byte chunk positions a
+ * proposal loaded (one per set bit of the union of its summaries; each is read from the five label sets),
+ * out[1] = chunk positions written by accepted rotations.  Both stay 0 without summaries.  No counterpart in
+ * the reference: it is the measured byte count of the summary path's roofline. */
+int tsa_chunk_stats(tsa_ctx* ctx, uint64_t out[2]);
 
 /* Device-side best tracking for runs without population steps (scheme indep): after a level's sweeps,
  * tsa_track enqueues the energy kernel and a selection kernel that scores every chain (lower is better,

@@ -32,8 +32,8 @@ int main(int argc, char** argv) {
   std::vector<uint32_t> fix(TSA_LOG2FIX_WORDS + TSA_LOG2MAP_WORDS, 0u);
 #pragma omp parallel for reduction(+ : far, fixed) schedule(static)
   for (long long k = 0; k <= (1ll << 23); k++) {
-    const float y = tsa_ffrom(0x3f800000u + (uint32_t)k);  // [1, 2], k = 2^23 is 2.0
-    const int32_t d = (int32_t)(tsa_fbits(log2f(y)) - tsa_fbits(tsa_log2f_core(y)));
+    const float y = tsa_ffrom(0x3f800000u + (uint32_t)k);  // [1, 2], k = 2^23 is 2.0 (log2f_12 returns 1)
+    const int32_t d = (int32_t)(tsa_fbits(log2f(y)) - tsa_fbits(k == (1ll << 23) ? 1.0f : tsa_log2f_core(y)));
     if (d != 0) fixed++;
     if (d > 1 || d < -1 || (k == (1ll << 23) && d != 0)) far++;
   }
@@ -50,13 +50,14 @@ int main(int argc, char** argv) {
   // pairs on a grid of maxima and differences, dense around the shortcut's threshold d = -24
   uint64_t tab[32];
   for (int i = 0; i < 32; i++) tab[i] = tsa_exp2_tab_h[i];
-  const TsaMathTabs T{tab, fix.data(), fix.data() + TSA_LOG2FIX_WORDS};
-  const TsaMathTabs T0{tab, fix.data(), nullptr};
+  const TsaMathTabs T{tab, fix.data(), fix.data() + TSA_LOG2FIX_WORDS, tsa_log2_tab_h};
+  const TsaMathTabs T0{tab, fix.data(), nullptr, tsa_log2_tab_h};
   long long bad_lse = 0;
 #pragma omp parallel for reduction(+ : bad_lse) schedule(static)
   for (int ia = 0; ia < 4096; ia++) {
     uint32_t st = 0x9e3779b9u * (uint32_t)(ia + 1);
-    const float a = ia == 0 ? -0.0f : ia < 2048 ? (float)(ia % 200) - 20.0f
+    const float a = ia == 0 ? -0.0f : ia == 1 ? INFINITY : ia == 2 ? -INFINITY : ia == 3 ? NAN
+                  : ia < 2048 ? (float)(ia % 200) - 20.0f
                                                  : tsa_ffrom(0x3f000000u + (uint32_t)ia * 4093u) * 97.0f;
     for (int j = 0; j < 4096; j++) {
       st = st * 1664525u + 1013904223u;
@@ -64,10 +65,16 @@ int main(int argc, char** argv) {
       if (j < 1024) d = -24.0f + (float)(j - 512) * 0x1p-10f;        // around the threshold
       else if (j < 1040) d = tsa_ffrom(tsa_fbits(-24.0f) + (uint32_t)(j - 1032));  // neighbours of -24
       else if (j == 1040) d = -INFINITY;
+      else if (j == 1041) d = NAN;
+      else if (j == 1042) d = 0.0f;
+      else if (j == 1043) d = -0.0f;
       else d = -40.0f * (float)(st >> 8) * 0x1p-24f;
       const float b = a + d;
-      const float r0 = lse_libm(a, b), r1 = tsa_lse_f(a, b, T), r2 = tsa_lse_f(b, a, T0);
-      if (tsa_fbits(r0) != tsa_fbits(r1) || tsa_fbits(r0) != tsa_fbits(r2)) bad_lse++;
+      // both argument orders (with a NaN operand the formula is not symmetric), the second without the
+      // bitmap; NaN results compare as NaN (payloads are not specified)
+      const float r0 = lse_libm(a, b), r1 = tsa_lse_f(a, b, T), q0 = lse_libm(b, a), q1 = tsa_lse_f(b, a, T0);
+      if (std::isnan(r0) ? !std::isnan(r1) : tsa_fbits(r0) != tsa_fbits(r1)) bad_lse++;
+      if (std::isnan(q0) ? !std::isnan(q1) : tsa_fbits(q0) != tsa_fbits(q1)) bad_lse++;
     }
   }
   printf("%lld %lld %lld %lld %lld\n", bad_e, bad_2, far, fixed, bad_lse);

@@ -29,7 +29,7 @@ def leaf_sets(m, ixs, W):
 class Case:
     def __init__(self, inst, order, mode, init="greedy", random_slices=0, par_follow=False, par_band=0, slicing=False,
                  slice_moves=1, slice_every=1, nchains=NCHAINS, kernel=capi.KERNEL_AUTO, wide=False, seed=None,
-                 sc_target=None, wide_waves=0, wide_wgs=0):
+                 sc_target=None, wide_waves=0, wide_wgs=0, sums=0, lanes=0):
         self.inst, self.order = inst, order
         m, nlab, ixs, iy = common.load_instance(inst)
         self.m, self.nlab, self.ixs = m, nlab, ixs
@@ -43,7 +43,7 @@ class Case:
         self.cfg = capi.make_config(mode=mode, sc_target=common.CHECK_SC_TARGET if sc_target is None else sc_target,
                                     seed=seed, slicing=sl, slice_moves=slice_moves if slicing else 0,
                                     slice_every=slice_every, par_follow=par_follow, par_band=par_band, kernel=kernel,
-                                    wide_waves=wide_waves, wide_wgs=wide_wgs)
+                                    wide_waves=wide_waves, wide_wgs=wide_wgs, sums=sums, wide_lanes=lanes)
         self.leaf_sc = max(len(x) for x in ixs)
         self.P = orc.params_from_config(self.cfg, self.leaf_sc, nlab)
         self.leaf = leaf_sets(m, ixs, self.lay.W)
@@ -53,7 +53,7 @@ class Case:
     def run_gpu(self, betas=common.CHECK_BETAS, niters=common.CHECK_NITERS):
         print(f"[gpu] {self.inst} {self.order} mode={self.cfg.mode} slicing={self.cfg.slicing} "
               f"kernel={self.cfg.kernel} W={self.lay.W} chains={self.nchains} wide_waves={self.cfg.wide_waves} "
-              f"wide_wgs={self.cfg.wide_wgs}", flush=True)
+              f"wide_wgs={self.cfg.wide_wgs} sums={self.cfg.sums} lanes={self.cfg.wide_lanes}", flush=True)
         with capi.Context(self.lay, self.leaf, self.leaf_sc, self.cfg, self.nchains) as ctx:
             ctx.upload(self.pop0)
             for lev, b in enumerate(betas):
@@ -122,31 +122,79 @@ def test_slice_moves_match_oracle_mirror(inst, order, mode, moves, every):
 
 
 # The wide kernel (runtime-width chains, par order): every plan -- one workgroup per chain, or K co-resident
-# workgroups per chain with chain barriers -- gives the oracle's phase-by-phase sweep bit for bit, and so does
-# its two-step energy kernel.
-@pytest.mark.parametrize("inst,mode,waves,wgs,follow,band", [
-    ("sq46", "tc", 0, 0, False, 0), ("sq46", "tc", 16, 1, False, 0), ("sq46", "tc", 4, 1, True, 0),
-    ("sq46", "gpu", 8, 3, False, 3), ("sq46", "h100", 16, 5, True, 0), ("grid24", "tc", 8, 2, False, 0),
-    ("grid24", "gpu", 4, 1, True, 4), ("grid45", "tc", 16, 4, False, 0), ("lat14", "tc", 2, 2, False, 0)])
-def test_wide_kernel_matches_oracle(inst, mode, waves, wgs, follow, band):
+# workgroups per chain with chain barriers; dense streaming (sums -1) or chunk summaries (sums 1) with 1, 2,
+# 4, 8 or 16 lanes per proposal -- gives the oracle's phase-by-phase sweep bit for bit, and so does its
+# two-step energy kernel.
+@pytest.mark.parametrize("inst,mode,waves,wgs,follow,band,sums,lanes", [
+    ("sq46", "tc", 0, 0, False, 0, -1, 0), ("sq46", "tc", 16, 1, False, 0, -1, 0), ("sq46", "tc", 4, 1, True, 0, -1, 0),
+    ("sq46", "gpu", 8, 3, False, 3, -1, 0), ("sq46", "h100", 16, 5, True, 0, -1, 0), ("grid24", "tc", 8, 2, False, 0, -1, 0),
+    ("grid24", "gpu", 4, 1, True, 4, -1, 0), ("grid45", "tc", 16, 4, False, 0, -1, 0), ("lat14", "tc", 2, 2, False, 0, -1, 0),
+    ("sq46", "tc", 0, 0, False, 0, 0, 0), ("sq46", "tc", 8, 1, False, 0, 1, 4), ("sq46", "tc", 4, 3, True, 0, 1, 16),
+    ("sq46", "gpu", 8, 2, False, 3, 1, 8), ("sq46", "h100", 2, 5, True, 0, 1, 4), ("grid24", "tc", 8, 2, False, 0, 1, 8),
+    ("grid45", "tc", 8, 4, False, 0, 1, 16), ("lat14", "tc", 2, 2, False, 0, 1, 4), ("lat14", "gpu", 8, 1, True, 2, 1, 8),
+    ("sq46", "tc", 8, 2, False, 0, 1, 1), ("sq46", "gpu", 4, 1, True, 0, 1, 2), ("grid45", "h100", 8, 3, False, 2, 1, 1)])
+def test_wide_kernel_matches_oracle(inst, mode, waves, wgs, follow, band, sums, lanes):
     case = Case(inst, "par", mode, wide=True, kernel=capi.KERNEL_WIDE, wide_waves=waves, wide_wgs=wgs,
-                par_follow=follow, par_band=band)
+                par_follow=follow, par_band=band, sums=sums, lanes=lanes)
     gpu = case.run_gpu()
     assert gpu[3].startswith("wide"), gpu[3]
     if wgs:
         assert f"blocks/chain={wgs}" in gpu[3], gpu[3]
+    if sums:
+        assert (" sums=0 " in gpu[3]) == (sums < 0), gpu[3]
+    if lanes:
+        assert f" G={lanes} " in gpu[3], gpu[3]
     compare(case, gpu, case.run_oracle())
 
 
-@pytest.mark.parametrize("inst,init,nchains", [("reg3_2000", None, 6), ("sq64", None, 4)])
-def test_wide_kernel_at_benchmark_widths(inst, init, nchains):
-    # the 3-regular n=2000 graph (48 words) and the 64 x 64 lattice (126 words) from random trees,
-    # three levels of one sweep
-    case = Case(inst, "par", "tc", init=init, nchains=nchains, kernel=capi.KERNEL_WIDE, sc_target=40)
+@pytest.mark.parametrize("inst,init,nchains,sums,lanes", [("reg3_2000", None, 6, 0, 0), ("sq64", None, 4, -1, 0),
+                                                          ("sq64", None, 4, 0, 0), ("sq64", None, 4, 1, 4),
+                                                          ("reg3_2000", None, 6, 1, 8), ("sq64", None, 4, 1, 1),
+                                                          ("sq64", None, 4, 1, 2)])
+def test_wide_kernel_at_benchmark_widths(inst, init, nchains, sums, lanes):
+    # the 3-regular n=2000 graph (48 words) and the 64 x 64 lattice (126 words) from random trees, three
+    # levels of one sweep; random trees give unions of up to all 63 chunks, so the summary path also runs
+    # its later rounds (more than 2G chunks per proposal)
+    case = Case(inst, "par", "tc", init=init, nchains=nchains, kernel=capi.KERNEL_WIDE, sc_target=40, sums=sums,
+                lanes=lanes)
     betas = [0.5, 2.0, 8.0]
     gpu = case.run_gpu(betas=betas, niters=1)
     assert gpu[3].startswith("wide"), gpu[3]
     compare(case, gpu, case.run_oracle(betas=betas, niters=1))
+
+
+# Chunk summaries stay exact across everything that rewrites label sets outside the sweep kernel: an upload,
+# a population step (resample) and pre-order sweeps (the one-wave kernel), each followed by more par sweeps.
+def test_wide_summaries_across_upload_resample_and_preorder():
+    case = Case("sq46", "par", "tc", kernel=capi.KERNEL_WIDE, nchains=24, sums=1, lanes=8, wide_wgs=2)
+    rng = np.random.default_rng(5)
+    anc = rng.integers(0, case.nchains, case.nchains).astype(np.int32)
+    opop = case.pop0.copy()
+    print("[gpu] summaries across upload / resample / preorder sq46", flush=True)
+    with capi.Context(case.lay, case.leaf, case.leaf_sc, case.cfg, case.nchains) as ctx:
+        assert " sums=1 " in ctx.describe()
+        ctx.upload(case.pop0)
+        ctx.sweeps(capi.ORDER_PAR, 1.0, 0, 2)
+        case.O.sweeps(case.P, case.lay, opop, capi.ORDER_PAR, 1.0, 0, 2)
+        ctx.resample(anc)
+        opop = opop[anc].copy()
+        ctx.sweeps(capi.ORDER_PAR, 2.0, 2, 1)
+        case.O.sweeps(case.P, case.lay, opop, capi.ORDER_PAR, 2.0, 2, 1)
+        ctx.sweeps(capi.ORDER_PREORDER, 3.0, 3, 1)
+        case.O.sweeps(case.P, case.lay, opop, capi.ORDER_PREORDER, 3.0, 3, 1)
+        ctx.sweeps(capi.ORDER_PAR, 4.0, 4, 1)
+        case.O.sweeps(case.P, case.lay, opop, capi.ORDER_PAR, 4.0, 4, 1)
+        assert np.array_equal(ctx.download(), opop), "after resample / preorder"
+        ctx.upload(case.pop0)
+        opop = case.pop0.copy()
+        ctx.sweeps(capi.ORDER_PAR, 5.0, 5, 2)
+        case.O.sweeps(case.P, case.lay, opop, capi.ORDER_PAR, 5.0, 5, 2)
+        assert np.array_equal(ctx.download(), opop), "after a second upload"
+        glc, gsc, gns = ctx.energy()
+        olc, osc, ons = case.O.energy(case.P, case.lay, opop)
+        assert np.array_equal(glc.view(np.uint32), olc.view(np.uint32))
+        ck = ctx.chunk_stats()
+    assert ck[0] > 0 and ck[1] > 0, ck
 
 
 # Energies from the node-cost cache the wide sweep kernel keeps: after every level the fold of the cached

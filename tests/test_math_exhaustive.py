@@ -77,3 +77,34 @@ def test_lse_table_matches_reference_definition():
     t = orc.lse_table()
     assert t[0] == 1.0 and t[63] == 0.0 and t[53] == 0.0
     assert float(t[1]) == float.fromhex("0x1.2b8034p-1") and float(t[2]) == float.fromhex("0x1.49a784p-2")
+
+
+def test_log2_core_table_matches_its_generator():
+    # the constants of the log2 core in tsa_math.h are exactly what gen_log2_table.py prints; the generator
+    # itself is pinned by the identities it must satisfy: inv_j * c_j rounds to 1, t_j is -log2(inv_j)
+    # to double precision, and A_k are the series coefficients of log2(1 + z)
+    import importlib.util
+    import math
+    import re
+    import struct
+    from fractions import Fraction
+    spec = importlib.util.spec_from_file_location("gen_log2_table",
+                                                  os.path.join(ROOT, "treesa_gpu_amd", "csrc", "gen_log2_table.py"))
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    hdr = open(os.path.join(ROOT, "treesa_gpu_amd", "csrc", "tsa_math.h")).read()
+    body = hdr[hdr.index("#define TSA_LOG2_TAB"):]
+    body = body[:body.index("}")]
+    words = [int(x, 16) for x in re.findall(r"0x([0-9a-f]{16})ull", body)]
+    rows = gen.table()
+    assert words == [w for r in rows for w in r]
+    for k, a in enumerate(gen.coeffs(), 1):
+        m = re.search(rf"#define TSA_LOG2_A{k} (\S+)", hdr)
+        assert m and float.fromhex(m.group(1)) == a
+        assert abs(a - (-1) ** (k + 1) / (k * math.log(2))) <= 2e-16 * abs(a)
+    d = lambda b: struct.unpack("<d", struct.pack("<Q", b))[0]
+    for j, (bi, bt) in enumerate(rows):
+        inv, t = d(bi), d(bt)
+        c = Fraction(128 + j, 128)
+        assert abs(Fraction(inv) * c - 1) <= Fraction(1, 2 ** 53)
+        assert abs(t + math.log2(inv)) <= 4e-16 * max(t, 1e-300) + 1e-300

@@ -24,7 +24,7 @@ DEFAULT_GM = (11.9e15, 1.6e13, 6, 6, 8, 4e-6)
 DEFAULT_H100 = (4e-6, 1.23e13, 5.44e-14, 7.68e-15, 6.37e-14, 2.02e-16, 1.77e-13, 14, 1e-12)
 
 EXPORTS = ("tsa_layout", "tsa_create", "tsa_upload", "tsa_download", "tsa_sweeps", "tsa_sweeps_ms", "tsa_energy",
-           "tsa_resample", "tsa_set_mode", "tsa_stats", "tsa_describe", "tsa_destroy", "tsa_last_error",
+           "tsa_resample", "tsa_set_mode", "tsa_stats", "tsa_chunk_stats", "tsa_describe", "tsa_destroy", "tsa_last_error",
            "tsa_host_math")
 
 
@@ -44,7 +44,8 @@ class Config(ctypes.Structure):
                 ("v2_l3launch", ctypes.c_float), ("v2_lperm2", ctypes.c_float), ("v2_lcc_bit", ctypes.c_float),
                 ("v2_lcc_cell", ctypes.c_float), ("v2_ltc_bit", ctypes.c_float), ("v2_ltc_pad", ctypes.c_float),
                 ("v2_ltc_out", ctypes.c_float), ("v2_lsmall_cell", ctypes.c_float), ("v2_small_rank", ctypes.c_int32),
-                ("wide_waves", ctypes.c_int32), ("wide_wgs", ctypes.c_int32), ("fused_energy", ctypes.c_int32)]
+                ("wide_waves", ctypes.c_int32), ("wide_wgs", ctypes.c_int32), ("fused_energy", ctypes.c_int32),
+                ("sums", ctypes.c_int32), ("wide_lanes", ctypes.c_int32)]
 
 
 _lib = None
@@ -70,6 +71,7 @@ def load():
     lib.tsa_resample.argtypes = [P, P]
     lib.tsa_set_mode.argtypes = [P, I32]
     lib.tsa_stats.argtypes = [P, P]
+    lib.tsa_chunk_stats.argtypes = [P, P]
     lib.tsa_describe.argtypes = [P, ctypes.c_char_p, I32]
     lib.tsa_destroy.argtypes = [P]
     lib.tsa_last_error.argtypes = [P]
@@ -110,7 +112,7 @@ def layout(m, nlab, wide=False):
 
 def make_config(mode="tc", sc_target=20.0, sc_weight=1.0, seed=1, slicing=False, slice_moves=1, slice_every=1,
                 max_slices=0, par_follow=False, par_band=0, kernel=KERNEL_AUTO, gm=DEFAULT_GM, h100=DEFAULT_H100,
-                wide_waves=0, wide_wgs=0, fused_energy=False):
+                wide_waves=0, wide_wgs=0, fused_energy=False, sums=0, wide_lanes=0):
     """Config with the fields the reference's Runner derives from its options (csrc/treesa_gpu.cu:1449-1474)."""
     k = splitmix64(seed)
     c = Config()
@@ -134,6 +136,8 @@ def make_config(mode="tc", sc_target=20.0, sc_weight=1.0, seed=1, slicing=False,
     c.v2_small_rank, c.v2_lsmall_cell = int(h[7]), f32_log2(h[8])
     c.wide_waves, c.wide_wgs = wide_waves, wide_wgs
     c.fused_energy = 1 if fused_energy else 0
+    c.sums = int(sums)
+    c.wide_lanes = int(wide_lanes)
     return c
 
 
@@ -191,6 +195,12 @@ class Context:
     def stats(self):
         out = np.zeros(7, np.uint64)
         self._check(self.lib.tsa_stats(self.h, out.ctypes.data))
+        return [int(x) for x in out]
+
+    def chunk_stats(self):
+        """Chunk positions loaded by proposals and written by accepts on the summary path."""
+        out = np.zeros(2, np.uint64)
+        self._check(self.lib.tsa_chunk_stats(self.h, out.ctypes.data))
         return [int(x) for x in out]
 
     def describe(self):

@@ -50,6 +50,10 @@ struct tsa_ctx {
   float* d_ncost = nullptr;    // per-node costs of the wide energy kernel, nchains * nint4
   uint16_t* d_nz = nullptr;    // per-node masked sizes, nchains * nint4
   unsigned* d_fcnt = nullptr;  // per-chain workgroup counters of the wide energy kernel
+  uint64_t* d_sum = nullptr;   // chunk summaries of the internal sets, nchains * nint4 * wide.nsw
+  uint64_t* d_leafsum = nullptr;  // chunk summaries of the input tensors, m * wide.nsw
+  bool sums_valid = false;     // d_sum matches the population (k_wsum since the last upload or resample,
+                               // and every sweep since ran the wide kernel)
   bool costs_valid = false;    // d_ncost / d_nz hold every node's cost (full pass since the last upload,
                                // resample or mode switch, and every sweep since ran the wide kernel)
   bool energy_fresh = false;   // d_lc / d_sc / d_ns hold the energies of the current population (written by
@@ -111,7 +115,7 @@ static void build_log2_fix() {
   for (uint32_t w = 0; w < nw; w++)
     if (g_fix[w]) g_fix[nw + (w >> 5)] |= 1u << (w & 31u);
   for (long long f : far) g_fix_far += f;
-  if (tsa_fbits(log2f(2.0f)) != tsa_fbits(tsa_log2f_core(2.0f))) g_fix_far++;
+  if (tsa_fbits(log2f(2.0f)) != tsa_fbits(1.0f)) g_fix_far++;  // tsa_log2f_12 returns 1 at 2
 }
 
 // Sampled comparison of the restated expf / exp2f with this process's libm (the exhaustive comparison
@@ -208,6 +212,8 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_ncost) (void)hipFree(c->d_ncost);
   if (c->d_nz) (void)hipFree(c->d_nz);
   if (c->d_fcnt) (void)hipFree(c->d_fcnt);
+  if (c->d_sum) (void)hipFree(c->d_sum);
+  if (c->d_leafsum) (void)hipFree(c->d_leafsum);
   if (c->d_tpart) (void)hipFree(c->d_tpart);
   if (c->d_tdone) (void)hipFree(c->d_tdone);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
@@ -309,7 +315,7 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   const int nodew2 = (nodew + 1) & ~1;
   const int leafw = (lay->m * lay->W + 1) & ~1;
   const int per_wave_lds = lay->chain_words + nodew2;
-  const int ldsw = lds_max / 8;
+  const int ldsw = (lds_max - 1024) / 8;  // less room for the kernel's static LDS (under 1 KB)
   const bool reg = !lay->runtime_width;
   const bool lds_fits = reg && leafw + per_wave_lds <= ldsw;
   bool use_lds;
@@ -347,15 +353,17 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   const bool want_wide = cfg->kernel == TSA_KERNEL_WIDE || (cfg->kernel == TSA_KERNEL_AUTO && !use_lds);
   if (want_wide) {
     hipError_t we = hipErrorInvalidValue;
-    if (lay->runtime_width && !cfg->slicing) we = tsa_wide_plan(c->P, nchains, cfg->wide_waves, cfg->wide_wgs, &c->wide);
+    if (lay->runtime_width && !cfg->slicing)
+      we = tsa_wide_plan(c->P, nchains, cfg->wide_waves, cfg->wide_wgs, cfg->wide_lanes, cfg->sums, &c->wide);
     if (we != hipSuccess) {
       (void)hipGetLastError();  // clear the runtime's last error: the context goes on without the wide path
       c->wide = TsaWide{};
-      if (cfg->kernel == TSA_KERNEL_WIDE || cfg->wide_waves > 0 || cfg->wide_wgs > 0) {
+      if (cfg->kernel == TSA_KERNEL_WIDE || cfg->wide_waves > 0 || cfg->wide_wgs > 0 || cfg->wide_lanes > 0) {
         free_ctx(c);
         return fail(nullptr, TSA_ERR_FIT,
-                    std::string("wide kernel: no plan (it needs runtime width, no slicing, W <= 256 words, the node "
-                                "arrays in LDS, and nchains x workgroups per chain co-resident): ") +
+                    std::string("wide kernel: no plan (it needs runtime width, no slicing, W <= 256 words, lanes per "
+                                "proposal 4/8/16 with summaries or enough for W without, the node arrays in LDS, "
+                                "and nchains x workgroups per chain co-resident): ") +
                         hipGetErrorString(we));
       }
     }
@@ -363,8 +371,9 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   char kb[200];
   if (c->wide.on)
     snprintf(kb, sizeof kb,
-             "wide W=%d G=%d waves/block=%d blocks/chain=%d lds_bytes/block=%d energy_blocks/chain=%d fold_stage=%d",
-             lay->W, c->wide.G, c->wide.nt / 64, c->wide.K, c->wide.smem, c->wide.eK, c->wide.fold_stage);
+             "wide W=%d G=%d sums=%d waves/block=%d blocks/chain=%d lds_bytes/block=%d energy_blocks/chain=%d "
+             "fold_stage=%d",
+             lay->W, c->wide.G, c->wide.nsw, c->wide.nt / 64, c->wide.K, c->wide.smem, c->wide.eK, c->wide.fold_stage);
   else
     snprintf(kb, sizeof kb, "%s W=%d waves/block=%d lds_bytes/wave=%d", use_lds ? "lds" : "global",
              use_lds ? c->Wt : lay->W, c->L.wpb, c->L.lds_words * 8);
@@ -387,8 +396,8 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   TSA_CREATE_HIP(hipMemcpyAsync(c->d_leaf, leaf, (size_t)lay->m * lay->W * 8, hipMemcpyHostToDevice, c->st));
   TSA_CREATE_HIP(hipMalloc(&c->d_fix, g_fix.size() * 4));
   TSA_CREATE_HIP(hipMemcpyAsync(c->d_fix, g_fix.data(), g_fix.size() * 4, hipMemcpyHostToDevice, c->st));
-  TSA_CREATE_HIP(hipMalloc(&c->d_stats, TSA_NSTAT * TSA_STAT_SLOTS * sizeof(unsigned long long)));
-  TSA_CREATE_HIP(hipMemsetAsync(c->d_stats, 0, TSA_NSTAT * TSA_STAT_SLOTS * sizeof(unsigned long long), c->st));
+  TSA_CREATE_HIP(hipMalloc(&c->d_stats, TSA_NSTAT_ALL * TSA_STAT_SLOTS * sizeof(unsigned long long)));
+  TSA_CREATE_HIP(hipMemsetAsync(c->d_stats, 0, TSA_NSTAT_ALL * TSA_STAT_SLOTS * sizeof(unsigned long long), c->st));
   TSA_CREATE_HIP(hipMalloc(&c->d_lc, (size_t)nchains * 12 + 16));  // + the wide path's error word
   TSA_CREATE_HIP(hipMemsetAsync(c->d_lc, 0, (size_t)nchains * 12 + 16, c->st));
   c->d_sc = reinterpret_cast<int*>(c->d_lc) + nchains;
@@ -408,6 +417,22 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
     c->wsync.nz = c->d_nz;
     TSA_CREATE_HIP(hipMalloc(&c->d_fcnt, (size_t)nchains * 4));
     TSA_CREATE_HIP(hipMemsetAsync(c->d_fcnt, 0, (size_t)nchains * 4, c->st));
+    if (c->wide.nsw) {
+      const int nsw = c->wide.nsw, nch = lay->W / 2;
+      std::vector<uint64_t> ls((size_t)lay->m * nsw, 0ull);
+      for (int i = 0; i < lay->m; i++)
+        for (int cc = 0; cc < nch; cc++)
+          if (leaf[(size_t)i * lay->W + 2 * cc] | leaf[(size_t)i * lay->W + 2 * cc + 1])
+            ls[(size_t)i * nsw + cc / 64] |= 1ull << (cc % 64);
+      TSA_CREATE_HIP(hipMalloc(&c->d_sum, (size_t)nchains * nint4 * nsw * 8));
+      TSA_CREATE_HIP(hipMalloc(&c->d_leafsum, ls.size() * 8));
+      TSA_CREATE_HIP(hipMemcpyAsync(c->d_leafsum, ls.data(), ls.size() * 8, hipMemcpyHostToDevice, c->st));
+      TSA_CREATE_HIP(hipStreamSynchronize(c->st));  // ls is a local
+      c->wsync.sum = c->d_sum;
+      c->wsync.leafsum = c->d_leafsum;
+      c->wsync.nsw = nsw;
+      c->wsync.lsum_lds = c->wide.lsum_lds;
+    }
   }
   TSA_CREATE_HIP(hipMalloc(&c->d_anc, (size_t)nchains * 4));
   TSA_CREATE_HIP(hipStreamSynchronize(c->st));
@@ -434,6 +459,7 @@ static hipError_t launch_energy(tsa_ctx* c) {
 static int wide_error(tsa_ctx* c, uint32_t word) {
   if (word == 0) return TSA_OK;
   c->costs_valid = false;
+  c->sums_valid = false;
   (void)hipMemsetAsync(c->wsync.err, 0, 4, c->st);
   (void)hipStreamSynchronize(c->st);
   return fail(c, TSA_ERR_HIP, "wide sweep kernel: a chain barrier timed out; the population is undefined");
@@ -451,6 +477,7 @@ extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
   }
   ctx->costs_valid = false;
   ctx->energy_fresh = false;
+  ctx->sums_valid = false;
   TSA_HIP(ctx, hipMemcpyAsync(ctx->d_rec, population, (size_t)ctx->nchains * L.chain_words * 8,
                               hipMemcpyHostToDevice, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
@@ -483,10 +510,15 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
   if (ctx->wide.on && order == TSA_ORDER_PAR) {
     // energies stay a separate fold of the node-cost cache: every chain ends its sweep at about the same
     // time, so folding inside the sweep kernel would only lengthen it
+    if (ctx->wide.nsw && !ctx->sums_valid) {
+      TSA_HIP(ctx, tsa_launch_wsum(ctx->wide, ctx->P, ctx->d_rec, ctx->nchains, ctx->d_sum, ctx->st));
+      ctx->sums_valid = true;
+    }
     TSA_HIP(ctx, tsa_launch_wide(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains, beta,
                                  sweep0, nsweeps, ctx->d_stats, ctx->wsync, ctx->st));
   } else {
     ctx->costs_valid = false;
+    ctx->sums_valid = false;
     const bool fuse = ctx->cfg.fused_energy != 0;
     const TsaEnergyOut eo{fuse ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns};
     TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
@@ -606,6 +638,7 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
   TSA_HIP(ctx, hipMemcpyAsync(ctx->d_anc, anc, (size_t)ctx->nchains * 4, hipMemcpyHostToDevice, ctx->st));
   ctx->costs_valid = false;
   ctx->energy_fresh = false;
+  ctx->sums_valid = false;
   TSA_HIP(ctx, tsa_launch_copy(ctx->d_rec, ctx->d_rec2, ctx->d_anc, ctx->nchains, ctx->lay.chain_words, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
   std::swap(ctx->d_rec, ctx->d_rec2);
@@ -632,6 +665,19 @@ extern "C" int tsa_stats(tsa_ctx* ctx, uint64_t out[7]) {
   return TSA_OK;
 }
 
+extern "C" int tsa_chunk_stats(tsa_ctx* ctx, uint64_t out[2]) {
+  if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_chunk_stats: null argument");
+  unsigned long long s[2 * TSA_STAT_SLOTS];
+  TSA_HIP(ctx, hipMemcpyAsync(s, ctx->d_stats + TSA_ST_CHUNKS * TSA_STAT_SLOTS, sizeof s, hipMemcpyDeviceToHost,
+                              ctx->st));
+  TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  for (int i = 0; i < 2; i++) {
+    out[i] = 0;
+    for (int k = 0; k < TSA_STAT_SLOTS; k++) out[i] += s[i * TSA_STAT_SLOTS + k];
+  }
+  return TSA_OK;
+}
+
 extern "C" int tsa_describe(tsa_ctx* ctx, char* buf, int32_t len) {
   if (!ctx || !buf || len < 1) return fail(ctx, TSA_ERR_ARG, "tsa_describe: null argument");
   snprintf(buf, (size_t)len, "%s", ctx->kname.c_str());
@@ -651,5 +697,6 @@ extern "C" float tsa_host_math(int32_t which, float x) {
   if (which == 0) return tsa_expf(x);
   if (which == 1) return tsa_exp2f(x);
   std::call_once(g_fix_once, build_log2_fix);
-  return tsa_log2f_12(x, g_fix.data(), g_fix.data() + TSA_LOG2FIX_WORDS);
+  const TsaMathTabs T{tsa_exp2_tab_h, g_fix.data(), g_fix.data() + TSA_LOG2FIX_WORDS, tsa_log2_tab_h};
+  return tsa_log2f_12(x, T);
 }

@@ -38,15 +38,28 @@ __device__ __forceinline__ float tsa_node_eval(const TsaKParams& P, const uint64
 }
 
 // The 32-lane fold of cost[0..nint) / z[0..nint) (l32 = lane within a 32-lane group; every lane of the
-// group returns the result).  lf / S / NW serve the masked leaf sizes when S is set.
+// group returns the result).  lf / S / NW serve the masked leaf sizes when S is set.  The lse chain of a
+// lane is serial; its operands are read TSA_FOLD_BATCH at a time ahead of it, so that no step waits on a
+// load, and the size statistics run in a loop of their own.
+#define TSA_FOLD_BATCH 8
 __device__ __forceinline__ TsaEvalOut tsa_fold32(const TsaKParams& P, const float* cost, const uint16_t* z,
                                                  const uint64_t* S, const uint64_t* lf, int NW, const TsaMathTabs& T,
                                                  int l32) {
   const int nint = P.nint, m = P.m;
   float acc = -INFINITY;
+  for (int i0 = l32; i0 < nint; i0 += 32 * TSA_FOLD_BATCH) {
+    float cb[TSA_FOLD_BATCH];
+#pragma unroll
+    for (int q = 0; q < TSA_FOLD_BATCH; q++) {
+      const int i = i0 + 32 * q;
+      cb[q] = i < nint ? cost[i] : 0.0f;
+    }
+#pragma unroll
+    for (int q = 0; q < TSA_FOLD_BATCH; q++)
+      if (i0 + 32 * q < nint) acc = tsa_lse_f(acc, cb[q], T);
+  }
   int scl = 0, cntl = 0;
   for (int i = l32; i < nint; i += 32) {
-    acc = tsa_lse_f(acc, cost[i], T);
     const int Z = z[i];
     if (Z > scl) {
       scl = Z;

@@ -20,6 +20,9 @@ struct TsaKParams {
 
 // Statistic slots (the reference's d_stats order, csrc/treesa_gpu.cu:713-721).
 enum { TSA_ST_PROP = 0, TSA_ST_ACC, TSA_ST_STEPS, TSA_ST_VISITS, TSA_ST_SPROP, TSA_ST_SACC, TSA_ST_BUSY, TSA_NSTAT };
+// Two more counters of the wide kernel with chunk summaries: chunk positions loaded by proposals and
+// written by accepts.
+enum { TSA_ST_CHUNKS = TSA_NSTAT, TSA_ST_XCHUNKS, TSA_NSTAT_ALL };
 // Each counter is spread over TSA_STAT_SLOTS device words (slot = chain % TSA_STAT_SLOTS) so that thousands
 // of waves do not serialize their atomics on one address; the host sums the slots.
 #define TSA_STAT_SLOTS 64
@@ -41,6 +44,25 @@ struct TsaEnergyOut {
   int* sc;
   int* ns;
 };
+
+// Copy n elements with nthr threads (this one is tid), U loads per thread in flight at once: a loop that
+// stores each element before it loads the next waits a memory latency per element.
+template <typename T, int U>
+__device__ __forceinline__ void tsa_copy_inflight(T* dst, const T* __restrict__ src, int n, int tid, int nthr) {
+  for (int i0 = tid; i0 < n; i0 += U * nthr) {
+    T v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int i = i0 + u * nthr;
+      if (i < n) v[u] = src[i];
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int i = i0 + u * nthr;
+      if (i < n) dst[i] = v[u];
+    }
+  }
+}
 
 // Host-side launchers (tsa_kernels.hip).  All return hipError_t of the launch.
 hipError_t tsa_launch_sweeps(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
@@ -85,19 +107,24 @@ hipError_t tsa_launch_copy(const uint64_t* src, uint64_t* dst, const int* anc, i
 struct TsaWide {
   int on;     // 1: par-order sweeps of this context run k_wide
   int G;      // lanes per proposal (4..64)
-  int K;      // workgroups per chain (K > 1: cooperative launch with chain barriers)
+  int K;      // workgroups per chain (K > 1: all co-resident, chain barriers between phases)
   int nt;     // threads per workgroup
   int smem;   // dynamic LDS bytes per workgroup
   int eG, eK; // energy: lanes per node, workgroups per chain
   int fold_stage;     // energy fold: 0 reads node costs from HBM, 1 stages them in LDS, 2 also the log2f bitmap
   int fold_smem;      // LDS bytes of stage 1 (0: the costs do not fit)
   int fold_smem_map;  // LDS bytes of stage 2
+  int nsw;            // 64-bit words of a chunk summary per label set (0: no summaries; dense streaming)
+  int lsum_lds;       // summaries: the input tensors' summaries are staged in LDS too
 };
 
 // Device state of the wide sweep kernel: the chain barrier words bar[nchains], done[nchains], err[1] (all
 // zero between launches); outcome bytes of the visits of the last two phases, out[nchains][2][nint4]
 // (K > 1 only); the per-node cost cache ncost / nz [nchains][nint4] (cost and masked size of every internal
 // node), which the sweep kernel keeps current on every accepted rotation and the energy kernel folds.
+// With chunk summaries (nsw > 0): sum[nchains][nint4][nsw] holds, for every internal node, bit c set iff
+// 16-byte chunk c of its label set is nonzero (kept current by the sweep kernel), leafsum[m][nsw] the
+// same for the input tensors.
 struct TsaWideSync {
   unsigned* bar;
   unsigned* done;
@@ -105,20 +132,27 @@ struct TsaWideSync {
   uint8_t* out;
   float* ncost;
   uint16_t* nz;
+  uint64_t* sum;
+  const uint64_t* leafsum;
+  int nsw;
+  int lsum_lds;  // 1: the sweep kernel stages leafsum in LDS (when it fits beside the node arrays)
 };
 
 // LDS byte offsets of k_wide (same function on host and device).
+// With chunk summaries (nsw > 0) the summaries of the internal sets (sum) are staged too, and those of the
+// input tensors (lsum) when mlds = m (0: read from HBM).
 struct TsaWideLds {
-  int masks, ch, dw, offs, pri, par, wl, out, bytes;
+  int masks, ch, dw, sum, lsum, pri, par, wl, out, bytes;
 };
-__host__ __device__ static inline TsaWideLds tsa_wide_lds(int nint, int band, int coop) {
+__host__ __device__ static inline TsaWideLds tsa_wide_lds(int nint, int band, int coop, int nsw, int mlds) {
   const int nint4 = (nint + 3) & ~3, ngrp = (nint + 63) / 64;
   TsaWideLds L;
   int b = 0;
   L.masks = b;  b += ngrp * 8;
   L.ch = b;     b += nint4 * 4;
   L.dw = b;     b += band ? nint4 * 4 : 0;
-  L.offs = b;   b += ((ngrp + 1) & ~1) * 4;
+  L.sum = b;    b += nint4 * nsw * 8;
+  L.lsum = b;   b += mlds * nsw * 8;
   L.pri = b;    b += nint4 * 2;
   L.par = b;    b += nint4 * 2;
   L.wl = b;     b += nint4 * 2;
@@ -127,10 +161,17 @@ __host__ __device__ static inline TsaWideLds tsa_wide_lds(int nint, int band, in
   return L;
 }
 
-// Plan a wide launch for nchains chains on the current device: G from W, threads per workgroup (want_waves
-// waves, 0 = by chain count), workgroups per chain (want_k, 0 = as many as stay co-resident).  Returns
-// hipErrorInvalidValue when the chain does not qualify (W > 2 * TSA_WIDE_CPL * 64 or LDS too small).
-hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int want_k, TsaWide* out);
+// Plan a wide launch for nchains chains on the current device: chunk summaries (sums: 1 on, -1 off, 0 on
+// from 64 words per set), lanes per proposal (want_g, 0 = from W, or 8 with summaries), threads per
+// workgroup (want_waves waves, 0 = by chain count), workgroups per chain (want_k, 0 = as many as stay
+// co-resident).  Returns hipErrorInvalidValue when the chain does not qualify (W > 2 * TSA_WIDE_CPL * 64,
+// a lane count that cannot hold a set, or LDS too small).
+hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int want_k, int want_g, int sums,
+                         TsaWide* out);
+// Chunk summaries of every internal node of every chain from the label sets (after an upload or a
+// population step).
+hipError_t tsa_launch_wsum(const TsaWide& X, const TsaKParams& P, const uint64_t* rec, int nchains, uint64_t* sum,
+                           hipStream_t st);
 hipError_t tsa_launch_wide(const TsaWide& X, int mode, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
                            const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
                            unsigned long long* stats, const TsaWideSync& sy, hipStream_t st);

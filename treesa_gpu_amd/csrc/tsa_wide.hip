@@ -25,11 +25,11 @@
 // and the replays, of one phase commute.  Every proposal draws Philox((v, sweep, chain)), so the result is
 // the CPU phase-by-phase sweep bit for bit, whatever K and G.
 //
-// Chain barrier: cooperative launch (all workgroups co-resident).  Thread 0 of each workgroup releases at
-// agent scope, adds 1 to the chain's counter and polls it until K * (barriers so far) with a bounded number
-// of polls; a workgroup that runs out of polls sets the error word, and every workgroup that sees the error
-// word stops, so every wave reaches the end of the kernel.  The last workgroup of a chain to finish resets
-// the chain's counters to zero for the next launch.
+// Chain barrier: all K * nchains workgroups are co-resident (the plan checks occupancy).  Thread 0 of each
+// workgroup releases at agent scope, adds 1 to the chain's counter and polls it until K * (barriers so far)
+// with a bounded number of polls; a workgroup that runs out of polls sets the error word, and every
+// workgroup that sees the error word stops, so every wave reaches the end of the kernel.  The last
+// workgroup of a chain to finish resets the chain's counters to zero for the next launch.
 #include "tsa_kernels.h"
 #include "tsa_fold.h"
 
@@ -142,17 +142,44 @@ __device__ __forceinline__ long long wide_wave_sum(long long x) {
   return x;
 }
 
+// Chunk summaries: the chunks of a proposal are the set bits of the union u = u0 | u1 << 64 of the
+// summaries of D, O, K and M; lane t of a group of G takes the bits of rank t, t + G, t + 2G, ... so that the
+// loads spread evenly over the group whatever the positions, SC of them per round.  sum_pick returns the
+// positions of ranks r, r + G, ..., r + (SC - 1) G (-1 where u has fewer set bits).
+template <int G>
+struct TsaSumRound {
+  static constexpr int SC = G <= 2 ? 4 : 2;  // chunks per lane and round
+};
+
+template <int G, int SC>
+__device__ __forceinline__ void sum_pick(uint64_t u0, uint64_t u1, int r, int (&ii)[SC]) {
+#pragma unroll
+  for (int q = 0; q < SC; q++) ii[q] = -1;
+  int k = 0;
+  for (uint64_t u = u0; u; u &= u - 1ull, k++) {
+    const int d = k - r;
+#pragma unroll
+    for (int q = 0; q < SC; q++)
+      if (d == q * G) ii[q] = __builtin_ctzll(u);
+  }
+  for (uint64_t u = u1; u; u &= u - 1ull, k++) {
+    const int d = k - r;
+#pragma unroll
+    for (int q = 0; q < SC; q++)
+      if (d == q * G) ii[q] = 64 + __builtin_ctzll(u);
+  }
+}
+
 // The fold of one chain's cached node costs by the calling workgroup: with stage >= 1 the costs (and with
 // stage 2 the log2f summary bitmap) are first copied into the workgroup's LDS at lds (vector copies, all
 // loads in flight at once: the fold reads them in a serial chain per lane); lanes 0..31 then fold in the
 // reference's order and lane 0 writes lc / sc / ns of chain c.  Every thread of the workgroup calls it.
-__device__ void wide_fold(const TsaKParams& P, int c, const float* cst, const uint16_t* zz, const uint64_t* S,
-                          const uint64_t* leaf, const uint32_t* fix, const uint64_t* s_exp2, int stage,
-                          unsigned char* lds, float* lc, int* sc, int* ns) {
+__device__ __forceinline__ void wide_fold(const TsaKParams& P, int c, const float* cst, const uint16_t* zz,
+                                          const uint64_t* S, const uint64_t* leaf, const uint32_t* fix,
+                                          const uint64_t* s_mt, int stage, unsigned char* lds, float* lc, int* sc,
+                                          int* ns) {
   const int nint4 = (P.nint + 3) & ~3;
   const uint32_t* const gmap = fix + TSA_LOG2FIX_WORDS;
-  const float* fc = cst;
-  const uint16_t* fz = zz;
   const uint32_t* map = gmap;
   if (stage) {
     float* const scst = reinterpret_cast<float*>(lds);
@@ -173,12 +200,14 @@ __device__ void wide_fold(const TsaKParams& P, int c, const float* cst, const ui
       map = reinterpret_cast<const uint32_t*>(smap);
     }
     __syncthreads();
-    fc = scst;
-    fz = szz;
   }
   if (threadIdx.x < 32) {
-    const TsaMathTabs T{s_exp2, fix, map};
-    const TsaEvalOut e = tsa_fold32(P, fc, fz, S, leaf, P.W, T, (int)threadIdx.x);
+    const TsaMathTabs T{s_mt, fix, map, s_mt + 32};
+    // two call sites, so that each inlined fold knows whether it reads LDS or global memory
+    const TsaEvalOut e = stage ? tsa_fold32(P, reinterpret_cast<const float*>(lds),
+                                            reinterpret_cast<const uint16_t*>(lds + (size_t)nint4 * 4), S, leaf, P.W,
+                                            T, (int)threadIdx.x)
+                               : tsa_fold32(P, cst, zz, S, leaf, P.W, T, (int)threadIdx.x);
     if (threadIdx.x == 0) {
       lc[c] = e.lcost;
       sc[c] = e.sc;
@@ -187,35 +216,44 @@ __device__ void wide_fold(const TsaKParams& P, int c, const float* cst, const ui
   }
 }
 
-template <int G, int MODE, bool COOP>
-__global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restrict__ rec,
+// (SUMS: at most 512 threads, so that the summary visit has 256 registers and does not spill)
+template <int G, int MODE, bool COOP, bool SUMS>
+__global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64_t* __restrict__ rec,
                                                const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
                                                int nchains, int K, float beta, uint32_t sweep0, int nsweeps,
                                                unsigned long long* __restrict__ stats, TsaWideSync sy) {
   extern __shared__ __align__(16) unsigned char tsa_wsm[];
   __shared__ float s_lse[64];
-  __shared__ uint64_t s_exp2[32];
+  __shared__ uint64_t s_mt[TSA_MT_WORDS];
   __shared__ int s_cnt, s_ok, s_next;
   const int NT = blockDim.x, nwv = NT >> 6, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m = P.m, nint = P.nint, nint4 = (nint + 3) & ~3, ngrp = (nint + 63) >> 6;
   const int NW = P.W, nch = NW >> 1;
   const int c = blockIdx.x / K, k = blockIdx.x - c * K;
   if (c >= nchains) return;  // whole workgroups; the grid is nchains * K
-  const TsaWideLds Lo = tsa_wide_lds(nint, P.par_band > 0, COOP ? 1 : 0);
+  const int nsw = SUMS ? sy.nsw : 0;
+  const bool lsum_in_lds = SUMS && sy.lsum_lds;
+  const TsaWideLds Lo = tsa_wide_lds(nint, P.par_band > 0, COOP ? 1 : 0, nsw, lsum_in_lds ? m : 0);
   uint64_t* const masks = reinterpret_cast<uint64_t*>(tsa_wsm + Lo.masks);
   uint32_t* const ch = reinterpret_cast<uint32_t*>(tsa_wsm + Lo.ch);
   uint32_t* const dw = reinterpret_cast<uint32_t*>(tsa_wsm + Lo.dw);
-  uint32_t* const offs = reinterpret_cast<uint32_t*>(tsa_wsm + Lo.offs);
   uint16_t* const pri = reinterpret_cast<uint16_t*>(tsa_wsm + Lo.pri);
   uint16_t* const par = reinterpret_cast<uint16_t*>(tsa_wsm + Lo.par);
   uint16_t* const wl = reinterpret_cast<uint16_t*>(tsa_wsm + Lo.wl);
   uint8_t* const outl = tsa_wsm + Lo.out;
+  uint64_t* const ssum = reinterpret_cast<uint64_t*>(tsa_wsm + Lo.sum);  // SUMS: summaries of the internal sets
+  uint64_t* const lsum = reinterpret_cast<uint64_t*>(tsa_wsm + Lo.lsum);  // and of the input tensors
   if (threadIdx.x < 64) s_lse[threadIdx.x] = P.lse[threadIdx.x];
-  if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
-  const TsaMathTabs T{s_exp2, fix, fix + TSA_LOG2FIX_WORDS};
+  tsa_math_stage(s_mt);
+  const TsaMathTabs T{s_mt, fix, fix + TSA_LOG2FIX_WORDS, s_mt + 32};
   uint64_t* const lab = rec + (size_t)c * P.chain_words;
   uint32_t* const gch = reinterpret_cast<uint32_t*>(lab + P.ch_off);
-  for (int i = threadIdx.x; i < nint; i += NT) ch[i] = gch[i];
+  tsa_copy_inflight<uint32_t, 8>(ch, gch, nint, threadIdx.x, NT);
+  uint64_t* const gsum = SUMS ? sy.sum + (size_t)c * nint4 * nsw : nullptr;
+  if constexpr (SUMS) {
+    tsa_copy_inflight<uint64_t, 8>(ssum, gsum, nint * nsw, threadIdx.x, NT);
+    if (lsum_in_lds) tsa_copy_inflight<uint64_t, 8>(lsum, sy.leafsum, m * nsw, threadIdx.x, NT);
+  }
   __syncthreads();
   for (int i = threadIdx.x; i < nint; i += NT) {
     const uint32_t cw = ch[i];
@@ -230,7 +268,7 @@ __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restric
   const int ngr = nwv * gpw;
   const int t = lane & (G - 1);
   const int gsub = lane / G;  // lane group within the wave
-  int np = 0, na = 0, nv = 0, nst = 0;
+  int np = 0, na = 0, nv = 0, nst = 0, nck = 0, nxk = 0;
   unsigned nb = 0;
   bool ok = true;
 
@@ -261,58 +299,53 @@ __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restric
     }
     __syncthreads();
     for (;;) {
-      // 1. scan
+      // 1. scan: a wave takes 64-node groups; each lane reads its node's priority, parent and children
+      // words, then the three neighbour priorities, in two rounds of independent LDS reads
+#pragma unroll 2
       for (int gi = wv; gi < ngrp; gi += nwv) {
         const int i = gi * 64 + lane;
         bool act = false;
         if (i < nint) {
-          const uint32_t pv = pri[i];
-          if (pv) {
-            const uint32_t key = (pv << 16) | (uint32_t)(m + i);
-            act = true;
-            const uint32_t p = par[i];
-            if (p != 0xFFFFu) {
-              const uint32_t pp = pri[p - m];
-              if (pp && ((pp << 16) | p) > key) act = false;
-            }
-            const uint32_t cw = ch[i];
-            const uint32_t l = cw & 0xFFFFu, r = cw >> 16;
-            if (act && l >= (uint32_t)m) {
-              const uint32_t pl = pri[l - m];
-              if (pl && ((pl << 16) | l) > key) act = false;
-            }
-            if (act && r >= (uint32_t)m) {
-              const uint32_t pr = pri[r - m];
-              if (pr && ((pr << 16) | r) > key) act = false;
-            }
-          }
+          const uint32_t pv = pri[i], p = par[i], cw = ch[i];
+          const uint32_t l = cw & 0xFFFFu, r = cw >> 16;
+          const uint32_t pp = p != 0xFFFFu ? pri[p - m] : 0u;
+          const uint32_t pl = l >= (uint32_t)m ? pri[l - m] : 0u;
+          const uint32_t pr = r >= (uint32_t)m ? pri[r - m] : 0u;
+          const uint32_t key = (pv << 16) | (uint32_t)(m + i);
+          act = pv != 0u && !(pp && ((pp << 16) | p) > key) && !(pl && ((pl << 16) | l) > key) &&
+                !(pr && ((pr << 16) | r) > key);
         }
         const uint64_t b = __ballot(act);
         if (lane == 0) masks[gi] = b;
       }
       __syncthreads();
-      if (wv == 0) {
+      // every wave forms the prefix over the group counts itself and compacts its own groups into the work
+      // list, in node order (the same list in every workgroup of the chain)
+      {
         int base = 0;
         for (int g0 = 0; g0 < ngrp; g0 += 64) {
-          const int gi = g0 + lane;
-          const int x = gi < ngrp ? __popcll(masks[gi]) : 0;
+          const int gl = g0 + lane;
+          const uint64_t b = gl < ngrp ? masks[gl] : 0ull;
+          const int x = __popcll(b);
           int y = x;
+#pragma unroll
           for (int o = 1; o < 64; o <<= 1) {
             const int u = __shfl_up(y, o, 64);
             if (lane >= o) y += u;
           }
-          if (gi < ngrp) offs[gi] = (uint32_t)(base + y - x);
+          const int excl = base + y - x;
+          const int gend = g0 + 64 < ngrp ? g0 + 64 : ngrp;
+          for (int gi = g0 + (wv - g0 % nwv + nwv) % nwv; gi < gend; gi += nwv) {
+            const uint64_t bm = __shfl(b, gi - g0, 64);
+            const int off = __shfl(excl, gi - g0, 64);
+            if ((bm >> lane) & 1ull) wl[off + __popcll(bm & wide_lt_mask(lane))] = (uint16_t)(m + gi * 64 + lane);
+          }
           base += __shfl(y, 63, 64);
         }
-        if (lane == 0) {
+        if (threadIdx.x == 0) {
           s_cnt = base;
           s_next = 0;
         }
-      }
-      __syncthreads();
-      for (int gi = wv; gi < ngrp; gi += nwv) {
-        const uint64_t b = masks[gi];
-        if ((b >> lane) & 1ull) wl[offs[gi] + __popcll(b & wide_lt_mask(lane))] = (uint16_t)(m + gi * 64 + lane);
       }
       __syncthreads();
       const int cnt = s_cnt;
@@ -350,29 +383,81 @@ __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restric
             const TsaW2* qO = reinterpret_cast<const TsaW2*>(On >= m ? lab + (size_t)(On - m) * NW : leaf + (size_t)On * NW);
             const TsaW2* qK = reinterpret_cast<const TsaW2*>(Kn >= m ? lab + (size_t)(Kn - m) * NW : leaf + (size_t)Kn * NW);
             const TsaW2* qM = reinterpret_cast<const TsaW2*>(Mn >= m ? lab + (size_t)(Mn - m) * NW : leaf + (size_t)Mn * NW);
-            TsaW2 dd[TSA_WIDE_CPL], pp[TSA_WIDE_CPL], oo[TSA_WIDE_CPL], kk[TSA_WIDE_CPL], mm[TSA_WIDE_CPL];
-#pragma unroll
-            for (int q = 0; q < TSA_WIDE_CPL; q++) {
-              const int cc = t + q * G;
-              if (cc < nch) {
-                dd[q] = qD[cc];
-                pp[q] = qP[cc];
-                oo[q] = qO[cc];
-                kk[q] = qK[cc];
-                mm[q] = qM[cc];
-              } else {
-                dd[q] = pp[q] = oo[q] = kk[q] = mm[q] = TsaW2{0ull, 0ull};
-              }
-            }
             TsaCounts cn;
             tsa_counts_zero(cn);
-            TsaW2 xx[TSA_WIDE_CPL];  // only X stays live across the energy evaluation
+            constexpr int SC = TsaSumRound<G>::SC;
+            constexpr int XN = SUMS ? SC : TSA_WIDE_CPL;
+            TsaW2 xx[XN];  // only X stays live across the energy evaluation
+            // SUMS: the population count of the union (uniform in the group) and the chunk positions of this
+            // lane's first round
+            int pc = 0, ix[SC];
+            if constexpr (SUMS) {
+              // summary word q of node n: LDS, or HBM for an input tensor whose table is not staged
+              auto sumw = [&](int n, int q) -> uint64_t {
+                if (n >= m) return ssum[(size_t)(n - m) * nsw + q];
+                return lsum_in_lds ? lsum[(size_t)n * nsw + q] : sy.leafsum[(size_t)n * nsw + q];
+              };
+              const uint64_t u0 = sumw(v, 0) | sumw(On, 0) | sumw(Kn, 0) | sumw(Mn, 0);
+              const uint64_t u1 = nsw > 1 ? (sumw(v, 1) | sumw(On, 1) | sumw(Kn, 1) | sumw(Mn, 1)) : 0ull;
+              pc = __popcll(u0) + __popcll(u1);
 #pragma unroll
-            for (int q = 0; q < TSA_WIDE_CPL; q++) {
-              xx[q].a = (kk[q].a | oo[q].a) & (mm[q].a | dd[q].a);
-              xx[q].b = (kk[q].b | oo[q].b) & (mm[q].b | dd[q].b);
-              tsa_acc<MODE>(cn, kk[q].a, mm[q].a, pp[q].a, oo[q].a, dd[q].a, xx[q].a);
-              tsa_acc<MODE>(cn, kk[q].b, mm[q].b, pp[q].b, oo[q].b, dd[q].b, xx[q].b);
+              for (int q = 0; q < SC; q++) {
+                xx[q] = TsaW2{0ull, 0ull};
+                ix[q] = -1;
+              }
+              // a chunk outside the union is zero in D, O, K and M, hence in P (a subset of K | M) and in X:
+              // it adds nothing to any count, and P's and X's values there are both zero
+              for (int r0 = 0; r0 < pc; r0 += SC * G) {  // one round unless the union has more than SC * G chunks
+                int ii[SC];
+                sum_pick<G, SC>(u0, u1, r0 + t, ii);
+                TsaW2 dd[SC], pp[SC], oo[SC], kk[SC], mm[SC];
+#pragma unroll
+                for (int q = 0; q < SC; q++) {
+                  if (ii[q] >= 0) {
+                    dd[q] = qD[ii[q]];
+                    pp[q] = qP[ii[q]];
+                    oo[q] = qO[ii[q]];
+                    kk[q] = qK[ii[q]];
+                    mm[q] = qM[ii[q]];
+                  } else {
+                    dd[q] = pp[q] = oo[q] = kk[q] = mm[q] = TsaW2{0ull, 0ull};
+                  }
+                }
+#pragma unroll
+                for (int q = 0; q < SC; q++) {
+                  TsaW2 x;
+                  x.a = (kk[q].a | oo[q].a) & (mm[q].a | dd[q].a);
+                  x.b = (kk[q].b | oo[q].b) & (mm[q].b | dd[q].b);
+                  tsa_acc<MODE>(cn, kk[q].a, mm[q].a, pp[q].a, oo[q].a, dd[q].a, x.a);
+                  tsa_acc<MODE>(cn, kk[q].b, mm[q].b, pp[q].b, oo[q].b, dd[q].b, x.b);
+                  if (r0 == 0) {
+                    xx[q] = x;
+                    ix[q] = ii[q];
+                  }
+                }
+              }
+            } else {
+              TsaW2 dd[TSA_WIDE_CPL], pp[TSA_WIDE_CPL], oo[TSA_WIDE_CPL], kk[TSA_WIDE_CPL], mm[TSA_WIDE_CPL];
+#pragma unroll
+              for (int q = 0; q < TSA_WIDE_CPL; q++) {
+                const int cc = t + q * G;
+                if (cc < nch) {
+                  dd[q] = qD[cc];
+                  pp[q] = qP[cc];
+                  oo[q] = qO[cc];
+                  kk[q] = qK[cc];
+                  mm[q] = qM[cc];
+                } else {
+                  dd[q] = pp[q] = oo[q] = kk[q] = mm[q] = TsaW2{0ull, 0ull};
+                }
+              }
+#pragma unroll
+              for (int q = 0; q < TSA_WIDE_CPL; q++) {
+                xx[q].a = (kk[q].a | oo[q].a) & (mm[q].a | dd[q].a);
+                xx[q].b = (kk[q].b | oo[q].b) & (mm[q].b | dd[q].b);
+                tsa_acc<MODE>(cn, kk[q].a, mm[q].a, pp[q].a, oo[q].a, dd[q].a, xx[q].a);
+                tsa_acc<MODE>(cn, kk[q].b, mm[q].b, pp[q].b, oo[q].b, dd[q].b, xx[q].b);
+              }
             }
             uint32_t pk[TsaFlat<MODE>::NP];
             counts_pack<MODE>(cn, pk);
@@ -381,11 +466,83 @@ __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restric
             const float dE = tsa_energy_from_counts<MODE>(cn, P.model, s_lse, T);
             const bool acc = tsa_metropolis(rnd.y, beta, dE, T.exp2);
             if (acc) {
+              if constexpr (SUMS) {
+                // X's chunks inside the union, and P's new summary (OR over the group).  The first round's
+                // chunks are still in registers; later rounds (more than SC * G chunks, rare) rebuild the union
+                // and the set pointers from LDS, so that neither stays live across the energy evaluation
+                uint64_t xs0 = 0, xs1 = 0;
 #pragma unroll
-              for (int q = 0; q < TSA_WIDE_CPL; q++) {
-                const int cc = t + q * G;
-                if (cc < nch) qP[cc] = xx[q];
+                for (int q = 0; q < SC; q++) {
+                  if (ix[q] >= 0) {
+                    qP[ix[q]] = xx[q];
+                    if (xx[q].a | xx[q].b) {
+                      if (ix[q] < 64) xs0 |= 1ull << ix[q];
+                      else xs1 |= 1ull << (ix[q] - 64);
+                    }
+                  }
+                }
+                if (pc > SC * G) {  // uniform within the group
+                  const uint32_t cv2 = ch[v - m];
+                  const int l2 = (int)(cv2 & 0xFFFFu), r2 = (int)(cv2 >> 16);
+                  const int O2 = slotP ? l2 : r2;
+                  const uint32_t cp2 = ch[Pn - m];
+                  const int M2 = slotM ? (int)(cp2 >> 16) : (int)(cp2 & 0xFFFFu);
+                  const int K2 = slotM ? (int)(cp2 & 0xFFFFu) : (int)(cp2 >> 16);
+                  const TsaW2* rD = reinterpret_cast<const TsaW2*>(lab + (size_t)(v - m) * NW);
+                  const TsaW2* rO = reinterpret_cast<const TsaW2*>(O2 >= m ? lab + (size_t)(O2 - m) * NW : leaf + (size_t)O2 * NW);
+                  const TsaW2* rK = reinterpret_cast<const TsaW2*>(K2 >= m ? lab + (size_t)(K2 - m) * NW : leaf + (size_t)K2 * NW);
+                  const TsaW2* rM = reinterpret_cast<const TsaW2*>(M2 >= m ? lab + (size_t)(M2 - m) * NW : leaf + (size_t)M2 * NW);
+                  auto sumw = [&](int n, int q) -> uint64_t {
+                    if (n >= m) return ssum[(size_t)(n - m) * nsw + q];
+                    return lsum_in_lds ? lsum[(size_t)n * nsw + q] : sy.leafsum[(size_t)n * nsw + q];
+                  };
+                  const uint64_t w0 = sumw(v, 0) | sumw(O2, 0) | sumw(K2, 0) | sumw(M2, 0);
+                  const uint64_t w1 = nsw > 1 ? (sumw(v, 1) | sumw(O2, 1) | sumw(K2, 1) | sumw(M2, 1)) : 0ull;
+                  for (int r0 = SC * G; r0 < pc; r0 += SC * G) {
+                    int ii[SC];
+                    sum_pick<G, SC>(w0, w1, r0 + t, ii);
+#pragma unroll
+                    for (int q = 0; q < SC; q++) {
+                      if (ii[q] >= 0) {
+                        const TsaW2 d = rD[ii[q]], o2 = rO[ii[q]], k2 = rK[ii[q]], m2 = rM[ii[q]];
+                        TsaW2 x;
+                        x.a = (k2.a | o2.a) & (m2.a | d.a);
+                        x.b = (k2.b | o2.b) & (m2.b | d.b);
+                        qP[ii[q]] = x;
+                        if (x.a | x.b) {
+                          if (ii[q] < 64) xs0 |= 1ull << ii[q];
+                          else xs1 |= 1ull << (ii[q] - 64);
+                        }
+                      }
+                    }
+                  }
+                }
+#pragma unroll
+                for (int o2 = G / 2; o2 > 0; o2 >>= 1) {
+                  xs0 |= (uint64_t)__shfl_xor((unsigned long long)xs0, o2, G);
+                  xs1 |= (uint64_t)__shfl_xor((unsigned long long)xs1, o2, G);
+                }
+                if (t == 0) {
+                  // this workgroup's copy now (no other visit of the phase reads P's summary), the other
+                  // workgroups' copies from HBM in their replay
+                  ssum[(size_t)(Pn - m) * nsw] = xs0;
+                  gsum[(size_t)(Pn - m) * nsw] = xs0;
+                  if (nsw > 1) {
+                    ssum[(size_t)(Pn - m) * nsw + 1] = xs1;
+                    gsum[(size_t)(Pn - m) * nsw + 1] = xs1;
+                  }
+                }
+              } else {
+#pragma unroll
+                for (int q = 0; q < TSA_WIDE_CPL; q++) {
+                  const int cc = t + q * G;
+                  if (cc < nch) qP[cc] = xx[q];
+                }
               }
+            }
+            if (SUMS && t == 0) {
+              nck += pc;
+              nxk += acc ? pc : 0;
             }
             o = 8u | (acc ? 1u : 0u) | ((uint32_t)slotP << 1) | ((uint32_t)slotM << 2);
             if (t == 0) {
@@ -438,6 +595,8 @@ __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restric
           if (On >= m) par[On - m] = (uint16_t)Pn;
           if (Mn >= m) par[Mn - m] = (uint16_t)v;
           if (P.par_follow && (pv & 1u) && pri[Pn - m] == 0) pri[Pn - m] = (uint16_t)tsa_follow_pri((uint32_t)Pn, hs);
+          if (SUMS && (j < lo || j >= hi))  // P's new summary, written by another workgroup's visit
+            for (int q = 0; q < nsw; q++) ssum[(size_t)(Pn - m) * nsw + q] = gsum[(size_t)(Pn - m) * nsw + q];
         }
         pri[v - m] = 0;
       }
@@ -448,6 +607,7 @@ __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restric
   if (ok && k == 0)
     for (int i = threadIdx.x; i < nint; i += NT) gch[i] = ch[i];
   const long long sp_ = wide_wave_sum(np), sa_ = wide_wave_sum(na), sv_ = wide_wave_sum(nv);
+  const long long sk_ = SUMS ? wide_wave_sum(nck) : 0, sx_ = SUMS ? wide_wave_sum(nxk) : 0;
   if (lane == 0) {  // counters spread over TSA_STAT_SLOTS addresses each, summed by the host
     unsigned long long* st = stats + ((c * 16 + wv) & (TSA_STAT_SLOTS - 1));
     atomicAdd(&st[TSA_ST_PROP * TSA_STAT_SLOTS], (unsigned long long)sp_);
@@ -455,6 +615,10 @@ __global__ void __launch_bounds__(1024) k_wide(TsaKParams P, uint64_t* __restric
     atomicAdd(&st[TSA_ST_VISITS * TSA_STAT_SLOTS], (unsigned long long)sv_);
     atomicAdd(&st[TSA_ST_BUSY * TSA_STAT_SLOTS], (unsigned long long)sv_);
     if (k == 0 && wv == 0) atomicAdd(&st[TSA_ST_STEPS * TSA_STAT_SLOTS], (unsigned long long)nst);
+    if (SUMS) {
+      atomicAdd(&st[TSA_ST_CHUNKS * TSA_STAT_SLOTS], (unsigned long long)sk_);
+      atomicAdd(&st[TSA_ST_XCHUNKS * TSA_STAT_SLOTS], (unsigned long long)sx_);
+    }
   }
   if constexpr (COOP) {
     __syncthreads();
@@ -484,9 +648,9 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
   // LDS (stage != 0): the chain's node costs f32[nint4] and sizes u16[nint4], then (stage == 2) the log2f
   // summary bitmap at the next 16-byte boundary
   extern __shared__ __align__(16) unsigned char s_dyn[];
-  __shared__ uint64_t s_exp2[32];
+  __shared__ uint64_t s_mt[TSA_MT_WORDS];
   __shared__ int s_last;
-  if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
+  tsa_math_stage(s_mt);
   __syncthreads();
   const uint32_t* const gmap = fix + TSA_LOG2FIX_WORDS;
   const int c = blockIdx.x / K2, k = blockIdx.x - c * K2;
@@ -498,7 +662,7 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
   uint16_t* const zz = nz + (size_t)c * nint4;
 
   if (nodes) {
-    const TsaMathTabs T{s_exp2, fix, gmap};
+    const TsaMathTabs T{s_mt, fix, gmap, s_mt + 32};
     const uint32_t* const ch = reinterpret_cast<const uint32_t*>(lab + P.ch_off);
     const int gpb = (int)blockDim.x / G, grp = (int)threadIdx.x / G, t = (int)threadIdx.x & (G - 1);
     const int npb = (nint + K2 - 1) / K2, i0 = k * npb, i1 = (i0 + npb < nint) ? i0 + npb : nint;
@@ -570,33 +734,36 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
     if (!s_last) return;
   }
 
-  wide_fold(P, c, cst, zz, S, leaf, fix, s_exp2, stage, s_dyn, lc, sc, ns);
+  wide_fold(P, c, cst, zz, S, leaf, fix, s_mt, stage, s_dyn, lc, sc, ns);
 }
 
-template <int G, int MODE>
-hipError_t launch_wide_gm(const TsaWide& X, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
-                          const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
-                          unsigned long long* stats, const TsaWideSync& sy, hipStream_t st) {
+template <int G, int MODE, bool SUMS>
+hipError_t launch_wide_gms(const TsaWide& X, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
+                           const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
+                           unsigned long long* stats, const TsaWideSync& sy, hipStream_t st) {
   if (X.K > 1) {
-    TsaKParams p = P;
-    int K = X.K;
-    TsaWideSync s = sy;
-    void* args[] = {&p, &rec, &leaf, &fix, &nchains, &K, &beta, &sweep0, &nsweeps, &stats, &s};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&k_wide<G, MODE, true>), dim3(nchains * X.K),
-                                      dim3(X.nt), args, (unsigned)X.smem, st);
+    // an ordinary launch: the plan admits K > 1 only when all nchains * K workgroups fit on the device at
+    // once, so on an idle device they are all resident together (the cooperative launch API gives the same
+    // guarantee but costs tens of microseconds per launch on the host side); if they ever are not, a chain
+    // barrier runs out of polls, sets the error word and every workgroup leaves
+    hipLaunchKernelGGL((k_wide<G, MODE, true, SUMS>), dim3(nchains * X.K), dim3(X.nt), (size_t)X.smem, st, P, rec,
+                       leaf, fix, nchains, X.K, beta, sweep0, nsweeps, stats, sy);
+    return hipGetLastError();
   }
-  hipLaunchKernelGGL((k_wide<G, MODE, false>), dim3(nchains), dim3(X.nt), (size_t)X.smem, st, P, rec, leaf, fix,
-                     nchains, 1, beta, sweep0, nsweeps, stats, sy);
+  hipLaunchKernelGGL((k_wide<G, MODE, false, SUMS>), dim3(nchains), dim3(X.nt), (size_t)X.smem, st, P, rec, leaf,
+                     fix, nchains, 1, beta, sweep0, nsweeps, stats, sy);
   return hipGetLastError();
 }
 
-template <int G>
+template <int G, bool SUMS>
 hipError_t launch_wide_g(const TsaWide& X, int mode, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
                          const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
                          unsigned long long* stats, const TsaWideSync& sy, hipStream_t st) {
-  if (mode == 0) return launch_wide_gm<G, 0>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-  if (mode == 1) return launch_wide_gm<G, 1>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-  return launch_wide_gm<G, 2>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+  if (mode == 0)
+    return launch_wide_gms<G, 0, SUMS>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+  if (mode == 1)
+    return launch_wide_gms<G, 1, SUMS>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+  return launch_wide_gms<G, 2, SUMS>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
 }
 
 template <int G, int MODE>
@@ -620,29 +787,26 @@ hipError_t launch_wcost_g(const TsaWide& X, int mode, const TsaKParams& P, const
   return launch_wcost_gm<G, 2>(X, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
 }
 
-// Largest number of co-resident workgroups per CU of the cooperative sweep kernel over the three modes, at
-// smem bytes of dynamic LDS.  Raises the dynamic-LDS cap of every sweep and energy instantiation of this G to
+// Largest number of co-resident workgroups per CU of the multi-workgroup sweep kernel over the three modes,
+// at smem bytes of dynamic LDS.  Raises the dynamic-LDS cap of every sweep instantiation of this G to
 // lds_cap first (the largest any context asks for).
-template <int G>
+template <int G, bool SUMS>
 hipError_t wide_occupancy(int nt, int smem, int lds_cap, int* per_cu) {
-  const void* fns[3] = {reinterpret_cast<const void*>(&k_wide<G, 0, true>),
-                        reinterpret_cast<const void*>(&k_wide<G, 1, true>),
-                        reinterpret_cast<const void*>(&k_wide<G, 2, true>)};
-  const void* others[6] = {reinterpret_cast<const void*>(&k_wide<G, 0, false>),
-                           reinterpret_cast<const void*>(&k_wide<G, 1, false>),
-                           reinterpret_cast<const void*>(&k_wide<G, 2, false>),
-                           reinterpret_cast<const void*>(&k_wcost<G, 0>),
-                           reinterpret_cast<const void*>(&k_wcost<G, 1>),
-                           reinterpret_cast<const void*>(&k_wcost<G, 2>)};
-  for (int i = 0; i < 9; i++) {
-    const hipError_t e = hipFuncSetAttribute(i < 3 ? fns[i] : others[i - 3],
-                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds_cap);
+  const void* coop[3] = {reinterpret_cast<const void*>(&k_wide<G, 0, true, SUMS>),
+                         reinterpret_cast<const void*>(&k_wide<G, 1, true, SUMS>),
+                         reinterpret_cast<const void*>(&k_wide<G, 2, true, SUMS>)};
+  const void* one[3] = {reinterpret_cast<const void*>(&k_wide<G, 0, false, SUMS>),
+                        reinterpret_cast<const void*>(&k_wide<G, 1, false, SUMS>),
+                        reinterpret_cast<const void*>(&k_wide<G, 2, false, SUMS>)};
+  for (int i = 0; i < 6; i++) {
+    const hipError_t e =
+        hipFuncSetAttribute(i < 3 ? coop[i] : one[i - 3], hipFuncAttributeMaxDynamicSharedMemorySize, lds_cap);
     if (e != hipSuccess) return e;
   }
   int best = 1 << 30;
   for (int i = 0; i < 3; i++) {
     int nb = 0;
-    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fns[i], nt, (size_t)smem);
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, coop[i], nt, (size_t)smem);
     if (e != hipSuccess) return e;
     best = nb < best ? nb : best;
   }
@@ -650,24 +814,86 @@ hipError_t wide_occupancy(int nt, int smem, int lds_cap, int* per_cu) {
   return hipSuccess;
 }
 
-hipError_t wide_occupancy_g(int G, int nt, int smem, int lds_cap, int* per_cu) {
+template <int G>
+hipError_t wcost_lds_cap(int lds_cap) {
+  const void* fns[3] = {reinterpret_cast<const void*>(&k_wcost<G, 0>), reinterpret_cast<const void*>(&k_wcost<G, 1>),
+                        reinterpret_cast<const void*>(&k_wcost<G, 2>)};
+  for (int i = 0; i < 3; i++) {
+    const hipError_t e = hipFuncSetAttribute(fns[i], hipFuncAttributeMaxDynamicSharedMemorySize, lds_cap);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t wide_occupancy_g(int G, bool sums, int nt, int smem, int lds_cap, int* per_cu) {
+  if (sums) {
+    switch (G) {
+      case 1: return wide_occupancy<1, true>(nt, smem, lds_cap, per_cu);
+      case 2: return wide_occupancy<2, true>(nt, smem, lds_cap, per_cu);
+      case 4: return wide_occupancy<4, true>(nt, smem, lds_cap, per_cu);
+      case 8: return wide_occupancy<8, true>(nt, smem, lds_cap, per_cu);
+      case 16: return wide_occupancy<16, true>(nt, smem, lds_cap, per_cu);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (G) {
-    case 4: return wide_occupancy<4>(nt, smem, lds_cap, per_cu);
-    case 8: return wide_occupancy<8>(nt, smem, lds_cap, per_cu);
-    case 16: return wide_occupancy<16>(nt, smem, lds_cap, per_cu);
-    case 32: return wide_occupancy<32>(nt, smem, lds_cap, per_cu);
-    default: return wide_occupancy<64>(nt, smem, lds_cap, per_cu);
+    case 4: return wide_occupancy<4, false>(nt, smem, lds_cap, per_cu);
+    case 8: return wide_occupancy<8, false>(nt, smem, lds_cap, per_cu);
+    case 16: return wide_occupancy<16, false>(nt, smem, lds_cap, per_cu);
+    case 32: return wide_occupancy<32, false>(nt, smem, lds_cap, per_cu);
+    case 64: return wide_occupancy<64, false>(nt, smem, lds_cap, per_cu);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t wcost_lds_cap_g(int G, int lds_cap) {
+  switch (G) {
+    case 4: return wcost_lds_cap<4>(lds_cap);
+    case 8: return wcost_lds_cap<8>(lds_cap);
+    case 16: return wcost_lds_cap<16>(lds_cap);
+    case 32: return wcost_lds_cap<32>(lds_cap);
+    case 64: return wcost_lds_cap<64>(lds_cap);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+// Summaries of every internal set of every chain: one wave per set, lane l tests chunks l and l + 64.
+__global__ void __launch_bounds__(256) k_wsum(TsaKParams P, const uint64_t* __restrict__ rec, int nchains, int nsw,
+                                              uint64_t* __restrict__ sum) {
+  const int lane = threadIdx.x & 63, nint = P.nint, nint4 = (nint + 3) & ~3, nch = P.W >> 1;
+  const long long nsets = (long long)nchains * nint;
+  const long long step = (long long)gridDim.x * (blockDim.x >> 6);
+  for (long long s = (long long)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); s < nsets; s += step) {
+    const int c = (int)(s / nint), i = (int)(s - (long long)c * nint);
+    const TsaW2* q = reinterpret_cast<const TsaW2*>(rec + (size_t)c * P.chain_words + (size_t)i * P.W);
+    for (int h = 0; h < nsw; h++) {
+      const int cc = h * 64 + lane;
+      bool nz = false;
+      if (cc < nch) {
+        const TsaW2 x = q[cc];
+        nz = (x.a | x.b) != 0ull;
+      }
+      const uint64_t b = __ballot(nz);
+      if (lane == 0) sum[((size_t)c * nint4 + i) * nsw + h] = b;
+    }
   }
 }
 
 }  // namespace
 
-hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int want_k, TsaWide* out) {
+hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int want_k, int want_g, int sums,
+                         TsaWide* out) {
   TsaWide X{};
   const int nch = P.W / 2;
   if ((P.W & 1) || nch < 1 || nch > TSA_WIDE_CPL * 64) return hipErrorInvalidValue;
-  int G = 4;
-  while (G < 64 && (nch + G - 1) / G > TSA_WIDE_CPL) G *= 2;
+  // dense streaming needs G * TSA_WIDE_CPL >= chunks per set; the energy kernel always streams densely
+  int Gd = 4;
+  while (Gd < 64 && (nch + Gd - 1) / Gd > TSA_WIDE_CPL) Gd *= 2;
+  X.nsw = (sums > 0 || (sums == 0 && P.W >= 64)) ? (nch + 63) / 64 : 0;
+  // summaries: one lane per proposal (the union of a visit is a few chunks: whole-wave SIMD efficiency
+  // matters more than spreading loads) and one workgroup per chain (no chain barriers)
+  int G = want_g > 0 ? want_g : (X.nsw ? 1 : Gd);
+  if (X.nsw ? (G < 1 || G > 16 || (G & (G - 1))) : (G < Gd || G > 64 || (G & (G - 1)))) return hipErrorInvalidValue;
   X.G = G;
   int dev = 0, ncu = 0, lds_max = 0;
   hipError_t e = hipGetDevice(&dev);
@@ -676,30 +902,46 @@ hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int w
   if (e != hipSuccess) return e;
   // measured on MI355X: with at least one chain per CU, one 8-wave workgroup per chain streams best; with
   // fewer chains, 16-wave workgroups, as many per chain as stay co-resident
-  int waves = want_waves > 0 ? want_waves : (nchains >= ncu ? 8 : 16);
-  waves = waves < 1 ? 1 : (waves > 16 ? 16 : waves);
+  // (the summary path is compiled for at most 8 waves per workgroup: its visit needs more registers)
+  const int max_waves = X.nsw ? 8 : 16;
+  int waves = want_waves > 0 ? want_waves : (nchains >= ncu ? 8 : max_waves);
+  waves = waves < 1 ? 1 : (waves > max_waves ? max_waves : waves);
   X.nt = 64 * waves;
   const int band = P.par_band > 0 ? 1 : 0;
-  const TsaWideLds L1 = tsa_wide_lds(P.nint, band, 0), Lc = tsa_wide_lds(P.nint, band, 1);
-  if (L1.bytes > lds_max) return hipErrorInvalidValue;
-  int per_cu = 0;
-  // the fold stages a chain's node costs (6 B per node) and, when it also fits, the log2f summary bitmap
   // dynamic LDS cap: the device maximum less room for the kernels' static LDS (under 1 KB today)
-  const int nint4 = (P.nint + 3) & ~3, fold_budget = lds_max - 4096;
-  X.fold_smem = nint4 * 6 <= fold_budget ? nint4 * 6 : 0;
+  const int nint4 = (P.nint + 3) & ~3, lds_cap = lds_max - 4096;
+  if (X.nsw) {  // the input tensors' summaries go to LDS too when they fit
+    X.lsum_lds = tsa_wide_lds(P.nint, band, 0, X.nsw, P.m).bytes <= lds_cap ? 1 : 0;
+    if (!X.lsum_lds && tsa_wide_lds(P.nint, band, 0, X.nsw, 0).bytes > lds_cap) {
+      if (sums > 0 || want_g > 0) return hipErrorInvalidValue;
+      X.nsw = 0;  // automatic summaries: the summary table does not fit beside the node arrays
+      G = Gd;
+      X.G = G;
+      waves = want_waves > 0 ? want_waves : (nchains >= ncu ? 8 : 16);
+      waves = waves < 1 ? 1 : (waves > 16 ? 16 : waves);
+      X.nt = 64 * waves;
+    }
+  }
+  const int mlds = X.lsum_lds ? P.m : 0;
+  const TsaWideLds L1 = tsa_wide_lds(P.nint, band, 0, X.nsw, mlds), Lc = tsa_wide_lds(P.nint, band, 1, X.nsw, mlds);
+  if (L1.bytes > lds_cap) return hipErrorInvalidValue;
+  // the fold stages a chain's node costs (6 B per node) and, when it also fits, the log2f summary bitmap
+  X.fold_smem = nint4 * 6 <= lds_cap ? nint4 * 6 : 0;
   X.fold_smem_map = ((nint4 * 6 + 15) & ~15) + (int)TSA_LOG2MAP_WORDS * 4;
-  X.fold_stage = X.fold_smem == 0 ? 0 : (X.fold_smem_map <= fold_budget ? 2 : 1);
-  e = wide_occupancy_g(G, X.nt, L1.bytes, fold_budget, &per_cu);
+  X.fold_stage = X.fold_smem == 0 ? 0 : (X.fold_smem_map <= lds_cap ? 2 : 1);
+  int per_cu = 0;
+  e = wide_occupancy_g(G, X.nsw > 0, X.nt, L1.bytes, lds_cap, &per_cu);
+  if (e == hipSuccess) e = wcost_lds_cap_g(Gd, lds_cap);
   if (e != hipSuccess) return e;
   if (per_cu < 1) return hipErrorInvalidValue;
   const int cap = per_cu * ncu;
-  int K = want_k > 0 ? want_k : cap / nchains;
+  int K = want_k > 0 ? want_k : (X.nsw ? 1 : cap / nchains);
   K = K < 1 ? 1 : (K > TSA_WIDE_MAX_K ? TSA_WIDE_MAX_K : K);
   if (K > 1 && K * nchains > cap) return hipErrorCooperativeLaunchTooLarge;
   X.K = K;
   X.smem = K > 1 ? Lc.bytes : L1.bytes;
-  X.eG = G;
-  const int gpb = 256 / G, maxk = (P.nint + gpb - 1) / gpb;
+  X.eG = Gd;
+  const int gpb = 256 / Gd, maxk = (P.nint + gpb - 1) / gpb;
   int eK = (4 * ncu + nchains - 1) / nchains;
   X.eK = eK < 1 ? 1 : (eK > maxk ? maxk : eK);
   X.on = 1;
@@ -710,14 +952,34 @@ hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int w
 hipError_t tsa_launch_wide(const TsaWide& X, int mode, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
                            const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
                            unsigned long long* stats, const TsaWideSync& sy, hipStream_t st) {
+  if (X.nsw) {
+    switch (X.G) {
+      case 1: return launch_wide_g<1, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+      case 2: return launch_wide_g<2, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+      case 4: return launch_wide_g<4, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+      case 8: return launch_wide_g<8, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+      case 16: return launch_wide_g<16, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+      default: return hipErrorInvalidValue;
+    }
+  }
   switch (X.G) {
-    case 4: return launch_wide_g<4>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-    case 8: return launch_wide_g<8>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-    case 16: return launch_wide_g<16>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-    case 32: return launch_wide_g<32>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-    case 64: return launch_wide_g<64>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    case 4: return launch_wide_g<4, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    case 8: return launch_wide_g<8, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    case 16: return launch_wide_g<16, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    case 32: return launch_wide_g<32, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    case 64: return launch_wide_g<64, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t tsa_launch_wsum(const TsaWide& X, const TsaKParams& P, const uint64_t* rec, int nchains, uint64_t* sum,
+                           hipStream_t st) {
+  if (!X.nsw) return hipSuccess;
+  const long long nsets = (long long)nchains * P.nint;
+  const long long nb = (nsets + 3) / 4;
+  const int grid = (int)(nb < 8192 ? nb : 8192);
+  hipLaunchKernelGGL(k_wsum, dim3(grid), dim3(256), 0, st, P, rec, nchains, X.nsw, sum);
+  return hipGetLastError();
 }
 
 hipError_t tsa_launch_wide_energy(const TsaWide& X, int mode, const TsaKParams& P, const uint64_t* rec,

@@ -32,7 +32,7 @@ struct Opts {
   bool check = false, quiet = false, cross = true, wide = false, slicing = false, no_sum = false, force_sum = false;
   bool select_sc = false;
   int slice_moves = 1, slice_every = 1, max_slices = 0, random_slices = 0;
-  int coop_max = 0, coop_min_units = -1, coop_min = 1, coop_full = 0, coop_cpl = 2, par_follow = 0, par_band = 0, wpc = 0, wide_wgs = 0;
+  int coop_max = 0, coop_min_units = -1, coop_min = 1, coop_full = 0, coop_cpl = 2, par_follow = 0, par_band = 0, wpc = 0, wide_wgs = 0, wide_lanes = 0;
   double sc_target = 20.0, sc_weight = 1.0, trunc_frac = 0.25;
   uint64_t seed = 1;
   ModelConsts mc;
@@ -59,7 +59,7 @@ std::string jnum(double x) {
           "  [--stage2-betas SPEC [--stage2-niters K] [--stage2-mode gpu|h100]]  (continue the population)\n"
           "  [--sc-target x] [--sc-weight y] [--scheme indep|pa|trunc] [--trunc-frac f]\n"
           "  [--slicing [--slice-moves k] [--slice-every s] [--max-slices n] [--init-slices l1,l2,..]]\n"
-          "  [--order par|preorder] [--kernel auto|seq|seqsm|warp|warpsm|block|par [--wpc n]] [--lpc 32|16|8] [--coop-max G] [--coop-min G0] [--coop-full G1] [--par-follow] [--par-band L] [--coop-min-units u] [--wide] [--sums|--no-sum] [--select-sc] [--block B] [--wpb W] [--seed s] [--wide-wgs K]\n"
+          "  [--order par|preorder] [--kernel auto|seq|seqsm|warp|warpsm|block|par [--wpc n]] [--lpc 32|16|8] [--coop-max G] [--coop-min G0] [--coop-full G1] [--par-follow] [--par-band L] [--coop-min-units u] [--wide] [--sums|--no-sum] [--select-sc] [--block B] [--wpb W] [--seed s] [--wide-wgs K] [--wide-lanes G]\n"
           "  [--eval-every k] [--out result.json] [--check [--ref-chains R] [--random-slices k]] [--quiet]\n"
           "  [--bench-warmup W]  (W untimed levels first, then the initial population again)\n"
           "  [--host-select]  (select the best chain on the host at every level, also for --scheme indep)\n");
@@ -134,6 +134,7 @@ Opts parse(int argc, char** argv) {
       else if (a == "--par-band") o.par_band = std::stoi(nx());
       else if (a == "--wpc") o.wpc = std::stoi(nx());
       else if (a == "--wide-wgs") o.wide_wgs = std::stoi(nx());
+      else if (a == "--wide-lanes") o.wide_lanes = std::stoi(nx());
       else if (a == "--wide") o.wide = true;
       else if (a == "--no-sum") o.no_sum = true;
       else if (a == "--select-sc") o.select_sc = true;
@@ -210,7 +211,9 @@ class Runner {
     cfg.v2_small_rank = ML.v2_small_rank;
     cfg.wide_waves = O.wpc > 0 ? (O.wpc + 1) / 2 : 0;  // --wpc counts 32-lane warps
     cfg.wide_wgs = O.wide_wgs;
+    cfg.wide_lanes = O.wide_lanes;
     cfg.fused_energy = O.eval_every == 1 ? 1 : 0;  // every level is evaluated: the sweep kernel evaluates too
+    cfg.sums = O.no_sum ? -1 : (O.force_sum ? 1 : 0);
   }
   ~Runner() {
     if (ctx) tsa_destroy(ctx);
@@ -365,7 +368,7 @@ int Runner::run_anneal() {
   bool staged = false;
   uint32_t sweep_ctr = 0;
   const double t_start = now_s();
-  uint64_t stats0[7] = {0, 0, 0, 0, 0, 0, 0};
+  uint64_t stats0[7] = {0, 0, 0, 0, 0, 0, 0}, chunks0[2] = {0, 0};
   {
     const std::vector<uint64_t> pop = init_population();  // input errors surface before the device is touched
     create(&ctx, cfg.kernel);
@@ -395,6 +398,7 @@ int Runner::run_anneal() {
       ck(tsa_sweeps_ms(ctx, &ms));
       ck(tsa_upload(ctx, pop.data()));
       ck(tsa_stats(ctx, stats0));
+      ck(tsa_chunk_stats(ctx, chunks0));
     }
   }
   const double t_init = now_s() - t_start;
@@ -505,9 +509,11 @@ int Runner::run_anneal() {
     }
   }
   const double t_anneal = now_s() - t0;
-  uint64_t stats[7];
+  uint64_t stats[7], chunks[2];
   ck(tsa_stats(ctx, stats));
   for (int k = 0; k < 7; k++) stats[k] -= stats0[k];
+  ck(tsa_chunk_stats(ctx, chunks));
+  for (int k = 0; k < 2; k++) chunks[k] -= chunks0[k];
 
   // final best tree: verified from scratch; with slicing, sc > sc_target is repaired greedily
   const uint32_t* bch = chCh(best.data());
@@ -529,6 +535,9 @@ int Runner::run_anneal() {
   if (!f) die("cannot open " + O.out);
   char desc[256] = {0};
   tsa_describe(ctx, desc, sizeof desc);
+  // summary words per label set in the reference's 32-bit count (one bit per 16-byte chunk)
+  const char* sp = strstr(desc, " sums=");
+  const int nsum = (sp && atoi(sp + 6) > 0) ? (lay.W / 2 + 31) / 32 : 0;
   fprintf(f, "{\"tc\": %.6f, \"sc\": %d, \"gpu_time\": %s, \"h100_time\": %s, \"valid\": %s, \"labels_ok\": %s, \"best_chain\": %d,\n",
           HE.tc, HE.sc, jnum(HE.time).c_str(), jnum(HE.time2).c_str(), valid ? "true" : "false",
           labels_ok ? "true" : "false", best_chain);
@@ -544,11 +553,13 @@ int Runner::run_anneal() {
   fprintf(f, "],\n \"t_anneal\": %.6f, \"t_init\": %.6f, \"kernel_s\": %.6f, \"proposals\": %llu, \"accepts\": %llu, \"warp_steps\": %llu, \"node_visits\": %llu, \"slice_proposals\": %llu, \"slice_accepts\": %llu, \"busy_lanes\": %llu, \"coop_max\": %d, \"coop_min\": %d, \"coop_full\": %d, \"par_follow\": %d, \"par_band\": %d, \"nsum\": %d, \"wpc\": %d, \"order\": \"%s\",\n",
           t_anneal, t_init, ks, (unsigned long long)stats[0], (unsigned long long)stats[1], (unsigned long long)stats[2],
           (unsigned long long)stats[3], (unsigned long long)stats[4], (unsigned long long)stats[5],
-          (unsigned long long)stats[6], 1, 1, 1, O.par_follow, O.par_band, 0, 1,
+          (unsigned long long)stats[6], 1, 1, 1, O.par_follow, O.par_band, nsum, 1,
           order == TSA_ORDER_PAR ? "par" : "preorder");
   fprintf(f, " \"nchains\": %d, \"niters\": %d, \"nlevels\": %zu, \"total_sweeps\": %u, \"W\": %d, \"nw\": %d, \"word_bits\": 64, \"lpc\": 64, \"kernel\": \"%s\", \"hip_kernel\": \"%s\", \"scheme\": \"%s\", \"mode\": %d, \"nresample\": %d,\n",
           nc, O.niters, betas.size(), sweep_ctr, lay.runtime_width ? 0 : lay.W, lay.W, kernel_name().c_str(), desc,
           O.scheme.c_str(), O.mode, nresample);
+  fprintf(f, " \"sum_chunks\": %llu, \"sum_xchunks\": %llu,\n", (unsigned long long)chunks[0],
+          (unsigned long long)chunks[1]);
   if (staged)
     fprintf(f, " \"stage1_tc\": %.6f, \"stage1_sc\": %d, \"stage1_nsliced\": %d, \"stage1_gpu_time\": %s, \"stage1_h100_time\": %s, \"stage1_h100_time_total\": %s,\n",
             H1.tc, H1.sc, H1.ns, jnum(H1.time).c_str(), jnum(H1.time2).c_str(),
