@@ -149,8 +149,10 @@ int tsa_chunk_stats(tsa_ctx* ctx, uint64_t out[2]);
  * tsa_track enqueues the energy kernel and a selection kernel that scores every chain (lower is better,
  * the reference's score, csrc/treesa_gpu.cu:1737-1748, evaluated with the restated double log2 / exp2 of
  * tsa_select.h), keeps the lowest score over all tracked levels (first chain and first level on ties, as
- * the reference's loop at csrc/treesa_gpu.cu:1810-1824) and snapshots that chain's record on the device,
- * and writes one trace row per tracked level.  Nothing synchronizes until tsa_track_end. */
+ * the reference's loop at csrc/treesa_gpu.cu:1810-1824) and copies that chain's tree (children words and
+ * S) on the device, and writes one trace row per tracked level.  On the wide path each sweep launch leaves
+ * a snapshot of the trees and node costs, and the energy fold and selection of a level run on a second
+ * stream beside the next level's sweep.  Nothing synchronizes until tsa_track_end. */
 typedef struct tsa_select_t {
   int32_t mode, slicing, select_sc;
   double sc_target, sc_weight;
@@ -170,14 +172,22 @@ typedef struct tsa_trace_row_t {
 int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t max_levels);
 /* Enqueue energy + selection for level (0 <= level < max_levels).  Asynchronous. */
 int tsa_track(tsa_ctx* ctx, int32_t level);
-/* Wait and return the best over the tracked levels (best_chain -1 if none), its record (chain_words words),
- * max_levels trace rows (rows of untracked levels are zero) and the device wall-clock rate in Hz;
- * ticks0 = device wall clock at tsa_track_begin. */
+/* Wait and return the best over the tracked levels (best_chain -1 if none), its tree in best_record (a
+ * chain_words record of which the children words and S are written; its label words are a function of the
+ * tree and are left as they were), max_levels trace rows (rows of untracked levels are zero) and the device
+ * wall-clock rate in Hz; ticks0 = device wall clock at tsa_track_begin. */
 int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_level, double* best_score, uint64_t* best_record,
                   tsa_trace_row_t* rows, uint64_t* ticks0, double* tick_hz);
 
 /* Human-readable description of the kernels this context launches (name, lanes, LDS bytes). */
 int tsa_describe(tsa_ctx* ctx, char* buf, int32_t len);
+
+/* Page-locked host memory for buffers the library copies chain records into (tsa_download,
+ * tsa_track_end): copies into it run at the link's full speed instead of through the runtime's staging of
+ * pageable memory.  NULL on failure; tsa_host_free(NULL) is a no-op.  No counterpart in the reference (it
+ * copies into pageable memory); for callers that time the whole level loop. */
+void* tsa_host_alloc(size_t bytes);
+void tsa_host_free(void* p);
 
 /* Release everything.  Replaces Runner::release, csrc/treesa_gpu.cu:1579-1582. */
 int tsa_destroy(tsa_ctx* ctx);

@@ -25,7 +25,7 @@ DEFAULT_H100 = (4e-6, 1.23e13, 5.44e-14, 7.68e-15, 6.37e-14, 2.02e-16, 1.77e-13,
 
 EXPORTS = ("tsa_layout", "tsa_create", "tsa_upload", "tsa_download", "tsa_sweeps", "tsa_sweeps_ms", "tsa_energy",
            "tsa_resample", "tsa_set_mode", "tsa_stats", "tsa_chunk_stats", "tsa_describe", "tsa_destroy", "tsa_last_error",
-           "tsa_host_math")
+           "tsa_host_math", "tsa_host_alloc", "tsa_host_free")
 
 
 class Layout(ctypes.Structure):
@@ -78,6 +78,10 @@ def load():
     lib.tsa_last_error.restype = ctypes.c_char_p
     lib.tsa_host_math.argtypes = [I32, F32]
     lib.tsa_host_math.restype = F32
+    lib.tsa_host_alloc.argtypes = [ctypes.c_size_t]
+    lib.tsa_host_alloc.restype = P
+    lib.tsa_host_free.argtypes = [P]
+    lib.tsa_host_free.restype = None
     _lib = lib
     return lib
 

@@ -60,6 +60,19 @@ struct tsa_ctx {
                                // the last sweep launch, cfg.fused_energy)
   TsaTrackPart* d_tpart = nullptr;  // selection kernel: per-workgroup results and its counter
   unsigned* d_tdone = nullptr;
+  // Overlapped tracking on the wide path: each sweep launch leaves a snapshot of every chain's tree and
+  // node costs in slot `slot` (two slots, alternating), and tsa_track runs the fold and the selection of that
+  // snapshot on the second stream st2 while st goes on with the next level's sweep.  ev_sweep[s] marks the
+  // sweep that filled slot s, ev_track[s] the selection that read it (a sweep waits for it before it
+  // overwrites the slot).
+  bool overlap = false;
+  hipStream_t st2 = nullptr;
+  hipEvent_t ev_sweep[2] = {nullptr, nullptr}, ev_track[2] = {nullptr, nullptr};
+  bool track_pending[2] = {false, false};
+  int slot = 0, last_slot = -1;  // slot of the next sweep launch / of the last one (-1: none since a reset)
+  uint32_t* d_snap_ch[2] = {nullptr, nullptr};
+  float* d_snap_cost[2] = {nullptr, nullptr};
+  uint16_t* d_snap_nz[2] = {nullptr, nullptr};
   std::string err;
 };
 
@@ -217,6 +230,15 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_tpart) (void)hipFree(c->d_tpart);
   if (c->d_tdone) (void)hipFree(c->d_tdone);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
+  if (c->st2) (void)hipStreamSynchronize(c->st2);
+  for (int k = 0; k < 2; k++) {
+    if (c->ev_sweep[k]) (void)hipEventDestroy(c->ev_sweep[k]);
+    if (c->ev_track[k]) (void)hipEventDestroy(c->ev_track[k]);
+    if (c->d_snap_ch[k]) (void)hipFree(c->d_snap_ch[k]);
+    if (c->d_snap_cost[k]) (void)hipFree(c->d_snap_cost[k]);
+    if (c->d_snap_nz[k]) (void)hipFree(c->d_snap_nz[k]);
+  }
+  if (c->st2) (void)hipStreamDestroy(c->st2);
   if (c->d_track) (void)hipFree(c->d_track);
   if (c->d_trace) (void)hipFree(c->d_trace);
   if (c->d_best) (void)hipFree(c->d_best);
@@ -441,7 +463,24 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   return TSA_OK;
 }
 
+// Overlapped tracking: order the main stream after every selection still pending on st2 (they read d_lc /
+// d_sc / d_ns and write the tracking state), or wait for st2 on the host and forget the snapshots (before
+// the population is replaced).
+static void join_track(tsa_ctx* c) {
+  for (int k = 0; k < 2; k++)
+    if (c->track_pending[k]) (void)hipStreamWaitEvent(c->st, c->ev_track[k], 0);
+}
+
+static hipError_t quiesce_track(tsa_ctx* c) {
+  hipError_t e = hipSuccess;
+  if (c->st2) e = hipStreamSynchronize(c->st2);
+  c->track_pending[0] = c->track_pending[1] = false;
+  c->last_slot = -1;
+  return e;
+}
+
 static hipError_t launch_energy(tsa_ctx* c) {
+  join_track(c);
   if (c->energy_fresh) return hipSuccess;  // the last sweep launch left them in d_lc / d_sc / d_ns
   if (c->wide.on) {
     const hipError_t e = tsa_launch_wide_energy(c->wide, c->mode, c->P, c->d_rec, c->d_leaf, c->d_fix, c->nchains,
@@ -475,6 +514,7 @@ extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
     if (!valid_tree(reinterpret_cast<const uint32_t*>(rec + L.ch_off), L.m, seen, st))
       return fail(ctx, TSA_ERR_ARG, "tsa_upload: chain " + std::to_string(c) + " is not a valid tree");
   }
+  TSA_HIP(ctx, quiesce_track(ctx));
   ctx->costs_valid = false;
   ctx->energy_fresh = false;
   ctx->sums_valid = false;
@@ -514,11 +554,36 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
       TSA_HIP(ctx, tsa_launch_wsum(ctx->wide, ctx->P, ctx->d_rec, ctx->nchains, ctx->d_sum, ctx->st));
       ctx->sums_valid = true;
     }
+    TsaWideSync sy = ctx->wsync;
+    int s = -1;
+    if (ctx->overlap) {
+      // the node-cost cache must be exact before the sweep: the snapshot it leaves is folded as it stands
+      if (!ctx->costs_valid) {
+        join_track(ctx);
+        TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
+                                            ctx->nchains, ctx->d_ncost, ctx->d_nz, ctx->d_fcnt, ctx->d_lc, ctx->d_sc,
+                                            ctx->d_ns, 1, ctx->st));
+        ctx->costs_valid = true;
+      }
+      s = ctx->slot;
+      if (ctx->track_pending[s]) TSA_HIP(ctx, hipStreamWaitEvent(ctx->st, ctx->ev_track[s], 0));
+      ctx->track_pending[s] = false;
+      sy.snap_ch = ctx->d_snap_ch[s];
+      sy.snap_cost = ctx->d_snap_cost[s];
+      sy.snap_nz = ctx->d_snap_nz[s];
+    }
     TSA_HIP(ctx, tsa_launch_wide(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains, beta,
-                                 sweep0, nsweeps, ctx->d_stats, ctx->wsync, ctx->st));
+                                 sweep0, nsweeps, ctx->d_stats, sy, ctx->st));
+    if (s >= 0) {
+      TSA_HIP(ctx, hipEventRecord(ctx->ev_sweep[s], ctx->st));
+      ctx->last_slot = s;
+      ctx->slot = s ^ 1;
+    }
   } else {
     ctx->costs_valid = false;
     ctx->sums_valid = false;
+    ctx->last_slot = -1;  // the snapshots no longer describe the population
+    join_track(ctx);      // a pending fold may still read the node-cost snapshot; d_lc is rewritten below
     const bool fuse = ctx->cfg.fused_energy != 0;
     const TsaEnergyOut eo{fuse ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns};
     TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
@@ -568,6 +633,20 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
     TSA_HIP(ctx, hipMalloc(&ctx->d_trace, (size_t)max_levels * sizeof(TsaTraceRowD)));
   }
   ctx->track_levels = max_levels;
+  TSA_HIP(ctx, quiesce_track(ctx));
+  if (ctx->wide.on && !ctx->st2) {  // the wide path folds and selects beside the next level's sweep
+    const size_t nint = (size_t)ctx->lay.nint, nint4 = (nint + 3) & ~(size_t)3;
+    TSA_HIP(ctx, hipStreamCreateWithFlags(&ctx->st2, hipStreamNonBlocking));
+    for (int k = 0; k < 2; k++) {
+      TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_sweep[k], hipEventDisableTiming));
+      TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_track[k], hipEventDisableTiming));
+      TSA_HIP(ctx, hipMalloc(&ctx->d_snap_ch[k], (size_t)ctx->nchains * nint * 4));
+      TSA_HIP(ctx, hipMalloc(&ctx->d_snap_cost[k], (size_t)ctx->nchains * nint4 * 4));
+      TSA_HIP(ctx, hipMalloc(&ctx->d_snap_nz[k], (size_t)ctx->nchains * nint4 * 2));
+    }
+  }
+  ctx->overlap = ctx->st2 != nullptr;
+  ctx->slot = 0;
   TSA_HIP(ctx, hipMemsetAsync(ctx->d_trace, 0, (size_t)max_levels * sizeof(TsaTraceRowD), ctx->st));
   TSA_HIP(ctx, hipMemsetAsync(ctx->d_best, 0, (size_t)ctx->lay.chain_words * 8, ctx->st));
   TSA_HIP(ctx, tsa_launch_track_init(ctx->d_track, ctx->d_ticks0, ctx->st));
@@ -578,12 +657,28 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_track: null context");
   if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_track: no tsa_track_begin");
   if (level < 0 || level >= ctx->track_levels) return fail(ctx, TSA_ERR_ARG, "tsa_track: level out of range");
-  TSA_HIP(ctx, launch_energy(ctx));
   TsaSelect S = ctx->sel;
   S.mode = ctx->mode;
-  TSA_HIP(ctx, tsa_launch_track(ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->nchains, S, level, ctx->d_rec,
-                                ctx->lay.chain_words, ctx->d_track, ctx->d_trace, ctx->d_best, ctx->d_tpart,
-                                ctx->d_tdone, ctx->st));
+  const tsa_layout_t& L = ctx->lay;
+  if (ctx->overlap && ctx->last_slot >= 0) {
+    // the last sweep's snapshot: fold its node costs and select on st2, beside the next sweep on st
+    const int s = ctx->last_slot;
+    TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_sweep[s], 0));
+    TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
+                                        ctx->nchains, ctx->d_snap_cost[s], ctx->d_snap_nz[s], ctx->d_fcnt, ctx->d_lc,
+                                        ctx->d_sc, ctx->d_ns, 0, ctx->st2));
+    TSA_HIP(ctx, tsa_launch_track(ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->nchains, S, level, ctx->d_rec,
+                                  L.chain_words, L.ch_off, L.s_off, L.W, L.nint, ctx->d_snap_ch[s], ctx->d_track,
+                                  ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2));
+    TSA_HIP(ctx, hipEventRecord(ctx->ev_track[s], ctx->st2));
+    ctx->track_pending[s] = true;
+    ctx->energy_fresh = false;  // d_lc / d_sc / d_ns now hold the snapshot's energies
+    return TSA_OK;
+  }
+  TSA_HIP(ctx, launch_energy(ctx));  // (orders st after any selection pending on st2)
+  TSA_HIP(ctx, tsa_launch_track(ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->nchains, S, level, ctx->d_rec, L.chain_words,
+                                L.ch_off, L.s_off, L.W, L.nint, nullptr, ctx->d_track, ctx->d_trace, ctx->d_best,
+                                ctx->d_tpart, ctx->d_tdone, ctx->st));
   return TSA_OK;
 }
 
@@ -595,16 +690,20 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
   static_assert(sizeof(TsaTraceRowD) == sizeof(tsa_trace_row_t), "trace row layout");
   TsaTrackState h;
   unsigned long long t0 = 0;
+  join_track(ctx);
   TSA_HIP(ctx, hipMemcpyAsync(&h, ctx->d_track, sizeof h, hipMemcpyDeviceToHost, ctx->st));
   TSA_HIP(ctx, hipMemcpyAsync(&t0, ctx->d_ticks0, sizeof t0, hipMemcpyDeviceToHost, ctx->st));
-  TSA_HIP(ctx, hipMemcpyAsync(best_record, ctx->d_best, (size_t)ctx->lay.chain_words * 8, hipMemcpyDeviceToHost,
-                              ctx->st));
+  // the best chain's tree: children words and S (the label words of best_record are not written)
+  const tsa_layout_t& L = ctx->lay;
+  TSA_HIP(ctx, hipMemcpyAsync(best_record + L.ch_off, ctx->d_best + L.ch_off, (size_t)(L.s_off + L.W - L.ch_off) * 8,
+                              hipMemcpyDeviceToHost, ctx->st));
   TSA_HIP(ctx, hipMemcpyAsync(rows, ctx->d_trace, (size_t)ctx->track_levels * sizeof(TsaTraceRowD),
                               hipMemcpyDeviceToHost, ctx->st));
   uint32_t werr = 0;
   if (ctx->wide.on)
     TSA_HIP(ctx, hipMemcpyAsync(&werr, ctx->wsync.err, 4, hipMemcpyDeviceToHost, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  TSA_HIP(ctx, quiesce_track(ctx));
   if (wide_error(ctx, werr) != TSA_OK) return TSA_ERR_HIP;
   int dev = 0, khz = 0;
   TSA_HIP(ctx, hipGetDevice(&dev));
@@ -635,6 +734,7 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
   for (int c = 0; c < ctx->nchains; c++)
     if (anc[c] < 0 || anc[c] >= ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_resample: ancestor out of range");
   if (!ctx->d_rec2) TSA_HIP(ctx, hipMalloc(&ctx->d_rec2, (size_t)ctx->nchains * ctx->lay.chain_words * 8));
+  TSA_HIP(ctx, quiesce_track(ctx));
   TSA_HIP(ctx, hipMemcpyAsync(ctx->d_anc, anc, (size_t)ctx->nchains * 4, hipMemcpyHostToDevice, ctx->st));
   ctx->costs_valid = false;
   ctx->energy_fresh = false;
@@ -648,7 +748,10 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
 extern "C" int tsa_set_mode(tsa_ctx* ctx, int32_t mode) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: null context");
   if (mode < 0 || mode > 2) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: mode must be 0, 1 or 2");
-  if (mode != ctx->mode) ctx->costs_valid = ctx->energy_fresh = false;
+  if (mode != ctx->mode) {
+    TSA_HIP(ctx, quiesce_track(ctx));
+    ctx->costs_valid = ctx->energy_fresh = false;
+  }
   ctx->mode = mode;
   return TSA_OK;
 }
@@ -692,6 +795,19 @@ extern "C" int tsa_destroy(tsa_ctx* ctx) {
 }
 
 extern "C" const char* tsa_last_error(const tsa_ctx* ctx) { return ctx ? ctx->err.c_str() : g_err.c_str(); }
+
+extern "C" void* tsa_host_alloc(size_t bytes) {
+  void* p = nullptr;
+  if (hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return p;
+}
+
+extern "C" void tsa_host_free(void* p) {
+  if (p) (void)hipHostFree(p);
+}
 
 extern "C" float tsa_host_math(int32_t which, float x) {
   if (which == 0) return tsa_expf(x);

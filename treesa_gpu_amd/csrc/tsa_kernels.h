@@ -73,7 +73,7 @@ hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64
 struct TsaTrackState {
   double best_score;
   int best_chain, best_level;
-  int snap;  // chain whose record the last tracked level snapshots, -1 if none
+  int snap;  // chain whose tree the last tracked level copied, -1 if none
 };
 struct TsaTraceRowD {  // same layout as tsa_trace_row_t
   float lc;
@@ -81,17 +81,19 @@ struct TsaTraceRowD {  // same layout as tsa_trace_row_t
   double score, meanE, meanNs;
   unsigned long long ticks;
 };
-// Chains above TSA_TRACK_INLINE_WORDS words are snapshot by a separate many-workgroup copy kernel.
-#define TSA_TRACK_INLINE_WORDS 16384
 // Result of one selection workgroup (256 chains): best score and chain, sums of E and |S|.
 struct TsaTrackPart {
   double score, sumE, sumNs;
   int idx;
 };
-// part: ceil(nchains / 256) entries; done: one zeroed counter (left zero after every launch).
+// part: ceil(nchains / 256) entries; done: one zeroed counter (left zero after every launch).  When a level
+// improves the best score, the chain's tree is copied into best_rec: its children words (from ch_snap,
+// nint words per chain, when not null, else from rec) and its S words (from rec); label words are left as
+// they are.
 hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int nchains, const TsaSelect& S, int level,
-                            const uint64_t* rec, int chain_words, TsaTrackState* st, TsaTraceRowD* trace,
-                            uint64_t* best_rec, TsaTrackPart* part, unsigned* done, hipStream_t stream);
+                            const uint64_t* rec, int chain_words, int ch_off, int s_off, int W, int nint,
+                            const uint32_t* ch_snap, TsaTrackState* st, TsaTraceRowD* trace, uint64_t* best_rec,
+                            TsaTrackPart* part, unsigned* done, hipStream_t stream);
 hipError_t tsa_launch_track_init(TsaTrackState* st, unsigned long long* ticks0, hipStream_t stream);
 hipError_t tsa_launch_copy(const uint64_t* src, uint64_t* dst, const int* anc, int nchains, int chain_words,
                            hipStream_t st);
@@ -136,6 +138,12 @@ struct TsaWideSync {
   const uint64_t* leafsum;
   int nsw;
   int lsum_lds;  // 1: the sweep kernel stages leafsum in LDS (when it fits beside the node arrays)
+  // Snapshot of every chain's tree and node-cost cache at the end of the launch (null: none), so that the
+  // energy fold and the selection of this level can run beside the next level's sweep:
+  // snap_ch[nchains][nint], snap_cost / snap_nz [nchains][nint4].
+  uint32_t* snap_ch;
+  float* snap_cost;
+  uint16_t* snap_nz;
 };
 
 // LDS byte offsets of k_wide (same function on host and device).

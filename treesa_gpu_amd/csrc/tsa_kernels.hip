@@ -534,7 +534,8 @@ __global__ void __launch_bounds__(256) k_copy(const uint4* __restrict__ src, uin
 // row, keeps the best so far and snapshots it when it improves.  Sums are therefore deterministic.
 __global__ void __launch_bounds__(256) k_track(const float* __restrict__ lc, const int* __restrict__ sc,
                                                const int* __restrict__ ns, int n, TsaSelect S, int level,
-                                               const uint64_t* __restrict__ rec, int chain_words,
+                                               const uint64_t* __restrict__ rec, int chain_words, int ch_off,
+                                               int s_off, int W, int nint, const uint32_t* __restrict__ ch_snap,
                                                TsaTrackState* __restrict__ st, TsaTraceRowD* __restrict__ trace,
                                                uint64_t* __restrict__ best_rec, TsaTrackPart* __restrict__ part,
                                                unsigned* __restrict__ done) {
@@ -636,19 +637,13 @@ __global__ void __launch_bounds__(256) k_track(const float* __restrict__ lc, con
     s_bi = b;
   }
   __syncthreads();
-  if (s_copy && chain_words <= TSA_TRACK_INLINE_WORDS) {
+  if (s_copy) {  // the new best chain's tree: children words and S (label words follow from the tree)
     const uint64_t* src = rec + (size_t)s_bi * chain_words;
-    for (int w = t; w < chain_words; w += 256) best_rec[w] = src[w];
+    const uint32_t* chs = ch_snap ? ch_snap + (size_t)s_bi * nint : reinterpret_cast<const uint32_t*>(src + ch_off);
+    uint32_t* chd = reinterpret_cast<uint32_t*>(best_rec + ch_off);
+    for (int i = t; i < nint; i += 256) chd[i] = chs[i];
+    for (int w = t; w < W; w += 256) best_rec[s_off + w] = src[s_off + w];
   }
-}
-
-// Snapshot of a large best chain (after k_track, which names it in st->snap), by many workgroups.
-__global__ void __launch_bounds__(256) k_snap(const TsaTrackState* __restrict__ st, const uint4* __restrict__ rec,
-                                              int n4, uint4* __restrict__ best_rec) {
-  const int b = st->snap;
-  if (b < 0) return;
-  const uint4* src = rec + (size_t)b * n4;
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) best_rec[i] = src[i];
 }
 
 __global__ void k_track_init(TsaTrackState* st, unsigned long long* ticks0) {
@@ -750,15 +745,11 @@ hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64
 }
 
 hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int nchains, const TsaSelect& S, int level,
-                            const uint64_t* rec, int chain_words, TsaTrackState* stt, TsaTraceRowD* trace,
-                            uint64_t* best_rec, TsaTrackPart* part, unsigned* done, hipStream_t stream) {
+                            const uint64_t* rec, int chain_words, int ch_off, int s_off, int W, int nint,
+                            const uint32_t* ch_snap, TsaTrackState* stt, TsaTraceRowD* trace, uint64_t* best_rec,
+                            TsaTrackPart* part, unsigned* done, hipStream_t stream) {
   hipLaunchKernelGGL(k_track, dim3((nchains + 255) / 256), dim3(256), 0, stream, lc, sc, ns, nchains, S, level, rec,
-                     chain_words, stt, trace, best_rec, part, done);
-  if (chain_words > TSA_TRACK_INLINE_WORDS) {
-    const int n4 = chain_words / 2, nb = (n4 + 1023) / 1024;
-    hipLaunchKernelGGL(k_snap, dim3(nb < 512 ? nb : 512), dim3(256), 0, stream, stt,
-                       reinterpret_cast<const uint4*>(rec), n4, reinterpret_cast<uint4*>(best_rec));
-  }
+                     chain_words, ch_off, s_off, W, nint, ch_snap, stt, trace, best_rec, part, done);
   return hipGetLastError();
 }
 

