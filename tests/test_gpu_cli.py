@@ -32,11 +32,13 @@ def run(args, tmp_path, name="out.json"):
         return json.load(f)
 
 
+# sq46 runs the wide path: with chunk summaries (one workgroup per chain: the fold and selection of a level
+# run on a second stream beside the next sweep) and without (several workgroups per chain: no overlap)
 @pytest.mark.parametrize("order", ["par", "preorder"])
-@pytest.mark.parametrize("inst", ["sat60", "lat14", "sq46"])  # sq46: the wide path and the many-block snapshot
-def test_device_selection_equals_host_selection(inst, order, tmp_path):
+@pytest.mark.parametrize("inst,extra", [("sat60", []), ("lat14", []), ("sq46", []), ("sq46", ["--no-sum"])])
+def test_device_selection_equals_host_selection(inst, extra, order, tmp_path):
     args = ["-i", common.inst_path(inst), "--nchains", "96", "--niters", "2", "--betas", "0.01:0.05:15",
-            "--sc-target", "30", "--order", order, "--seed", "3"]
+            "--sc-target", "30", "--order", order, "--seed", "3"] + extra
     a = run(args, tmp_path, "a.json")
     b = run(args + ["--host-select"], tmp_path, "b.json")
     for k in ("tc", "sc", "best_chain", "tree", "proposals", "accepts", "node_visits", "valid", "labels_ok"):

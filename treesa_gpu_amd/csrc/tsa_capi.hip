@@ -634,7 +634,14 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   }
   ctx->track_levels = max_levels;
   TSA_HIP(ctx, quiesce_track(ctx));
-  if (ctx->wide.on && !ctx->st2) {  // the wide path folds and selects beside the next level's sweep
+  // The wide path folds and selects beside the next level's sweep when that sweep leaves the device room:
+  // one workgroup per chain (no chain barrier, whose workgroups must all be resident at once) and fewer
+  // chains than compute units (with at least one chain per unit the sweep already fills the device).
+  int dev = 0, ncu = 0;
+  TSA_HIP(ctx, hipGetDevice(&dev));
+  TSA_HIP(ctx, hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+  const bool want_overlap = ctx->wide.on && ctx->wide.K == 1 && ctx->nchains < ncu;
+  if (want_overlap && !ctx->st2) {
     const size_t nint = (size_t)ctx->lay.nint, nint4 = (nint + 3) & ~(size_t)3;
     TSA_HIP(ctx, hipStreamCreateWithFlags(&ctx->st2, hipStreamNonBlocking));
     for (int k = 0; k < 2; k++) {
@@ -645,7 +652,7 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
       TSA_HIP(ctx, hipMalloc(&ctx->d_snap_nz[k], (size_t)ctx->nchains * nint4 * 2));
     }
   }
-  ctx->overlap = ctx->st2 != nullptr;
+  ctx->overlap = want_overlap;
   ctx->slot = 0;
   TSA_HIP(ctx, hipMemsetAsync(ctx->d_trace, 0, (size_t)max_levels * sizeof(TsaTraceRowD), ctx->st));
   TSA_HIP(ctx, hipMemsetAsync(ctx->d_best, 0, (size_t)ctx->lay.chain_words * 8, ctx->st));
