@@ -297,31 +297,42 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
       for (int i = threadIdx.x; i < nint; i += NT)
         pri[i] = (uint16_t)((((uint32_t)((L - 1 - (int)(dw[i] >> 16) % L) & 15)) << 12) | (pri[i] & 0x0FFEu) | 1u);
     }
+    if (threadIdx.x == 0) {  // the counters of the work list and of the visits (reset again after each replay)
+      s_cnt = 0;
+      s_next = 0;
+    }
     __syncthreads();
     for (;;) {
       // 1. scan: a wave takes 64-node groups; each lane reads its node's priority, parent and children
-      // words, then the three neighbour priorities, in two rounds of independent LDS reads
+      // words, then the three neighbour priorities, in two rounds of independent LDS reads (indices are
+      // clamped instead of branched on, so that every read of a round is in flight at once)
 #pragma unroll 2
       for (int gi = wv; gi < ngrp; gi += nwv) {
         const int i = gi * 64 + lane;
-        bool act = false;
-        if (i < nint) {
-          const uint32_t pv = pri[i], p = par[i], cw = ch[i];
-          const uint32_t l = cw & 0xFFFFu, r = cw >> 16;
-          const uint32_t pp = p != 0xFFFFu ? pri[p - m] : 0u;
-          const uint32_t pl = l >= (uint32_t)m ? pri[l - m] : 0u;
-          const uint32_t pr = r >= (uint32_t)m ? pri[r - m] : 0u;
-          const uint32_t key = (pv << 16) | (uint32_t)(m + i);
-          act = pv != 0u && !(pp && ((pp << 16) | p) > key) && !(pl && ((pl << 16) | l) > key) &&
-                !(pr && ((pr << 16) | r) > key);
-        }
+        const int ic = i < nint ? i : nint - 1;
+        const uint32_t pv = pri[ic], p = par[ic], cw = ch[ic];
+        const uint32_t l = cw & 0xFFFFu, r = cw >> 16;
+        const bool hp = p != 0xFFFFu, hl = l >= (uint32_t)m, hr = r >= (uint32_t)m;
+        const uint32_t pp = pri[hp ? (int)p - m : ic], pl = pri[hl ? (int)l - m : ic], pr = pri[hr ? (int)r - m : ic];
+        const uint32_t key = (pv << 16) | (uint32_t)(m + i);
+        const bool act = i < nint && pv != 0u && !(hp && pp && ((pp << 16) | p) > key) &&
+                         !(hl && pl && ((pl << 16) | l) > key) && !(hr && pr && ((pr << 16) | r) > key);
         const uint64_t b = __ballot(act);
-        if (lane == 0) masks[gi] = b;
+        if constexpr (COOP) {
+          if (lane == 0) masks[gi] = b;
+        } else {
+          // one workgroup per chain: append the group's active nodes (any order will do: the visits of a
+          // phase commute and every entry carries its own node id)
+          int base = 0;
+          if (lane == 0 && b) base = atomicAdd(&s_cnt, __popcll(b));
+          base = __builtin_amdgcn_readfirstlane(base);
+          if (act) wl[base + __popcll(b & wide_lt_mask(lane))] = (uint16_t)(m + i);
+        }
       }
       __syncthreads();
-      // every wave forms the prefix over the group counts itself and compacts its own groups into the work
-      // list, in node order (the same list in every workgroup of the chain)
-      {
+      if constexpr (COOP) {
+        // every workgroup of the chain builds the same list: each wave forms the prefix over the group counts
+        // itself and compacts its own groups, in node order
         int base = 0;
         for (int g0 = 0; g0 < ngrp; g0 += 64) {
           const int gl = g0 + lane;
@@ -336,18 +347,17 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
           const int excl = base + y - x;
           const int gend = g0 + 64 < ngrp ? g0 + 64 : ngrp;
           for (int gi = g0 + (wv - g0 % nwv + nwv) % nwv; gi < gend; gi += nwv) {
-            const uint64_t bm = __shfl(b, gi - g0, 64);
-            const int off = __shfl(excl, gi - g0, 64);
+            const uint32_t blo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, gi - g0);
+            const uint32_t bhi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), gi - g0);
+            const uint64_t bm = ((uint64_t)bhi << 32) | blo;
+            const int off = __builtin_amdgcn_readlane(excl, gi - g0);
             if ((bm >> lane) & 1ull) wl[off + __popcll(bm & wide_lt_mask(lane))] = (uint16_t)(m + gi * 64 + lane);
           }
-          base += __shfl(y, 63, 64);
+          base += __builtin_amdgcn_readlane(y, 63);
         }
-        if (threadIdx.x == 0) {
-          s_cnt = base;
-          s_next = 0;
-        }
+        if (threadIdx.x == 0) s_cnt = base;
+        __syncthreads();
       }
-      __syncthreads();
       const int cnt = s_cnt;
       if (cnt == 0) break;
       nst++;
@@ -579,6 +589,10 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
       }
 
       // 4. replay
+      if (threadIdx.x == 0) {  // every thread read cnt before the visits; the next scan appends from 0
+        s_cnt = 0;
+        s_next = 0;
+      }
       for (int j = threadIdx.x; j < cnt; j += NT) {
         const int v = wl[j];
         const uint32_t o = out[j];
