@@ -306,27 +306,39 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
       // 1. scan: a wave takes 64-node groups; each lane reads its node's priority, parent and children
       // words, then the three neighbour priorities, in two rounds of independent LDS reads (indices are
       // clamped instead of branched on, so that every read of a round is in flight at once)
-#pragma unroll 2
-      for (int gi = wv; gi < ngrp; gi += nwv) {
-        const int i = gi * 64 + lane;
-        const int ic = i < nint ? i : nint - 1;
-        const uint32_t pv = pri[ic], p = par[ic], cw = ch[ic];
-        const uint32_t l = cw & 0xFFFFu, r = cw >> 16;
-        const bool hp = p != 0xFFFFu, hl = l >= (uint32_t)m, hr = r >= (uint32_t)m;
-        const uint32_t pp = pri[hp ? (int)p - m : ic], pl = pri[hl ? (int)l - m : ic], pr = pri[hr ? (int)r - m : ic];
-        const uint32_t key = (pv << 16) | (uint32_t)(m + i);
-        const bool act = i < nint && pv != 0u && !(hp && pp && ((pp << 16) | p) > key) &&
-                         !(hl && pl && ((pl << 16) | l) > key) && !(hr && pr && ((pr << 16) | r) > key);
-        const uint64_t b = __ballot(act);
-        if constexpr (COOP) {
-          if (lane == 0) masks[gi] = b;
-        } else {
-          // one workgroup per chain: append the group's active nodes (any order will do: the visits of a
-          // phase commute and every entry carries its own node id)
+      // a wave takes its groups eight at a time: eight ballots, then (one workgroup per chain) one append
+      for (int g0 = wv; g0 < ngrp; g0 += 8 * nwv) {
+        uint64_t bb[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+          const int gi = g0 + q * nwv;
+          const int i = gi * 64 + lane;
+          const int ic = i < nint ? i : nint - 1;
+          const uint32_t pv = pri[ic], p = par[ic], cw = ch[ic];
+          const uint32_t l = cw & 0xFFFFu, r = cw >> 16;
+          const bool hp = p != 0xFFFFu, hl = l >= (uint32_t)m, hr = r >= (uint32_t)m;
+          const uint32_t pp = pri[hp ? (int)p - m : ic], pl = pri[hl ? (int)l - m : ic], pr = pri[hr ? (int)r - m : ic];
+          const uint32_t key = (pv << 16) | (uint32_t)(m + i);
+          const bool act = gi < ngrp && i < nint && pv != 0u && !(hp && pp && ((pp << 16) | p) > key) &&
+                           !(hl && pl && ((pl << 16) | l) > key) && !(hr && pr && ((pr << 16) | r) > key);
+          bb[q] = __ballot(act);
+          if (COOP && lane == 0 && gi < ngrp) masks[gi] = bb[q];
+        }
+        if constexpr (!COOP) {
+          // one workgroup per chain: append the active nodes (any order will do: the visits of a phase
+          // commute and every entry carries its own node id)
+          int tot = 0;
+#pragma unroll
+          for (int q = 0; q < 8; q++) tot += __popcll(bb[q]);
           int base = 0;
-          if (lane == 0 && b) base = atomicAdd(&s_cnt, __popcll(b));
+          if (lane == 0 && tot) base = atomicAdd(&s_cnt, tot);
           base = __builtin_amdgcn_readfirstlane(base);
-          if (act) wl[base + __popcll(b & wide_lt_mask(lane))] = (uint16_t)(m + i);
+#pragma unroll
+          for (int q = 0; q < 8; q++) {
+            const uint64_t b = bb[q];
+            if ((b >> lane) & 1ull) wl[base + __popcll(b & wide_lt_mask(lane))] = (uint16_t)(m + (g0 + q * nwv) * 64 + lane);
+            base += __popcll(b);
+          }
         }
       }
       __syncthreads();
