@@ -67,7 +67,8 @@ struct tsa_ctx {
   // overwrites the slot).
   bool overlap = false;
   hipStream_t st2 = nullptr;
-  hipEvent_t ev_sweep[2] = {nullptr, nullptr}, ev_track[2] = {nullptr, nullptr};
+  hipEvent_t ev_sweep[2] = {nullptr, nullptr};  // (the stop events of those sweeps' timing pairs)
+  hipEvent_t ev_track[2] = {nullptr, nullptr};
   bool track_pending[2] = {false, false};
   int slot = 0, last_slot = -1;  // slot of the next sweep launch / of the last one (-1: none since a reset)
   uint32_t* d_snap_ch[2] = {nullptr, nullptr};
@@ -232,7 +233,6 @@ static void free_ctx(tsa_ctx* c) {
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   if (c->st2) (void)hipStreamSynchronize(c->st2);
   for (int k = 0; k < 2; k++) {
-    if (c->ev_sweep[k]) (void)hipEventDestroy(c->ev_sweep[k]);
     if (c->ev_track[k]) (void)hipEventDestroy(c->ev_track[k]);
     if (c->d_snap_ch[k]) (void)hipFree(c->d_snap_ch[k]);
     if (c->d_snap_cost[k]) (void)hipFree(c->d_snap_cost[k]);
@@ -544,8 +544,8 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     TSA_HIP(ctx, hipEventCreate(&e));
     ctx->ev.push_back(e);
   }
+  // e0 / e1 bracket the sweep kernel alone (the summary and cost passes some launches need go before e0)
   hipEvent_t e0 = ctx->ev[2 * ctx->npending], e1 = ctx->ev[2 * ctx->npending + 1];
-  TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
   ctx->energy_fresh = false;
   if (ctx->wide.on && order == TSA_ORDER_PAR) {
     // energies stay a separate fold of the node-cost cache: every chain ends its sweep at about the same
@@ -566,16 +566,22 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
         ctx->costs_valid = true;
       }
       s = ctx->slot;
-      if (ctx->track_pending[s]) TSA_HIP(ctx, hipStreamWaitEvent(ctx->st, ctx->ev_track[s], 0));
+      // the selection that last read slot s must be done (a wait that is already satisfied is skipped: each
+      // wait costs the queue tens of microseconds)
+      if (ctx->track_pending[s] && hipEventQuery(ctx->ev_track[s]) != hipSuccess)
+        TSA_HIP(ctx, hipStreamWaitEvent(ctx->st, ctx->ev_track[s], 0));
+      (void)hipGetLastError();  // a query of an unfinished event leaves hipErrorNotReady behind
       ctx->track_pending[s] = false;
       sy.snap_ch = ctx->d_snap_ch[s];
       sy.snap_cost = ctx->d_snap_cost[s];
       sy.snap_nz = ctx->d_snap_nz[s];
     }
+    TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
     TSA_HIP(ctx, tsa_launch_wide(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains, beta,
                                  sweep0, nsweeps, ctx->d_stats, sy, ctx->st));
+    TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
     if (s >= 0) {
-      TSA_HIP(ctx, hipEventRecord(ctx->ev_sweep[s], ctx->st));
+      ctx->ev_sweep[s] = e1;  // the selection of this snapshot waits for the sweep's stop event
       ctx->last_slot = s;
       ctx->slot = s ^ 1;
     }
@@ -586,11 +592,12 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     join_track(ctx);      // a pending fold may still read the node-cost snapshot; d_lc is rewritten below
     const bool fuse = ctx->cfg.fused_energy != 0;
     const TsaEnergyOut eo{fuse ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns};
+    TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
     TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
                                    ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st));
+    TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
     ctx->energy_fresh = fuse;
   }
-  TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
   ctx->npending++;
   return TSA_OK;
 }
@@ -645,7 +652,6 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
     const size_t nint = (size_t)ctx->lay.nint, nint4 = (nint + 3) & ~(size_t)3;
     TSA_HIP(ctx, hipStreamCreateWithFlags(&ctx->st2, hipStreamNonBlocking));
     for (int k = 0; k < 2; k++) {
-      TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_sweep[k], hipEventDisableTiming));
       TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_track[k], hipEventDisableTiming));
       TSA_HIP(ctx, hipMalloc(&ctx->d_snap_ch[k], (size_t)ctx->nchains * nint * 4));
       TSA_HIP(ctx, hipMalloc(&ctx->d_snap_cost[k], (size_t)ctx->nchains * nint4 * 4));

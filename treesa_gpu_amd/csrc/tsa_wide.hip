@@ -229,8 +229,20 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
   const int NT = blockDim.x, nwv = NT >> 6, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m = P.m, nint = P.nint, nint4 = (nint + 3) & ~3, ngrp = (nint + 63) >> 6;
   const int NW = P.W, nch = NW >> 1;
-  const int c = blockIdx.x / K, k = blockIdx.x - c * K;
-  if (c >= nchains) return;  // whole workgroups; the grid is nchains * K
+  // Workgroups are dealt to the 8 XCDs of the device in turn (workgroup b to XCD b % 8), each XCD with its
+  // own L2.  With K > 1 the K workgroups of a chain are taken from one XCD -- b = 8 (K (c / 8) + k) + c % 8
+  // -- so that they share that L2 for the chain's label sets; the grid is K * nchains rounded up to a
+  // multiple of 8 chains, and workgroups past the last chain leave at once.
+  int c, k;
+  if constexpr (COOP) {
+    const int x = (int)(blockIdx.x & 7u), sl = (int)(blockIdx.x >> 3);
+    c = (sl / K) * 8 + x;
+    k = sl - (sl / K) * K;
+  } else {
+    c = (int)blockIdx.x;
+    k = 0;
+  }
+  if (c >= nchains) return;  // whole workgroups
   const int nsw = SUMS ? sy.nsw : 0;
   const bool lsum_in_lds = SUMS && sy.lsum_lds;
   const TsaWideLds Lo = tsa_wide_lds(nint, P.par_band > 0, COOP ? 1 : 0, nsw, lsum_in_lds ? m : 0);
@@ -375,16 +387,17 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
       nst++;
       uint8_t* const out = COOP ? sy.out + ((size_t)c * 2 + (nb & 1u)) * (size_t)nint4 : outl;
 
-      // 2. visits: this workgroup's contiguous share [lo, hi) of the work list, handed out gpw entries at a
-      // time to whichever wave asks next (an LDS counter), so that waves that run ahead take more
-      const int lo = (int)(((long long)cnt * k) / K), hi = (int)(((long long)cnt * (k + 1)) / K);
+      // 2. visits: this workgroup's share of the work list -- entries k, k + K, k + 2K, ... (interleaved, so
+      // that neighbouring entries, which cost alike, spread over the workgroups) -- handed out gpw at a time
+      // to whichever wave asks next (an LDS counter), so that waves that run ahead take more
+      const int nk = (cnt - k + K - 1) / K;
       for (;;) {
-        int j0 = 0;
-        if (lane == 0) j0 = atomicAdd(&s_next, gpw);
-        j0 = lo + __shfl(j0, 0, 64);
-        if (j0 >= hi) break;  // uniform within the wave
-        const int j = j0 + gsub;
-        if (j < hi) {  // uniform within a lane group
+        int i0 = 0;
+        if (lane == 0) i0 = atomicAdd(&s_next, gpw);
+        i0 = __shfl(i0, 0, 64);
+        if (i0 >= nk) break;  // uniform within the wave
+        const int j = k + K * (i0 + gsub);
+        if (i0 + gsub < nk) {  // uniform within a lane group
           const int v = wl[j];
           const uint32_t chv = ch[v - m];
           const int l = (int)(chv & 0xFFFFu), r = (int)(chv >> 16);
@@ -621,7 +634,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
           if (On >= m) par[On - m] = (uint16_t)Pn;
           if (Mn >= m) par[Mn - m] = (uint16_t)v;
           if (P.par_follow && (pv & 1u) && pri[Pn - m] == 0) pri[Pn - m] = (uint16_t)tsa_follow_pri((uint32_t)Pn, hs);
-          if (SUMS && (j < lo || j >= hi))  // P's new summary, written by another workgroup's visit
+          if (SUMS && j % K != k)  // P's new summary, written by another workgroup's visit
             for (int q = 0; q < nsw; q++) ssum[(size_t)(Pn - m) * nsw + q] = gsum[(size_t)(Pn - m) * nsw + q];
         }
         pri[v - m] = 0;
@@ -780,7 +793,8 @@ hipError_t launch_wide_gms(const TsaWide& X, const TsaKParams& P, uint64_t* rec,
     // once, so on an idle device they are all resident together (the cooperative launch API gives the same
     // guarantee but costs tens of microseconds per launch on the host side); if they ever are not, a chain
     // barrier runs out of polls, sets the error word and every workgroup leaves
-    hipLaunchKernelGGL((k_wide<G, MODE, true, SUMS>), dim3(nchains * X.K), dim3(X.nt), (size_t)X.smem, st, P, rec,
+    const int nchains8 = (nchains + 7) & ~7;  // (chains grouped by XCD, see k_wide)
+    hipLaunchKernelGGL((k_wide<G, MODE, true, SUMS>), dim3(nchains8 * X.K), dim3(X.nt), (size_t)X.smem, st, P, rec,
                        leaf, fix, nchains, X.K, beta, sweep0, nsweeps, stats, sy);
     return hipGetLastError();
   }
@@ -968,10 +982,12 @@ hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int w
   if (e == hipSuccess) e = wcost_lds_cap_g(Gd, lds_cap);
   if (e != hipSuccess) return e;
   if (per_cu < 1) return hipErrorInvalidValue;
-  const int cap = per_cu * ncu;
-  int K = want_k > 0 ? want_k : (X.nsw ? 1 : cap / nchains);
+  // with K > 1 a chain's workgroups share one XCD (8 per device, see k_wide): the chains of the fullest XCD
+  // times K must be resident on its ncu / 8 compute units at once
+  const int kmax = per_cu * (ncu / 8) / ((nchains + 7) / 8);
+  int K = want_k > 0 ? want_k : (X.nsw ? 1 : kmax);
   K = K < 1 ? 1 : (K > TSA_WIDE_MAX_K ? TSA_WIDE_MAX_K : K);
-  if (K > 1 && K * nchains > cap) return hipErrorCooperativeLaunchTooLarge;
+  if (K > 1 && K > kmax) return hipErrorCooperativeLaunchTooLarge;
   X.K = K;
   X.smem = K > 1 ? Lc.bytes : L1.bytes;
   X.eG = Gd;
