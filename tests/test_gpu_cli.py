@@ -78,3 +78,29 @@ def test_result_is_valid_and_consistent(scheme, tmp_path):
         rec[lay.s_off + (l >> 6)] |= np.uint64(1) << np.uint64(l & 63)
     tc, sc, _, _, ns = inst.host_energy(lay, rec, slicing=True)
     assert abs(tc - r["tc"]) < 1e-6 and sc == r["sc"] and ns == r["nsliced"] and sc <= 24
+
+
+# --init spectral / greedy make the start trees natively; the run equals the same trees passed as a --tree file
+@pytest.mark.parametrize("inst,init", [("sat60", "spectral"), ("lat14", "spectral"), ("reg3_250", "greedy")])
+def test_native_start_trees_equal_tree_file(inst, init, tmp_path):
+    from treesa_gpu_amd import starts as S
+    m, nlab, ixs, iy = common.load_instance(inst)
+    if init == "spectral":
+        so = S.spectral_orders(ixs, iy, k=3, seed=5)
+        trees, tcs = [S.path_tree(o) for _, _, o in so], [t for t, _, _ in so]
+        extra = ["--init", "spectral", "--spectral-k", "3"]
+    else:
+        g = S.greedy_tree(ixs, iy, nrepeat=4, seed=5)
+        trees, tcs = [g], None
+        extra = ["--init", "greedy", "--greedy-repeat", "4"]
+    tf = str(tmp_path / "t.tree")
+    S.write_trees(tf, trees)
+    base = ["-i", common.inst_path(inst), "--nchains", "64", "--niters", "1", "--betas", "1:0.5:15",
+            "--sc-target", "30", "--seed", "5"]
+    a = run(base + extra, tmp_path, "a.json")
+    b = run(base + ["--tree", tf], tmp_path, "b.json")
+    for k in ("tc", "sc", "best_chain", "tree", "proposals", "accepts", "valid", "labels_ok"):
+        assert a[k] == b[k], k
+    assert a["valid"] and a["labels_ok"] and a["init"] == init
+    if tcs is not None:
+        assert a["init_tcs"] == [round(t, 4) for t in tcs]

@@ -1,0 +1,164 @@
+"""CPU tests of the native start-tree generators (treesa_gpu_amd/host/tsa_starts.cpp through
+treesa_gpu_amd/starts.py).
+
+* The candidate search, given numpy's eigenvectors and numpy's random directions (the reference's inputs to
+  it, treesa_gpu/spectral.py:63-67, 143-160), returns the path tc values the reference's own test run
+  printed (tests/test_python_results.txt:63-66).
+* The Laplacian eigenvectors, dense (up to 400 tensors) and block Krylov (above), have numpy.linalg.eigh's
+  eigenvalues and span its eigenvectors; the graph is built here independently from the label lists.
+* path_cost equals the exact energy of the path tree from the host layer (labels from topology + host_energy),
+  also with open labels.
+* Spectral and greedy start trees are valid binary trees; greedy trees are within 1.0 of the tc of the
+  reference's committed omeco greedy trees (tests/data/*.tree; the greedy method is unversioned, so this
+  compares quality, not trees).
+"""
+import numpy as np
+import pytest
+
+import common
+from treesa_gpu_amd import capi, host
+from treesa_gpu_amd import starts as S
+
+# tests/test_python_results.txt:63-66 -- spectral_orders(ixs, iy, k=3) of the reference, rounded to 3 places
+REFERENCE_ORDERS = {
+    "sat60": [52.682, 52.682, 53.067],
+    "reg3_250": [51.315, 51.315, 51.315],
+    "lat14": [35.171, 35.171, 35.182],
+    "grid24": [59.04, 59.04, 59.066],
+}
+
+
+def laplacian(ixs, m):
+    L = np.zeros((m, m))
+    holders = {}
+    for t, ix in enumerate(ixs):
+        for l in ix:
+            holders.setdefault(l, []).append(t)
+    for ts in holders.values():
+        if len(ts) < 2:
+            continue
+        w = 1.0 / (len(ts) - 1)
+        for i in range(len(ts)):
+            for j in range(i + 1, len(ts)):
+                L[ts[i], ts[j]] -= w
+                L[ts[j], ts[i]] -= w
+    L[np.arange(m), np.arange(m)] = -L.sum(axis=1)
+    return L
+
+
+def exact_energy(name, ch):
+    inst = host.Instance(common.inst_path(name))
+    lay = capi.layout(inst.m, inst.nlab)
+    rec = inst.population(lay, np.array([ch]), 1, seed=0)[0]  # population() validates the tree
+    return inst.host_energy(lay, rec, slicing=False)[:2]
+
+
+@pytest.mark.parametrize("name", sorted(REFERENCE_ORDERS))
+def test_candidate_search_reproduces_reference_orders(name):
+    m, nlab, ixs, iy = common.load_instance(name)
+    _, V = np.linalg.eigh(laplacian(ixs, m))
+    rng = np.random.default_rng(0)
+    dirs = []
+    for _ in range(24):
+        v = rng.standard_normal(3)
+        dirs.append(v / np.linalg.norm(v))
+    so = S.spectral_search(ixs, iy, V[:, 1:4], np.array(dirs), k=3, nangles=24)
+    assert [round(t, 3) for t, _, _ in so] == REFERENCE_ORDERS[name]
+    for t, sc, o in so:
+        assert sorted(o) == list(range(m))
+        tc, sc2 = exact_energy(name, S.path_tree(o))
+        assert abs(t - tc) < 1e-9 and sc == sc2
+
+
+@pytest.mark.parametrize("name", ["sat60", "reg3_250", "lat14", "grid24"])
+def test_laplacian_vectors_match_numpy(name):
+    m, nlab, ixs, iy = common.load_instance(name)
+    L = laplacian(ixs, m)
+    ev, Vn = np.linalg.eigh(L)
+    V, vals = S.laplacian_vectors(ixs, 3, seed=1)
+    assert V.shape == (m, 3)
+    np.testing.assert_allclose(vals, ev[1:4], rtol=0, atol=1e-9)
+    # residuals and orthonormality
+    assert np.abs(L @ V - V * vals).max() < 1e-6
+    np.testing.assert_allclose(V.T @ V, np.eye(3), atol=1e-9)
+    # same subspace as numpy's eigenvectors 1..3 (the gap to eigenvalue 4 separates it)
+    assert ev[4] - ev[3] > 1e-3
+    s = np.linalg.svd(Vn[:, 1:4].T @ V, compute_uv=False)
+    np.testing.assert_allclose(s, 1.0, atol=1e-6)
+
+
+def test_laplacian_constant_vector_is_skipped():
+    m, nlab, ixs, iy = common.load_instance("sat40")
+    V, vals = S.laplacian_vectors(ixs, 2)
+    assert vals[0] > 1e-6  # the graph is connected: eigenvalue 0 belongs to the constant vector alone
+    np.testing.assert_allclose(V.sum(axis=0), 0.0, atol=1e-9)
+
+
+@pytest.mark.parametrize("name", ["sat40", "lat10", "sq46"])
+def test_path_cost_equals_exact_energy_with_open_labels(name):
+    m, nlab, ixs, iy = common.load_instance(name)
+    rng = np.random.default_rng(7)
+    labels = sorted({l for ix in ixs for l in ix})
+    for open_ in ([], list(rng.choice(labels, 5, replace=False))):
+        iy2 = sorted(set(iy) | set(int(x) for x in open_))
+        inst = host.Instance(m=m, nlab=nlab, ixs=ixs, iy=iy2)
+        lay = capi.layout(m, nlab)
+        for order in (np.arange(m), rng.permutation(m)):
+            rec = inst.population(lay, np.array([S.path_tree(order)]), 1, seed=0)[0]
+            tc, sc = inst.host_energy(lay, rec, slicing=False)[:2]
+            t2, s2 = S.path_cost(order, ixs, iy2)
+            assert abs(t2 - tc) < 1e-9 and s2 == sc
+
+
+def test_path_tree_layout():
+    ch = S.path_tree([3, 1, 0, 2])
+    assert [(int(w) & 0xFFFF, int(w) >> 16) for w in ch] == [(3, 1), (4, 0), (5, 2)]
+    d = S.path_tree_dict([3, 1, 0])
+    assert d == {"args": [{"args": [{"tensor_index": 3}, {"tensor_index": 1}]}, {"tensor_index": 0}]}
+
+
+@pytest.mark.parametrize("name", ["sat60", "reg3_250", "lat14"])
+def test_spectral_orders_are_exact_permutations(name):
+    m, nlab, ixs, iy = common.load_instance(name)
+    so = S.spectral_orders(ixs, iy, k=4, seed=1)
+    assert len(so) == 4
+    assert all(so[i][0] <= so[i + 1][0] for i in range(3))
+    assert len({tuple(o) for _, _, o in so}) == 4
+    for t, sc, o in so:
+        assert sorted(o) == list(range(m))
+        tc, sc2 = exact_energy(name, S.path_tree(o))
+        assert abs(t - tc) < 1e-9 and sc == sc2
+    # quality: within 0.5 of the reference's best printed ordering
+    assert so[0][0] <= REFERENCE_ORDERS[name][0] + 0.5
+
+
+def test_spectral_orders_small_and_disconnected():
+    assert S.spectral_orders([[0, 1], [1]], [0])[0][2] == [0, 1]
+    ixs = [[0, 1], [1, 2], [2, 0], [3, 4], [4, 5], [5, 3]]  # two triangles, no shared label between them
+    so = S.spectral_orders(ixs, [], k=2)
+    for t, sc, o in so:
+        assert sorted(o) == list(range(6))
+        assert abs(t - S.path_cost(o, ixs)[0]) < 1e-12
+
+
+@pytest.mark.parametrize("name", ["sat40", "sat60", "sat100", "reg3_100", "reg3_250", "lat10", "lat14", "grid24"])
+def test_greedy_tree_is_valid_and_near_omeco(name):
+    m, nlab, ixs, iy = common.load_instance(name)
+    inst = host.Instance(common.inst_path(name))
+    omeco = inst.read_trees(common.inst_path(name)[:-4] + ".tree")[0]
+    g = S.greedy_tree(ixs, iy, nrepeat=10, seed=1)
+    assert len(g) == m - 1
+    tc_g, _ = exact_energy(name, g)
+    tc_o, _ = exact_energy(name, omeco)
+    assert tc_g <= tc_o + 1.0
+    _, tc_native = inst.greedy_tree(10, 1)
+    assert abs(tc_native - tc_g) < 1e-9
+
+
+def test_greedy_disconnected_and_deterministic():
+    ixs = [[0, 1], [1, 2], [3], [3, 4], [5]]
+    g = S.greedy_tree(ixs, [], nrepeat=4, seed=3)
+    assert len(g) == 4
+    kids = sorted(int(w) & 0xFFFF for w in g) + sorted(int(w) >> 16 for w in g)
+    assert sorted(kids) == sorted(set(kids)) and set(range(5)) <= set(kids)
+    assert np.array_equal(g, S.greedy_tree(ixs, [], nrepeat=4, seed=3))

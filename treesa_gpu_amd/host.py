@@ -39,6 +39,11 @@ def load():
     lib.tsh_build_population.argtypes = [P, I, I, I, I, P, I, I, U64, P, I, P, ctypes.c_char_p, I]
     lib.tsh_host_energy.argtypes = [P, I, P, P, P, P, P, P]
     lib.tsh_greedy_repair.argtypes = [P, I, P, P, D]
+    lib.tsh_path_cost.argtypes = [P, P, I, P]
+    lib.tsh_spectral_orders.argtypes = [P, I, I, I, U64, P, P, P]
+    lib.tsh_spectral_search.argtypes = [P, P, I, P, I, I, I, P, P, P]
+    lib.tsh_laplacian_vectors.argtypes = [P, I, U64, P, P]
+    lib.tsh_greedy_tree.argtypes = [P, I, U64, P, P]
     _lib = lib
     return lib
 
@@ -117,6 +122,49 @@ class Instance:
                                  S.ctypes.data if slicing else None, out.ctypes.data)
         return float(out[0]), int(out[1]), float(out[2]), float(out[3]), int(out[4])
 
+    def path_cost(self, order):
+        """(tc, sc) of the path tree contracting the tensors in `order` left to right."""
+        o = np.ascontiguousarray(order, np.int32)
+        out = np.zeros(2, np.float64)
+        if self.lib.tsh_path_cost(self.h, o.ctypes.data, len(o), out.ctypes.data) != 0:
+            raise HostError("path_cost: the order must list every tensor")
+        return float(out[0]), int(out[1])
+
+    def laplacian_vectors(self, k, seed=1):
+        """Eigenvectors 1..k of the tensor graph's Laplacian (m x k) and their eigenvalues."""
+        vecs = np.zeros((self.m, k), np.float64)
+        vals = np.zeros(k, np.float64)
+        kk = self.lib.tsh_laplacian_vectors(self.h, k, seed, vecs.ctypes.data, vals.ctypes.data)
+        return vecs[:, :kk].copy(), vals[:kk].copy()
+
+    def spectral_orders(self, k=4, nangles=64, nrandom=64, seed=1):
+        """The k best spectral orderings as a list of (tc, sc, order), best first."""
+        orders = np.zeros((k, self.m), np.int32)
+        tc = np.zeros(k, np.float64)
+        sc = np.zeros(k, np.int32)
+        n = self.lib.tsh_spectral_orders(self.h, k, nangles, nrandom, seed, orders.ctypes.data, tc.ctypes.data,
+                                         sc.ctypes.data)
+        return [(float(tc[i]), int(sc[i]), orders[i].copy()) for i in range(n)]
+
+    def spectral_search(self, V, dirs, k=8, nangles=24):
+        """spectral_orders' candidate search over given eigenvectors V (m x d) and directions dirs (r x d)."""
+        V = np.ascontiguousarray(V, np.float64)
+        d = V.shape[1]
+        dirs = np.ascontiguousarray(np.reshape(dirs, (-1, d)), np.float64)
+        orders = np.zeros((k, self.m), np.int32)
+        tc = np.zeros(k, np.float64)
+        sc = np.zeros(k, np.int32)
+        n = self.lib.tsh_spectral_search(self.h, V.ctypes.data, d, dirs.ctypes.data, len(dirs), k, nangles,
+                                         orders.ctypes.data, tc.ctypes.data, sc.ctypes.data)
+        return [(float(tc[i]), int(sc[i]), orders[i].copy()) for i in range(n)]
+
+    def greedy_tree(self, nrepeat=1, seed=1):
+        """(children words, tc) of the greedy contraction tree, best of nrepeat runs."""
+        out = np.zeros(self.m - 1, np.uint32)
+        tc = ctypes.c_double()
+        self.lib.tsh_greedy_tree(self.h, nrepeat, seed, out.ctypes.data, ctypes.byref(tc))
+        return out, tc.value
+
     def close(self):
         if self.h:
             self.lib.tsh_instance_free(self.h)
@@ -138,6 +186,14 @@ def parse_betas(spec):
     if k < 0:
         raise HostError(err.value.decode())
     return out[:k].copy()
+
+
+def path_tree(order):
+    """Children words of the path tree over `order`: node m = (order[0], order[1]), node m+i = (m+i-1, order[i+1])."""
+    o = np.asarray(order, np.uint32)
+    m = len(o)
+    left = np.concatenate([o[:1], np.arange(m, 2 * m - 2, dtype=np.uint32)])
+    return left | (o[1:] << np.uint32(16))
 
 
 def random_tree(m, seed):

@@ -46,7 +46,8 @@ namespace {
 
 struct Opts {
   std::string inst, tree, out, kernel = "auto", scheme = "indep", betas = "0.01:0.05:15", order = "par";
-  std::string betas2, init_slices;
+  std::string betas2, init_slices, init = "tree";
+  int spectral_k = 4, greedy_repeat = 10;
   int niters2 = -1;
   int nchains = 1024, niters = 50, block = 0, wpb = 0, lpc = 32, eval_every = 1, ref_chains = 8, mode = 0;
   bool check = false, quiet = false, cross = true, wide = false, slicing = false, no_sum = false, force_sum = false;
@@ -82,7 +83,9 @@ std::string jnum(double x) {
           "  [--order par|preorder] [--kernel auto|seq|seqsm|warp|warpsm|block|par [--wpc n]] [--lpc 32|16|8] [--coop-max G] [--coop-min G0] [--coop-full G1] [--par-follow] [--par-band L] [--coop-min-units u] [--wide] [--sums|--no-sum] [--select-sc] [--block B] [--wpb W] [--seed s] [--wide-wgs K] [--wide-lanes G]\n"
           "  [--eval-every k] [--out result.json] [--check [--ref-chains R] [--random-slices k]] [--quiet]\n"
           "  [--bench-warmup W]  (W untimed levels first, then the initial population again)\n"
-          "  [--host-select]  (select the best chain on the host at every level, also for --scheme indep)\n");
+          "  [--host-select]  (select the best chain on the host at every level, also for --scheme indep)\n"
+          "  [--init tree|spectral|greedy [--spectral-k K] [--greedy-repeat R]]  (start trees made natively when no --tree\n"
+          "   is given: the K best spectral path trees, chain c from tree c %% K, or the best of R greedy runs)\n");
   exit(1);
 }
 
@@ -102,6 +105,11 @@ Opts parse(int argc, char** argv) {
       };
       if (a == "-i") o.inst = nx();
       else if (a == "--tree") o.tree = nx();
+      else if (a == "--init") {
+        o.init = nx();
+        if (o.init != "tree" && o.init != "spectral" && o.init != "greedy") usage();
+      } else if (a == "--spectral-k") o.spectral_k = std::stoi(nx());
+      else if (a == "--greedy-repeat") o.greedy_repeat = std::stoi(nx());
       else if (a == "--out") o.out = nx();
       else if (a == "--nchains") o.nchains = std::stoi(nx());
       else if (a == "--niters") o.niters = std::stoi(nx());
@@ -177,6 +185,10 @@ Opts parse(int argc, char** argv) {
 
 class Runner {
  public:
+  std::vector<std::vector<uint32_t>> trees_;
+  std::vector<double> init_tcs;  // tc of each start tree made by --init spectral / greedy
+  double t_trees = 0.0;
+  bool have_trees = false;
   Runner(const Inst& I, const Opts& O) : I(I), O(O) {
     if (tsa_layout(I.m, I.nlab, O.wide ? 1 : 0, &lay) != TSA_OK) die(tsa_last_error(nullptr));
     G = Geometry{lay.W, lay.ch_off, lay.s_off, lay.chain_words};
@@ -270,9 +282,27 @@ class Runner {
       die("treesa_hip: " + msg);
     }
   }
+  // start trees: the --tree file, else (--init spectral / greedy) made once here on the host
+  const std::vector<std::vector<uint32_t>>& start_trees() {
+    if (have_trees) return trees_;
+    const double t = now_s();
+    if (!O.tree.empty()) trees_ = read_trees(O.tree, I.m);
+    else if (O.init == "spectral") {
+      for (const SpectralOrder& so : spectral_orders(I, std::max(1, O.spectral_k), 24, 24, O.seed)) {
+        trees_.push_back(path_tree(so.order));
+        init_tcs.push_back(so.tc);
+      }
+    } else if (O.init == "greedy") {
+      double tc = 0.0;
+      trees_.push_back(greedy_tree(I, std::max(1, O.greedy_repeat), O.seed, &tc));
+      init_tcs.push_back(tc);
+    }
+    t_trees = now_s() - t;
+    have_trees = true;
+    return trees_;
+  }
   std::vector<uint64_t> init_population() {
-    std::vector<std::vector<uint32_t>> trees;
-    if (!O.tree.empty()) trees = read_trees(O.tree, I.m);
+    const std::vector<std::vector<uint32_t>>& trees = start_trees();
     std::vector<uint64_t> S0(lay.W, 0);
     if (!O.init_slices.empty()) {
       const char* p = O.init_slices.c_str();
@@ -597,6 +627,11 @@ int Runner::run_anneal() {
           O.scheme.c_str(), O.mode, nresample);
   fprintf(f, " \"sum_chunks\": %llu, \"sum_xchunks\": %llu,\n", (unsigned long long)chunks[0],
           (unsigned long long)chunks[1]);
+  if (!init_tcs.empty()) {
+    fprintf(f, " \"init\": \"%s\", \"t_start_trees\": %.6f, \"init_tcs\": [", O.init.c_str(), t_trees);
+    for (size_t i = 0; i < init_tcs.size(); i++) fprintf(f, "%s%.4f", i ? ", " : "", init_tcs[i]);
+    fprintf(f, "],\n");
+  }
   if (staged)
     fprintf(f, " \"stage1_tc\": %.6f, \"stage1_sc\": %d, \"stage1_nsliced\": %d, \"stage1_gpu_time\": %s, \"stage1_h100_time\": %s, \"stage1_h100_time_total\": %s,\n",
             H1.tc, H1.sc, H1.ns, jnum(H1.time).c_str(), jnum(H1.time2).c_str(),

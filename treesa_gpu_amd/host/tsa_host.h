@@ -94,4 +94,37 @@ void build_population(const Inst& I, const Geometry& G, const std::vector<std::v
                       int nchains, uint64_t seed, const std::vector<uint64_t>& S0, int random_slices,
                       std::vector<uint64_t>& pop);
 
+// ---- start trees (tsa_starts.cpp) ----
+
+// Exact (tc, sc) in log2 of the path tree that contracts the tensors in `order` left to right, in
+// O(sum of tensor sizes): step i contracts the prefix's surviving labels with tensor order[i], and for
+// dimension-2 indices its cost is the size of the union of the two label sets (treesa_gpu/spectral.py:97-131).
+std::pair<double, int> path_cost(const Inst& I, const std::vector<int>& order);
+
+// Children words of that path tree: node m+0 = (order[0], order[1]), node m+i = (m+i-1, order[i+1]).
+std::vector<uint32_t> path_tree(const std::vector<int>& order);
+
+// Eigenvectors 1..k of the tensor graph's Laplacian (the lowest, constant one skipped), row-major m x k;
+// evals (optional) receives their eigenvalues (treesa_gpu/spectral.py:20-92).
+std::vector<double> laplacian_vectors(const Inst& I, int k, uint64_t seed, std::vector<double>* evals);
+
+struct SpectralOrder {
+  double tc;
+  int sc;
+  std::vector<int> order;
+};
+// The candidate search over given eigenvectors V (m x d, row-major) and random unit directions rdirs
+// (consecutive d-vectors): orderings along nangles directions in the (v1, v2) plane and along rdirs, each
+// also reversed, then a halving-step angle search around the three best, every candidate scored with
+// path_cost; the k best distinct orderings, best first (treesa_gpu/spectral.py:141-199).
+std::vector<SpectralOrder> spectral_search(const Inst& I, const std::vector<double>& V, int d,
+                                           const std::vector<double>& rdirs, int k, int nangles);
+// spectral_search over eigenvectors 1..3 of the tensor graph's Laplacian and nrandom seeded directions.
+std::vector<SpectralOrder> spectral_orders(const Inst& I, int k, int nangles, int nrandom, uint64_t seed);
+
+// Greedy contraction tree: the lowest-tc tree of nrepeat runs that repeatedly contract the pair of tensors
+// sharing a label with the smallest result (ties by discovery order in run 0, at random in the others);
+// tc (optional) receives its tc.  The reference takes greedy trees from omeco (treesa_gpu/driver.py:117-122).
+std::vector<uint32_t> greedy_tree(const Inst& I, int nrepeat, uint64_t seed, double* tc);
+
 }  // namespace tsa

@@ -133,4 +133,59 @@ int tsh_greedy_repair(void* h, int W, const uint64_t* lab, uint64_t* S, double s
   return greedy_repair(I, W, lab, leaf_sets(I, W), S, sc_target);
 }
 
+// path_cost of an ordering: out = {tc, sc}.
+int tsh_path_cost(void* h, const int* order, int m, double* out) {
+  const Inst& I = *static_cast<Inst*>(h);
+  if (m != I.m) return -1;
+  const auto r = path_cost(I, std::vector<int>(order, order + m));
+  out[0] = r.first;
+  out[1] = r.second;
+  return 0;
+}
+
+// Up to k spectral orderings: orders (k * m ints), tc[k], sc[k]; returns how many were written.
+int tsh_spectral_orders(void* h, int k, int nangles, int nrandom, uint64_t seed, int* orders, double* tc, int* sc) {
+  const Inst& I = *static_cast<Inst*>(h);
+  const auto so = spectral_orders(I, k, nangles, nrandom, seed);
+  for (size_t i = 0; i < so.size(); i++) {
+    memcpy(orders + i * (size_t)I.m, so[i].order.data(), (size_t)I.m * 4);
+    tc[i] = so[i].tc;
+    sc[i] = so[i].sc;
+  }
+  return (int)so.size();
+}
+
+// spectral_search over caller-given eigenvectors (m x d) and random directions (ndirs x d); as above.
+int tsh_spectral_search(void* h, const double* V, int d, const double* dirs, int ndirs, int k, int nangles,
+                        int* orders, double* tc, int* sc) {
+  const Inst& I = *static_cast<Inst*>(h);
+  const auto so = spectral_search(I, std::vector<double>(V, V + (size_t)I.m * d), d,
+                                  std::vector<double>(dirs, dirs + (size_t)ndirs * d), k, nangles);
+  for (size_t i = 0; i < so.size(); i++) {
+    memcpy(orders + i * (size_t)I.m, so[i].order.data(), (size_t)I.m * 4);
+    tc[i] = so[i].tc;
+    sc[i] = so[i].sc;
+  }
+  return (int)so.size();
+}
+
+// Laplacian eigenvectors 1..k (m * k doubles, row-major) and eigenvalues (k); returns the k computed.
+int tsh_laplacian_vectors(void* h, int k, uint64_t seed, double* vecs, double* vals) {
+  const Inst& I = *static_cast<Inst*>(h);
+  std::vector<double> ev;
+  const auto V = laplacian_vectors(I, k, seed, &ev);
+  const int kk = (int)ev.size();
+  memcpy(vecs, V.data(), V.size() * 8);
+  memcpy(vals, ev.data(), (size_t)kk * 8);
+  return kk;
+}
+
+// Greedy tree into out (m - 1 children words); tc receives its tc.
+int tsh_greedy_tree(void* h, int nrepeat, uint64_t seed, uint32_t* out, double* tc) {
+  const Inst& I = *static_cast<Inst*>(h);
+  const auto ch = greedy_tree(I, nrepeat, seed, tc);
+  memcpy(out, ch.data(), ch.size() * 4);
+  return 0;
+}
+
 }  // extern "C"
