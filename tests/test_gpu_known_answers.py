@@ -22,12 +22,12 @@ import subprocess
 import pytest
 
 import common
-from treesa_gpu_amd import capi
+from treesa_gpu_amd import capi, formats
 
 pytestmark = pytest.mark.gpu
 
 PAT = re.compile(r"ok   (\w+) (indep|pa|trunc)\s+(greedy|random) ([\w+]+)\s*: valid=True iy=True tc ([\d.]+)==.* "
-                 r"sc (\d+)==")
+                 r"sc (\d+)==\d+ time ([\d.e+-]+)==([\d.e+-]+) time2 ([\d.e+-]+)==([\d.e+-]+)")
 
 
 def known(order):
@@ -36,7 +36,8 @@ def known(order):
         for line in f:
             m = PAT.match(line)
             if m and m.group(2) == "indep" and m.group(4) == "tc":
-                out.append((order, m.group(1), m.group(3), float(m.group(5)), int(m.group(6))))
+                out.append((order, m.group(1), m.group(3), float(m.group(5)), int(m.group(6)),
+                            tuple(m.group(i) for i in (7, 8, 9, 10))))
     return out
 
 
@@ -48,8 +49,13 @@ def julia_betas(a=0.01, step=0.05, b=15.0):
     return [a + i * step for i in range(n)]
 
 
-@pytest.mark.parametrize("order,inst,init,tc,sc", CASES, ids=[f"{c[0]}-{c[1]}-{c[2]}" for c in CASES])
-def test_driver_argv_reproduces_reference_results(order, inst, init, tc, sc, tmp_path):
+def same_printed(x, printed):
+    """x printed with %.4e gives the reference's printed value."""
+    return f"{x:.4e}" == printed
+
+
+@pytest.mark.parametrize("order,inst,init,tc,sc,times", CASES, ids=[f"{c[0]}-{c[1]}-{c[2]}" for c in CASES])
+def test_driver_argv_reproduces_reference_results(order, inst, init, tc, sc, times, tmp_path):
     bf = tmp_path / "betas.txt"
     bf.write_text("\n".join(repr(float(b)) for b in julia_betas()) + "\n")
     out = str(tmp_path / "out.json")
@@ -68,3 +74,13 @@ def test_driver_argv_reproduces_reference_results(order, inst, init, tc, sc, tmp
         r = json.load(f)
     assert r["valid"] and r["labels_ok"]
     assert abs(r["tc"] - tc) < 6e-5 and r["sc"] == sc, (r["tc"], r["sc"])
+    # the driver's reading of the result (treesa_gpu/driver.py:313-328): the tree dict and its model times
+    # recomputed in Python equal the reference's printed values and the binary's own (1e-5 in log,
+    # tests/test_python.py:60-61)
+    m, nlab, ixs, iy = common.load_instance(inst)
+    tree, info = formats.result_tree(r, ixs, iy)
+    assert formats.recompute_outputs(tree, ixs, iy) == tree
+    assert abs(info["tc_py"] - r["tc"]) < 1e-4 and info["sc_py"] == r["sc"]
+    assert same_printed(info["gpu_time_py"], times[1]) and same_printed(info["h100_time_py"], times[3]), times
+    assert abs(math.log(r["gpu_time"]) - math.log(info["gpu_time_py"])) < 1e-5
+    assert abs(math.log(r["h100_time"]) - math.log(info["h100_time_py"])) < 1e-5
