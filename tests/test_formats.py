@@ -65,6 +65,34 @@ def test_round_trip_and_path_cost(name):
     assert F.dict_to_children(d, m) == pairs(S.path_tree(list(range(m))))
 
 
+def relabel(ch, m, rng):
+    """The same tree with its internal nodes renumbered at random (root kept last), as the annealer's records
+    hold them: a child may have a larger id than its parent."""
+    perm = list(range(m, 2 * m - 2))
+    rng.shuffle(perm)
+    mp = {old: new for old, new in zip(range(m, 2 * m - 2), perm)}
+    mp[2 * m - 2] = 2 * m - 2
+    out = [None] * (m - 1)
+    for i, (l, r) in enumerate(ch):
+        out[mp[m + i] - m] = (mp.get(l, l), mp.get(r, r))
+    return out
+
+
+@pytest.mark.parametrize("name", ["sat40", "lat10"])
+def test_children_in_any_order(name):
+    m, nlab, ixs, iy = common.load_instance(name)
+    rng = np.random.default_rng(3)
+    ch = pairs(host.random_tree(m, 9))
+    ch2 = relabel(ch, m, rng)
+    assert any(max(l, r) > m + i for i, (l, r) in enumerate(ch2))
+    d, d2 = F.children_to_dict(ch, m, ixs, iy), F.children_to_dict(ch2, m, ixs, iy)
+    assert d == d2 and F.dict_to_children(d2, m) == F.dict_to_children(d, m)
+    bad = list(ch2)
+    bad[0] = (bad[1][0], bad[0][1])  # a subtree shared by two parents
+    with pytest.raises(ValueError):
+        F.children_to_dict(bad, m, ixs, iy)
+
+
 def test_dict_to_children_rejects_bad_trees():
     with pytest.raises(ValueError):
         F.dict_to_children({"args": [{"tensor_index": 0}, {"tensor_index": 0}]}, 2)

@@ -288,7 +288,8 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
   // the small tables every proposal indexes per lane live in LDS
   if (threadIdx.x < 64) s_lse[threadIdx.x] = P.lse[threadIdx.x];
   if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
-  const TsaMathTabs T{s_exp2, fix, nullptr, tsa_log2_tab_d};  // (the log2 table only serves energies here)
+  // the log2 tables only serve energies here; the correction table's summary bitmap follows its words
+  const TsaMathTabs T{s_exp2, fix, fix + TSA_LOG2FIX_WORDS, tsa_log2_tab_d};
   const uint64_t* lf = leaf;
   int leafw = 0;
   if constexpr (LDS) {
@@ -505,7 +506,7 @@ __global__ void __launch_bounds__(256) k_energy(TsaKParams P, const uint64_t* __
   __shared__ uint64_t s_exp2[32];
   if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
   __syncthreads();
-  const TsaMathTabs T{s_exp2, fix, nullptr, tsa_log2_tab_d};  // (the log2 table only serves energies here)
+  const TsaMathTabs T{s_exp2, fix, fix + TSA_LOG2FIX_WORDS, tsa_log2_tab_d};
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   const int c = t >> 5, l32 = threadIdx.x & 31;
   const int cc = c < nchains ? c : nchains - 1;  // a half-wave past the end duplicates the last chain

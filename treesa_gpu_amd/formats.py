@@ -72,12 +72,35 @@ def dict_to_children(d, m):
 def children_to_dict(ch, m, ixs, iy):
     """Children list (node ids, root 2m-2; pairs or the binary's [l, r] lists) -> tree dict with
     topology-derived internal labels."""
+    if m == 1:
+        return recompute_outputs({"tensor_index": 0}, ixs, iy)
+    ch = [(int(l), int(r)) for l, r in ch]
+    if len(ch) != m - 1:
+        raise ValueError("a tree over m tensors has m - 1 internal nodes")
     node = {}
-    for v in range(m):
-        node[v] = {"tensor_index": v}
-    for i, (l, r) in enumerate(ch):
-        node[m + i] = {"args": [node[int(l)], node[int(r)]], "eins": {"ixs": [[], []], "iy": []}}
-    return recompute_outputs(node[2 * m - 2] if m > 1 else node[0], ixs, iy)
+    seen = set()
+    stack = [2 * m - 2]  # internal nodes may be numbered in any order: build from the root down
+    while stack:
+        v = stack[-1]
+        if v < m:
+            node[v] = {"tensor_index": v}
+            stack.pop()
+            continue
+        l, r = ch[v - m]
+        if l in node and r in node:
+            node[v] = {"args": [node[l], node[r]], "eins": {"ixs": [[], []], "iy": []}}
+            stack.pop()
+            continue
+        if v in seen:
+            raise ValueError("children list is not a binary tree over all m tensors")
+        seen.add(v)
+        for u in (r, l):
+            if not 0 <= u < 2 * m - 1 or u in seen or u in node:
+                raise ValueError("children list is not a binary tree over all m tensors")
+            stack.append(u)
+    if len(node) != 2 * m - 1:
+        raise ValueError("children list is not a binary tree over all m tensors")
+    return recompute_outputs(node[2 * m - 2], ixs, iy)
 
 
 def recompute_outputs(d, ixs, iy):
