@@ -270,6 +270,9 @@ __device__ __forceinline__ long long tsa_wave_sum(long long x) {
   return x;
 }
 
+// 64-node groups per batch of the par scan.
+#define TSA_SCAN_GROUPS 8
+
 // Sweep kernel.  ORDER 0: par, 1: pre-order.  LDS: chain and leaf table staged in LDS.
 // LDS layout (words): [leaf table (LDS variant only), rounded to even] then per wave lds_words:
 // [chain record (LDS variant only)][pri u16 x nint4][par u16 x nint4][work list u16 x nint4]
@@ -362,36 +365,53 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
       }
       tsa_wave_sync();
       for (;;) {
-        // scan: the phase's independent set into the work list
+        // scan: the phase's independent set into the work list.  Node v is active when its priority is
+        // nonzero and its (priority, id) key beats those of its unvisited parent and internal children.
+        // TSA_SCAN_GROUPS 64-node groups at a time, branch-free: every lane reads its node's priority,
+        // parent and children words, then the three neighbour priorities (index 0 where there is no such
+        // neighbour), so a batch costs two dependent LDS round trips.
         int cnt = 0;
-        for (int i0 = 0; i0 < nint; i0 += 64) {
-          const int i = i0 + lane;
-          bool act = false;
-          if (i < nint) {
-            const uint32_t pv = pri[i];
-            if (pv) {
-              const uint32_t key = (pv << 16) | (uint32_t)(m + i);
-              act = true;
-              const uint32_t p = par[i];
-              if (p != 0xFFFFu) {
-                const uint32_t pp = pri[p - m];
-                if (pp && ((pp << 16) | p) > key) act = false;
-              }
-              const uint32_t cw = ch[i];
-              const uint32_t l = cw & 0xFFFFu, r = cw >> 16;
-              if (act && l >= (uint32_t)m) {
-                const uint32_t pl = pri[l - m];
-                if (pl && ((pl << 16) | l) > key) act = false;
-              }
-              if (act && r >= (uint32_t)m) {
-                const uint32_t pr = pri[r - m];
-                if (pr && ((pr << 16) | r) > key) act = false;
-              }
+        for (int i0 = 0; i0 < nint; i0 += 64 * TSA_SCAN_GROUPS) {
+          const int ng = (nint - i0 + 63) >> 6;  // groups present in this batch (wave-uniform)
+          uint32_t pv[TSA_SCAN_GROUPS], pw[TSA_SCAN_GROUPS], cw[TSA_SCAN_GROUPS];
+#pragma unroll
+          for (int q = 0; q < TSA_SCAN_GROUPS; q++) {
+            pv[q] = 0u;
+            pw[q] = 0xFFFFu;
+            cw[q] = 0u;
+            if (q < ng) {
+              const int i = i0 + 64 * q + lane;
+              const int ii = i < nint ? i : 0;
+              pv[q] = pri[ii];
+              pw[q] = par[ii];
+              cw[q] = ch[ii];
             }
           }
-          const uint64_t b = __ballot(act);
-          if (act) wl[cnt + __popcll(b & tsa_lt_mask(lane))] = (uint16_t)(m + i);
-          cnt += __popcll(b);
+          uint32_t np_[TSA_SCAN_GROUPS], nl[TSA_SCAN_GROUPS], nr[TSA_SCAN_GROUPS];
+#pragma unroll
+          for (int q = 0; q < TSA_SCAN_GROUPS; q++) {
+            np_[q] = nl[q] = nr[q] = 0u;
+            if (q < ng) {
+              const uint32_t p = pw[q], l = cw[q] & 0xFFFFu, r = cw[q] >> 16;
+              np_[q] = pri[p != 0xFFFFu ? p - (uint32_t)m : 0u];
+              nl[q] = pri[l >= (uint32_t)m ? l - (uint32_t)m : 0u];
+              nr[q] = pri[r >= (uint32_t)m ? r - (uint32_t)m : 0u];
+            }
+          }
+#pragma unroll
+          for (int q = 0; q < TSA_SCAN_GROUPS; q++) {
+            if (q >= ng) break;
+            const int i = i0 + 64 * q + lane;
+            const uint32_t key = (pv[q] << 16) | (uint32_t)(m + i);
+            const uint32_t p = pw[q], l = cw[q] & 0xFFFFu, r = cw[q] >> 16;
+            const bool beat_p = p != 0xFFFFu && np_[q] != 0u && ((np_[q] << 16) | p) > key;
+            const bool beat_l = l >= (uint32_t)m && nl[q] != 0u && ((nl[q] << 16) | l) > key;
+            const bool beat_r = r >= (uint32_t)m && nr[q] != 0u && ((nr[q] << 16) | r) > key;
+            const bool act = i < nint && pv[q] != 0u && !beat_p && !beat_l && !beat_r;
+            const uint64_t b = __ballot(act);
+            if (act) wl[cnt + __popcll(b & tsa_lt_mask(lane))] = (uint16_t)(m + i);
+            cnt += __popcll(b);
+          }
         }
         if (cnt == 0) break;
         nst++;
