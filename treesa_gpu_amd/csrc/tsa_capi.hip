@@ -544,7 +544,8 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     TSA_HIP(ctx, hipEventCreate(&e));
     ctx->ev.push_back(e);
   }
-  // e0 / e1 bracket the sweep kernel alone (the summary and cost passes some launches need go before e0)
+  // e0 / e1 take the start and stop times of the sweep kernel alone, recorded by its dispatch (no marker
+  // packets between the kernels of a level)
   hipEvent_t e0 = ctx->ev[2 * ctx->npending], e1 = ctx->ev[2 * ctx->npending + 1];
   ctx->energy_fresh = false;
   if (ctx->wide.on && order == TSA_ORDER_PAR) {
@@ -576,10 +577,8 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
       sy.snap_cost = ctx->d_snap_cost[s];
       sy.snap_nz = ctx->d_snap_nz[s];
     }
-    TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
     TSA_HIP(ctx, tsa_launch_wide(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains, beta,
-                                 sweep0, nsweeps, ctx->d_stats, sy, ctx->st));
-    TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
+                                 sweep0, nsweeps, ctx->d_stats, sy, ctx->st, e0, e1));
     if (s >= 0) {
       ctx->ev_sweep[s] = e1;  // the selection of this snapshot waits for the sweep's stop event
       ctx->last_slot = s;
@@ -592,10 +591,8 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     join_track(ctx);      // a pending fold may still read the node-cost snapshot; d_lc is rewritten below
     const bool fuse = ctx->cfg.fused_energy != 0;
     const TsaEnergyOut eo{fuse ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns};
-    TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
     TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
-                                   ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st));
-    TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
+                                   ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st, e0, e1));
     ctx->energy_fresh = fuse;
   }
   ctx->npending++;

@@ -3,6 +3,7 @@
 #pragma once
 #include <stdint.h>
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include "tsa_arith.h"
 #include "tsa_select.h"
 
@@ -67,7 +68,8 @@ __device__ __forceinline__ void tsa_copy_inflight(T* dst, const T* __restrict__ 
 // Host-side launchers (tsa_kernels.hip).  All return hipError_t of the launch.
 hipError_t tsa_launch_sweeps(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
                              const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
-                             int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st);
+                             int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st,
+                             hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
                              const uint32_t* fix, int nchains, float* lc, int* sc, int* ns, hipStream_t st);
 struct TsaTrackState {
@@ -182,7 +184,8 @@ hipError_t tsa_launch_wsum(const TsaWide& X, const TsaKParams& P, const uint64_t
                            hipStream_t st);
 hipError_t tsa_launch_wide(const TsaWide& X, int mode, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
                            const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
-                           unsigned long long* stats, const TsaWideSync& sy, hipStream_t st);
+                           unsigned long long* stats, const TsaWideSync& sy, hipStream_t st,
+                           hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 // Energies through per-node costs: ncost / nz hold nchains * nint4 node costs and masked sizes, fcnt
 // nchains zeroed counters.  nodes = 1: recompute every node cost from the label sets first; nodes = 0: fold
 // the cached costs only.

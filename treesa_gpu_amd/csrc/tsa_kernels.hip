@@ -681,7 +681,8 @@ __global__ void k_track_init(TsaTrackState* st, unsigned long long* ticks0) {
 template <int W, int MODE, int ORDER, bool LDS>
 static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
                                  const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
-                                 unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st) {
+                                 unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st, hipEvent_t e0,
+                                 hipEvent_t e1) {
   const int NW = W > 0 ? W : P.W;
   const size_t leafw = LDS ? (size_t)((P.m * NW + 1) & ~1) : 0;
   const size_t smem = (leafw + (size_t)L.wpb * L.lds_words) * 8;
@@ -693,46 +694,50 @@ static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64
     attr_set = smem;
   }
   const int grid = (nchains + L.wpb - 1) / L.wpb;
-  hipLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS>), dim3(grid), dim3(64 * L.wpb), smem, st, P, rec, leaf, fix,
-                     nchains, L.lds_words, beta, sweep0, nsweeps, stats, eo);
+  // e0 / e1 (null: none) take the kernel's start and stop times in the dispatch itself
+  hipExtLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS>), dim3(grid), dim3(64 * L.wpb), (uint32_t)smem, st, e0, e1, 0u,
+                        P, rec, leaf, fix, nchains, L.lds_words, beta, sweep0, nsweeps, stats, eo);
   return hipGetLastError();
 }
 
 template <int W, int MODE>
 static hipError_t launch_sweep_wm(const TsaLaunch& L, int order, const TsaKParams& P, uint64_t* rec,
                                   const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
-                                  int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st) {
+                                  int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st,
+                                  hipEvent_t e0, hipEvent_t e1) {
   if constexpr (W > 0) {
     if (L.lds) {
-      if (order == 0) return launch_sweep_t<W, MODE, 0, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
-      return launch_sweep_t<W, MODE, 1, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+      if (order == 0) return launch_sweep_t<W, MODE, 0, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+      return launch_sweep_t<W, MODE, 1, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
     }
     return hipErrorInvalidValue;  // the register-width kernels exist only in the LDS variant
   } else {
     if (L.lds) return hipErrorInvalidValue;
-    if (order == 0) return launch_sweep_t<0, MODE, 0, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
-    return launch_sweep_t<0, MODE, 1, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+    if (order == 0) return launch_sweep_t<0, MODE, 0, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+    return launch_sweep_t<0, MODE, 1, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
   }
 }
 
 template <int W>
 static hipError_t launch_sweep_w(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
                                  const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
-                                 int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st) {
-  if (mode == 0) return launch_sweep_wm<W, 0>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
-  if (mode == 1) return launch_sweep_wm<W, 1>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
-  return launch_sweep_wm<W, 2>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+                                 int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st,
+                                 hipEvent_t e0, hipEvent_t e1) {
+  if (mode == 0) return launch_sweep_wm<W, 0>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+  if (mode == 1) return launch_sweep_wm<W, 1>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+  return launch_sweep_wm<W, 2>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
 }
 
 hipError_t tsa_launch_sweeps(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
                              const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
-                             int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st) {
+                             int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st,
+                             hipEvent_t e0, hipEvent_t e1) {
   switch (L.W) {
-    case 1: return launch_sweep_w<1>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
-    case 2: return launch_sweep_w<2>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
-    case 4: return launch_sweep_w<4>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
-    case 8: return launch_sweep_w<8>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
-    case 0: return launch_sweep_w<0>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st);
+    case 1: return launch_sweep_w<1>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+    case 2: return launch_sweep_w<2>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+    case 4: return launch_sweep_w<4>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+    case 8: return launch_sweep_w<8>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+    case 0: return launch_sweep_w<0>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
     default: return hipErrorInvalidValue;
   }
 }

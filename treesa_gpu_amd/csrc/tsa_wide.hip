@@ -787,31 +787,34 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
 template <int G, int MODE, bool SUMS>
 hipError_t launch_wide_gms(const TsaWide& X, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
                            const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
-                           unsigned long long* stats, const TsaWideSync& sy, hipStream_t st) {
+                           unsigned long long* stats, const TsaWideSync& sy, hipStream_t st, hipEvent_t e0,
+                           hipEvent_t e1) {
+  // e0 / e1 (null: none) take the kernel's start and stop times in the dispatch itself
   if (X.K > 1) {
     // an ordinary launch: the plan admits K > 1 only when all nchains * K workgroups fit on the device at
     // once, so on an idle device they are all resident together (the cooperative launch API gives the same
     // guarantee but costs tens of microseconds per launch on the host side); if they ever are not, a chain
     // barrier runs out of polls, sets the error word and every workgroup leaves
     const int nchains8 = (nchains + 7) & ~7;  // (chains grouped by XCD, see k_wide)
-    hipLaunchKernelGGL((k_wide<G, MODE, true, SUMS>), dim3(nchains8 * X.K), dim3(X.nt), (size_t)X.smem, st, P, rec,
-                       leaf, fix, nchains, X.K, beta, sweep0, nsweeps, stats, sy);
+    hipExtLaunchKernelGGL((k_wide<G, MODE, true, SUMS>), dim3(nchains8 * X.K), dim3(X.nt), (uint32_t)X.smem, st, e0,
+                          e1, 0u, P, rec, leaf, fix, nchains, X.K, beta, sweep0, nsweeps, stats, sy);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL((k_wide<G, MODE, false, SUMS>), dim3(nchains), dim3(X.nt), (size_t)X.smem, st, P, rec, leaf,
-                     fix, nchains, 1, beta, sweep0, nsweeps, stats, sy);
+  hipExtLaunchKernelGGL((k_wide<G, MODE, false, SUMS>), dim3(nchains), dim3(X.nt), (uint32_t)X.smem, st, e0, e1, 0u,
+                        P, rec, leaf, fix, nchains, 1, beta, sweep0, nsweeps, stats, sy);
   return hipGetLastError();
 }
 
 template <int G, bool SUMS>
 hipError_t launch_wide_g(const TsaWide& X, int mode, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
                          const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
-                         unsigned long long* stats, const TsaWideSync& sy, hipStream_t st) {
+                         unsigned long long* stats, const TsaWideSync& sy, hipStream_t st, hipEvent_t e0,
+                         hipEvent_t e1) {
   if (mode == 0)
-    return launch_wide_gms<G, 0, SUMS>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    return launch_wide_gms<G, 0, SUMS>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
   if (mode == 1)
-    return launch_wide_gms<G, 1, SUMS>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-  return launch_wide_gms<G, 2, SUMS>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    return launch_wide_gms<G, 1, SUMS>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
+  return launch_wide_gms<G, 2, SUMS>(X, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
 }
 
 template <int G, int MODE>
@@ -1001,23 +1004,24 @@ hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int w
 
 hipError_t tsa_launch_wide(const TsaWide& X, int mode, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
                            const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
-                           unsigned long long* stats, const TsaWideSync& sy, hipStream_t st) {
+                           unsigned long long* stats, const TsaWideSync& sy, hipStream_t st, hipEvent_t e0,
+                           hipEvent_t e1) {
   if (X.nsw) {
     switch (X.G) {
-      case 1: return launch_wide_g<1, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-      case 2: return launch_wide_g<2, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-      case 4: return launch_wide_g<4, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-      case 8: return launch_wide_g<8, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-      case 16: return launch_wide_g<16, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+      case 1: return launch_wide_g<1, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
+      case 2: return launch_wide_g<2, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
+      case 4: return launch_wide_g<4, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
+      case 8: return launch_wide_g<8, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
+      case 16: return launch_wide_g<16, true>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
       default: return hipErrorInvalidValue;
     }
   }
   switch (X.G) {
-    case 4: return launch_wide_g<4, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-    case 8: return launch_wide_g<8, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-    case 16: return launch_wide_g<16, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-    case 32: return launch_wide_g<32, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
-    case 64: return launch_wide_g<64, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st);
+    case 4: return launch_wide_g<4, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
+    case 8: return launch_wide_g<8, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
+    case 16: return launch_wide_g<16, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
+    case 32: return launch_wide_g<32, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
+    case 64: return launch_wide_g<64, false>(X, mode, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, sy, st, e0, e1);
     default: return hipErrorInvalidValue;
   }
 }
