@@ -29,14 +29,16 @@ def leaf_sets(m, ixs, W):
 class Case:
     def __init__(self, inst, order, mode, init="greedy", random_slices=0, par_follow=False, par_band=0, slicing=False,
                  slice_moves=1, slice_every=1, nchains=NCHAINS, kernel=capi.KERNEL_AUTO, wide=False, seed=None,
-                 sc_target=None, wide_waves=0, wide_wgs=0, sums=0, lanes=0):
+                 sc_target=None, wide_waves=0, wide_wgs=0, sums=0, lanes=0, data=None):
+        """inst names a fixture; data = (m, nlab, ixs, iy) gives an instance directly (then init must be a
+        start-tree kind without fixture, e.g. "random")."""
         self.inst, self.order = inst, order
-        m, nlab, ixs, iy = common.load_instance(inst)
+        m, nlab, ixs, iy = common.load_instance(inst) if data is None else data
         self.m, self.nlab, self.ixs = m, nlab, ixs
         self.O = orc.Oracle(m, nlab, ixs, iy)
         self.lay = capi.layout(m, nlab, wide)
         seed = common.CHECK_SEED if seed is None else seed
-        tf = common.tree_file(inst, init)
+        tf = common.tree_file(inst, init) if data is None else None
         trees = orc.read_trees_py(tf, m) if tf else None
         self.pop0 = common.oracle_population(self.O, self.lay, m, nchains, seed, trees, random_slices)
         sl = slicing or random_slices > 0

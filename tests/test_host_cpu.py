@@ -9,8 +9,9 @@ import numpy as np
 import pytest
 
 import common
+import edge_instances
 import oracle as orc
-from treesa_gpu_amd import capi, host
+from treesa_gpu_amd import capi, formats, host
 
 ROOT = common.HERE.rsplit(os.sep, 1)[0]
 
@@ -136,3 +137,27 @@ def test_cli_errors_before_any_gpu_call(tmp_path):
     bt.write_text("".join(f"{i} {i}\n" for i in range(169)))  # 169 lines but not a tree
     p = cli("-i", inst, "--tree", str(bt))
     assert p.returncode == 1 and "invalid initial tree" in p.stderr
+
+
+@pytest.mark.parametrize("name", edge_instances.NAMES)
+def test_host_layer_on_edge_instances(name):
+    """Empty tensors, labels held by one tensor, open labels and every width boundary: the host layer's
+    topology labels equal the oracle's, and its exact energy equals the Python formats' closed form."""
+    m, nlab, ixs, iy = edge_instances.instance(name)
+    O = orc.Oracle(m, nlab, ixs, iy)
+    inst = host.Instance(m=m, nlab=nlab, ixs=ixs, iy=iy)
+    lay = capi.layout(m, nlab)
+    for seed in range(3):
+        ch = host.random_tree(m, 100 + seed)
+        assert np.array_equal(inst.labels(ch, lay.W), O.labels(ch, lay.W))
+        rec = inst.population(lay, np.array([ch]), 1, seed=0)[0]
+        tc, sc = inst.host_energy(lay, rec, slicing=False)[:2]
+        d = formats.children_to_dict([(int(w) & 0xFFFF, int(w) >> 16) for w in ch], m, ixs, iy)
+        t2, s2 = formats.complexity(d, ixs)
+        assert abs(tc - t2) < 1e-9 and sc == s2
+
+
+def test_layout_rejects_fewer_than_three_tensors():
+    m, nlab, ixs, iy = edge_instances.instance("pair")
+    with pytest.raises(capi.TsaError, match="at least 3 tensors"):
+        capi.layout(m, nlab)
