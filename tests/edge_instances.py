@@ -6,7 +6,9 @@
   labels held by two and by three tensors;
 * deg3_<L>: L labels each held by two tensors, three labels per tensor, at the label-count boundaries of the
   register widths (64 | 65, 128 | 129, 256 | 257 labels -> 1, 2, 4, 8 words) and of the runtime width
-  (513 labels).
+  (513 labels);
+* wide_<L>: 300 tensors and L labels each held by two tensors: 16384 labels is the widest chain the wide
+  kernel takes (256 words), 16385 falls back to the one-wave kernel with runtime width.
 """
 import numpy as np
 
@@ -43,6 +45,17 @@ def _mixed40():
     return m, nlab, [sorted(ix) for ix in ixs], [0, 13, 69]
 
 
+def _wide(nlab, seed):
+    m = 300
+    rng = np.random.default_rng(seed)
+    ixs = [[] for _ in range(m)]
+    for l in range(nlab):
+        a, b = rng.choice(m, 2, replace=False)
+        ixs[int(a)].append(l)
+        ixs[int(b)].append(l)
+    return m, nlab, ixs, []
+
+
 def instance(name):
     if name == "pair":
         return 2, 3, [[0, 1], [1, 2]], [0]
@@ -52,7 +65,10 @@ def instance(name):
         return _mixed40()
     if name.startswith("deg3_"):
         return _deg3(int(name[5:]), 3)
+    if name.startswith("wide_"):
+        return _wide(int(name[5:]), 5)
     raise KeyError(name)
 
 
 NAMES = ["triple", "mixed40", "deg3_64", "deg3_65", "deg3_129", "deg3_257", "deg3_513"]
+WIDE = ["wide_16384", "wide_16385"]

@@ -157,7 +157,10 @@ def test_host_layer_on_edge_instances(name):
         assert abs(tc - t2) < 1e-9 and sc == s2
 
 
-def test_layout_rejects_fewer_than_three_tensors():
+def test_layout_rejects_fewer_than_three_tensors_and_17_bit_node_ids():
     m, nlab, ixs, iy = edge_instances.instance("pair")
     with pytest.raises(capi.TsaError, match="at least 3 tensors"):
         capi.layout(m, nlab)
+    assert capi.layout(32768, 3).nint == 32767  # node ids up to 65534
+    with pytest.raises(capi.TsaError, match="16-bit"):
+        capi.layout(32769, 3)
