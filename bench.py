@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Throughput of the TreeSA sweep path on one MI355X (node visits/s), with its roofline and a CPU baseline.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--reps R] [--config c2] [--no-cpu]
 
 Workload (default c2, the headline): random 3-SAT n=100 (m=426 clause tensors, 100 labels,
 tests/golden/data/sat100.txt), par-order sweeps of 8192 independent chains starting from the reference's three
@@ -13,7 +13,8 @@ region; K steps run levels 0..K-1 of the schedule (wrapping after 200).
 
 The timed region is the drop-in binary's own level loop (bin/treesa_gpu, t_anneal: after the population is
 resident in HBM, until the last level's energies are back), after --bench-warmup W untimed levels.
-value = K * nchains * (m - 1) / that wall time (whole job).
+value = K * nchains * (m - 1) / that wall time (whole job), of the median of R runs (default 5; their results are
+identical, their spread is reported as "repetitions").
 kernel_visits_per_s = the reference's own definition (bench/throughput.py:64-70): node visits over the
 event-timed sweep kernels only.  roofline: algorithmic bytes of the sweep kernel per launch (5 label sets of
 W words + 8 B of children per proposal, W words + 8 B written per accept, 4 B per visit without a rule, from
@@ -241,6 +242,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="levels timed (default: the workload's schedule)")
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--reps", type=int, default=5, help="runs of the workload; the median run is reported")
     ap.add_argument("--config", default="c2", choices=sorted(CONFIGS))
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-chains", type=int, default=None, help="chains in the CPU sample (default per workload)")
@@ -275,9 +277,15 @@ def main():
     visits = steps * C["niters"] * nchains * (inst.m - 1)
 
     def measure(extra_args):
-        """One run of the binary: its JSON, the sweep kernel's algorithmic bytes and mean duration per launch,
-        and the roofline block of that kernel."""
-        r = run_binary(C, trees, betas, steps, a.warmup, a.scheme, extra_args)
+        """a.reps runs of the binary; of the run with the median wall time: its JSON, the sweep kernel's
+        algorithmic bytes and mean duration per launch, and the roofline block of that kernel.  The results of
+        the runs are identical (same seed); only their timings differ."""
+        runs = [run_binary(C, trees, betas, steps, a.warmup, a.scheme, extra_args) for _ in range(max(1, a.reps))]
+        assert all(x["tc"] == runs[0]["tc"] and x["tree"] == runs[0]["tree"] for x in runs), "runs disagree"
+        runs.sort(key=lambda x: x["t_anneal"])
+        r = runs[len(runs) // 2]
+        r["_spread"] = {"reps": len(runs), "value_min": visits / runs[-1]["t_anneal"],
+                        "value_max": visits / runs[0]["t_anneal"]}
         assert r["node_visits"] == visits, (r["node_visits"], visits)
         st = [r["proposals"], r["accepts"], r["warp_steps"], r["node_visits"], r["slice_proposals"]]
         slice_steps = steps * C["niters"] * nchains if C["slicing"] else 0
@@ -307,7 +315,7 @@ def main():
         "kernel_visits_per_s": visits / r["kernel_s"], "sweeps_per_s_per_chain": steps * C["niters"] / r["kernel_s"],
         "slice_proposals": r["slice_proposals"], "slice_accepts": r["slice_accepts"], "nsliced": r["nsliced"],
         "proposals": r["proposals"], "accepts": r["accepts"], "phases": r["warp_steps"],
-        "best_tc": r["tc"], "best_sc": r["sc"], "wall_s": wall,
+        "best_tc": r["tc"], "best_sc": r["sc"], "wall_s": wall, "repetitions": r["_spread"],
         "roofline": roof,
     }
     if label_path(r.get("hip_kernel") or "") == "sums" and a.sums == "auto":
@@ -317,7 +325,7 @@ def main():
         assert rd["tc"] == r["tc"] and rd["tree"] == r["tree"], "dense and summary paths disagree"
         res["dense_streaming"] = {"value": visits / rd["t_anneal"], "ms_per_step": rd["t_anneal"] * 1e3 / steps,
                                   "kernel_visits_per_s": visits / rd["kernel_s"], "kernel": rd.get("hip_kernel"),
-                                  "roofline": roofd}
+                                  "repetitions": rd["_spread"], "roofline": roofd}
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(a.config, C, inst, trees, betas, min(a.cpu_chains or C["cpu_chains"], nchains))
     print(json.dumps(res))
