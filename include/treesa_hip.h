@@ -77,10 +77,12 @@ typedef struct tsa_config_t {
   int32_t v2_small_rank;
   /* wide kernel plan (0 = automatic): waves per workgroup (1..16), workgroups per chain (1..16) */
   int32_t wide_waves, wide_wgs;
-  /* 1: every tsa_sweeps on the register-width path also leaves the energies of the swept population ready
-   * (each chain is evaluated by the sweep kernel while it is still staged in LDS), so that tsa_energy /
-   * tsa_track launch no energy kernel; for callers that evaluate after every level.  The wide path keeps a
-   * node-cost cache instead and its energy call only folds it. */
+  /* 1: every tsa_sweeps on the register-width path also leaves the energies of the swept population ready,
+   * so that tsa_energy / tsa_track launch no energy kernel; for callers that evaluate after every level.  The
+   * sweep kernel computes every node's cost while the chain is still staged in LDS and folds it there, or,
+   * with more than twice the chains that fit on the device at once (or with 2), leaves the costs to a fold
+   * kernel that folds every chain in one round.  The wide path keeps a node-cost cache instead and its energy call
+   * only folds it. */
   int32_t fused_energy;
   /* chunk summaries of the wide kernel (the reference's --sums / --no-sum, csrc/treesa_gpu.cu:1444-1448):
    * 0 = automatic (on from 64 words per label set, 4096 labels), 1 = on, -1 = off.  With summaries a

@@ -227,14 +227,19 @@ def test_wide_cached_energies_every_level(mode, gm):
 
 
 # Fused energies (every sweep launch also leaves the energies of the swept population): after every level
-# tsa_energy returns exactly the oracle's evaluation, on the LDS, HBM and wide kernels and both wide plans.
-@pytest.mark.parametrize("inst,kernel,wgs,mode", [("sat100", capi.KERNEL_LDS, 0, "tc"), ("sat60", capi.KERNEL_GLOBAL, 0, "h100"),
-                                                  ("sq46", capi.KERNEL_WIDE, 0, "tc"), ("sq46", capi.KERNEL_WIDE, 1, "gpu"),
-                                                  ("grid24", capi.KERNEL_WIDE, 3, "h100")])
-def test_fused_energies_every_level(inst, kernel, wgs, mode):
-    case = Case(inst, "par", mode, kernel=kernel, nchains=24, wide=kernel == capi.KERNEL_WIDE)
+# tsa_energy returns exactly the oracle's evaluation, on the LDS, HBM and wide kernels and both wide plans, with
+# the fold in the sweep kernel (fused 1 at these chain counts) or in the fold kernel (fused 2), also with
+# fixed slice sets.
+@pytest.mark.parametrize("inst,kernel,wgs,mode,fused,rs", [
+    ("sat100", capi.KERNEL_LDS, 0, "tc", 1, 0), ("sat60", capi.KERNEL_GLOBAL, 0, "h100", 1, 0),
+    ("sat100", capi.KERNEL_LDS, 0, "tc", 2, 0), ("sat60", capi.KERNEL_LDS, 0, "gpu", 2, 0),
+    ("sat40", capi.KERNEL_LDS, 0, "tc", 2, 8), ("sat60", capi.KERNEL_GLOBAL, 0, "h100", 2, 0),
+    ("sq46", capi.KERNEL_WIDE, 0, "tc", 1, 0), ("sq46", capi.KERNEL_WIDE, 1, "gpu", 1, 0),
+    ("grid24", capi.KERNEL_WIDE, 3, "h100", 1, 0)])
+def test_fused_energies_every_level(inst, kernel, wgs, mode, fused, rs):
+    case = Case(inst, "par", mode, kernel=kernel, nchains=24, wide=kernel == capi.KERNEL_WIDE, random_slices=rs)
     case.cfg = capi.make_config(mode=mode, sc_target=common.CHECK_SC_TARGET, seed=common.CHECK_SEED, kernel=kernel,
-                                wide_wgs=wgs, fused_energy=True)
+                                wide_wgs=wgs, fused_energy=fused, slicing=rs > 0, slice_moves=0)
     opop = case.pop0.copy()
     print(f"[gpu] fused energies {inst} kernel={kernel} wgs={wgs} mode={mode}", flush=True)
     with capi.Context(case.lay, case.leaf, case.leaf_sc, case.cfg, case.nchains) as ctx:
@@ -250,6 +255,30 @@ def test_fused_energies_every_level(inst, kernel, wgs, mode):
         desc = ctx.describe()
     if kernel == capi.KERNEL_WIDE:
         assert desc.startswith("wide") and "fold_stage=" in desc, desc
+    else:
+        assert ("fold=apart" in desc) == (fused == 2), desc
+
+
+def test_fold_kernel_at_benchmark_size():
+    """8192 chains of the 3-SAT n=100 instance: more than the device holds at once, so the automatic plan
+    leaves node costs to the fold kernel; one level against the oracle (records, counts, energies)."""
+    case = Case("sat100", "par", "tc", init="multi", nchains=8192)
+    case.cfg = capi.make_config(mode="tc", sc_target=20.0, seed=1, fused_energy=True)
+    case.P = orc.params_from_config(case.cfg, case.leaf_sc, case.nlab)
+    print("[gpu] fold kernel at 8192 chains", flush=True)
+    with capi.Context(case.lay, case.leaf, case.leaf_sc, case.cfg, case.nchains) as ctx:
+        ctx.upload(case.pop0)
+        ctx.sweeps(case.ord, 2.0, 0, 1)
+        gen = ctx.energy()
+        gpop = ctx.download()
+        desc = ctx.describe()
+    assert "fold=apart" in desc, desc
+    opop = case.pop0.copy()
+    case.O.sweeps(case.P, case.lay, opop, case.ord, 2.0, 0, 1)
+    oen = case.O.energy(case.P, case.lay, opop)
+    assert np.array_equal(gpop, opop)
+    assert np.array_equal(gen[0].view(np.uint32), oen[0].view(np.uint32))
+    assert np.array_equal(gen[1], oen[1]) and np.array_equal(gen[2], oen[2])
 
 
 @pytest.mark.parametrize("inst,nchains", [("sq46", 48), ("reg3_2000", 512), ("sq64", 72), ("grid45", 8)])

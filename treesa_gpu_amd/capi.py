@@ -139,7 +139,7 @@ def make_config(mode="tc", sc_target=20.0, sc_weight=1.0, seed=1, slicing=False,
     c.v2_ltc_bit, c.v2_ltc_pad, c.v2_ltc_out = f32_log2(h[4]), f32_log2(h[5]), f32_log2(h[6])
     c.v2_small_rank, c.v2_lsmall_cell = int(h[7]), f32_log2(h[8])
     c.wide_waves, c.wide_wgs = wide_waves, wide_wgs
-    c.fused_energy = 1 if fused_energy else 0
+    c.fused_energy = int(fused_energy)  # 0 / False: none, 1 / True: automatic, 2: fold kernel always
     c.sums = int(sums)
     c.wide_lanes = int(wide_lanes)
     return c

@@ -58,6 +58,9 @@ struct tsa_ctx {
                                // resample or mode switch, and every sweep since ran the wide kernel)
   bool energy_fresh = false;   // d_lc / d_sc / d_ns hold the energies of the current population (written by
                                // the last sweep launch, cfg.fused_energy)
+  bool fold_apart = false;     // cfg.fused_energy on the one-wave kernels with more than twice the chains that
+                               // fit on the device at once (or fused_energy 2): the sweep kernel leaves node
+                               // costs in d_ncost / d_nz and k_fold folds every chain in one round
   TsaTrackPart* d_tpart = nullptr;  // selection kernel: per-workgroup results and its counter
   unsigned* d_tdone = nullptr;
   // Overlapped tracking on the wide path: each sweep launch leaves a snapshot of every chain's tree and
@@ -324,9 +327,12 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   fill_params(c, leaf_sc);
 
   int dev = 0;
-  int lds_max = 0;
+  int lds_max = 0, ncu = 0, lds_cu = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+  if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
+  if (e == hipSuccess)
+    e = hipDeviceGetAttribute(&lds_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev);
   if (e != hipSuccess) {
     free_ctx(c);
     return fail(nullptr, TSA_ERR_HIP, std::string("no HIP device: ") + hipGetErrorString(e));
@@ -371,6 +377,15 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
     int wpb = ldsw / nodew2;
     c->L.wpb = wpb < 1 ? 1 : (wpb > 4 ? 4 : wpb);
   }
+  if (cfg->fused_energy) {
+    // chains resident at once: workgroups of wpb chains, as many per compute unit as its LDS holds
+    const long long smem = ((long long)(use_lds ? leafw : 0) + (long long)c->L.wpb * c->L.lds_words) * 8;
+    const long long per_cu = smem > 0 ? (long long)(lds_cu > 0 ? lds_cu : lds_max) / smem : 1;
+    const long long resident = (long long)ncu * (per_cu < 1 ? 1 : per_cu) * c->L.wpb;
+    // the fold kernel costs about as much as two rounds of in-kernel folds (it is bound by the double
+    // arithmetic of the lse chain, and adds a launch): worth it from three rounds of resident chains
+    c->fold_apart = cfg->fused_energy == 2 || (long long)nchains > 2 * resident;
+  }
   // wide path: runtime-width chains without slice moves run par sweeps and energies in tsa_wide.hip
   const bool want_wide = cfg->kernel == TSA_KERNEL_WIDE || (cfg->kernel == TSA_KERNEL_AUTO && !use_lds);
   if (want_wide) {
@@ -397,8 +412,9 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
              "fold_stage=%d",
              lay->W, c->wide.G, c->wide.nsw, c->wide.nt / 64, c->wide.K, c->wide.smem, c->wide.eK, c->wide.fold_stage);
   else
-    snprintf(kb, sizeof kb, "%s W=%d waves/block=%d lds_bytes/wave=%d", use_lds ? "lds" : "global",
-             use_lds ? c->Wt : lay->W, c->L.wpb, c->L.lds_words * 8);
+    snprintf(kb, sizeof kb, "%s W=%d waves/block=%d lds_bytes/wave=%d%s", use_lds ? "lds" : "global",
+             use_lds ? c->Wt : lay->W, c->L.wpb, c->L.lds_words * 8,
+             cfg->fused_energy && c->fold_apart ? " fold=apart" : "");
   c->kname = kb;
 
   const size_t recb = (size_t)nchains * lay->chain_words * 8;
@@ -425,6 +441,12 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   c->d_sc = reinterpret_cast<int*>(c->d_lc) + nchains;
   c->d_ns = reinterpret_cast<int*>(c->d_lc) + 2 * (size_t)nchains;
   TSA_CREATE_HIP(hipHostMalloc(&c->h_en, (size_t)nchains * 12 + 16, hipHostMallocDefault));
+  if (c->wide.on) c->fold_apart = false;
+  if (c->fold_apart) {
+    const size_t nint4 = (size_t)((lay->nint + 3) & ~3);
+    TSA_CREATE_HIP(hipMalloc(&c->d_ncost, (size_t)nchains * nint4 * 4));
+    TSA_CREATE_HIP(hipMalloc(&c->d_nz, (size_t)nchains * nint4 * 2));
+  }
   if (c->wide.on) {
     const size_t nint4 = (size_t)((lay->nint + 3) & ~3);
     TSA_CREATE_HIP(hipMalloc(&c->d_wsync, (size_t)nchains * 8));
@@ -590,9 +612,14 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     ctx->last_slot = -1;  // the snapshots no longer describe the population
     join_track(ctx);      // a pending fold may still read the node-cost snapshot; d_lc is rewritten below
     const bool fuse = ctx->cfg.fused_energy != 0;
-    const TsaEnergyOut eo{fuse ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns};
+    const bool apart = fuse && ctx->fold_apart;
+    const TsaEnergyOut eo{fuse && !apart ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns, apart ? ctx->d_ncost : nullptr,
+                          apart ? ctx->d_nz : nullptr};
     TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
                                    ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st, e0, e1));
+    if (apart)
+      TSA_HIP(ctx, tsa_launch_fold(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->d_ncost, ctx->d_nz, ctx->nchains,
+                                   ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->st));
     ctx->energy_fresh = fuse;
   }
   ctx->npending++;

@@ -40,10 +40,14 @@ struct TsaLaunch {
 
 // Per-chain energies a sweep launch also writes (lc == nullptr: none): the chain is evaluated by the sweep
 // kernel right after its last sweep, while it is still staged, exactly as the energy kernel would.
+// What a sweep launch leaves of its chains' energies: lc / sc / ns per chain (the sweep kernel folds them),
+// or, with cost set, only every node's cost and masked size (cost / z + chain * nint4; k_fold folds them).
 struct TsaEnergyOut {
   float* lc;
   int* sc;
   int* ns;
+  float* cost;
+  uint16_t* z;
 };
 
 // Copy n elements with nthr threads (this one is tid), U loads per thread in flight at once: a loop that
@@ -72,6 +76,10 @@ hipError_t tsa_launch_sweeps(const TsaLaunch& L, int mode, int order, const TsaK
                              hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
 hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
                              const uint32_t* fix, int nchains, float* lc, int* sc, int* ns, hipStream_t st);
+// The fold of node costs a sweep launch left in cost / z (nchains * nint4 each) into lc / sc / ns.
+hipError_t tsa_launch_fold(const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf, const uint32_t* fix,
+                           const float* cost, const uint16_t* z, int nchains, float* lc, int* sc, int* ns,
+                           hipStream_t st);
 struct TsaTrackState {
   double best_score;
   int best_chain, best_level;

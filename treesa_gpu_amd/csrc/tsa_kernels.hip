@@ -480,7 +480,16 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
     }
   }
 
-  if (eo.lc) {
+  if (eo.cost) {
+    // node costs and masked sizes by all 64 lanes, for k_fold
+    float* const gc = eo.cost + (size_t)c * nint4;
+    uint16_t* const gz = eo.z + (size_t)c * nint4;
+    for (int i = lane; i < nint; i += 64) {
+      int Z;
+      gc[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
+      gz[i] = (uint16_t)Z;
+    }
+  } else if (eo.lc) {
     // the chain's energy, as k_energy computes it: node costs by all 64 lanes into the node arrays (free
     // after the sweeps: pri and par hold nint4 floats, wl nint4 sizes), then the 32-lane fold
     tsa_wave_sync();
@@ -515,6 +524,39 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
     atomicAdd(&st[TSA_ST_SACC * TSA_STAT_SLOTS], (unsigned long long)nsa);
     atomicAdd(&st[TSA_ST_BUSY * TSA_STAT_SLOTS], (unsigned long long)sb_);
   }
+}
+
+// Per-chain energy from node costs a sweep launch left (TsaEnergyOut.cost / z), one 32-lane half-wave per
+// chain: the reference's fold (csrc/treesa_gpu.cu:386-434) of every chain at once, instead of at the end of
+// each chain's sweep, where the serial lse chain is paid once per round of resident chains.
+__global__ void __launch_bounds__(256) k_fold(TsaKParams P, const uint64_t* __restrict__ rec,
+                                              const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
+                                              const float* __restrict__ cost, const uint16_t* __restrict__ z,
+                                              int nchains, float* __restrict__ lc, int* __restrict__ sc,
+                                              int* __restrict__ ns) {
+  __shared__ uint64_t s_exp2[32];
+  if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
+  __syncthreads();
+  const TsaMathTabs T{s_exp2, fix, fix + TSA_LOG2FIX_WORDS, tsa_log2_tab_d};
+  const int t = blockIdx.x * blockDim.x + threadIdx.x;
+  const int c = t >> 5, l32 = threadIdx.x & 31;
+  const int cc = c < nchains ? c : nchains - 1;  // a half-wave past the end duplicates the last chain
+  const size_t nint4 = (size_t)((P.nint + 3) & ~3);
+  const uint64_t* S = P.slicing ? rec + (size_t)cc * P.chain_words + P.s_off : nullptr;
+  const TsaEvalOut e = tsa_fold32(P, cost + (size_t)cc * nint4, z + (size_t)cc * nint4, S, leaf, P.W, T, l32);
+  if (l32 == 0 && c < nchains) {
+    lc[c] = e.lcost;
+    sc[c] = e.sc;
+    ns[c] = e.ns;
+  }
+}
+
+hipError_t tsa_launch_fold(const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf, const uint32_t* fix,
+                           const float* cost, const uint16_t* z, int nchains, float* lc, int* sc, int* ns,
+                           hipStream_t st) {
+  const int threads = 256, grid = (nchains * 32 + threads - 1) / threads;
+  hipLaunchKernelGGL(k_fold, dim3(grid), dim3(threads), 0, st, P, rec, leaf, fix, cost, z, nchains, lc, sc, ns);
+  return hipGetLastError();
 }
 
 // Per-chain energy, one 32-lane half-wave per chain (csrc/treesa_gpu.cu:999-1014).
