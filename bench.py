@@ -255,6 +255,8 @@ def main():
     ap.add_argument("--wide-lanes", type=int, default=0, help="wide kernel: lanes per proposal (0: automatic)")
     ap.add_argument("--sums", default="auto", choices=("auto", "on", "off"),
                     help="wide kernel: chunk summaries (the binary's --sums / --no-sum; auto: on from 64 words)")
+    ap.add_argument("--no-overlap", action="store_true",
+                    help="fold and selection of a level on the sweep's stream, not beside the next sweep")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run identity population copies of the workload (counter calibration)")
     a = ap.parse_args()
@@ -273,7 +275,7 @@ def main():
     extra = (["--wpc", str(2 * a.wide_waves)] if a.wide_waves else []) + \
         (["--wide-wgs", str(a.wide_wgs)] if a.wide_wgs else []) + \
         (["--wide-lanes", str(a.wide_lanes)] if a.wide_lanes else []) + \
-        {"auto": [], "on": ["--sums"], "off": ["--no-sum"]}[a.sums]
+        {"auto": [], "on": ["--sums"], "off": ["--no-sum"]}[a.sums] + (["--no-overlap"] if a.no_overlap else [])
     visits = steps * C["niters"] * nchains * (inst.m - 1)
 
     def measure(extra_args):

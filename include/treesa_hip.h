@@ -90,6 +90,10 @@ typedef struct tsa_config_t {
   int32_t sums;
   /* wide kernel: lanes per proposal (4, 8, 16, 32 or 64; 0 = automatic) */
   int32_t wide_lanes;
+  /* tsa_track after a sweep whose node costs are folded apart (the wide path, or fused_energy with the fold
+   * kernel, without slice moves): 0 = automatic, the fold and the selection of that sweep's snapshot run on
+   * a second stream beside the next sweep; -1 = never, they run on the sweep's stream.  Results do not change */
+  int32_t track_overlap;
 } tsa_config_t;
 
 typedef struct tsa_ctx tsa_ctx;
@@ -115,7 +119,8 @@ int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* out);
 
 /* Enqueue nsweeps sweeps of every chain at inverse temperature beta, global sweep counter sweep0
  * (the RNG counter), in TSA_ORDER_*; slice moves follow every sweep s with (sweep0+s+1) % slice_every
- * == 0 when slice_moves > 0.  Asynchronous; event-timed.  Replaces Runner::sweeps / sweeps_mode,
+ * == 0 when slice_moves > 0.  Asynchronous (with overlapped tracking, see track_overlap, it first waits
+ * on the host for the selection of two launches back to finish); event-timed.  Replaces Runner::sweeps / sweeps_mode,
  * csrc/treesa_gpu.cu:1659-1716. */
 int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0, int32_t nsweeps);
 
@@ -172,7 +177,10 @@ typedef struct tsa_trace_row_t {
 /* Start tracking: best score +inf, room for max_levels rows.  Replaces the best-tracking state of
  * run_anneal, csrc/treesa_gpu.cu:1777-1779. */
 int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t max_levels);
-/* Enqueue energy + selection for level (0 <= level < max_levels).  Asynchronous. */
+/* Enqueue energy + selection for level (0 <= level < max_levels).  Asynchronous.  With overlapped tracking
+ * (tsa_config_t.track_overlap) they run on a second stream beside the next tsa_sweeps, on the snapshot the
+ * last sweep launch left.  Replaces the per-level energy call and score loop of run_anneal,
+ * csrc/treesa_gpu.cu:1805-1832. */
 int tsa_track(tsa_ctx* ctx, int32_t level);
 /* Wait and return the best over the tracked levels (best_chain -1 if none), its tree in best_record (a
  * chain_words record of which the children words and S are written; its label words are a function of the

@@ -63,8 +63,8 @@ struct tsa_ctx {
                                // costs in d_ncost / d_nz and k_fold folds every chain in one round
   TsaTrackPart* d_tpart = nullptr;  // selection kernel: per-workgroup results and its counter
   unsigned* d_tdone = nullptr;
-  // Overlapped tracking on the wide path: each sweep launch leaves a snapshot of every chain's tree and
-  // node costs in slot `slot` (two slots, alternating), and tsa_track runs the fold and the selection of that
+  // Overlapped tracking (the wide path, and the one-wave kernels with the fold kernel): each sweep launch
+  // leaves a snapshot of every chain's tree and node costs in slot `slot` (two slots, alternating), and tsa_track runs the fold and the selection of that
   // snapshot on the second stream st2 while st goes on with the next level's sweep.  ev_sweep[s] marks the
   // sweep that filled slot s, ev_track[s] the selection that read it (a sweep waits for it before it
   // overwrites the slot).
@@ -501,6 +501,17 @@ static hipError_t quiesce_track(tsa_ctx* c) {
   return e;
 }
 
+// Before a sweep overwrites snapshot slot s, the selection that last read it must be done.  The host waits
+// for it (it ran beside the previous sweep, which is still queued or running, so the device does not idle)
+// rather than putting a wait on the stream: a cross-stream wait in the queue costs about 10 us per level
+// even when it is already satisfied, and the host is normally many levels ahead of the device.
+static hipError_t claim_slot(tsa_ctx* c, int s) {
+  hipError_t e = hipSuccess;
+  if (c->track_pending[s]) e = hipEventSynchronize(c->ev_track[s]);
+  c->track_pending[s] = false;
+  return e;
+}
+
 static hipError_t launch_energy(tsa_ctx* c) {
   join_track(c);
   if (c->energy_fresh) return hipSuccess;  // the last sweep launch left them in d_lc / d_sc / d_ns
@@ -589,12 +600,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
         ctx->costs_valid = true;
       }
       s = ctx->slot;
-      // the selection that last read slot s must be done (a wait that is already satisfied is skipped: each
-      // wait costs the queue tens of microseconds)
-      if (ctx->track_pending[s] && hipEventQuery(ctx->ev_track[s]) != hipSuccess)
-        TSA_HIP(ctx, hipStreamWaitEvent(ctx->st, ctx->ev_track[s], 0));
-      (void)hipGetLastError();  // a query of an unfinished event leaves hipErrorNotReady behind
-      ctx->track_pending[s] = false;
+      TSA_HIP(ctx, claim_slot(ctx, s));
       sy.snap_ch = ctx->d_snap_ch[s];
       sy.snap_cost = ctx->d_snap_cost[s];
       sy.snap_nz = ctx->d_snap_nz[s];
@@ -609,18 +615,35 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
   } else {
     ctx->costs_valid = false;
     ctx->sums_valid = false;
-    ctx->last_slot = -1;  // the snapshots no longer describe the population
-    join_track(ctx);      // a pending fold may still read the node-cost snapshot; d_lc is rewritten below
     const bool fuse = ctx->cfg.fused_energy != 0;
     const bool apart = fuse && ctx->fold_apart;
-    const TsaEnergyOut eo{fuse && !apart ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns, apart ? ctx->d_ncost : nullptr,
-                          apart ? ctx->d_nz : nullptr};
+    TsaEnergyOut eo{fuse && !apart ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns, apart ? ctx->d_ncost : nullptr,
+                    apart ? ctx->d_nz : nullptr, nullptr};
+    int s = -1;
+    if (ctx->overlap && apart) {
+      // node costs and children words go to snapshot slot s, folded and selected on st2 by tsa_track
+      s = ctx->slot;
+      TSA_HIP(ctx, claim_slot(ctx, s));
+      eo.cost = ctx->d_snap_cost[s];
+      eo.z = ctx->d_snap_nz[s];
+      eo.ch = ctx->d_snap_ch[s];
+    } else {
+      ctx->last_slot = -1;  // the snapshots no longer describe the population
+      join_track(ctx);      // a pending fold may still read the node-cost snapshot; d_lc is rewritten below
+    }
     TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
                                    ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st, e0, e1));
-    if (apart)
-      TSA_HIP(ctx, tsa_launch_fold(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->d_ncost, ctx->d_nz, ctx->nchains,
-                                   ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->st));
-    ctx->energy_fresh = fuse;
+    if (s >= 0) {
+      ctx->ev_sweep[s] = e1;
+      ctx->last_slot = s;
+      ctx->slot = s ^ 1;
+      ctx->energy_fresh = false;  // the energies of this population exist only once tsa_track folds the slot
+    } else {
+      if (apart)
+        TSA_HIP(ctx, tsa_launch_fold(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->d_ncost, ctx->d_nz,
+                                     ctx->nchains, ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->st));
+      ctx->energy_fresh = fuse;
+    }
   }
   ctx->npending++;
   return TSA_OK;
@@ -667,11 +690,18 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   TSA_HIP(ctx, quiesce_track(ctx));
   // The wide path folds and selects beside the next level's sweep when that sweep leaves the device room:
   // one workgroup per chain (no chain barrier, whose workgroups must all be resident at once) and fewer
-  // chains than compute units (with at least one chain per unit the sweep already fills the device).
+  // chains than compute units (with at least one chain per unit the sweep already fills the device).  The
+  // one-wave kernels with the fold kernel (several rounds of resident chains) do so always: the fold and the
+  // selection are serial chains of dependent operations that fill the issue slots the sweep's LDS-bound
+  // waves leave, and the last round of sweep workgroups leaves compute units idle.  Slice moves rewrite S,
+  // which the fold and the selection read from the records, so they keep the serial order.
   int dev = 0, ncu = 0;
   TSA_HIP(ctx, hipGetDevice(&dev));
   TSA_HIP(ctx, hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
-  const bool want_overlap = ctx->wide.on && ctx->wide.K == 1 && ctx->nchains < ncu;
+  const bool want_overlap =
+      ctx->cfg.track_overlap >= 0 &&
+      ((ctx->wide.on && ctx->wide.K == 1 && ctx->nchains < ncu) ||
+       (!ctx->wide.on && ctx->fold_apart && ctx->cfg.fused_energy != 0 && !ctx->cfg.slicing));
   if (want_overlap && !ctx->st2) {
     const size_t nint = (size_t)ctx->lay.nint, nint4 = (nint + 3) & ~(size_t)3;
     TSA_HIP(ctx, hipStreamCreateWithFlags(&ctx->st2, hipStreamNonBlocking));
@@ -701,9 +731,13 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
     // the last sweep's snapshot: fold its node costs and select on st2, beside the next sweep on st
     const int s = ctx->last_slot;
     TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_sweep[s], 0));
-    TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
-                                        ctx->nchains, ctx->d_snap_cost[s], ctx->d_snap_nz[s], ctx->d_fcnt, ctx->d_lc,
-                                        ctx->d_sc, ctx->d_ns, 0, ctx->st2));
+    if (ctx->wide.on)
+      TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
+                                          ctx->nchains, ctx->d_snap_cost[s], ctx->d_snap_nz[s], ctx->d_fcnt,
+                                          ctx->d_lc, ctx->d_sc, ctx->d_ns, 0, ctx->st2));
+    else
+      TSA_HIP(ctx, tsa_launch_fold(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->d_snap_cost[s],
+                                   ctx->d_snap_nz[s], ctx->nchains, ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->st2));
     TSA_HIP(ctx, tsa_launch_track(ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->nchains, S, level, ctx->d_rec,
                                   L.chain_words, L.ch_off, L.s_off, L.W, L.nint, ctx->d_snap_ch[s], ctx->d_track,
                                   ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2));

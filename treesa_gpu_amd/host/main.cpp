@@ -51,7 +51,7 @@ struct Opts {
   int niters2 = -1;
   int nchains = 1024, niters = 50, block = 0, wpb = 0, lpc = 32, eval_every = 1, ref_chains = 8, mode = 0;
   bool check = false, quiet = false, cross = true, wide = false, slicing = false, no_sum = false, force_sum = false;
-  bool select_sc = false;
+  bool select_sc = false, no_overlap = false;
   int slice_moves = 1, slice_every = 1, max_slices = 0, random_slices = 0;
   int coop_max = 0, coop_min_units = -1, coop_min = 1, coop_full = 0, coop_cpl = 2, par_follow = 0, par_band = 0, wpc = 0, wide_wgs = 0, wide_lanes = 0;
   double sc_target = 20.0, sc_weight = 1.0, trunc_frac = 0.25;
@@ -84,6 +84,7 @@ std::string jnum(double x) {
           "  [--eval-every k] [--out result.json] [--check [--ref-chains R] [--random-slices k]] [--quiet]\n"
           "  [--bench-warmup W]  (W untimed levels first, then the initial population again)\n"
           "  [--host-select]  (select the best chain on the host at every level, also for --scheme indep)\n"
+          "  [--no-overlap]  (device-side selection on the sweep's stream, not beside the next sweep)\n"
           "  [--init tree|spectral|greedy [--spectral-k K] [--greedy-repeat R]]  (start trees made natively when no --tree\n"
           "   is given: the K best spectral path trees, chain c from tree c %% K, or the best of R greedy runs)\n");
   exit(1);
@@ -166,6 +167,7 @@ Opts parse(int argc, char** argv) {
       else if (a == "--wide") o.wide = true;
       else if (a == "--no-sum") o.no_sum = true;
       else if (a == "--select-sc") o.select_sc = true;
+      else if (a == "--no-overlap") o.no_overlap = true;
       else if (a == "--sums") o.force_sum = true;
       else if (a == "--check") o.check = true;
       else if (a == "--no-cross") o.cross = false;
@@ -246,6 +248,7 @@ class Runner {
     cfg.wide_lanes = O.wide_lanes;
     cfg.fused_energy = O.eval_every == 1 ? 1 : 0;  // every level is evaluated: the sweep kernel evaluates too
     cfg.sums = O.no_sum ? -1 : (O.force_sum ? 1 : 0);
+    cfg.track_overlap = O.no_overlap ? -1 : 0;
   }
   ~Runner() {
     if (ctx) tsa_destroy(ctx);
