@@ -120,7 +120,8 @@ def loaded_bytes(st, chunks):
 
 
 # committed rocprofv3 summaries by (workload, label-set path: "dense" streaming or chunk "sums")
-PROFILES = {("c2", "dense"): "k_sweep_c2_sat100_par.md", ("c4", "dense"): "k_wide_c4_reg3_2000_par.md",
+PROFILES = {("c1", "dense"): "k_sweep_c1_sat100_preorder.md", ("c2", "dense"): "k_sweep_c2_sat100_par.md",
+            ("c3", "dense"): "k_sweep_c3_sat70_par_slicing.md", ("c4", "dense"): "k_wide_c4_reg3_2000_par.md",
             ("c5", "dense"): "k_wide_c5_sq64_par.md", ("c5", "sums"): "k_wide_sums_c5_sq64_par.md"}
 
 
