@@ -50,16 +50,18 @@ def test_device_selection_equals_host_selection(inst, extra, order, tmp_path):
     assert max(abs(x[5] - y[5]) for x, y in zip(ta, tb)) < 1e-9
 
 
-# 8192 chains of sat100 are more than twice what the device holds at once: the sweep kernel leaves node costs
-# and children words in a snapshot slot, and the fold and the selection of each level run on a second stream
-# beside the next level's sweep.  The result equals the same run with them on the sweep's stream and the
-# host-side level loop.
+# The selection of each level runs on a second stream beside the next level's sweep, on a snapshot the sweep
+# left: with 8192 chains of sat100 (more than twice what the device holds at once) node costs and children
+# words, folded by the fold kernel there; with 256 chains (one wave per compute unit) energies folded by the
+# sweep kernel and children words.  The result equals the same run with the selection on the sweep's stream
+# and the host-side level loop.
 @pytest.mark.parametrize("order", ["par", "preorder"])
-def test_overlapped_selection_with_fold_kernel(order, tmp_path):
-    args = ["-i", common.inst_path("sat100"), "--tree", common.tree_file("sat100", "greedy"), "--nchains", "8192",
-            "--niters", "1", "--betas", "1:0.5:15", "--sc-target", "20", "--order", order, "--seed", "2"]
+@pytest.mark.parametrize("nchains", [8192, 256])
+def test_overlapped_selection(nchains, order, tmp_path):
+    args = ["-i", common.inst_path("sat100"), "--tree", common.tree_file("sat100", "greedy"), "--nchains",
+            str(nchains), "--niters", "1", "--betas", "1:0.5:15", "--sc-target", "20", "--order", order, "--seed", "2"]
     a = run(args, tmp_path, "a.json")
-    assert "fold=apart" in a["hip_kernel"], a["hip_kernel"]
+    assert ("fold=apart" in a["hip_kernel"]) == (nchains == 8192), a["hip_kernel"]
     b = run(args + ["--no-overlap"], tmp_path, "b.json")
     c = run(args + ["--host-select"], tmp_path, "c.json")
     for k in ("tc", "sc", "best_chain", "tree", "proposals", "accepts", "node_visits", "valid", "labels_ok"):

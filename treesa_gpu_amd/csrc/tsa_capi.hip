@@ -63,11 +63,11 @@ struct tsa_ctx {
                                // costs in d_ncost / d_nz and k_fold folds every chain in one round
   TsaTrackPart* d_tpart = nullptr;  // selection kernel: per-workgroup results and its counter
   unsigned* d_tdone = nullptr;
-  // Overlapped tracking (the wide path, and the one-wave kernels with the fold kernel): each sweep launch
-  // leaves a snapshot of every chain's tree and node costs in slot `slot` (two slots, alternating), and tsa_track runs the fold and the selection of that
-  // snapshot on the second stream st2 while st goes on with the next level's sweep.  ev_sweep[s] marks the
-  // sweep that filled slot s, ev_track[s] the selection that read it (a sweep waits for it before it
-  // overwrites the slot).
+  // Overlapped tracking (the wide path, and the one-wave kernels with fused energies): each sweep launch
+  // leaves a snapshot of every chain's tree and node costs (or energies) in slot `slot` (two slots,
+  // alternating), and tsa_track runs the fold and the selection of that snapshot on the second stream st2
+  // while st goes on with the next level's sweep.  ev_sweep[s] marks the sweep that filled slot s,
+  // ev_track[s] the selection that read it (the host waits for it before a sweep overwrites the slot).
   bool overlap = false;
   hipStream_t st2 = nullptr;
   hipEvent_t ev_sweep[2] = {nullptr, nullptr};  // (the stop events of those sweeps' timing pairs)
@@ -77,10 +77,16 @@ struct tsa_ctx {
   uint32_t* d_snap_ch[2] = {nullptr, nullptr};
   float* d_snap_cost[2] = {nullptr, nullptr};
   uint16_t* d_snap_nz[2] = {nullptr, nullptr};
+  uint32_t* d_snap_en[2] = {nullptr, nullptr};  // energies folded by the sweep kernel: lc, sc, ns per chain
+  int snap_kind[2] = {0, 0};  // what the sweep that filled a slot left there: a SNAP_* value
   std::string err;
 };
 
 static thread_local std::string g_err;
+
+// Contents of a snapshot slot: the wide kernel's node-cost cache, node costs of the one-wave kernel for the
+// fold kernel, or energies the one-wave kernel folded itself (with children words in every case).
+enum { SNAP_WIDE = 0, SNAP_COSTS = 1, SNAP_ENERGIES = 2 };
 
 static int fail(tsa_ctx* ctx, int code, const std::string& msg) {
   if (ctx) ctx->err = msg;
@@ -240,6 +246,7 @@ static void free_ctx(tsa_ctx* c) {
     if (c->d_snap_ch[k]) (void)hipFree(c->d_snap_ch[k]);
     if (c->d_snap_cost[k]) (void)hipFree(c->d_snap_cost[k]);
     if (c->d_snap_nz[k]) (void)hipFree(c->d_snap_nz[k]);
+    if (c->d_snap_en[k]) (void)hipFree(c->d_snap_en[k]);
   }
   if (c->st2) (void)hipStreamDestroy(c->st2);
   if (c->d_track) (void)hipFree(c->d_track);
@@ -376,6 +383,12 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
     c->L.lds_words = nodew2;
     int wpb = ldsw / nodew2;
     c->L.wpb = wpb < 1 ? 1 : (wpb > 4 ? 4 : wpb);
+  }
+  // fewer chains than full workgroups on every compute unit: smaller workgroups spread them over all units,
+  // so that a wave shares its unit's LDS, scalar unit and instruction issue with fewer others
+  if (ncu > 0 && (long long)nchains < (long long)ncu * c->L.wpb) {
+    const int spread = (nchains + ncu - 1) / ncu;
+    c->L.wpb = spread < 1 ? 1 : spread;
   }
   if (cfg->fused_energy) {
     // chains resident at once: workgroups of wpb chains, as many per compute unit as its LDS holds
@@ -604,6 +617,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
       sy.snap_ch = ctx->d_snap_ch[s];
       sy.snap_cost = ctx->d_snap_cost[s];
       sy.snap_nz = ctx->d_snap_nz[s];
+      ctx->snap_kind[s] = SNAP_WIDE;
     }
     TSA_HIP(ctx, tsa_launch_wide(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains, beta,
                                  sweep0, nsweeps, ctx->d_stats, sy, ctx->st, e0, e1));
@@ -620,12 +634,20 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     TsaEnergyOut eo{fuse && !apart ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns, apart ? ctx->d_ncost : nullptr,
                     apart ? ctx->d_nz : nullptr, nullptr};
     int s = -1;
-    if (ctx->overlap && apart) {
-      // node costs and children words go to snapshot slot s, folded and selected on st2 by tsa_track
+    if (ctx->overlap && fuse) {
+      // node costs (or, folded in the kernel, energies) and children words go to snapshot slot s, folded and
+      // selected on st2 by tsa_track
       s = ctx->slot;
       TSA_HIP(ctx, claim_slot(ctx, s));
-      eo.cost = ctx->d_snap_cost[s];
-      eo.z = ctx->d_snap_nz[s];
+      ctx->snap_kind[s] = apart ? SNAP_COSTS : SNAP_ENERGIES;
+      if (apart) {
+        eo.cost = ctx->d_snap_cost[s];
+        eo.z = ctx->d_snap_nz[s];
+      } else {
+        eo.lc = reinterpret_cast<float*>(ctx->d_snap_en[s]);
+        eo.sc = reinterpret_cast<int*>(ctx->d_snap_en[s]) + ctx->nchains;
+        eo.ns = reinterpret_cast<int*>(ctx->d_snap_en[s]) + 2 * (size_t)ctx->nchains;
+      }
       eo.ch = ctx->d_snap_ch[s];
     } else {
       ctx->last_slot = -1;  // the snapshots no longer describe the population
@@ -691,17 +713,18 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   // The wide path folds and selects beside the next level's sweep when that sweep leaves the device room:
   // one workgroup per chain (no chain barrier, whose workgroups must all be resident at once) and fewer
   // chains than compute units (with at least one chain per unit the sweep already fills the device).  The
-  // one-wave kernels with the fold kernel (several rounds of resident chains) do so always: the fold and the
-  // selection are serial chains of dependent operations that fill the issue slots the sweep's LDS-bound
-  // waves leave, and the last round of sweep workgroups leaves compute units idle.  Slice moves rewrite S,
-  // which the fold and the selection read from the records, so they keep the serial order.
+  // one-wave kernels with fused energies do so always: with the fold kernel (several rounds of resident
+  // chains) the fold and the selection are serial chains of dependent operations that fill the issue slots
+  // the sweep's LDS-bound waves leave and the compute units the last round of sweep workgroups leaves idle;
+  // with energies folded in the sweep kernel only the selection runs beside the next sweep.  Slice moves
+  // rewrite S, which the fold and the selection read from the records, so they keep the serial order.
   int dev = 0, ncu = 0;
   TSA_HIP(ctx, hipGetDevice(&dev));
   TSA_HIP(ctx, hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
   const bool want_overlap =
       ctx->cfg.track_overlap >= 0 &&
       ((ctx->wide.on && ctx->wide.K == 1 && ctx->nchains < ncu) ||
-       (!ctx->wide.on && ctx->fold_apart && ctx->cfg.fused_energy != 0 && !ctx->cfg.slicing));
+       (!ctx->wide.on && ctx->cfg.fused_energy != 0 && !ctx->cfg.slicing));
   if (want_overlap && !ctx->st2) {
     const size_t nint = (size_t)ctx->lay.nint, nint4 = (nint + 3) & ~(size_t)3;
     TSA_HIP(ctx, hipStreamCreateWithFlags(&ctx->st2, hipStreamNonBlocking));
@@ -710,6 +733,7 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
       TSA_HIP(ctx, hipMalloc(&ctx->d_snap_ch[k], (size_t)ctx->nchains * nint * 4));
       TSA_HIP(ctx, hipMalloc(&ctx->d_snap_cost[k], (size_t)ctx->nchains * nint4 * 4));
       TSA_HIP(ctx, hipMalloc(&ctx->d_snap_nz[k], (size_t)ctx->nchains * nint4 * 2));
+      TSA_HIP(ctx, hipMalloc(&ctx->d_snap_en[k], (size_t)ctx->nchains * 12));
     }
   }
   ctx->overlap = want_overlap;
@@ -731,14 +755,19 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
     // the last sweep's snapshot: fold its node costs and select on st2, beside the next sweep on st
     const int s = ctx->last_slot;
     TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_sweep[s], 0));
-    if (ctx->wide.on)
+    const int kind = ctx->snap_kind[s];
+    if (kind == SNAP_WIDE)
       TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
                                           ctx->nchains, ctx->d_snap_cost[s], ctx->d_snap_nz[s], ctx->d_fcnt,
                                           ctx->d_lc, ctx->d_sc, ctx->d_ns, 0, ctx->st2));
-    else
+    else if (kind == SNAP_COSTS)
       TSA_HIP(ctx, tsa_launch_fold(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->d_snap_cost[s],
                                    ctx->d_snap_nz[s], ctx->nchains, ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->st2));
-    TSA_HIP(ctx, tsa_launch_track(ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->nchains, S, level, ctx->d_rec,
+    const bool folded = kind == SNAP_ENERGIES;  // the sweep kernel left the energies in the slot
+    const float* lc = folded ? reinterpret_cast<const float*>(ctx->d_snap_en[s]) : ctx->d_lc;
+    const int* sc = folded ? reinterpret_cast<const int*>(ctx->d_snap_en[s]) + ctx->nchains : ctx->d_sc;
+    const int* ns = folded ? reinterpret_cast<const int*>(ctx->d_snap_en[s]) + 2 * (size_t)ctx->nchains : ctx->d_ns;
+    TSA_HIP(ctx, tsa_launch_track(lc, sc, ns, ctx->nchains, S, level, ctx->d_rec,
                                   L.chain_words, L.ch_off, L.s_off, L.W, L.nint, ctx->d_snap_ch[s], ctx->d_track,
                                   ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2));
     TSA_HIP(ctx, hipEventRecord(ctx->ev_track[s], ctx->st2));

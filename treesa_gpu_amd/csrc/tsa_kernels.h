@@ -41,9 +41,9 @@ struct TsaLaunch {
 // Per-chain energies a sweep launch also writes (lc == nullptr: none): the chain is evaluated by the sweep
 // kernel right after its last sweep, while it is still staged, exactly as the energy kernel would.
 // What a sweep launch leaves of its chains' energies: lc / sc / ns per chain (the sweep kernel folds them),
-// or, with cost set, only every node's cost and masked size (cost / z + chain * nint4; k_fold folds them),
-// and, with ch also set, a copy of every chain's children words (ch + chain * nint): a snapshot of the trees
-// those costs describe, which the selection reads while the next sweep rewrites the records.
+// or, with cost set, only every node's cost and masked size (cost / z + chain * nint4; k_fold folds them);
+// with ch set, also a copy of every chain's children words (ch + chain * nint): a snapshot of the trees those
+// energies describe, which the selection reads while the next sweep rewrites the records.
 struct TsaEnergyOut {
   float* lc;
   int* sc;

@@ -489,10 +489,6 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
       gc[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
       gz[i] = (uint16_t)Z;
     }
-    if (eo.ch) {
-      uint32_t* const gch = eo.ch + (size_t)c * nint;
-      for (int i = lane; i < nint; i += 64) gch[i] = ch[i];
-    }
   } else if (eo.lc) {
     // the chain's energy, as k_energy computes it: node costs by all 64 lanes into the node arrays (free
     // after the sweeps: pri and par hold nint4 floats, wl nint4 sizes), then the 32-lane fold
@@ -510,6 +506,10 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
       eo.sc[c] = e.sc;
       eo.ns[c] = e.ns;
     }
+  }
+  if (eo.ch) {
+    uint32_t* const gch = eo.ch + (size_t)c * nint;
+    for (int i = lane; i < nint; i += 64) gch[i] = ch[i];
   }
   if constexpr (LDS) {
     tsa_wave_sync();
