@@ -134,7 +134,8 @@ int tsa_sweeps_ms(tsa_ctx* ctx, double* ms);
  * csrc/treesa_gpu.cu:999-1014, 1717-1729. */
 int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns);
 
-/* Population step: chain c <- chain anc[c] for every c.  Replaces Runner::resample + k_copy,
+/* Population step: chain c <- chain anc[c] for every c.  Asynchronous (anc is copied before the call
+ * returns); later calls on the context see the new population.  Replaces Runner::resample + k_copy,
  * csrc/treesa_gpu.cu:1016-1022, 1925-1933. */
 int tsa_resample(tsa_ctx* ctx, const int32_t* anc);
 

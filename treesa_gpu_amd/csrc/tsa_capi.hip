@@ -43,13 +43,19 @@ struct tsa_ctx {
   int* d_sc = nullptr;
   int* d_ns = nullptr;
   uint32_t* h_en = nullptr;  // pinned host copy of the three energy arrays
+  uint32_t* d_hen = nullptr;  // the device's address of h_en (null: not mapped)
+  bool energy_host = false;   // the last sweep launch wrote the energies of the current population into h_en
   int* d_anc = nullptr;
+  int* h_anc = nullptr;            // pinned staging of the ancestor list
+  hipEvent_t ev_anc = nullptr;     // recorded after the ancestor upload that read h_anc last
+  bool anc_pending = false;
   TsaWide wide{};              // wide path plan (wide.on: par sweeps and energies run tsa_wide.hip)
   TsaWideSync wsync{};         // chain barrier words (one allocation) and visit outcomes
   unsigned* d_wsync = nullptr;
   float* d_ncost = nullptr;    // per-node costs of the wide energy kernel, nchains * nint4
   uint16_t* d_nz = nullptr;    // per-node masked sizes, nchains * nint4
   unsigned* d_fcnt = nullptr;  // per-chain workgroup counters of the wide energy kernel
+  int ncu = 0;                 // compute units of the device
   uint64_t* d_sum = nullptr;   // chunk summaries of the internal sets, nchains * nint4 * wide.nsw
   uint64_t* d_leafsum = nullptr;  // chunk summaries of the input tensors, m * wide.nsw
   bool sums_valid = false;     // d_sum matches the population (k_wsum since the last upload or resample,
@@ -230,6 +236,8 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_lc) (void)hipFree(c->d_lc);
   if (c->h_en) (void)hipHostFree(c->h_en);
   if (c->d_anc) (void)hipFree(c->d_anc);
+  if (c->h_anc) (void)hipHostFree(c->h_anc);
+  if (c->ev_anc) (void)hipEventDestroy(c->ev_anc);
   if (c->d_wsync) (void)hipFree(c->d_wsync);
   if (c->wsync.out) (void)hipFree(c->wsync.out);
   if (c->d_ncost) (void)hipFree(c->d_ncost);
@@ -344,6 +352,7 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
     free_ctx(c);
     return fail(nullptr, TSA_ERR_HIP, std::string("no HIP device: ") + hipGetErrorString(e));
   }
+  c->ncu = ncu;
 
   // kernel choice: chain + leaf table in LDS when it fits and the width is a register width
   const int nodew = tsa_node_words(lay->nint) + (cfg->par_band > 0 ? ((lay->nint + 3) & ~3) / 2 : 0);
@@ -454,6 +463,10 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   c->d_sc = reinterpret_cast<int*>(c->d_lc) + nchains;
   c->d_ns = reinterpret_cast<int*>(c->d_lc) + 2 * (size_t)nchains;
   TSA_CREATE_HIP(hipHostMalloc(&c->h_en, (size_t)nchains * 12 + 16, hipHostMallocDefault));
+  if (hipHostGetDevicePointer(reinterpret_cast<void**>(&c->d_hen), c->h_en, 0) != hipSuccess) {
+    (void)hipGetLastError();  // not mapped: energies take the copy path
+    c->d_hen = nullptr;
+  }
   if (c->wide.on) c->fold_apart = false;
   if (c->fold_apart) {
     const size_t nint4 = (size_t)((lay->nint + 3) & ~3);
@@ -492,6 +505,8 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
     }
   }
   TSA_CREATE_HIP(hipMalloc(&c->d_anc, (size_t)nchains * 4));
+  TSA_CREATE_HIP(hipHostMalloc(&c->h_anc, (size_t)nchains * 4, hipHostMallocDefault));
+  TSA_CREATE_HIP(hipEventCreateWithFlags(&c->ev_anc, hipEventDisableTiming));
   TSA_CREATE_HIP(hipStreamSynchronize(c->st));
 #undef TSA_CREATE_HIP
   *out = c;
@@ -562,7 +577,7 @@ extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
   }
   TSA_HIP(ctx, quiesce_track(ctx));
   ctx->costs_valid = false;
-  ctx->energy_fresh = false;
+  ctx->energy_fresh = ctx->energy_host = false;
   ctx->sums_valid = false;
   TSA_HIP(ctx, hipMemcpyAsync(ctx->d_rec, population, (size_t)ctx->nchains * L.chain_words * 8,
                               hipMemcpyHostToDevice, ctx->st));
@@ -593,7 +608,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
   // e0 / e1 take the start and stop times of the sweep kernel alone, recorded by its dispatch (no marker
   // packets between the kernels of a level)
   hipEvent_t e0 = ctx->ev[2 * ctx->npending], e1 = ctx->ev[2 * ctx->npending + 1];
-  ctx->energy_fresh = false;
+  ctx->energy_fresh = ctx->energy_host = false;
   if (ctx->wide.on && order == TSA_ORDER_PAR) {
     // energies stay a separate fold of the node-cost cache: every chain ends its sweep at about the same
     // time, so folding inside the sweep kernel would only lengthen it
@@ -652,6 +667,14 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     } else {
       ctx->last_slot = -1;  // the snapshots no longer describe the population
       join_track(ctx);      // a pending fold may still read the node-cost snapshot; d_lc is rewritten below
+      if (fuse && !apart && ctx->track_levels == 0 && ctx->d_hen) {
+        // a host-side level loop reads the energies after every launch: the sweep kernel writes them into
+        // the page-locked buffer tsa_energy reads, with no copy after it
+        eo.lc = reinterpret_cast<float*>(ctx->d_hen);
+        eo.sc = reinterpret_cast<int*>(ctx->d_hen) + ctx->nchains;
+        eo.ns = reinterpret_cast<int*>(ctx->d_hen) + 2 * (size_t)ctx->nchains;
+        ctx->energy_host = true;
+      }
     }
     TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
                                    ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st, e0, e1));
@@ -664,7 +687,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
       if (apart)
         TSA_HIP(ctx, tsa_launch_fold(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->d_ncost, ctx->d_nz,
                                      ctx->nchains, ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->st));
-      ctx->energy_fresh = fuse;
+      ctx->energy_fresh = fuse && !ctx->energy_host;
     }
   }
   ctx->npending++;
@@ -710,20 +733,17 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   }
   ctx->track_levels = max_levels;
   TSA_HIP(ctx, quiesce_track(ctx));
-  // The wide path folds and selects beside the next level's sweep when that sweep leaves the device room:
-  // one workgroup per chain (no chain barrier, whose workgroups must all be resident at once) and fewer
-  // chains than compute units (with at least one chain per unit the sweep already fills the device).  The
-  // one-wave kernels with fused energies do so always: with the fold kernel (several rounds of resident
-  // chains) the fold and the selection are serial chains of dependent operations that fill the issue slots
-  // the sweep's LDS-bound waves leave and the compute units the last round of sweep workgroups leaves idle;
-  // with energies folded in the sweep kernel only the selection runs beside the next sweep.  Slice moves
-  // rewrite S, which the fold and the selection read from the records, so they keep the serial order.
-  int dev = 0, ncu = 0;
-  TSA_HIP(ctx, hipGetDevice(&dev));
-  TSA_HIP(ctx, hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev));
+  // The fold and the selection of a level run beside the next level's sweep, on the snapshot the sweep
+  // left: on the wide path with one workgroup per chain (a chain barrier, K > 1, needs all of the sweep's
+  // workgroups resident at once, so nothing may take their place) and fewer chains than compute units (with
+  // more, the fold's workgroups, which stage 64 KB of tables in LDS, take the places of sweep workgroups:
+  // C4's sweep 265 -> 353 us), and on the one-wave kernels with fused energies.  The fold and the selection are serial chains of dependent operations: beside a sweep they
+  // fill issue slots and compute units the sweep leaves idle (its last round of workgroups, its waves'
+  // memory or LDS waits) instead of adding their latency to every level.  Slice moves rewrite S, which the
+  // fold and the selection read from the records, so they keep the serial order.
   const bool want_overlap =
       ctx->cfg.track_overlap >= 0 &&
-      ((ctx->wide.on && ctx->wide.K == 1 && ctx->nchains < ncu) ||
+      ((ctx->wide.on && ctx->wide.K == 1 && ctx->nchains < ctx->ncu) ||
        (!ctx->wide.on && ctx->cfg.fused_energy != 0 && !ctx->cfg.slicing));
   if (want_overlap && !ctx->st2) {
     const size_t nint = (size_t)ctx->lay.nint, nint4 = (nint + 3) & ~(size_t)3;
@@ -818,10 +838,14 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
 
 extern "C" int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns) {
   if (!ctx || !lc || !sc || !ns) return fail(ctx, TSA_ERR_ARG, "tsa_energy: null argument");
-  TSA_HIP(ctx, launch_energy(ctx));
   const size_t b = (size_t)ctx->nchains * 4;
-  TSA_HIP(ctx, hipMemcpyAsync(ctx->h_en, ctx->d_lc, 3 * b + 4, hipMemcpyDeviceToHost, ctx->st));
-  TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  if (ctx->energy_host) {  // the last sweep launch wrote them into h_en
+    TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  } else {
+    TSA_HIP(ctx, launch_energy(ctx));
+    TSA_HIP(ctx, hipMemcpyAsync(ctx->h_en, ctx->d_lc, 3 * b + 4, hipMemcpyDeviceToHost, ctx->st));
+    TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  }
   if (ctx->wide.on && wide_error(ctx, ctx->h_en[3 * (size_t)ctx->nchains]) != TSA_OK) return TSA_ERR_HIP;
   memcpy(lc, ctx->h_en, b);
   memcpy(sc, ctx->h_en + ctx->nchains, b);
@@ -835,12 +859,18 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
     if (anc[c] < 0 || anc[c] >= ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_resample: ancestor out of range");
   if (!ctx->d_rec2) TSA_HIP(ctx, hipMalloc(&ctx->d_rec2, (size_t)ctx->nchains * ctx->lay.chain_words * 8));
   TSA_HIP(ctx, quiesce_track(ctx));
-  TSA_HIP(ctx, hipMemcpyAsync(ctx->d_anc, anc, (size_t)ctx->nchains * 4, hipMemcpyHostToDevice, ctx->st));
+  // the ancestors go through the pinned staging buffer (an asynchronous copy); the last upload from it must
+  // have been read before it is overwritten
+  if (ctx->anc_pending) TSA_HIP(ctx, hipEventSynchronize(ctx->ev_anc));
+  memcpy(ctx->h_anc, anc, (size_t)ctx->nchains * 4);
+  TSA_HIP(ctx, hipMemcpyAsync(ctx->d_anc, ctx->h_anc, (size_t)ctx->nchains * 4, hipMemcpyHostToDevice, ctx->st));
+  TSA_HIP(ctx, hipEventRecord(ctx->ev_anc, ctx->st));
+  ctx->anc_pending = true;
   ctx->costs_valid = false;
-  ctx->energy_fresh = false;
+  ctx->energy_fresh = ctx->energy_host = false;
   ctx->sums_valid = false;
+  // the copy and everything after it run in stream order: no wait here
   TSA_HIP(ctx, tsa_launch_copy(ctx->d_rec, ctx->d_rec2, ctx->d_anc, ctx->nchains, ctx->lay.chain_words, ctx->st));
-  TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
   std::swap(ctx->d_rec, ctx->d_rec2);
   return TSA_OK;
 }
@@ -850,7 +880,7 @@ extern "C" int tsa_set_mode(tsa_ctx* ctx, int32_t mode) {
   if (mode < 0 || mode > 2) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: mode must be 0, 1 or 2");
   if (mode != ctx->mode) {
     TSA_HIP(ctx, quiesce_track(ctx));
-    ctx->costs_valid = ctx->energy_fresh = false;
+    ctx->costs_valid = ctx->energy_fresh = ctx->energy_host = false;
   }
   ctx->mode = mode;
   return TSA_OK;

@@ -468,6 +468,7 @@ int Runner::run_anneal() {
   const int nc = O.nchains;
   std::vector<float> lc(nc);
   std::vector<int> sc(nc), ns(nc);
+  std::vector<double> E(nc);  // energyE of every chain at the last evaluated level
   double best_score = INFINITY;
   int best_chain = -1;
   std::vector<int> family(nc), nfam(nc);
@@ -506,7 +507,8 @@ int Runner::run_anneal() {
           bs = s;
           bi = c;
         }
-        meanE += energyE(lc[c], sc[c], ns[c]);
+        E[c] = energyE(lc[c], sc[c], ns[c]);  // the population step below reuses it
+        meanE += E[c];
         meanNs += ns[c];
       }
       meanE /= nc;
@@ -533,10 +535,10 @@ int Runner::run_anneal() {
         beta_last_resample = betas[lev + 1];
         std::vector<double> w(nc);
         double Emin = INFINITY;
-        for (int c = 0; c < nc; c++) Emin = std::min(Emin, energyE(lc[c], sc[c], ns[c]));
+        for (int c = 0; c < nc; c++) Emin = std::min(Emin, E[c]);
         double wsum = 0;
         for (int c = 0; c < nc; c++) {
-          w[c] = std::exp(-db * (energyE(lc[c], sc[c], ns[c]) - Emin));
+          w[c] = std::exp(-db * (E[c] - Emin));
           wsum += w[c];
         }
         std::vector<int> anc(nc);
@@ -554,8 +556,7 @@ int Runner::run_anneal() {
         // truncation selection: the worst trunc_frac are replaced by copies of the best
         std::vector<int> idx(nc);
         std::iota(idx.begin(), idx.end(), 0);
-        std::sort(idx.begin(), idx.end(),
-                  [&](int a, int b) { return energyE(lc[a], sc[a], ns[a]) < energyE(lc[b], sc[b], ns[b]); });
+        std::sort(idx.begin(), idx.end(), [&](int a, int b) { return E[a] < E[b]; });
         std::vector<int> anc(nc);
         std::iota(anc.begin(), anc.end(), 0);
         const int nrep = (int)(O.trunc_frac * nc);
