@@ -21,6 +21,8 @@ W words + 8 B of children per proposal, W words + 8 B written per accept, 4 B pe
 the kernel's own counters) over its average event-timed launch duration, against the 8 TB/s HBM peak.
 cpu_baseline: the reference's own CPU port (csrc/cpu_ref.h, oracle/_ref/ref_harness) on one core, over a
 bounded sample of the same workload (a subset of the chains, every level).
+long_variant (c1 and c5, whose literal runs are 1.1e7 and 5.9e6 node visits): the same workload with its schedule
+repeated ten times, so that the level loop's fixed costs are spread over more levels; reported beside value.
 """
 import argparse
 import json
@@ -48,7 +50,7 @@ def linear_betas(a, b, n):
 
 CONFIGS = {
     # the reference's CPU-runnable check case: greedy start, pre-order, 256 chains x 100 sweeps
-    "c1": dict(cpu_chains=256, inst="sat100", trees=("sat100.tree", None), order="preorder", nchains=256, levels=100, niters=1,
+    "c1": dict(long=10, cpu_chains=256, inst="sat100", trees=("sat100.tree", None), order="preorder", nchains=256, levels=100, niters=1,
                betas=(0.01, 15.0), sc_target=20.0, scheme="indep", slicing=False,
                desc="random 3-SAT n=100 (m=426), greedy start, pre-order, 256 chains x 100 sweeps, beta 0.01->15"),
     "c2": dict(cpu_chains=256, inst="sat100", trees=("sat100_multi.tree", (1, 2, 3)), order="par", nchains=8192, levels=200, niters=1,
@@ -63,7 +65,7 @@ CONFIGS = {
                niters=1, betas=(1.0, 15.0), sc_target=40.0, scheme="indep", slicing=False,
                desc="random 3-regular graph n=2000 (3000 labels, 47 words), spectral path starts, par order, "
                     "512 chains x 100 sweeps, beta 1->15"),
-    "c5": dict(cpu_chains=72, inst="sq64", trees=("sq64_row.tree", None), order="par", nchains=72, levels=20, niters=1,
+    "c5": dict(long=10, cpu_chains=72, inst="sq64", trees=("sq64_row.tree", None), order="par", nchains=72, levels=20, niters=1,
                betas=(0.01, 15.0), sc_target=70.0, scheme="indep", slicing=False,
                desc="64x64 open lattice (4096 tensors, 8064 labels, 126 words), row-major path start, par order, "
                     "72 chains x 20 sweeps, beta 0.01->15"),
@@ -256,6 +258,9 @@ def main():
     ap.add_argument("--wide-lanes", type=int, default=0, help="wide kernel: lanes per proposal (0: automatic)")
     ap.add_argument("--sums", default="auto", choices=("auto", "on", "off"),
                     help="wide kernel: chunk summaries (the binary's --sums / --no-sum; auto: on from 64 words)")
+    ap.add_argument("--long", type=int, default=None,
+                    help="also run the workload over this many times its levels (default: 10 for the short c1 and "
+                         "c5, none otherwise; 0 or 1: none)")
     ap.add_argument("--no-overlap", action="store_true",
                     help="fold and selection of a level on the sweep's stream, not beside the next sweep")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -329,6 +334,16 @@ def main():
         res["dense_streaming"] = {"value": visits / rd["t_anneal"], "ms_per_step": rd["t_anneal"] * 1e3 / steps,
                                   "kernel_visits_per_s": visits / rd["kernel_s"], "kernel": rd.get("hip_kernel"),
                                   "repetitions": rd["_spread"], "roofline": roofd}
+    long_k = a.long if a.long is not None else C.get("long", 0)
+    if long_k > 1 and a.steps is None:
+        # the literal workload is short enough that the level loop's fixed costs (first-level set-up, the final
+        # copies) weigh on the rate: the same workload over long_k times the levels, the schedule repeated
+        lsteps = steps * long_k
+        lv = lsteps * C["niters"] * nchains * (inst.m - 1)
+        lr = run_binary(C, trees, betas, lsteps, a.warmup, a.scheme, extra)
+        res["long_variant"] = {"levels": lsteps, "value": lv / lr["t_anneal"], "ms_per_step": lr["t_anneal"] * 1e3 / lsteps,
+                               "kernel_visits_per_s": lv / lr["kernel_s"], "best_tc": lr["tc"],
+                               "note": f"the same workload with its {steps}-level schedule run {long_k} times in a row"}
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(a.config, C, inst, trees, betas, min(a.cpu_chains or C["cpu_chains"], nchains))
     print(json.dumps(res))

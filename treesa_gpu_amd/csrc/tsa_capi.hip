@@ -732,6 +732,13 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
     TSA_HIP(ctx, hipMalloc(&ctx->d_trace, (size_t)max_levels * sizeof(TsaTraceRowD)));
   }
   ctx->track_levels = max_levels;
+  // timing events for one sweep launch per level, created here rather than one pair per launch inside the
+  // level loop, where their creation would hold up the host's enqueueing of short levels
+  while ((int)ctx->ev.size() < 2 * (ctx->npending + max_levels)) {
+    hipEvent_t e;
+    TSA_HIP(ctx, hipEventCreate(&e));
+    ctx->ev.push_back(e);
+  }
   TSA_HIP(ctx, quiesce_track(ctx));
   // The fold and the selection of a level run beside the next level's sweep, on the snapshot the sweep
   // left: on the wide path with one workgroup per chain (a chain barrier, K > 1, needs all of the sweep's
