@@ -364,7 +364,12 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
           pri[i] = (uint16_t)((((uint32_t)((L - 1 - (int)(dw[i] >> 16) % L) & 15)) << 12) | (pri[i] & 0x0FFEu) | 1u);
       }
       tsa_wave_sync();
+      // nodes with a nonzero priority: while any is left, the one with the largest key beats its unvisited
+      // neighbours, so the next scan finds a nonempty phase; when none is left that scan would find nothing
+      // and is skipped
+      int unvisited = nint;
       for (;;) {
+        if (unvisited == 0) break;
         // scan: the phase's independent set into the work list.  Node v is active when its priority is
         // nonzero and its (priority, id) key beats those of its unvisited parent and internal children.
         // TSA_SCAN_GROUPS 64-node groups at a time, branch-free: every lane reads its node's priority,
@@ -415,9 +420,11 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
         }
         if (cnt == 0) break;
         nst++;
+        unvisited -= cnt;
         tsa_wave_sync();
         for (int b0 = 0; b0 < cnt; b0 += 64) {
           const int j = b0 + lane;
+          bool rearm = false;
           if (j < cnt) {
             const int v = wl[j];
             const bool rev = (pri[v - m] & 1u) == 0;  // a follow-up visit draws its own numbers
@@ -430,11 +437,14 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
               na++;
               if (o.On >= m) par[o.On - m] = (uint16_t)o.Pn;
               if (o.Mn >= m) par[o.Mn - m] = (uint16_t)v;
-              if (P.par_follow && !rev && pri[o.Pn - m] == 0)
+              if (P.par_follow && !rev && pri[o.Pn - m] == 0) {
                 pri[o.Pn - m] = (uint16_t)tsa_follow_pri((uint32_t)o.Pn, hs);
+                rearm = true;  // the pivots of one phase are distinct nodes
+              }
             }
             pri[v - m] = 0;
           }
+          if (P.par_follow) unvisited += __popcll(__ballot(rearm));
         }
         tsa_wave_sync();
       }

@@ -314,7 +314,12 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
       s_next = 0;
     }
     __syncthreads();
+    // nodes not yet visited (without par_follow, which re-arms visited pivots): when none is left the next
+    // scan would find no active node, and it is skipped (while any is left, the one with the largest key is
+    // active)
+    int unvisited = nint;
     for (;;) {
+      if (!P.par_follow && unvisited == 0) break;  // uniform across the workgroup
       // 1. scan: a wave takes 64-node groups; each lane reads its node's priority, parent and children
       // words, then the three neighbour priorities, in two rounds of independent LDS reads (indices are
       // clamped instead of branched on, so that every read of a round is in flight at once)
@@ -385,6 +390,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
       const int cnt = s_cnt;
       if (cnt == 0) break;
       nst++;
+      unvisited -= cnt;
       uint8_t* const out = COOP ? sy.out + ((size_t)c * 2 + (nb & 1u)) * (size_t)nint4 : outl;
 
       // 2. visits: this workgroup's share of the work list -- entries k, k + K, k + 2K, ... (interleaved, so
