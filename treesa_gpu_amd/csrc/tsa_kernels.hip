@@ -368,25 +368,43 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
       // neighbours, so the next scan finds a nonempty phase; when none is left that scan would find nothing
       // and is skipped
       int unvisited = nint;
+      // Scan list: with at most 64 * TSA_SCAN_GROUPS internal nodes (one batch: every list entry is read
+      // before the scan writes any) and without par_follow (which re-arms visited pivots), a scan reads only
+      // the nodes not yet visited, kept in any order at the top of the work-list array, wl[nint4 - unvisited,
+      // nint4); the scan writes the phase's active nodes at the bottom, wl[0, cnt), and the others back at the
+      // top.  Otherwise every scan reads all nodes.  The visits of a phase commute, so the order of the
+      // work list changes no result.
+      const bool shrink = nint <= 64 * TSA_SCAN_GROUPS && !P.par_follow;
+      if (shrink) {
+        for (int i = lane; i < nint; i += 64) wl[nint4 - nint + i] = (uint16_t)(m + i);
+        tsa_wave_sync();
+      }
       for (;;) {
         if (unvisited == 0) break;
         // scan: the phase's independent set into the work list.  Node v is active when its priority is
         // nonzero and its (priority, id) key beats those of its unvisited parent and internal children.
-        // TSA_SCAN_GROUPS 64-node groups at a time, branch-free: every lane reads its node's priority,
-        // parent and children words, then the three neighbour priorities (index 0 where there is no such
-        // neighbour), so a batch costs two dependent LDS round trips.
-        int cnt = 0;
-        for (int i0 = 0; i0 < nint; i0 += 64 * TSA_SCAN_GROUPS) {
-          const int ng = (nint - i0 + 63) >> 6;  // groups present in this batch (wave-uniform)
+        // TSA_SCAN_GROUPS 64-entry groups at a time, branch-free: every lane reads its node (from the list),
+        // the node's priority, parent and children words, then the three neighbour priorities (index 0
+        // where there is no such neighbour), so a batch costs two (three with the list) dependent LDS round
+        // trips.
+        const int total = shrink ? unvisited : nint;  // entries to scan
+        const int ubase = nint4 - unvisited;          // the list's first entry
+        int cnt = 0, kept = 0;
+        for (int i0 = 0; i0 < total; i0 += 64 * TSA_SCAN_GROUPS) {
+          const int ng = (total - i0 + 63) >> 6;  // groups present in this batch (wave-uniform)
+          int ni[TSA_SCAN_GROUPS];
           uint32_t pv[TSA_SCAN_GROUPS], pw[TSA_SCAN_GROUPS], cw[TSA_SCAN_GROUPS];
 #pragma unroll
           for (int q = 0; q < TSA_SCAN_GROUPS; q++) {
+            ni[q] = 0;
             pv[q] = 0u;
             pw[q] = 0xFFFFu;
             cw[q] = 0u;
             if (q < ng) {
-              const int i = i0 + 64 * q + lane;
-              const int ii = i < nint ? i : 0;
+              const int j = i0 + 64 * q + lane;
+              const int jj = j < total ? j : 0;
+              const int ii = shrink ? (int)wl[ubase + jj] - m : jj;
+              ni[q] = ii;
               pv[q] = pri[ii];
               pw[q] = par[ii];
               cw[q] = ch[ii];
@@ -406,16 +424,23 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
 #pragma unroll
           for (int q = 0; q < TSA_SCAN_GROUPS; q++) {
             if (q >= ng) break;
-            const int i = i0 + 64 * q + lane;
-            const uint32_t key = (pv[q] << 16) | (uint32_t)(m + i);
+            const bool valid = i0 + 64 * q + lane < total;
+            const uint32_t v = (uint32_t)(m + ni[q]);
+            const uint32_t key = (pv[q] << 16) | v;
             const uint32_t p = pw[q], l = cw[q] & 0xFFFFu, r = cw[q] >> 16;
             const bool beat_p = p != 0xFFFFu && np_[q] != 0u && ((np_[q] << 16) | p) > key;
             const bool beat_l = l >= (uint32_t)m && nl[q] != 0u && ((nl[q] << 16) | l) > key;
             const bool beat_r = r >= (uint32_t)m && nr[q] != 0u && ((nr[q] << 16) | r) > key;
-            const bool act = i < nint && pv[q] != 0u && !beat_p && !beat_l && !beat_r;
+            const bool act = valid && pv[q] != 0u && !beat_p && !beat_l && !beat_r;
             const uint64_t b = __ballot(act);
-            if (act) wl[cnt + __popcll(b & tsa_lt_mask(lane))] = (uint16_t)(m + i);
+            if (act) wl[cnt + __popcll(b & tsa_lt_mask(lane))] = (uint16_t)v;
             cnt += __popcll(b);
+            if (shrink) {
+              const bool keep = valid && !act;
+              const uint64_t bk = __ballot(keep);
+              if (keep) wl[nint4 - 1 - (kept + __popcll(bk & tsa_lt_mask(lane)))] = (uint16_t)v;
+              kept += __popcll(bk);
+            }
           }
         }
         if (cnt == 0) break;
