@@ -8,7 +8,10 @@
   register widths (64 | 65, 128 | 129, 256 | 257 labels -> 1, 2, 4, 8 words) and of the runtime width
   (513 labels);
 * wide_<L>: 300 tensors and L labels each held by two tensors: 16384 labels is the widest chain the wide
-  kernel takes (256 words), 16385 falls back to the one-wave kernel with runtime width.
+  kernel takes (256 words), 16385 falls back to the one-wave kernel with runtime width;
+* sparse_<m>: m tensors over 256 labels (register width 4: the chain stays in LDS), each label on two random
+  tensors and every tensor without one given one more: 513 tensors are 512 internal nodes, the most whose
+  par scan keeps the list of unvisited nodes; 514 tensors scan every node in two batches of 512.
 """
 import numpy as np
 
@@ -56,6 +59,19 @@ def _wide(nlab, seed):
     return m, nlab, ixs, []
 
 
+def _sparse(m, seed, nlab=256):
+    rng = np.random.default_rng(seed)
+    ixs = [set() for _ in range(m)]
+    for l in range(nlab):
+        a, b = rng.choice(m, 2, replace=False)
+        ixs[int(a)].add(l)
+        ixs[int(b)].add(l)
+    for t in range(m):
+        if not ixs[t]:
+            ixs[t].add(int(rng.integers(nlab)))
+    return m, nlab, [sorted(ix) for ix in ixs], []
+
+
 def instance(name):
     if name == "pair":
         return 2, 3, [[0, 1], [1, 2]], [0]
@@ -67,8 +83,10 @@ def instance(name):
         return _deg3(int(name[5:]), 3)
     if name.startswith("wide_"):
         return _wide(int(name[5:]), 5)
+    if name.startswith("sparse_"):
+        return _sparse(int(name[7:]), 9)
     raise KeyError(name)
 
 
-NAMES = ["triple", "mixed40", "deg3_64", "deg3_65", "deg3_129", "deg3_257", "deg3_513"]
+NAMES = ["triple", "mixed40", "deg3_64", "deg3_65", "deg3_129", "deg3_257", "deg3_513", "sparse_513", "sparse_514"]
 WIDE = ["wide_16384", "wide_16385"]

@@ -1,5 +1,6 @@
 """GPU parity at the edges of the input space (tests/edge_instances.py): the smallest instance, empty tensors,
-labels held by one tensor, open labels, every register width and the first runtime width, both sweep orders,
+labels held by one tensor, open labels, every register width and the first runtime width, the largest chain
+whose par scan keeps a list of unvisited nodes (512 internal nodes) and the next one, both sweep orders,
 float node costs, and chain counts that leave workgroups partly filled -- the HIP path through the C ABI
 against the oracle, bit for bit (records, counts, energies)."""
 import numpy as np
@@ -24,6 +25,8 @@ def test_edge_instance_matches_oracle(name, order, nchains, mode):
         assert "wide" in gpu[3], gpu[3]  # the widest chain the wide kernel takes
     if name == "wide_16385":
         assert "wide" not in gpu[3], gpu[3]  # past it: the one-wave kernel with runtime width
+    if name.startswith("sparse_"):
+        assert gpu[3].startswith("lds"), gpu[3]  # the chain in LDS: the par scan's list or its full form
     compare(case, gpu, case.run_oracle())
 
 
