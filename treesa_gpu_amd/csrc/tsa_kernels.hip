@@ -6,10 +6,11 @@
 // the per-node arrays live in LDS (global variant, runtime label width).
 //
 // A sweep gives every internal node exactly one proposal.  Par order (the reference's k_par,
-// csrc/treesa_gpu.cu:829-997): random 16-bit priorities per node and sweep; each phase scans all
-// internal nodes, compacts the independent set (unvisited nodes whose (priority, id) key beats their
-// unvisited parent and internal children) into a work list with a 64-lane ballot, and visits it 64
-// nodes at a time, one node per lane.  Pre-order (the reference's k_warp, csrc/treesa_gpu.cu:585-722):
+// csrc/treesa_gpu.cu:829-997): random 16-bit priorities per node and sweep; each phase scans the
+// internal nodes not yet visited (all of them on chains of more than 512 nodes or with par_follow),
+// compacts the independent set (unvisited nodes whose (priority, id) key beats their unvisited parent and
+// internal children) into a work list with a 64-lane ballot, and visits it 64 nodes at a time, one node
+// per lane; the sweep ends when no node is left unvisited.  Pre-order (the reference's k_warp, csrc/treesa_gpu.cu:585-722):
 // a work list of ready nodes (parent already visited), up to 64 visited per step, children pushed by
 // ballot prefix.  Every visit draws Philox((node, sweep, chain)), so both mappings reproduce the CPU
 // recursion and the CPU phase-by-phase sweep bit for bit.
