@@ -97,23 +97,35 @@ float lse_flt(float a, float b) {
   if (hi == -INFINITY) return hi;
   return hi + log2f(1.0f + exp2f(lo - hi));
 }
+// Rounding variants for perturbation experiments (oracle_set_variant): bit 0 evaluates the energy fold's lse
+// in double and rounds once (an equally accurate float lse whose last bit differs from the libm form now and
+// then, as another device's log2f / exp2f would), bit 1 does the same in the float energy models of the
+// sweeps.  0 (the default) is the reference's arithmetic on this host.
+int g_variant = 0;
+float lse_dbl(float a, float b) {
+  const float hi = a > b ? a : b, lo = a > b ? b : a;
+  if (hi == -INFINITY) return hi;
+  return (float)((double)hi + std::log2(1.0 + std::exp2((double)lo - (double)hi)));
+}
+float lse_fold(float a, float b) { return (g_variant & 1) ? lse_dbl(a, b) : lse_flt(a, b); }
+float lse_model(float a, float b) { return (g_variant & 2) ? lse_dbl(a, b) : lse_flt(a, b); }
 float model_lt(int mode, int B, int M, int N, int K, const OParams& P) {
   if (mode == 1) {
     const float lops = (float)(1 + B + std::max(M, P.m0) + std::max(N, P.n0) + std::max(K, P.k0)) - P.lpeak;
-    const float lbits = lse_flt(lse_flt((float)(B + M + K), (float)(B + N + K)), (float)(B + M + N)) - P.lbw;
-    return lse_flt(lops > lbits ? lops : lbits, P.llaunch);
+    const float lbits = lse_model(lse_model((float)(B + M + K), (float)(B + N + K)), (float)(B + M + N)) - P.lbw;
+    return lse_model(lops > lbits ? lops : lbits, P.llaunch);
   }
   if (B + M + N <= P.v2_small_rank) return P.v2_lsmall_cell + (float)(B + M + N + K);
   const float la = (float)(B + M + K), lb = (float)(B + N + K), lc = (float)(B + M + N);
-  const float lab = lse_flt(la, lb), lmv = lse_flt(lab, lc);
-  float best = lse_flt(P.v2_lcc_bit + lmv, P.v2_lcc_cell + (float)(B + M + N + K));
+  const float lab = lse_model(la, lb), lmv = lse_model(lab, lc);
+  float best = lse_model(P.v2_lcc_bit + lmv, P.v2_lcc_cell + (float)(B + M + N + K));
   if (K >= 7 && std::max(M, N) >= 5) {
-    const float t = lse_flt(lse_flt(P.v2_ltc_bit + lmv, P.v2_ltc_pad + (float)(B + std::max(M, 6) + std::max(N, 6) +
+    const float t = lse_model(lse_model(P.v2_ltc_bit + lmv, P.v2_ltc_pad + (float)(B + std::max(M, 6) + std::max(N, 6) +
                                                                                 std::max(K, 8))),
                             P.v2_ltc_out + lc);
     if (t < best) best = t;
   }
-  return lse_flt(lse_flt(P.v2_l3launch, P.v2_lperm2 + lab), best);
+  return lse_model(lse_model(P.v2_l3launch, P.v2_lperm2 + lab), best);
 }
 bool accept(uint32_t r, float beta, float dE) {
   const float u = (float)(r >> 8) * (1.0f / 16777216.0f);
@@ -298,14 +310,14 @@ Eval eval_chain(const Tree& T, const OParams& P, int mode) {
       contraction_counts(T.lab[T.L[v]], T.lab[T.R[v]], T.lab[v], T.cut, B, M, N, K);
       const int Z = live_size(T.lab[v], T.cut);
       const float cost = mode == 0 ? (float)(Z + K) : model_lt(mode, B, M, N, K, P);
-      acc[t] = lse_flt(acc[t], cost);
+      acc[t] = lse_fold(acc[t], cost);
       if (Z > best[t]) { best[t] = Z; nbest[t] = 1; }
       else if (Z == best[t]) nbest[t]++;
     }
   }
   for (int o = 16; o > 0; o >>= 1) {
     float nxt[32];
-    for (int t = 0; t < 32; t++) nxt[t] = lse_flt(acc[t], acc[t ^ o]);
+    for (int t = 0; t < 32; t++) nxt[t] = lse_fold(acc[t], acc[t ^ o]);
     std::memcpy(acc, nxt, sizeof acc);
   }
   int scmax = 0;
@@ -477,6 +489,152 @@ bool topo_labels(const Inst& I, const uint32_t* ch, std::vector<Set>& out) {
   return true;
 }
 
+// ---- the level loop (csrc/treesa_gpu.cu:1730-1933) -------------------------------------------------------
+// Selection score and population energy in double with the host libm, as the reference's host loop
+// evaluates them (csrc/treesa_gpu.cu:1737-1753).
+struct Selector {
+  int slicing, select_sc;
+  double sct, w;
+  double energy(float lc, int sc, int ns) const {
+    return (double)ns + (double)lc + w * std::max(0.0, (double)sc - sct);
+  }
+  double score(int mode, float lc, int sc, int ns) const {
+    if (slicing) return (double)ns + (double)lc + 1000.0 * std::max(0.0, (double)sc - sct);
+    if (select_sc) return 4096.0 * std::max(0.0, (double)sc - sct) + (double)lc;
+    if (mode != 0) return energy(lc, sc, ns);
+    const double tc = (double)lc;
+    if ((double)sc <= sct || w <= 0) return tc;
+    // log2(2^tc + w (2^sc - 2^sct)), both terms in log2
+    const double pen = std::log2(w) + (double)sc + std::log2(1.0 - std::exp2(sct - (double)sc));
+    const double hi = std::max(tc, pen), lo = std::min(tc, pen);
+    return hi + std::log2(1.0 + std::exp2(lo - hi));
+  }
+};
+
+// Systematic resampling (csrc/treesa_gpu.cu:1837-1856): weights exp(-db (E - Emin)); one uniform u places
+// nc equally spaced pointers j + u on the cumulative scaled weights.  margin (optional) receives the smallest
+// |cumulative - (j + u)| met at a pointer decision.
+void systematic(const std::vector<double>& E, double db, double u, std::vector<int>& anc, double* margin) {
+  const int nc = (int)E.size();
+  double lo = INFINITY;
+  for (double e : E) lo = std::min(lo, e);
+  std::vector<double> wt(nc);
+  double tot = 0;
+  for (int c = 0; c < nc; c++) {
+    wt[c] = std::exp(-db * (E[c] - lo));
+    tot += wt[c];
+  }
+  anc.assign(nc, nc - 1);
+  double cum = 0, mg = INFINITY;
+  int j = 0;
+  for (int c = 0; c < nc; c++) {
+    cum += wt[c] / tot * nc;
+    for (; j < nc; j++) {
+      mg = std::min(mg, std::fabs(cum - (j + u)));
+      if (!(j + u < cum)) break;
+      anc[j] = c;
+    }
+  }
+  if (margin) *margin = mg;
+}
+
+// Truncation selection (csrc/treesa_gpu.cu:1857-1869): chains ordered by E with std::sort (the reference's
+// unstable libstdc++ introsort), then the k-th worst becomes a copy of the k-th best for k < frac * nc.
+void truncation(const std::vector<double>& E, double frac, std::vector<int>& anc, std::vector<int>* order) {
+  const int nc = (int)E.size();
+  std::vector<int> ix(nc);
+  for (int c = 0; c < nc; c++) ix[c] = c;
+  std::sort(ix.begin(), ix.end(), [&](int a, int b) { return E[a] < E[b]; });
+  anc.resize(nc);
+  for (int c = 0; c < nc; c++) anc[c] = c;
+  const int nrep = (int)(frac * nc);
+  for (int k = 0; k < nrep; k++) anc[ix[nc - 1 - k]] = ix[k];
+  if (order) *order = ix;
+}
+
+bool same_tree(const Tree& a, const Tree& b) { return a.L == b.L && a.R == b.R && a.cut == b.cut; }
+
+// Final slice repair (csrc/treesa_gpu.cu:1248-1274): while the largest masked tensor (leaves included)
+// exceeds sct, cut the label that occurs in most of the largest tensors, lowest id on ties.
+int repair_slices(Tree& T, double sct) {
+  const int n = 2 * T.m - 1;
+  int added = 0;
+  for (;;) {
+    std::vector<int> sz(n);
+    int top = 0;
+    for (int v = 0; v < n; v++) top = std::max(top, sz[v] = live_size(T.lab[v], T.cut));
+    if (top == 0 || (double)top <= sct) return added;
+    std::vector<int> hits(T.nlab, 0);
+    for (int v = 0; v < n; v++)
+      if (sz[v] == top)
+        for (int l : T.lab[v])
+          if (!T.cut[l]) hits[l]++;
+    int pick = 0;
+    for (int l = 1; l < T.nlab; l++)
+      if (hits[l] > hits[pick]) pick = l;
+    T.cut[pick] = 1;
+    added++;
+  }
+}
+
+// nsweeps sweeps of one chain (slot `chain`) from global sweep sweep0, slice steps after every sweep s with
+// (s + 1) % slice_every == 0 when slice moves are on (csrc/treesa_gpu.cu:975-978).
+void run_chain(Tree& T, const OParams& P, int order, float beta, uint32_t sweep0, int nsweeps, uint32_t chain,
+               Counter& C) {
+  for (int s = 0; s < nsweeps; s++) {
+    const uint32_t sw = sweep0 + (uint32_t)s;
+    if (order == 0) par_sweep(T, beta, sw, chain, P, P.mode, C);
+    else preorder_sweep(T, 2 * T.m - 2, beta, sw, chain, P, P.mode, C);
+    if (P.slicing && P.slice_moves > 0 && (sw + 1u) % (uint32_t)(P.slice_every > 0 ? P.slice_every : 1) == 0u)
+      slice_step(T, beta, sw, chain, P, P.mode, C);
+  }
+}
+
+// Host double-precision complexities of a tree on its sliced network (csrc/treesa_gpu.cu:1206-1244):
+// out = {tc, sc, gpu_time, h100_time, |S|}.  gm / hm: the model constants as given on the command line.
+void tree_host_energy(const Tree& T, const double* gm, const double* hm, double* out) {
+  const int m = T.m;
+  int sc = 0, ns = 0;
+  for (int l = 0; l < T.nlab; l++) ns += T.cut[l] ? 1 : 0;
+  for (int i = 0; i < m; i++) sc = std::max(sc, live_size(T.lab[i], T.cut));
+  std::vector<double> t;
+  double time = 0, time2 = 0;
+  const float lpeak = (float)std::log2(gm[0]), lbw = (float)std::log2(gm[1]), lla = (float)std::log2(gm[5]);
+  const float hl[9] = {(float)std::log2(3 * hm[0]), (float)std::log2(2 / hm[1]), (float)std::log2(hm[2]),
+                       (float)std::log2(hm[3]),     (float)std::log2(hm[4]),     (float)std::log2(hm[5]),
+                       (float)std::log2(hm[6]),     0.f,                         (float)std::log2(hm[8])};
+  auto e2 = [](float l) { return std::exp2((double)l); };
+  for (int v = m; v < 2 * m - 1; v++) {
+    int B, M, N, K;
+    contraction_counts(T.lab[T.L[v]], T.lab[T.R[v]], T.lab[v], T.cut, B, M, N, K);
+    t.push_back((double)(B + M + N + K));
+    sc = std::max(sc, live_size(T.lab[v], T.cut));
+    const double ops = std::exp2((double)(1 + B + std::max(M, (int)gm[2]) + std::max(N, (int)gm[3]) + std::max(K, (int)gm[4])));
+    const double bits = std::exp2((double)(B + M + K)) + std::exp2((double)(B + N + K)) + std::exp2((double)(B + M + N));
+    time += std::max(ops / std::exp2((double)lpeak), bits / std::exp2((double)lbw)) + std::exp2((double)lla);
+    if (B + M + N <= (int)hm[7]) {
+      time2 += e2(hl[8]) * std::exp2((double)(B + M + N + K));
+    } else {
+      const double a = std::exp2((double)(B + M + K)), b = std::exp2((double)(B + N + K)), c = std::exp2((double)(B + M + N));
+      double best = e2(hl[2]) * (a + b + c) + e2(hl[3]) * std::exp2((double)(B + M + N + K));
+      if (K >= 7 && std::max(M, N) >= 5)
+        best = std::min(best, e2(hl[4]) * (a + b + c) +
+                                  e2(hl[5]) * std::exp2((double)(B + std::max(M, 6) + std::max(N, 6) + std::max(K, 8))) +
+                                  e2(hl[6]) * c);
+      time2 += e2(hl[0]) + e2(hl[1]) * (a + b) + best;
+    }
+  }
+  double mx = -1e300;
+  for (double x : t) mx = std::max(mx, x);
+  double s = 0;
+  for (double x : t) s += std::exp2(x - mx);
+  out[0] = mx + std::log2(s);
+  out[1] = sc;
+  out[2] = time;
+  out[3] = time2;
+  out[4] = ns;
+}
+
 }  // namespace
 
 // =========================================================================================================
@@ -506,6 +664,9 @@ void* oracle_new(int m, int nlab, const int* offs, const int* labels, int ny, co
 void oracle_free(void* h) { delete static_cast<Inst*>(h); }
 
 uint64_t oracle_splitmix64(uint64_t x) { return smix64(x); }
+
+// Perturbation experiments only: see g_variant (0 restores the reference's arithmetic).
+void oracle_set_variant(int v) { g_variant = v; }
 
 void oracle_philox(const uint32_t* ctr, uint32_t k0, uint32_t k1, uint32_t* out) {
   const R4 r = philox10(R4{ctr[0], ctr[1], ctr[2], ctr[3]}, k0, k1);
@@ -587,14 +748,7 @@ int oracle_sweeps(void* h, const OParams* P, int W, int ch_off, int s_off, int c
     uint64_t* rec = pop + (size_t)k * chain_words;
     Tree T = from_record(I, Lo, rec, P->slicing != 0);
     Counter C;
-    const uint32_t chain = (uint32_t)(c0 + k);
-    for (int s = 0; s < nsweeps; s++) {
-      const uint32_t sw = sweep0 + (uint32_t)s;
-      if (order == 0) par_sweep(T, beta, sw, chain, *P, P->mode, C);
-      else preorder_sweep(T, 2 * I.m - 2, beta, sw, chain, *P, P->mode, C);
-      if (P->slicing && P->slice_moves > 0 && (sw + 1u) % (uint32_t)(P->slice_every > 0 ? P->slice_every : 1) == 0u)
-        slice_step(T, beta, sw, chain, *P, P->mode, C);
-    }
+    run_chain(T, *P, order, beta, sweep0, nsweeps, (uint32_t)(c0 + k), C);
     to_record(T, Lo, rec, P->slicing != 0);
     sp += C.prop;
     sa += C.acc;
@@ -636,46 +790,213 @@ void oracle_host_energy(void* h, const double* gm, const double* hm, int W, int 
                         const uint64_t* rec, int slicing, double* out) {
   const Inst& I = *static_cast<Inst*>(h);
   const Layout Lo{W, ch_off, s_off, chain_words};
-  const Tree T = from_record(I, Lo, rec, slicing != 0);
-  int sc = 0, ns = 0;
-  for (int l = 0; l < I.nlab; l++) ns += T.cut[l] ? 1 : 0;
-  for (int i = 0; i < I.m; i++) sc = std::max(sc, live_size(T.lab[i], T.cut));
-  std::vector<double> t;
-  double time = 0, time2 = 0;
-  const float lpeak = (float)std::log2(gm[0]), lbw = (float)std::log2(gm[1]), lla = (float)std::log2(gm[5]);
-  const float hl[9] = {(float)std::log2(3 * hm[0]), (float)std::log2(2 / hm[1]), (float)std::log2(hm[2]),
-                       (float)std::log2(hm[3]),     (float)std::log2(hm[4]),     (float)std::log2(hm[5]),
-                       (float)std::log2(hm[6]),     0.f,                         (float)std::log2(hm[8])};
-  auto e2 = [](float l) { return std::exp2((double)l); };
-  for (int v = I.m; v < 2 * I.m - 1; v++) {
-    int B, M, N, K;
-    contraction_counts(T.lab[T.L[v]], T.lab[T.R[v]], T.lab[v], T.cut, B, M, N, K);
-    t.push_back((double)(B + M + N + K));
-    sc = std::max(sc, live_size(T.lab[v], T.cut));
-    const double ops = std::exp2((double)(1 + B + std::max(M, (int)gm[2]) + std::max(N, (int)gm[3]) + std::max(K, (int)gm[4])));
-    const double bits = std::exp2((double)(B + M + K)) + std::exp2((double)(B + N + K)) + std::exp2((double)(B + M + N));
-    time += std::max(ops / std::exp2((double)lpeak), bits / std::exp2((double)lbw)) + std::exp2((double)lla);
-    if (B + M + N <= (int)hm[7]) {
-      time2 += e2(hl[8]) * std::exp2((double)(B + M + N + K));
-    } else {
-      const double a = std::exp2((double)(B + M + K)), b = std::exp2((double)(B + N + K)), c = std::exp2((double)(B + M + N));
-      double best = e2(hl[2]) * (a + b + c) + e2(hl[3]) * std::exp2((double)(B + M + N + K));
-      if (K >= 7 && std::max(M, N) >= 5)
-        best = std::min(best, e2(hl[4]) * (a + b + c) +
-                                  e2(hl[5]) * std::exp2((double)(B + std::max(M, 6) + std::max(N, 6) + std::max(K, 8))) +
-                                  e2(hl[6]) * c);
-      time2 += e2(hl[0]) + e2(hl[1]) * (a + b) + best;
+  tree_host_energy(from_record(I, Lo, rec, slicing != 0), gm, hm, out);
+}
+
+// ---- the level loop -----------------------------------------------------------------------------------
+// Inputs of oracle_anneal (field order matches tests/oracle.py).
+struct OAnnealIn {
+  int32_t nlev;
+  int32_t order;       // 0 par, 1 pre-order
+  int32_t scheme;      // 0 indep, 1 pa, 2 trunc
+  int32_t eval_every;
+  int32_t select_sc;
+  int32_t pad;
+  double trunc_frac, sc_target, sc_weight;
+  uint64_t seed;
+  const float* betas;      // nlev
+  const int32_t* lmode;    // nlev: energy mode of every level (stage 2 continues the population in another)
+  const int32_t* lniters;  // nlev: sweeps of every level
+  const double* gm;        // model constants as given on the command line (6 and 9 values)
+  const double* hm;
+};
+
+// What one level left (field order matches tests/oracle.py).
+struct OLevel {
+  int32_t evaluated, best, sc, ns, families, mode, resampled;
+  float lc;
+  double score, meanE, meanNs;
+  double sel_margin;  // smallest gap between the level's best score and another tree's score, or the incumbent's
+  double pop_margin;  // resampling: smallest |cumulative - pointer| (pa) or E gap between ranked neighbours (trunc)
+};
+
+// The reference's run_anneal (csrc/treesa_gpu.cu:1756-1877) over the population pop (nc records, chain c in
+// slot c), in place: per level a stage switch when its energy mode changes (the incumbent is rescored in the
+// new energy from the host double energy of its record, 1790-1798), niters sweeps of every chain with the
+// global sweep counter, then at evaluated levels (every eval_every-th, the last, and the one before a switch)
+// the energies, the lowest score over chains (first index on ties) replacing the incumbent only when strictly
+// lower (1810-1824), the trace row, and pa / trunc population steps except at the last level and before a
+// switch (1836-1869; the pa uniform from mt19937_64(splitmix64(seed + 777))).  anc receives nlev x nc
+// ancestor lists (identity where nothing was resampled).  best_rec: the incumbent's record as it was copied
+// (maintained labels, children, S).  iout = {best_chain, nresample, staged, total_sweeps}; h1 = the stage-1
+// incumbent's host energy {tc, sc, gpu_time, h100_time, |S|} when staged.
+int oracle_anneal(void* h, const OParams* P0, int W, int ch_off, int s_off, int chain_words, uint64_t* pop, int nc,
+                  const OAnnealIn* in, OLevel* lev_out, int32_t* anc, uint64_t* best_rec, int32_t* iout, double* h1) {
+  const Inst& I = *static_cast<Inst*>(h);
+  const Layout Lo{W, ch_off, s_off, chain_words};
+  const bool sl = P0->slicing != 0;
+  std::vector<Tree> trees(nc);
+  for (int c = 0; c < nc; c++) trees[c] = from_record(I, Lo, pop + (size_t)c * chain_words, sl);
+  Selector sel{P0->slicing, in->select_sc, in->sc_target, in->sc_weight};
+  int mode = P0->mode;
+  Tree best;
+  bool have_best = false;
+  double best_score = INFINITY;
+  int best_chain = -1, nresample = 0, staged = 0;
+  uint32_t sweeps = 0;
+  std::vector<int> family(nc);
+  for (int c = 0; c < nc; c++) family[c] = c;
+  std::mt19937_64 prng(smix64(in->seed + 777));
+  float beta_mark = in->nlev > 0 ? in->betas[0] : 0.f;
+  std::vector<float> lc(nc);
+  std::vector<int> sc(nc), ns(nc);
+  for (int L = 0; L < in->nlev; L++) {
+    OLevel& o = lev_out[L];
+    std::memset(&o, 0, sizeof o);
+    o.best = -1;
+    int32_t* a = anc + (size_t)L * nc;
+    for (int c = 0; c < nc; c++) a[c] = c;
+    if (in->lmode[L] != mode) {
+      double e[5];
+      tree_host_energy(best, in->gm, in->hm, e);
+      std::memcpy(h1, e, sizeof e);
+      staged = 1;
+      mode = in->lmode[L];
+      best_score = sel.score(mode, (float)std::log2(mode == 1 ? e[2] : e[3]), (int)e[1], (int)e[4]);
+      beta_mark = in->betas[L];
     }
+    OParams P = *P0;
+    P.mode = mode;
+    const float beta = in->betas[L];
+    const int nsw = in->lniters[L];
+#pragma omp parallel for schedule(dynamic, 1)
+    for (int c = 0; c < nc; c++) {
+      Counter C;
+      run_chain(trees[c], P, in->order, beta, sweeps, nsw, (uint32_t)c, C);
+    }
+    sweeps += (uint32_t)nsw;
+    const bool last = L + 1 == in->nlev;
+    const bool switching = !last && in->lmode[L + 1] != mode;
+    o.mode = mode;
+    if (!(L % in->eval_every == in->eval_every - 1 || last || switching)) continue;
+    o.evaluated = 1;
+#pragma omp parallel for schedule(dynamic, 4)
+    for (int c = 0; c < nc; c++) {
+      const Eval e = eval_chain(trees[c], P, mode);
+      lc[c] = e.lcost;
+      sc[c] = e.sc;
+      ns[c] = e.ns;
+    }
+    std::vector<double> s(nc), E(nc);
+    int bi = 0;
+    double sumE = 0, sumNs = 0;
+    for (int c = 0; c < nc; c++) {
+      s[c] = sel.score(mode, lc[c], sc[c], ns[c]);
+      E[c] = sel.energy(lc[c], sc[c], ns[c]);
+      if (s[c] < s[bi]) bi = c;
+      sumE += E[c];
+      sumNs += ns[c];
+    }
+    double mg = std::isfinite(best_score) ? std::fabs(s[bi] - best_score) : INFINITY;
+    for (int c = 0; c < nc; c++)
+      if (c != bi && !(s[c] == s[bi] && same_tree(trees[c], trees[bi]))) mg = std::min(mg, s[c] - s[bi]);
+    o.sel_margin = mg;
+    if (s[bi] < best_score) {
+      best_score = s[bi];
+      best_chain = bi;
+      best = trees[bi];
+      have_best = true;
+    }
+    std::vector<int> seen(nc, 0);
+    int nf = 0;
+    for (int c = 0; c < nc; c++) nf += seen[family[c]]++ == 0;
+    o.best = bi;
+    o.score = s[bi];
+    o.lc = lc[bi];
+    o.sc = sc[bi];
+    o.ns = ns[bi];
+    o.families = nf;
+    o.meanE = sumE / nc;
+    o.meanNs = sumNs / nc;
+    if (last || switching || in->scheme == 0) continue;
+    std::vector<int> an;
+    if (in->scheme == 1) {
+      const double db = (double)(in->betas[L + 1] - beta_mark);  // float difference, as the reference
+      beta_mark = in->betas[L + 1];
+      const double u = std::uniform_real_distribution<double>(0, 1)(prng);
+      systematic(E, db, u, an, &o.pop_margin);
+    } else {
+      std::vector<int> ix;
+      truncation(E, in->trunc_frac, an, &ix);
+      const int nrep = (int)(in->trunc_frac * nc);
+      double g = INFINITY;
+      for (int p = 0; p + 1 < nc; p++) {
+        if (!(p < nrep || p + 1 >= nc - nrep)) continue;
+        const int x = ix[p], y = ix[p + 1];
+        if (E[x] == E[y] && same_tree(trees[x], trees[y])) continue;
+        g = std::min(g, E[y] - E[x]);
+      }
+      o.pop_margin = g;
+    }
+    std::vector<Tree> next(nc);
+    std::vector<int> fam(nc);
+    for (int c = 0; c < nc; c++) {
+      next[c] = trees[an[c]];
+      fam[c] = family[an[c]];
+      a[c] = an[c];
+    }
+    trees.swap(next);
+    family.swap(fam);
+    o.resampled = 1;
+    nresample++;
   }
-  double mx = -1e300;
-  for (double x : t) mx = std::max(mx, x);
-  double s = 0;
-  for (double x : t) s += std::exp2(x - mx);
-  out[0] = mx + std::log2(s);
-  out[1] = sc;
-  out[2] = time;
-  out[3] = time2;
-  out[4] = ns;
+  for (int c = 0; c < nc; c++) to_record(trees[c], Lo, pop + (size_t)c * chain_words, sl);
+  std::memset(best_rec, 0, (size_t)chain_words * 8);
+  if (have_best) to_record(best, Lo, best_rec, true);
+  iout[0] = best_chain;
+  iout[1] = nresample;
+  iout[2] = staged;
+  iout[3] = (int32_t)sweeps;
+  return 0;
+}
+
+// The final slice repair of a record's tree (labels from its topology, S from the record), S updated in
+// place; returns the number of labels added.
+int oracle_repair(void* h, int W, int ch_off, int s_off, int chain_words, uint64_t* rec, double sc_target) {
+  const Inst& I = *static_cast<Inst*>(h);
+  const Layout Lo{W, ch_off, s_off, chain_words};
+  Tree T = from_record(I, Lo, rec, true);
+  std::vector<Set> lab;
+  if (!topo_labels(I, reinterpret_cast<const uint32_t*>(rec + ch_off), lab)) return -1;
+  for (int v = I.m; v < 2 * I.m - 1; v++) T.lab[v] = lab[v];
+  const int k = repair_slices(T, sc_target);
+  for (int w = 0; w < W; w++) rec[s_off + w] = 0;
+  for (int l = 0; l < I.nlab; l++)
+    if (T.cut[l]) rec[s_off + (l >> 6)] |= 1ull << (l & 63);
+  return k;
+}
+
+// The population steps alone, on given energies: pa with one uniform u, and trunc.
+void oracle_systematic(const double* E, int nc, double db, double u, int32_t* anc) {
+  std::vector<int> an;
+  systematic(std::vector<double>(E, E + nc), db, u, an, nullptr);
+  std::copy(an.begin(), an.end(), anc);
+}
+void oracle_truncation(const double* E, int nc, double frac, int32_t* anc) {
+  std::vector<int> an;
+  truncation(std::vector<double>(E, E + nc), frac, an, nullptr);
+  std::copy(an.begin(), an.end(), anc);
+}
+// The selection score and the population energy of one chain, in double with the host libm.
+double oracle_score(int mode, int slicing, int select_sc, double sct, double w, float lc, int sc, int ns, int energy) {
+  const Selector S{slicing, select_sc, sct, w};
+  return energy ? S.energy(lc, sc, ns) : S.score(mode, lc, sc, ns);
+}
+// The pa uniforms of a run: the first n draws of uniform_real_distribution<double>(0, 1) over
+// mt19937_64(splitmix64(seed + 777)) (csrc/treesa_gpu.cu:1786, 1846).
+void oracle_pa_uniforms(uint64_t seed, int n, double* out) {
+  std::mt19937_64 g(smix64(seed + 777));
+  for (int i = 0; i < n; i++) out[i] = std::uniform_real_distribution<double>(0, 1)(g);
 }
 
 }  // extern "C"

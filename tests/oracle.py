@@ -29,6 +29,25 @@ class OParams(ctypes.Structure):
                 ("leaf_sc", ctypes.c_int32)]
 
 
+class OAnnealIn(ctypes.Structure):
+    _fields_ = [("nlev", ctypes.c_int32), ("order", ctypes.c_int32), ("scheme", ctypes.c_int32),
+                ("eval_every", ctypes.c_int32), ("select_sc", ctypes.c_int32), ("pad", ctypes.c_int32),
+                ("trunc_frac", ctypes.c_double), ("sc_target", ctypes.c_double), ("sc_weight", ctypes.c_double),
+                ("seed", ctypes.c_uint64), ("betas", ctypes.c_void_p), ("lmode", ctypes.c_void_p),
+                ("lniters", ctypes.c_void_p), ("gm", ctypes.c_void_p), ("hm", ctypes.c_void_p)]
+
+
+# one level of oracle_anneal (struct OLevel)
+LEVEL_DTYPE = np.dtype([("evaluated", "<i4"), ("best", "<i4"), ("sc", "<i4"), ("ns", "<i4"), ("families", "<i4"),
+                        ("mode", "<i4"), ("resampled", "<i4"), ("lc", "<f4"), ("score", "<f8"), ("meanE", "<f8"),
+                        ("meanNs", "<f8"), ("sel_margin", "<f8"), ("pop_margin", "<f8")])
+
+SCHEMES = {"indep": 0, "pa": 1, "trunc": 2}
+
+DEFAULT_GM = (11.9e15, 1.6e13, 6, 6, 8, 4e-6)
+DEFAULT_H100 = (4e-6, 1.23e13, 5.44e-14, 7.68e-15, 6.37e-14, 2.02e-16, 1.77e-13, 14, 1e-12)
+
+
 def build():
     subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle")], check=True)
 
@@ -56,6 +75,15 @@ def load():
     lib.oracle_sweeps.argtypes = [P, ctypes.POINTER(OParams), I, I, I, I, P, I, I, I, F, U32, I, P]
     lib.oracle_energy.argtypes = [P, ctypes.POINTER(OParams), I, I, I, I, P, I, P, P, P]
     lib.oracle_host_energy.argtypes = [P, P, P, I, I, I, I, P, I, P]
+    lib.oracle_anneal.argtypes = [P, ctypes.POINTER(OParams), I, I, I, I, P, I, ctypes.POINTER(OAnnealIn), P, P, P,
+                                  P, P]
+    lib.oracle_repair.argtypes = [P, I, I, I, I, P, ctypes.c_double]
+    lib.oracle_systematic.argtypes = [P, I, ctypes.c_double, ctypes.c_double, P]
+    lib.oracle_truncation.argtypes = [P, I, ctypes.c_double, P]
+    lib.oracle_score.argtypes = [I, I, I, ctypes.c_double, ctypes.c_double, F, I, I, I]
+    lib.oracle_score.restype = ctypes.c_double
+    lib.oracle_pa_uniforms.argtypes = [U64, I, P]
+    lib.oracle_set_variant.argtypes = [I]
     _lib = lib
     return lib
 
@@ -120,6 +148,37 @@ class Oracle:
                                     lay.chain_words, rec.ctypes.data, 1 if slicing else 0, out.ctypes.data)
         return float(out[0]), int(out[1]), float(out[2]), float(out[3]), int(out[4])
 
+    def anneal(self, params, lay, pop, betas, lmode, lniters, order, scheme="indep", eval_every=1, select_sc=False,
+               trunc_frac=0.25, sc_target=20.0, sc_weight=1.0, seed=1, gm=DEFAULT_GM, h100=DEFAULT_H100):
+        """The reference's level loop over a (nc, chain_words) population, in place (oracle_anneal).  Returns
+        a dict: levels (LEVEL_DTYPE per level), anc (nlev x nc), best_rec, best_chain, nresample, staged,
+        total_sweeps, h1 (the stage-1 incumbent's host energy when staged)."""
+        assert pop.dtype == np.uint64 and pop.flags.c_contiguous
+        nlev, nc = len(betas), pop.shape[0]
+        b = np.array(betas, np.float32)
+        lm = np.array(lmode, np.int32)
+        ln = np.array(lniters, np.int32)
+        g = np.array(gm, np.float64)
+        hm = np.array(h100, np.float64)
+        a = OAnnealIn(nlev, order, SCHEMES[scheme], eval_every, 1 if select_sc else 0, 0, trunc_frac, sc_target,
+                      sc_weight, seed, b.ctypes.data, lm.ctypes.data, ln.ctypes.data, g.ctypes.data, hm.ctypes.data)
+        levels = np.zeros(nlev, LEVEL_DTYPE)
+        anc = np.zeros((nlev, nc), np.int32)
+        best = np.zeros(lay.chain_words, np.uint64)
+        iout = np.zeros(4, np.int32)
+        h1 = np.zeros(5, np.float64)
+        self.lib.oracle_anneal(self.h, ctypes.byref(params), lay.W, lay.ch_off, lay.s_off, lay.chain_words,
+                               pop.ctypes.data, nc, ctypes.byref(a), levels.ctypes.data, anc.ctypes.data,
+                               best.ctypes.data, iout.ctypes.data, h1.ctypes.data)
+        return {"levels": levels, "anc": anc, "best_rec": best, "best_chain": int(iout[0]), "nresample": int(iout[1]),
+                "staged": bool(iout[2]), "total_sweeps": int(iout[3]), "h1": h1}
+
+    def repair(self, lay, rec, sc_target):
+        """Final greedy slice repair of rec's tree, S updated in place; returns the labels added."""
+        assert rec.dtype == np.uint64 and rec.flags.c_contiguous
+        return self.lib.oracle_repair(self.h, lay.W, lay.ch_off, lay.s_off, lay.chain_words, rec.ctypes.data,
+                                      float(sc_target))
+
     def __del__(self):
         try:
             self.lib.oracle_free(self.h)
@@ -176,3 +235,33 @@ def read_trees_py(path, m):
         v = vals[k * per:(k + 1) * per]
         out.append(np.array([v[2 * i] | (v[2 * i + 1] << 16) for i in range(m - 1)], np.uint32))
     return np.array(out, np.uint32)
+
+
+def systematic(E, db, u):
+    E = np.ascontiguousarray(E, np.float64)
+    out = np.zeros(len(E), np.int32)
+    load().oracle_systematic(E.ctypes.data, len(E), float(db), float(u), out.ctypes.data)
+    return out
+
+
+def truncation(E, frac):
+    E = np.ascontiguousarray(E, np.float64)
+    out = np.zeros(len(E), np.int32)
+    load().oracle_truncation(E.ctypes.data, len(E), float(frac), out.ctypes.data)
+    return out
+
+
+def score(mode, lc, sc, ns, slicing=False, select_sc=False, sc_target=20.0, sc_weight=1.0, energy=False):
+    return load().oracle_score(mode, 1 if slicing else 0, 1 if select_sc else 0, float(sc_target), float(sc_weight),
+                               float(lc), int(sc), int(ns), 1 if energy else 0)
+
+
+def pa_uniforms(seed, n):
+    out = np.zeros(n, np.float64)
+    load().oracle_pa_uniforms(seed, n, out.ctypes.data)
+    return out
+
+
+def set_variant(v):
+    """Rounding variant of the oracle's float lse (0: the reference's arithmetic; see oracle_set_variant)."""
+    load().oracle_set_variant(int(v))

@@ -1,9 +1,12 @@
 // main.cpp -- bin/treesa_gpu: the MI355X drop-in for the reference's treesa_gpu binary.
 //
-// Same command line (csrc/treesa_gpu.cu:1279-1406), same instance / tree / betas files, same JSON result
-// (csrc/treesa_gpu.cu:1896-1920) and exit codes (0 ok, 1 usage / input / device error, 2 invalid final
-// tree, 3 failed --check), so treesa_gpu/driver.py runs it through TREESA_GPU_BINARY unchanged.  The level
-// loop (csrc/treesa_gpu.cu:1756-1933) runs here on the host; every device step goes through the C ABI of
+// The interface is the reference's: its flags (tsa_cli.cpp), instance / tree / betas files (tsa_host.cpp),
+// JSON result keys and trace columns (csrc/treesa_gpu.cu:1896-1920) and exit codes (0 ok, 1 usage, input or
+// device error, 2 invalid final tree, 3 failed --check), so treesa_gpu/driver.py runs it through
+// TREESA_GPU_BINARY unchanged.  The level loop (csrc/treesa_gpu.cu:1756-1933) is organised here as a
+// schedule of levels driven by one of two loops: with independent chains in one energy mode the device
+// selects the best chain itself and the host only enqueues; otherwise the host evaluates every selected
+// level, keeps the incumbent and runs the population step.  Every device step goes through the C ABI of
 // libtreesa_hip.so (include/treesa_hip.h).
 #include <algorithm>
 #include <chrono>
@@ -11,715 +14,736 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
-#include <numeric>
+#include <memory>
+#include <new>
 #include <random>
 #include <string>
 #include <vector>
 
 #include "treesa_hip.h"
-#include <new>
+#include "tsa_cli.h"
 #include "tsa_host.h"
-#include "tsa_select.h"
-
-// Page-locked host memory from the library: device-to-host copies of chain records into it run at the link's
-// full speed (the best record of a 64 x 64 lattice chain is 4 MB).
-template <typename T>
-struct PinnedAlloc {
-  using value_type = T;
-  PinnedAlloc() = default;
-  template <typename U>
-  PinnedAlloc(const PinnedAlloc<U>&) {}
-  T* allocate(size_t n) {
-    void* p = tsa_host_alloc(n * sizeof(T));
-    if (!p) throw std::bad_alloc();
-    return static_cast<T*>(p);
-  }
-  void deallocate(T* p, size_t) { tsa_host_free(p); }
-  bool operator==(const PinnedAlloc&) const { return true; }
-  bool operator!=(const PinnedAlloc&) const { return false; }
-};
-using PinnedRecord = std::vector<uint64_t, PinnedAlloc<uint64_t>>;
 
 using namespace tsa;
 
 namespace {
 
-struct Opts {
-  std::string inst, tree, out, kernel = "auto", scheme = "indep", betas = "0.01:0.05:15", order = "par";
-  std::string betas2, init_slices, init = "tree";
-  int spectral_k = 4, greedy_repeat = 10;
-  int niters2 = -1;
-  int nchains = 1024, niters = 50, block = 0, wpb = 0, lpc = 32, eval_every = 1, ref_chains = 8, mode = 0;
-  bool check = false, quiet = false, cross = true, wide = false, slicing = false, no_sum = false, force_sum = false;
-  bool select_sc = false, no_overlap = false;
-  int slice_moves = 1, slice_every = 1, max_slices = 0, random_slices = 0;
-  int coop_max = 0, coop_min_units = -1, coop_min = 1, coop_full = 0, coop_cpl = 2, par_follow = 0, par_band = 0, wpc = 0, wide_wgs = 0, wide_lanes = 0;
-  double sc_target = 20.0, sc_weight = 1.0, trunc_frac = 0.25;
-  uint64_t seed = 1;
-  ModelConsts mc;
-  int mode2 = 1;
-  int max_levels = -1;
-  int bench_warmup = 0;  // untimed levels before the level loop (then the population is re-uploaded)
-  bool host_select = false;  // select on the host every level even for indep runs
+double wall_seconds() {
+  return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+// An error from the device library; the binary prints it and exits 1.
+struct DeviceError : std::runtime_error {
+  using std::runtime_error::runtime_error;
 };
 
-double now_s() { return std::chrono::duration<double>(std::chrono::steady_clock::now().time_since_epoch()).count(); }
-
-std::string jnum(double x) {
-  if (!std::isfinite(x)) return "null";
-  char b[64];
-  snprintf(b, sizeof b, "%.6e", x);
-  return b;
-}
-
-[[noreturn]] void usage() {
-  fprintf(stderr,
-          "usage: treesa_gpu -i instance.txt [--tree init_tree.txt] [--nchains N] [--niters K]\n"
-          "  [--betas a:step:b | --betas file:PATH | --betas b1,b2,..] [--mode tc|gpu|h100]\n"
-          "  [--gm peak,bw,m0,n0,k0,launch] [--h100-model launch,perm_bw,cc_bit,cc_cell,tc_bit,tc_pad,tc_out,small_rank,small_cell]\n"
-          "  [--stage2-betas SPEC [--stage2-niters K] [--stage2-mode gpu|h100]]  (continue the population)\n"
-          "  [--sc-target x] [--sc-weight y] [--scheme indep|pa|trunc] [--trunc-frac f]\n"
-          "  [--slicing [--slice-moves k] [--slice-every s] [--max-slices n] [--init-slices l1,l2,..]]\n"
-          "  [--order par|preorder] [--kernel auto|seq|seqsm|warp|warpsm|block|par [--wpc n]] [--lpc 32|16|8] [--coop-max G] [--coop-min G0] [--coop-full G1] [--par-follow] [--par-band L] [--coop-min-units u] [--wide] [--sums|--no-sum] [--select-sc] [--block B] [--wpb W] [--seed s] [--wide-wgs K] [--wide-lanes G]\n"
-          "  [--eval-every k] [--out result.json] [--check [--ref-chains R] [--random-slices k]] [--quiet]\n"
-          "  [--bench-warmup W]  (W untimed levels first, then the initial population again)\n"
-          "  [--host-select]  (select the best chain on the host at every level, also for --scheme indep)\n"
-          "  [--no-overlap]  (device-side selection on the sweep's stream, not beside the next sweep)\n"
-          "  [--init tree|spectral|greedy [--spectral-k K] [--greedy-repeat R]]  (start trees made natively when no --tree\n"
-          "   is given: the K best spectral path trees, chain c from tree c %% K, or the best of R greedy runs)\n");
-  exit(1);
-}
-
-[[noreturn]] void die(const std::string& msg, int code = 1) {
-  fprintf(stderr, "%s\n", msg.c_str());
-  exit(code);
-}
-
-Opts parse(int argc, char** argv) {
-  Opts o;
-  try {
-    for (int i = 1; i < argc; i++) {
-      const std::string a = argv[i];
-      auto nx = [&]() -> std::string {
-        if (i + 1 >= argc) usage();
-        return argv[++i];
-      };
-      if (a == "-i") o.inst = nx();
-      else if (a == "--tree") o.tree = nx();
-      else if (a == "--init") {
-        o.init = nx();
-        if (o.init != "tree" && o.init != "spectral" && o.init != "greedy") usage();
-      } else if (a == "--spectral-k") o.spectral_k = std::stoi(nx());
-      else if (a == "--greedy-repeat") o.greedy_repeat = std::stoi(nx());
-      else if (a == "--out") o.out = nx();
-      else if (a == "--nchains") o.nchains = std::stoi(nx());
-      else if (a == "--niters") o.niters = std::stoi(nx());
-      else if (a == "--betas") o.betas = nx();
-      else if (a == "--stage2-betas") o.betas2 = nx();
-      else if (a == "--stage2-niters") o.niters2 = std::stoi(nx());
-      else if (a == "--mode") {
-        const std::string s = nx();
-        o.mode = (s == "gpu") ? 1 : (s == "h100" || s == "gpu2") ? 2 : 0;
-      } else if (a == "--stage2-mode") {
-        const std::string s = nx();
-        o.mode2 = (s == "h100" || s == "gpu2") ? 2 : 1;
-      } else if (a == "--h100-model" || a == "--gm2") {
-        const std::string s = nx();
-        double* h = o.mc.h100;
-        if (sscanf(s.c_str(), "%lf,%lf,%lf,%lf,%lf,%lf,%lf,%lf,%lf", &h[0], &h[1], &h[2], &h[3], &h[4], &h[5], &h[6],
-                   &h[7], &h[8]) != 9)
-          usage();
-      } else if (a == "--sc-target") o.sc_target = std::stod(nx());
-      else if (a == "--sc-weight") o.sc_weight = std::stod(nx());
-      else if (a == "--scheme") o.scheme = nx();
-      else if (a == "--trunc-frac") o.trunc_frac = std::stod(nx());
-      else if (a == "--kernel") o.kernel = nx();
-      else if (a == "--order") o.order = nx();
-      else if (a == "--block") o.block = std::stoi(nx());
-      else if (a == "--wpb") o.wpb = std::stoi(nx());
-      else if (a == "--lpc") o.lpc = std::stoi(nx());
-      else if (a == "--seed") o.seed = std::stoull(nx());
-      else if (a == "--eval-every") o.eval_every = std::stoi(nx());
-      else if (a == "--ref-chains") o.ref_chains = std::stoi(nx());
-      else if (a == "--max-levels") o.max_levels = std::stoi(nx());
-      else if (a == "--bench-warmup") o.bench_warmup = std::stoi(nx());
-      else if (a == "--host-select") o.host_select = true;
-      else if (a == "--slicing") o.slicing = true;
-      else if (a == "--slice-moves") o.slice_moves = std::stoi(nx());
-      else if (a == "--slice-every") o.slice_every = std::stoi(nx());
-      else if (a == "--max-slices") o.max_slices = std::stoi(nx());
-      else if (a == "--init-slices") {
-        o.init_slices = nx();
-        o.slicing = true;
-      } else if (a == "--random-slices") {
-        o.random_slices = std::stoi(nx());
-        o.slicing = true;
-      } else if (a == "--coop-max") o.coop_max = std::stoi(nx());
-      else if (a == "--coop-min-units") o.coop_min_units = std::stoi(nx());
-      else if (a == "--coop-min") o.coop_min = std::stoi(nx());
-      else if (a == "--coop-full") o.coop_full = std::stoi(nx());
-      else if (a == "--coop-chunks") o.coop_cpl = std::max(1, std::stoi(nx()));
-      else if (a == "--par-follow") o.par_follow = 1;
-      else if (a == "--par-band") o.par_band = std::stoi(nx());
-      else if (a == "--wpc") o.wpc = std::stoi(nx());
-      else if (a == "--wide-wgs") o.wide_wgs = std::stoi(nx());
-      else if (a == "--wide-lanes") o.wide_lanes = std::stoi(nx());
-      else if (a == "--wide") o.wide = true;
-      else if (a == "--no-sum") o.no_sum = true;
-      else if (a == "--select-sc") o.select_sc = true;
-      else if (a == "--no-overlap") o.no_overlap = true;
-      else if (a == "--sums") o.force_sum = true;
-      else if (a == "--check") o.check = true;
-      else if (a == "--no-cross") o.cross = false;
-      else if (a == "--quiet") o.quiet = true;
-      else if (a == "--gm") {
-        const std::string s = nx();
-        double* g = o.mc.gm;
-        if (sscanf(s.c_str(), "%lf,%lf,%lf,%lf,%lf,%lf", &g[0], &g[1], &g[2], &g[3], &g[4], &g[5]) != 6) usage();
-      } else usage();
-    }
-  } catch (const std::logic_error&) {  // std::stoi / std::stod on a malformed number
-    usage();
+// Page-locked host memory from the library, so that copies of chain records into it run at the link's speed
+// (the best record of a 64 x 64 lattice chain is 4 MB).
+struct PinnedWords {
+  uint64_t* p = nullptr;
+  size_t n = 0;
+  explicit PinnedWords(size_t words) : n(words) {
+    p = static_cast<uint64_t*>(tsa_host_alloc(words * 8));
+    if (!p) throw std::bad_alloc();
+    std::memset(p, 0, words * 8);
   }
-  if (o.inst.empty()) usage();
-  return o;
-}
+  ~PinnedWords() { tsa_host_free(p); }
+  PinnedWords(const PinnedWords&) = delete;
+  PinnedWords& operator=(const PinnedWords&) = delete;
+};
 
-class Runner {
+// One device context (tsa_ctx) with every call checked.
+class Device {
  public:
-  std::vector<std::vector<uint32_t>> trees_;
-  std::vector<double> init_tcs;  // tc of each start tree made by --init spectral / greedy
-  double t_trees = 0.0;
-  bool have_trees = false;
-  Runner(const Inst& I, const Opts& O) : I(I), O(O) {
-    if (tsa_layout(I.m, I.nlab, O.wide ? 1 : 0, &lay) != TSA_OK) die(tsa_last_error(nullptr));
-    G = Geometry{lay.W, lay.ch_off, lay.s_off, lay.chain_words};
-    leaf = leaf_sets(I, lay.W);
-    lsc = leaf_sc(I);
-    ML = model_log2(O.mc);
-    mode = O.mode;
-    if (O.order != "par" && O.order != "preorder") die("--order par|preorder");
-    // order "par" (default) runs the par kernel; an explicit --kernel other than auto/par means the
-    // pre-order sweep (csrc/treesa_gpu.cu:1480-1483)
-    kernel = O.kernel;
-    if (kernel == "auto" && O.order == "par" && O.lpc == 32) kernel = "par";
-    const bool known = kernel == "auto" || kernel == "par" || kernel == "seq" || kernel == "seqsm" ||
-                       kernel == "warp" || kernel == "warpsm" || kernel == "block";
-    if (!known) die("unknown --kernel " + kernel);
-    order = kernel == "par" ? TSA_ORDER_PAR : TSA_ORDER_PREORDER;
-    if (O.par_band == 1 || O.par_band > 16 || O.par_band < 0) die("--par-band L: 0 (off) or 2..16");
-    const int slice_moves = (O.slicing && O.random_slices == 0) ? O.slice_moves : 0;
-    if (slice_moves > 0 && (kernel == "seq" || kernel == "seqsm" || O.lpc != 32))
-      die("slice moves need the warp kernels with --lpc 32");
-    if (O.nchains < 1) die("--nchains must be at least 1");
-    memset(&cfg, 0, sizeof cfg);
-    cfg.mode = mode;
-    cfg.sc_target = (float)O.sc_target;
-    cfg.sc_weight = (float)O.sc_weight;
-    const uint64_t k = splitmix64(O.seed);
-    cfg.key0 = (uint32_t)k;
-    cfg.key1 = (uint32_t)(k >> 32);
-    cfg.slicing = O.slicing ? 1 : 0;
-    cfg.slice_moves = slice_moves;
-    cfg.slice_every = std::max(1, O.slice_every);
-    cfg.max_slices = O.max_slices > 0 ? O.max_slices : I.nlab;
-    cfg.par_follow = O.par_follow;
-    cfg.par_band = O.par_band;
-    cfg.kernel = (kernel == "warpsm" || kernel == "seqsm") ? TSA_KERNEL_LDS
-                 : (kernel == "warp" || kernel == "seq" || kernel == "block") ? TSA_KERNEL_GLOBAL
-                                                                               : TSA_KERNEL_AUTO;
-    cfg.lpeak = ML.lpeak;
-    cfg.lbw = ML.lbw;
-    cfg.llaunch = ML.llaunch;
-    cfg.m0 = ML.m0;
-    cfg.n0 = ML.n0;
-    cfg.k0 = ML.k0;
-    cfg.v2_l3launch = ML.v2_l3launch;
-    cfg.v2_lperm2 = ML.v2_lperm2;
-    cfg.v2_lcc_bit = ML.v2_lcc_bit;
-    cfg.v2_lcc_cell = ML.v2_lcc_cell;
-    cfg.v2_ltc_bit = ML.v2_ltc_bit;
-    cfg.v2_ltc_pad = ML.v2_ltc_pad;
-    cfg.v2_ltc_out = ML.v2_ltc_out;
-    cfg.v2_lsmall_cell = ML.v2_lsmall_cell;
-    cfg.v2_small_rank = ML.v2_small_rank;
-    cfg.wide_waves = O.wpc > 0 ? (O.wpc + 1) / 2 : 0;  // --wpc counts 32-lane warps
-    cfg.wide_wgs = O.wide_wgs;
-    cfg.wide_lanes = O.wide_lanes;
-    cfg.fused_energy = O.eval_every == 1 ? 1 : 0;  // every level is evaluated: the sweep kernel evaluates too
-    cfg.sums = O.no_sum ? -1 : (O.force_sum ? 1 : 0);
-    cfg.track_overlap = O.no_overlap ? -1 : 0;
-  }
-  ~Runner() {
-    if (ctx) tsa_destroy(ctx);
-  }
-
-  int run_anneal();
-  int run_check();
-
- private:
-  const Inst& I;
-  const Opts& O;
-  tsa_layout_t lay{};
-  tsa_config_t cfg{};
-  Geometry G{};
-  tsa_ctx* ctx = nullptr;
-  std::vector<uint64_t> leaf;
-  int lsc = 0;
-  ModelLog2 ML{};
-  int mode = 0;
-  std::string kernel;
-  int order = TSA_ORDER_PAR;
-  double kernel_ms = 0;
-
-  void ck(int rc) {
-    if (rc != TSA_OK) die(std::string("treesa_hip: ") + tsa_last_error(ctx));
-  }
-  void create(tsa_ctx** c, int kflag) {
-    tsa_config_t c2 = cfg;
-    c2.kernel = kflag;
-    if (tsa_create(&lay, leaf.data(), lsc, &c2, O.nchains, c) != TSA_OK) {
+  Device(const tsa_layout_t& lay, const std::vector<uint64_t>& leaf, int leaf_sc, const tsa_config_t& cfg,
+         int nchains) {
+    if (tsa_create(&lay, leaf.data(), leaf_sc, &cfg, nchains, &ctx_) != TSA_OK) {
       const std::string msg = tsa_last_error(nullptr);
       if (msg.find("fit") != std::string::npos)
-        die("chains do not fit in shared memory (try --kernel warp / --lpc 32)");
-      die("treesa_hip: " + msg);
+        throw DeviceError("chains do not fit in shared memory (try --kernel warp / --lpc 32)");
+      throw DeviceError("treesa_hip: " + msg);
     }
   }
-  // start trees: the --tree file, else (--init spectral / greedy) made once here on the host
-  const std::vector<std::vector<uint32_t>>& start_trees() {
-    if (have_trees) return trees_;
-    const double t = now_s();
-    if (!O.tree.empty()) trees_ = read_trees(O.tree, I.m);
-    else if (O.init == "spectral") {
-      for (const SpectralOrder& so : spectral_orders(I, std::max(1, O.spectral_k), 24, 24, O.seed)) {
-        trees_.push_back(path_tree(so.order));
-        init_tcs.push_back(so.tc);
-      }
-    } else if (O.init == "greedy") {
-      double tc = 0.0;
-      trees_.push_back(greedy_tree(I, std::max(1, O.greedy_repeat), O.seed, &tc));
-      init_tcs.push_back(tc);
-    }
-    t_trees = now_s() - t;
-    have_trees = true;
-    return trees_;
+  ~Device() { tsa_destroy(ctx_); }
+  Device(const Device&) = delete;
+  Device& operator=(const Device&) = delete;
+  tsa_ctx* get() const { return ctx_; }
+  void ok(int rc) const {
+    if (rc != TSA_OK) throw DeviceError(std::string("treesa_hip: ") + tsa_last_error(ctx_));
   }
-  std::vector<uint64_t> init_population() {
-    const std::vector<std::vector<uint32_t>>& trees = start_trees();
-    std::vector<uint64_t> S0(lay.W, 0);
-    if (!O.init_slices.empty()) {
-      const char* p = O.init_slices.c_str();
-      while (*p) {
-        char* q;
-        const long l = strtol(p, &q, 10);
-        if (q == p) break;
-        if (l < 0 || l >= I.nlab) die("bad --init-slices label");
-        S0[l >> 6] |= 1ull << (l & 63);
-        p = q;
-        while (*p == ',' || *p == ' ') p++;
-      }
-    }
-    std::vector<uint64_t> pop;
-    build_population(I, G, trees, O.nchains, O.seed, S0, O.random_slices, pop);
-    return pop;
-  }
-  const uint64_t* chS(const uint64_t* base) const { return O.slicing ? base + lay.s_off : nullptr; }
-  const uint32_t* chCh(const uint64_t* base) const { return reinterpret_cast<const uint32_t*>(base + lay.ch_off); }
-
-  // Selection score and population energy (tsa_select.h, the same functions the device-side tracking
-  // evaluates).
-  TsaSelect select_params() const {
-    TsaSelect S;
-    S.mode = mode;
-    S.slicing = O.slicing ? 1 : 0;
-    S.select_sc = O.select_sc ? 1 : 0;
-    S.sc_target = O.sc_target;
-    S.sc_weight = O.sc_weight;
-    return S;
-  }
-  double score(float lc, int sc, int ns) const { return tsa_score(lc, sc, ns, select_params()); }
-  double energyE(float lc, int sc, int ns) const { return tsa_energyE(lc, sc, ns, select_params()); }
-  int run_levels_tracked(const std::vector<float>& betas, const std::vector<int>& lniters, uint32_t& sweep_ctr,
-                         PinnedRecord& best, std::string& trace, double t0);
-  void resample(const std::vector<int>& anc, std::vector<int>& family) {
-    ck(tsa_resample(ctx, anc.data()));
-    std::vector<int> nfm(O.nchains);
-    for (int c = 0; c < O.nchains; c++) nfm[c] = family[anc[c]];
-    family.swap(nfm);
-  }
-  std::string kernel_name() const {
-    if (order == TSA_ORDER_PAR) return "par";
+  std::string describe() const {
     char b[256] = {0};
-    tsa_describe(ctx, b, sizeof b);
-    return strncmp(b, "lds", 3) == 0 ? "warpsm" : "warp";
+    tsa_describe(ctx_, b, sizeof b);
+    return b;
   }
+  double take_kernel_ms() const {
+    double ms = 0;
+    ok(tsa_sweeps_ms(ctx_, &ms));
+    return ms;
+  }
+  void counters(uint64_t st[7], uint64_t chunks[2]) const {
+    ok(tsa_stats(ctx_, st));
+    ok(tsa_chunk_stats(ctx_, chunks));
+  }
+
+ private:
+  tsa_ctx* ctx_ = nullptr;
 };
 
-// The level loop of an indep run with device-side selection: every level enqueues its sweeps and, at
-// evaluated levels, the energy and selection kernels; the host waits once at the end.  The selected chain,
-// the trace rows and the kernel time are those of the synchronous loop below (same score function, same
-// first-chain / first-level tie rule); only the trace's time column comes from the device clock.
-int Runner::run_levels_tracked(const std::vector<float>& betas, const std::vector<int>& lniters, uint32_t& sweep_ctr,
-                               PinnedRecord& best, std::string& trace, double t0) {
-  const TsaSelect S = select_params();
-  tsa_select_t sel;
-  sel.mode = S.mode;
-  sel.slicing = S.slicing;
-  sel.select_sc = S.select_sc;
-  sel.sc_target = S.sc_target;
-  sel.sc_weight = S.sc_weight;
-  const int nlev = (int)betas.size();
-  ck(tsa_track_begin(ctx, &sel, nlev));
-  std::vector<char> evaluated(nlev, 0);
-  for (int lev = 0; lev < nlev; lev++) {
-    ck(tsa_sweeps(ctx, order, betas[lev], sweep_ctr, lniters[lev]));
-    sweep_ctr += (uint32_t)lniters[lev];
-    const bool last = lev + 1 == nlev;
-    if (lev % O.eval_every == O.eval_every - 1 || last) {
-      ck(tsa_track(ctx, lev));
+// One β level of the schedule: its inverse temperature, energy mode and sweeps.
+struct Level {
+  float beta;
+  int mode;
+  int niters;
+};
+
+// A chain's energies at an evaluated level.
+struct Energies {
+  std::vector<float> lc;
+  std::vector<int32_t> sc, ns;
+  explicit Energies(int n) : lc(n), sc(n), ns(n) {}
+};
+
+// Small JSON writer: keys in insertion order, numbers in the reference's printed precision.
+class Json {
+ public:
+  void key(const char* k) {
+    out_ += first_ ? "{\"" : ",\n \"";
+    out_ += k;
+    out_ += "\": ";
+    first_ = false;
+  }
+  void fixed6(const char* k, double v) { put(k, "%.6f", v); }
+  // times in seconds: %.6e, non-finite values as null (csrc/treesa_gpu.cu:70-76)
+  void sci6(const char* k, double v) {
+    if (std::isfinite(v)) put(k, "%.6e", v);
+    else raw(k, "null");
+  }
+  void integer(const char* k, long long v) { put(k, "%lld", v); }
+  void boolean(const char* k, bool v) { raw(k, v ? "true" : "false"); }
+  void text(const char* k, const std::string& v) { raw(k, "\"" + v + "\""); }
+  void raw(const char* k, const std::string& v) {
+    key(k);
+    out_ += v;
+  }
+  std::string finish() { return out_ + "}\n"; }
+
+ private:
+  template <typename T>
+  void put(const char* k, const char* fmt, T v) {
+    char b[64];
+    snprintf(b, sizeof b, fmt, v);
+    raw(k, b);
+  }
+  std::string out_;
+  bool first_ = true;
+};
+
+// Widths as the reference reports them (32-bit words): its register template width (0 on the wide path) and
+// its words per label set (csrc/treesa_gpu.cu:1439, 2078-2085).
+void reference_widths(int nlab, bool wide, int* W32, int* nw32) {
+  const int w = (nlab + 31) / 32;
+  if (wide || w > 16) {
+    *W32 = 0;
+    *nw32 = (w + 3) & ~3;
+    return;
+  }
+  *W32 = w <= 1 ? 1 : w <= 2 ? 2 : w <= 4 ? 4 : w <= 8 ? 8 : w <= 12 ? 12 : 16;
+  *nw32 = *W32;
+}
+
+class Run {
+ public:
+  Run(const Network& N, const Options& O) : N_(N), O_(O) {
+    if (tsa_layout(N.m, N.nlab, O.wide ? 1 : 0, &lay_) != TSA_OK) throw DeviceError(tsa_last_error(nullptr));
+    geo_ = Geometry{lay_.W, lay_.ch_off, lay_.s_off, lay_.chain_words};
+    leaf_ = leaf_sets(N, lay_.W);
+    model_ = model_log2(O.model);
+    resolve_kernel();
+    fill_config();
+  }
+  int anneal();
+  int check();
+
+ private:
+  const Network& N_;
+  const Options& O_;
+  tsa_layout_t lay_{};
+  Geometry geo_{};
+  tsa_config_t cfg_{};
+  std::vector<uint64_t> leaf_;
+  ModelLog2 model_{};
+  std::string kernel_;  // the reference's kernel name after its automatic choice
+  int order_ = TSA_ORDER_PAR;
+  std::unique_ptr<Device> dev_;
+  // start trees (built once)
+  std::vector<std::vector<uint32_t>> trees_;
+  std::vector<double> init_tcs_;
+  double t_trees_ = 0;
+  bool have_trees_ = false;
+  // level loop state
+  std::vector<Level> sched_;
+  int mode_ = 0;
+  double kernel_ms_ = 0;
+  std::string trace_;
+  FILE* level_log_ = nullptr;
+
+  void resolve_kernel();
+  void fill_config();
+  const std::vector<std::vector<uint32_t>>& start_trees();
+  std::vector<uint64_t> start_population();
+  void build_schedule();
+  Scoring scoring(int mode) const {
+    Scoring S;
+    S.mode = mode;
+    S.slicing = O_.slicing;
+    S.select_sc = O_.select_sc;
+    S.sc_target = O_.sc_target;
+    S.sc_weight = O_.sc_weight;
+    return S;
+  }
+  tsa_select_t device_scoring() const {
+    tsa_select_t s{};
+    s.mode = O_.mode;
+    s.slicing = O_.slicing ? 1 : 0;
+    s.select_sc = O_.select_sc ? 1 : 0;
+    s.sc_target = O_.sc_target;
+    s.sc_weight = O_.sc_weight;
+    return s;
+  }
+  bool evaluated_level(int lev) const {
+    const int n = (int)sched_.size();
+    const bool last = lev + 1 == n;
+    return last || lev % O_.eval_every == O_.eval_every - 1 || sched_[lev + 1].mode != sched_[lev].mode;
+  }
+  const uint32_t* children(const uint64_t* rec) const { return reinterpret_cast<const uint32_t*>(rec + lay_.ch_off); }
+  const uint64_t* slices(const uint64_t* rec) const { return O_.slicing ? rec + lay_.s_off : nullptr; }
+  void add_trace(double t, int lev, float lc, int sc, double meanE, int families, int ns, double meanNs);
+  void progress(int lev, float lc, int sc, int ns, double meanE, double meanNs, int families, double t) const;
+  void warm_up(const std::vector<uint64_t>& pop, uint64_t st0[7], uint64_t ch0[2]);
+  int loop_on_device(PinnedWords& best, double t0);
+  int loop_on_host(PinnedWords& best, double t0, HostEnergy& h1, bool& staged, int& nresample);
+  std::string kernel_label() const;
+};
+
+void Run::resolve_kernel() {
+  if (O_.order != "par" && O_.order != "preorder") throw InputError("--order par|preorder");
+  // par order runs the par kernel; an explicit --kernel other than auto / par, or lanes per chain other than
+  // 32, means the pre-order sweep (csrc/treesa_gpu.cu:1480-1483)
+  kernel_ = O_.kernel;
+  if (kernel_ == "auto" && O_.order == "par" && O_.lpc == 32) kernel_ = "par";
+  static const char* known[] = {"auto", "par", "seq", "seqsm", "warp", "warpsm", "block"};
+  if (std::none_of(std::begin(known), std::end(known), [&](const char* k) { return kernel_ == k; }))
+    throw InputError("unknown --kernel " + kernel_);
+  order_ = kernel_ == "par" ? TSA_ORDER_PAR : TSA_ORDER_PREORDER;
+  if (O_.par_band == 1 || O_.par_band > 16 || O_.par_band < 0) throw InputError("--par-band L: 0 (off) or 2..16");
+  const bool moves = O_.slicing && O_.random_slices == 0 && O_.slice_moves > 0;
+  if (moves && (kernel_ == "seq" || kernel_ == "seqsm" || O_.lpc != 32))
+    throw InputError("slice moves need the warp kernels with --lpc 32");
+  if (O_.nchains < 1) throw InputError("--nchains must be at least 1");
+  if (O_.eval_every < 1) throw InputError("--eval-every must be at least 1");
+  if (O_.scheme != "indep" && O_.scheme != "pa" && O_.scheme != "trunc") throw InputError("--scheme indep|pa|trunc");
+}
+
+void Run::fill_config() {
+  std::memset(&cfg_, 0, sizeof cfg_);
+  mode_ = O_.mode;
+  cfg_.mode = O_.mode;
+  cfg_.sc_target = (float)O_.sc_target;
+  cfg_.sc_weight = (float)O_.sc_weight;
+  const uint64_t key = splitmix64(O_.seed);  // Philox key (csrc/treesa_gpu.cu:1457-1459)
+  cfg_.key0 = (uint32_t)key;
+  cfg_.key1 = (uint32_t)(key >> 32);
+  cfg_.slicing = O_.slicing ? 1 : 0;
+  cfg_.slice_moves = (O_.slicing && O_.random_slices == 0) ? O_.slice_moves : 0;
+  cfg_.slice_every = std::max(1, O_.slice_every);
+  cfg_.max_slices = O_.max_slices > 0 ? O_.max_slices : N_.nlab;
+  cfg_.par_follow = O_.par_follow;
+  cfg_.par_band = O_.par_band;
+  cfg_.kernel = (kernel_ == "warpsm" || kernel_ == "seqsm")                       ? TSA_KERNEL_LDS
+                : (kernel_ == "warp" || kernel_ == "seq" || kernel_ == "block") ? TSA_KERNEL_GLOBAL
+                                                                                : TSA_KERNEL_AUTO;
+  cfg_.lpeak = model_.lpeak;
+  cfg_.lbw = model_.lbw;
+  cfg_.llaunch = model_.llaunch;
+  cfg_.m0 = model_.m0;
+  cfg_.n0 = model_.n0;
+  cfg_.k0 = model_.k0;
+  cfg_.v2_l3launch = model_.v2_l3launch;
+  cfg_.v2_lperm2 = model_.v2_lperm2;
+  cfg_.v2_lcc_bit = model_.v2_lcc_bit;
+  cfg_.v2_lcc_cell = model_.v2_lcc_cell;
+  cfg_.v2_ltc_bit = model_.v2_ltc_bit;
+  cfg_.v2_ltc_pad = model_.v2_ltc_pad;
+  cfg_.v2_ltc_out = model_.v2_ltc_out;
+  cfg_.v2_lsmall_cell = model_.v2_lsmall_cell;
+  cfg_.v2_small_rank = model_.v2_small_rank;
+  cfg_.wide_waves = O_.wpc > 0 ? (O_.wpc + 1) / 2 : 0;  // --wpc counts 32-lane warps
+  cfg_.wide_wgs = O_.wide_wgs;
+  cfg_.wide_lanes = O_.wide_lanes;
+  cfg_.fused_energy = O_.eval_every == 1 ? 1 : 0;  // every level evaluated: the sweep kernel evaluates too
+  cfg_.sums = O_.no_sum ? -1 : (O_.force_sum ? 1 : 0);
+  cfg_.track_overlap = O_.no_overlap ? -1 : 0;
+}
+
+const std::vector<std::vector<uint32_t>>& Run::start_trees() {
+  if (have_trees_) return trees_;
+  const double t = wall_seconds();
+  if (!O_.tree_file.empty()) {
+    trees_ = read_tree_file(O_.tree_file, N_.m);
+  } else if (O_.init == "spectral") {
+    for (const SpectralOrder& so : spectral_orders(N_, std::max(1, O_.spectral_k), 24, 24, O_.seed)) {
+      trees_.push_back(path_tree(so.order));
+      init_tcs_.push_back(so.tc);
+    }
+  } else if (O_.init == "greedy") {
+    double tc = 0;
+    trees_.push_back(greedy_tree(N_, std::max(1, O_.greedy_repeat), O_.seed, &tc));
+    init_tcs_.push_back(tc);
+  }
+  t_trees_ = wall_seconds() - t;
+  have_trees_ = true;
+  return trees_;
+}
+
+std::vector<uint64_t> Run::start_population() {
+  std::vector<uint64_t> S0(lay_.W, 0ull);
+  for (size_t p = 0; p < O_.init_slices.size();) {
+    char* e = nullptr;
+    const long l = strtol(O_.init_slices.c_str() + p, &e, 10);
+    const size_t q = (size_t)(e - O_.init_slices.c_str());
+    if (q == p) break;
+    if (l < 0 || l >= N_.nlab) throw InputError("bad --init-slices label");
+    S0[l >> 6] |= 1ull << (l & 63);
+    p = q;
+    while (p < O_.init_slices.size() && (O_.init_slices[p] == ',' || O_.init_slices[p] == ' ')) p++;
+  }
+  std::vector<uint64_t> pop;
+  build_population(N_, geo_, start_trees(), O_.nchains, O_.seed, S0, O_.random_slices, pop);
+  return pop;
+}
+
+void Run::build_schedule() {
+  std::vector<float> b = parse_schedule(O_.betas);
+  if (O_.max_levels > 0 && (int)b.size() > O_.max_levels) b.resize(O_.max_levels);
+  sched_.clear();
+  for (float x : b) sched_.push_back({x, O_.mode, O_.niters});
+  if (!O_.stage2_betas.empty())
+    for (float x : parse_schedule(O_.stage2_betas))
+      sched_.push_back({x, O_.stage2_mode, O_.stage2_niters > 0 ? O_.stage2_niters : O_.niters});
+}
+
+void Run::add_trace(double t, int lev, float lc, int sc, double meanE, int families, int ns, double meanNs) {
+  char b[320];
+  snprintf(b, sizeof b, "%s[%.4f,%d,%.4f,%.6f,%d,%.6f,%d,%d,%d,%.3f]", trace_.empty() ? "" : ",", t, lev,
+           (double)sched_[lev].beta, (double)lc, sc, meanE, families, mode_, ns, meanNs);
+  trace_ += b;
+}
+
+void Run::progress(int lev, float lc, int sc, int ns, double meanE, double meanNs, int families, double t) const {
+  if (O_.quiet || !(lev % 25 == 0 || lev + 1 == (int)sched_.size())) return;
+  fprintf(stderr, "[level %d/%zu] beta %.3f | best: lcost %.3f sc %d |S| %d | mean E %.3f mean |S| %.2f | families %d | %.2f s\n",
+          lev, sched_.size(), (double)sched_[lev].beta, (double)lc, sc, ns, meanE, meanNs, families, t);
+}
+
+// Untimed levels before the timed loop (clocks up, code objects loaded, the tracking buffers and the second
+// stream used once), then the start population again; the counters are read so that the run reports only the
+// timed levels.
+void Run::warm_up(const std::vector<uint64_t>& pop, uint64_t st0[7], uint64_t ch0[2]) {
+  tsa_ctx* c = dev_->get();
+  const int n = (int)sched_.size();
+  const bool track = O_.scheme == "indep" && O_.stage2_betas.empty() && !O_.host_select;
+  Energies e(O_.nchains);
+  if (track) {
+    const tsa_select_t s = device_scoring();
+    dev_->ok(tsa_track_begin(c, &s, n));
+  }
+  for (int k = 0; k < O_.bench_warmup; k++) {
+    const Level& L = sched_[k % n];
+    dev_->ok(tsa_sweeps(c, order_, L.beta, (uint32_t)k, L.niters));
+    if (track) dev_->ok(tsa_track(c, k % n));
+    dev_->ok(tsa_energy(c, e.lc.data(), e.sc.data(), e.ns.data()));
+  }
+  if (track) {
+    std::vector<uint64_t> rec(lay_.chain_words);
+    std::vector<tsa_trace_row_t> rows(n);
+    int32_t bc, bl;
+    double bs, hz;
+    uint64_t tk;
+    dev_->ok(tsa_track_end(c, &bc, &bl, &bs, rec.data(), rows.data(), &tk, &hz));
+  }
+  (void)dev_->take_kernel_ms();
+  dev_->ok(tsa_upload(c, pop.data()));
+  dev_->counters(st0, ch0);
+}
+
+// Independent chains in one energy mode: every level's sweeps and, at evaluated levels, the device's own
+// energy and selection kernels are enqueued; the host waits once, at the end.  The selection is the
+// reference's (lowest score, first chain and first level on ties); the trace's time column comes from the
+// device clock, scaled to the host's wall time of the loop.
+int Run::loop_on_device(PinnedWords& best, double t0) {
+  tsa_ctx* c = dev_->get();
+  const int n = (int)sched_.size();
+  const tsa_select_t s = device_scoring();
+  dev_->ok(tsa_track_begin(c, &s, n));
+  std::vector<char> evaluated(n, 0);
+  uint32_t sweep = 0;
+  for (int lev = 0; lev < n; lev++) {
+    dev_->ok(tsa_sweeps(c, order_, sched_[lev].beta, sweep, sched_[lev].niters));
+    sweep += (uint32_t)sched_[lev].niters;
+    if (evaluated_level(lev)) {
+      dev_->ok(tsa_track(c, lev));
       evaluated[lev] = 1;
     }
   }
-  double ms = 0;
-  ck(tsa_sweeps_ms(ctx, &ms));
-  kernel_ms += ms;
-  std::vector<tsa_trace_row_t> rows(nlev);
-  int32_t bc = -1, bl = -1;
-  double bs = 0, hz = 1;
+  kernel_ms_ += dev_->take_kernel_ms();
+  std::vector<tsa_trace_row_t> rows(n);
+  int32_t best_chain = -1, best_level = -1;
+  double best_score = 0, hz = 1;
   uint64_t tk0 = 0;
-  ck(tsa_track_end(ctx, &bc, &bl, &bs, best.data(), rows.data(), &tk0, &hz));
-  const double t_dev0 = now_s() - t0;  // the level loop has finished; device times are scaled to it
-  const double span = std::max(1.0, (double)(rows[nlev - 1].ticks - tk0));
-  for (int lev = 0; lev < nlev; lev++) {
+  dev_->ok(tsa_track_end(c, &best_chain, &best_level, &best_score, best.p, rows.data(), &tk0, &hz));
+  const double wall = wall_seconds() - t0;
+  const double span = std::max(1.0, (double)(rows[n - 1].ticks - tk0));
+  for (int lev = 0; lev < n; lev++) {
     if (!evaluated[lev]) continue;
     const tsa_trace_row_t& r = rows[lev];
-    const double t = t_dev0 * (double)(r.ticks - tk0) / span;
-    char buf[320];
-    snprintf(buf, sizeof buf, "%s[%.4f,%d,%.4f,%.6f,%d,%.6f,%d,%d,%d,%.3f]", trace.empty() ? "" : ",", t, lev,
-             betas[lev], (double)r.lc, r.sc, r.meanE, O.nchains, mode, r.ns, r.meanNs);
-    trace += buf;
-    if (!O.quiet && (lev % 25 == 0 || lev + 1 == nlev))
-      fprintf(stderr, "lev %4d beta %7.3f  best(l2cost/slice %.3f sc %d |S| %d)  meanE %.3f  mean|S| %.2f  families %d  t=%.2fs\n",
-              lev, betas[lev], (double)r.lc, r.sc, r.ns, r.meanE, r.meanNs, O.nchains, t);
+    const double t = wall * (double)(r.ticks - tk0) / span;
+    add_trace(t, lev, r.lc, r.sc, r.meanE, O_.nchains, r.ns, r.meanNs);
+    progress(lev, r.lc, r.sc, r.ns, r.meanE, r.meanNs, O_.nchains, t);
+    if (level_log_) {
+      uint32_t bits;
+      std::memcpy(&bits, &r.lc, 4);
+      fprintf(level_log_,
+              "{\"level\": %d, \"best\": %d, \"score\": %.17g, \"lc_bits\": %u, \"sc\": %d, \"ns\": %d, "
+              "\"families\": %d, \"meanE\": %.17g, \"resampled\": false}\n",
+              lev, r.chain, r.score, bits, r.sc, r.ns, O_.nchains, r.meanE);
+    }
   }
-  (void)hz;
-  return bc;
+  return best_chain;
 }
 
-int Runner::run_anneal() {
-  std::vector<float> betas = parse_betas(O.betas);
-  if (O.max_levels > 0 && (int)betas.size() > O.max_levels) betas.resize(O.max_levels);
-  std::vector<int> lmode(betas.size(), O.mode), lniters(betas.size(), O.niters);
-  if (!O.betas2.empty()) {
-    for (float b : parse_betas(O.betas2)) {
-      betas.push_back(b);
-      lmode.push_back(O.mode2);
-      lniters.push_back(O.niters2 > 0 ? O.niters2 : O.niters);
-    }
-  }
-  HostEnergy H1;
-  bool staged = false;
-  uint32_t sweep_ctr = 0;
-  const double t_start = now_s();
-  uint64_t stats0[7] = {0, 0, 0, 0, 0, 0, 0}, chunks0[2] = {0, 0};
-  {
-    const std::vector<uint64_t> pop = init_population();  // input errors surface before the device is touched
-    create(&ctx, cfg.kernel);
-    ck(tsa_upload(ctx, pop.data()));
-    if (O.bench_warmup > 0 && !betas.empty()) {
-      // untimed warm-up levels (clocks, code objects, the tracking buffers of the level loop), then the same
-      // initial population again
-      std::vector<float> l(O.nchains);
-      std::vector<int> s(O.nchains), n(O.nchains);
-      const bool track = O.scheme == "indep" && O.betas2.empty() && !O.host_select;
-      tsa_select_t sel{};
-      if (track) {
-        const TsaSelect S = select_params();
-        sel.mode = S.mode;
-        sel.slicing = S.slicing;
-        sel.select_sc = S.select_sc;
-        sel.sc_target = S.sc_target;
-        sel.sc_weight = S.sc_weight;
-        ck(tsa_track_begin(ctx, &sel, (int)betas.size()));
-      }
-      for (int k = 0; k < O.bench_warmup; k++) {
-        ck(tsa_sweeps(ctx, order, betas[k % betas.size()], (uint32_t)k, lniters[k % betas.size()]));
-        if (track) ck(tsa_track(ctx, k % (int)betas.size()));
-        ck(tsa_energy(ctx, l.data(), s.data(), n.data()));
-      }
-      if (track) {  // the end of a tracked loop too (first use of its copies and of the second stream)
-        std::vector<uint64_t> rec(lay.chain_words);
-        std::vector<tsa_trace_row_t> rows(betas.size());
-        int32_t bc = -1, bl = -1;
-        double bs = 0, hz = 0;
-        uint64_t tk = 0;
-        ck(tsa_track_end(ctx, &bc, &bl, &bs, rec.data(), rows.data(), &tk, &hz));
-      }
-      double ms = 0;
-      ck(tsa_sweeps_ms(ctx, &ms));
-      ck(tsa_upload(ctx, pop.data()));
-      ck(tsa_stats(ctx, stats0));
-      ck(tsa_chunk_stats(ctx, chunks0));
-    }
-  }
-  PinnedRecord best(lay.chain_words, 0);  // allocated (and its pages touched) before the clock starts
-  const double t_init = now_s() - t_start;
-  const double t0 = now_s();
-  const int nc = O.nchains;
-  std::vector<float> lc(nc);
-  std::vector<int> sc(nc), ns(nc);
-  std::vector<double> E(nc);  // energyE of every chain at the last evaluated level
-  double best_score = INFINITY;
+// The host-side loop (population schemes, two-stage runs, --host-select): at every evaluated level the host
+// reads every chain's energies, selects, writes the trace row and, between levels of one energy mode, runs the
+// population step.
+int Run::loop_on_host(PinnedWords& best, double t0, HostEnergy& h1, bool& staged, int& nresample) {
+  tsa_ctx* c = dev_->get();
+  const int n = (int)sched_.size(), nc = O_.nchains;
+  Energies e(nc);
+  std::vector<double> E(nc);
+  std::vector<int> family(nc), mark(nc);
+  for (int k = 0; k < nc; k++) family[k] = k;
+  std::mt19937_64 pa_rng(splitmix64(O_.seed + 777));  // the uniforms of systematic resampling
+  float beta_resampled = n > 0 ? sched_[0].beta : 0.f;  // β of the population's last reweighting
+  double incumbent = INFINITY;
   int best_chain = -1;
-  std::vector<int> family(nc), nfam(nc);
-  std::iota(family.begin(), family.end(), 0);
-  std::string trace;
-  std::mt19937_64 hrng(splitmix64(O.seed + 777));
-  float beta_last_resample = betas.empty() ? 0.f : betas[0];
-  int nresample = 0;
-  // independent chains in one energy mode: selection runs on the device, no host round trip per level
-  const bool tracked = O.scheme == "indep" && O.betas2.empty() && !betas.empty() && !O.host_select;
-  if (tracked) best_chain = run_levels_tracked(betas, lniters, sweep_ctr, best, trace, t0);
-  for (size_t lev = 0; lev < (tracked ? 0 : betas.size()); lev++) {
-    if (lmode[lev] != mode) {
-      // stage switch: the stage-1 best stays the incumbent, scored in the new energy
-      H1 = host_energy(I, lay.W, ML, best.data(), chCh(best.data()), leaf, chS(best.data()));
+  uint32_t sweep = 0;
+  for (int lev = 0; lev < n; lev++) {
+    const Level& L = sched_[lev];
+    if (L.mode != mode_) {
+      // stage switch: the stage-1 incumbent stays, scored in the new energy by its host double energy
+      h1 = host_energy(N_, lay_.W, model_, best.p, children(best.p), leaf_, slices(best.p));
       staged = true;
-      mode = lmode[lev];
-      ck(tsa_set_mode(ctx, mode));
-      best_score = score((float)std::log2(mode == 1 ? H1.time : H1.time2), H1.sc, H1.ns);
-      beta_last_resample = betas[lev];
+      mode_ = L.mode;
+      dev_->ok(tsa_set_mode(c, mode_));
+      incumbent = selection_score(scoring(mode_), (float)std::log2(mode_ == 1 ? h1.time : h1.time2), h1.sc, h1.ns);
+      beta_resampled = L.beta;
     }
-    ck(tsa_sweeps(ctx, order, betas[lev], sweep_ctr, lniters[lev]));
-    sweep_ctr += (uint32_t)lniters[lev];
-    const bool last = lev + 1 == betas.size();
-    const bool switching = !last && lmode[lev + 1] != mode;
-    if ((int)(lev % O.eval_every) == O.eval_every - 1 || last || switching) {
-      ck(tsa_energy(ctx, lc.data(), sc.data(), ns.data()));
-      double ms = 0;
-      ck(tsa_sweeps_ms(ctx, &ms));
-      kernel_ms += ms;
-      int bi = 0;
-      double bs = INFINITY, meanE = 0, meanNs = 0;
-      for (int c = 0; c < nc; c++) {
-        const double s = score(lc[c], sc[c], ns[c]);
-        if (s < bs) {
-          bs = s;
-          bi = c;
-        }
-        E[c] = energyE(lc[c], sc[c], ns[c]);  // the population step below reuses it
-        meanE += E[c];
-        meanNs += ns[c];
+    dev_->ok(tsa_sweeps(c, order_, L.beta, sweep, L.niters));
+    sweep += (uint32_t)L.niters;
+    if (!evaluated_level(lev)) {
+      kernel_ms_ += dev_->take_kernel_ms();
+      continue;
+    }
+    dev_->ok(tsa_energy(c, e.lc.data(), e.sc.data(), e.ns.data()));
+    kernel_ms_ += dev_->take_kernel_ms();
+    const Scoring S = scoring(mode_);
+    int bi = 0;
+    double bs = INFINITY, sumE = 0, sumNs = 0;
+    for (int k = 0; k < nc; k++) {
+      const double s = selection_score(S, e.lc[k], e.sc[k], e.ns[k]);
+      if (s < bs) {
+        bs = s;
+        bi = k;
       }
-      meanE /= nc;
-      meanNs /= nc;
-      if (bs < best_score) {
-        best_score = bs;
-        best_chain = bi;
-        ck(tsa_download(ctx, bi, 1, best.data()));
+      E[k] = population_energy(S, e.lc[k], e.sc[k], e.ns[k]);
+      sumE += E[k];
+      sumNs += e.ns[k];
+    }
+    if (bs < incumbent) {
+      incumbent = bs;
+      best_chain = bi;
+      dev_->ok(tsa_download(c, bi, 1, best.p));
+    }
+    std::fill(mark.begin(), mark.end(), 0);
+    int families = 0;
+    for (int k = 0; k < nc; k++) families += mark[family[k]]++ == 0;
+    const double t = wall_seconds() - t0;
+    add_trace(t, lev, e.lc[bi], e.sc[bi], sumE / nc, families, e.ns[bi], sumNs / nc);
+    progress(lev, e.lc[bi], e.sc[bi], e.ns[bi], sumE / nc, sumNs / nc, families, t);
+    // population step, not at the last level nor across an energy change
+    const bool last = lev + 1 == n;
+    std::vector<int> anc;
+    if (!last && sched_[lev + 1].mode == mode_) {
+      if (O_.scheme == "pa") {
+        const double db = (double)(sched_[lev + 1].beta - beta_resampled);  // a float difference, as the reference
+        beta_resampled = sched_[lev + 1].beta;
+        const double u = std::uniform_real_distribution<double>(0, 1)(pa_rng);
+        anc = systematic_ancestors(E, db, u);
+      } else if (O_.scheme == "trunc") {
+        anc = truncation_ancestors(E, O_.trunc_frac);
       }
-      std::fill(nfam.begin(), nfam.end(), 0);
-      int nf = 0;
-      for (int c = 0; c < nc; c++)
-        if (nfam[family[c]]++ == 0) nf++;
-      char buf[320];
-      snprintf(buf, sizeof buf, "%s[%.4f,%zu,%.4f,%.6f,%d,%.6f,%d,%d,%d,%.3f]", trace.empty() ? "" : ",", now_s() - t0,
-               lev, betas[lev], (double)lc[bi], sc[bi], meanE, nf, mode, ns[bi], meanNs);
-      trace += buf;
-      if (!O.quiet && (lev % 25 == 0 || last))
-        fprintf(stderr, "lev %4zu beta %7.3f  best(l2cost/slice %.3f sc %d |S| %d)  meanE %.3f  mean|S| %.2f  families %d  t=%.2fs\n",
-                lev, betas[lev], (double)lc[bi], sc[bi], ns[bi], meanE, meanNs, nf, now_s() - t0);
-      if (!last && !switching && O.scheme == "pa") {
-        // population annealing: systematic resampling with weights exp(-(beta_next - beta_prev) * E)
-        const double db = betas[lev + 1] - beta_last_resample;
-        beta_last_resample = betas[lev + 1];
-        std::vector<double> w(nc);
-        double Emin = INFINITY;
-        for (int c = 0; c < nc; c++) Emin = std::min(Emin, E[c]);
-        double wsum = 0;
-        for (int c = 0; c < nc; c++) {
-          w[c] = std::exp(-db * (E[c] - Emin));
-          wsum += w[c];
-        }
-        std::vector<int> anc(nc);
-        const double u = std::uniform_real_distribution<double>(0, 1)(hrng);
-        double acc = 0;
-        int j = 0;
-        for (int c = 0; c < nc; c++) {
-          acc += w[c] / wsum * nc;
-          while (j < nc && j + u < acc) anc[j++] = c;
-        }
-        while (j < nc) anc[j++] = nc - 1;
-        resample(anc, family);
-        nresample++;
-      } else if (!last && !switching && O.scheme == "trunc") {
-        // truncation selection: the worst trunc_frac are replaced by copies of the best
-        std::vector<int> idx(nc);
-        std::iota(idx.begin(), idx.end(), 0);
-        std::sort(idx.begin(), idx.end(), [&](int a, int b) { return E[a] < E[b]; });
-        std::vector<int> anc(nc);
-        std::iota(anc.begin(), anc.end(), 0);
-        const int nrep = (int)(O.trunc_frac * nc);
-        for (int k = 0; k < nrep; k++) anc[idx[nc - 1 - k]] = idx[k];
-        resample(anc, family);
-        nresample++;
+    }
+    if (level_log_) {
+      uint32_t bits;
+      std::memcpy(&bits, &e.lc[bi], 4);
+      fprintf(level_log_,
+              "{\"level\": %d, \"best\": %d, \"score\": %.17g, \"lc_bits\": %u, \"sc\": %d, \"ns\": %d, "
+              "\"families\": %d, \"meanE\": %.17g, \"resampled\": %s",
+              lev, bi, bs, bits, e.sc[bi], e.ns[bi], families, sumE / nc, anc.empty() ? "false" : "true");
+      if (!anc.empty()) {
+        fprintf(level_log_, ", \"anc\": [");
+        for (int k = 0; k < nc; k++) fprintf(level_log_, "%s%d", k ? "," : "", anc[k]);
+        fprintf(level_log_, "]");
       }
-    } else {
-      double ms = 0;
-      ck(tsa_sweeps_ms(ctx, &ms));
-      kernel_ms += ms;
+      fprintf(level_log_, "}\n");
+    }
+    if (!anc.empty()) {
+      dev_->ok(tsa_resample(c, anc.data()));
+      std::vector<int> f2(nc);
+      for (int k = 0; k < nc; k++) f2[k] = family[anc[k]];
+      family.swap(f2);
+      nresample++;
     }
   }
-  const double t_anneal = now_s() - t0;
-  uint64_t stats[7], chunks[2];
-  ck(tsa_stats(ctx, stats));
-  for (int k = 0; k < 7; k++) stats[k] -= stats0[k];
-  ck(tsa_chunk_stats(ctx, chunks));
-  for (int k = 0; k < 2; k++) chunks[k] -= chunks0[k];
+  return best_chain;
+}
 
-  // final best tree: verified from scratch; with slicing, sc > sc_target is repaired greedily
-  const uint32_t* bch = chCh(best.data());
-  std::vector<uint64_t> lab2((size_t)lay.nint * lay.W, 0);
-  const bool valid = labels_from_topology(I, lay.W, bch, lab2.data());
-  bool labels_ok = valid && std::equal(lab2.begin(), lab2.end(), best.begin());
-  if (tracked && best_chain >= 0) {
-    // device-side tracking returns the best tree only; the label sets the device maintains are checked on
-    // that chain's final record instead, and the best record gets the sets of its own tree
-    std::vector<uint64_t> live(lay.chain_words), lab3((size_t)lay.nint * lay.W, 0);
-    ck(tsa_download(ctx, best_chain, 1, live.data()));
-    labels_ok = valid && labels_from_topology(I, lay.W, chCh(live.data()), lab3.data()) &&
-                std::equal(lab3.begin(), lab3.end(), live.begin());
-    std::copy(lab2.begin(), lab2.end(), best.begin());
+std::string Run::kernel_label() const {
+  if (order_ == TSA_ORDER_PAR) return "par";
+  return dev_->describe().compare(0, 3, "lds") == 0 ? "warpsm" : "warp";
+}
+
+int Run::anneal() {
+  build_schedule();
+  if (sched_.empty()) throw InputError("no levels (empty --betas)");
+  const double t_start = wall_seconds();
+  const std::vector<uint64_t> pop = start_population();  // input errors surface before the device is touched
+  dev_ = std::make_unique<Device>(lay_, leaf_, N_.largest_tensor(), cfg_, O_.nchains);
+  tsa_ctx* c = dev_->get();
+  dev_->ok(tsa_upload(c, pop.data()));
+  uint64_t st0[7] = {0, 0, 0, 0, 0, 0, 0}, ch0[2] = {0, 0};
+  if (O_.bench_warmup > 0) warm_up(pop, st0, ch0);
+  if (!O_.level_log.empty()) {
+    level_log_ = fopen(O_.level_log.c_str(), "w");
+    if (!level_log_) throw InputError("cannot open " + O_.level_log);
+  }
+  PinnedWords best(lay_.chain_words);  // allocated (its pages touched) before the clock starts
+  const double t_init = wall_seconds() - t_start;
+  const double t0 = wall_seconds();
+  HostEnergy h1;
+  bool staged = false;
+  int nresample = 0;
+  const bool on_device = O_.scheme == "indep" && O_.stage2_betas.empty() && !O_.host_select;
+  const int best_chain = on_device ? loop_on_device(best, t0) : loop_on_host(best, t0, h1, staged, nresample);
+  const double t_anneal = wall_seconds() - t0;
+  if (level_log_) fclose(level_log_);
+  uint32_t total_sweeps = 0;
+  for (const Level& L : sched_) total_sweeps += (uint32_t)L.niters;
+  uint64_t st[7], chunks[2];
+  dev_->counters(st, chunks);
+  for (int k = 0; k < 7; k++) st[k] -= st0[k];
+  for (int k = 0; k < 2; k++) chunks[k] -= ch0[k];
+
+  // the final tree, verified from scratch: its label sets from the topology must equal the maintained ones
+  // (the device-side loop returns only the tree; then the chain's live record is checked instead)
+  const uint32_t* bch = children(best.p);
+  std::vector<uint64_t> lab((size_t)lay_.nint * lay_.W, 0ull);
+  const bool valid = topology_labels(N_, lay_.W, bch, lab.data());
+  bool labels_ok = valid && std::equal(lab.begin(), lab.end(), best.p);
+  if (on_device && best_chain >= 0) {
+    std::vector<uint64_t> live(lay_.chain_words), lab2((size_t)lay_.nint * lay_.W, 0ull);
+    dev_->ok(tsa_download(c, best_chain, 1, live.data()));
+    labels_ok = valid && topology_labels(N_, lay_.W, children(live.data()), lab2.data()) &&
+                std::equal(lab2.begin(), lab2.end(), live.begin());
+    std::copy(lab.begin(), lab.end(), best.p);
   }
   int n_repair = 0;
-  if (O.slicing && valid) n_repair = greedy_repair(I, lay.W, lab2.data(), leaf, best.data() + lay.s_off, O.sc_target);
-  const HostEnergy HE = host_energy(I, lay.W, ML, lab2.data(), bch, leaf, chS(best.data()));
-  const double ks = kernel_ms / 1e3;
-  if (!O.quiet)
+  if (O_.slicing && valid) n_repair = greedy_repair(N_, lay_.W, lab.data(), leaf_, best.p + lay_.s_off, O_.sc_target);
+  const HostEnergy HE = host_energy(N_, lay_.W, model_, lab.data(), bch, leaf_, slices(best.p));
+  const double ks = kernel_ms_ / 1e3;
+  if (!O_.quiet)
     fprintf(stderr,
-            "done: best tc %.4f sc %d |S| %d (repair +%d) time %.4e s time2 %.4e s (per slice) | anneal %.2fs init %.2fs "
-            "kernel %.2fs | %.3e proposals/s | %.3e node visits/s | slice moves %llu/%llu accepted\n",
-            HE.tc, HE.sc, HE.ns, n_repair, HE.time, HE.time2, t_anneal, t_init, ks, ks > 0 ? stats[0] / ks : 0.0,
-            ks > 0 ? (double)sweep_ctr * nc * (I.m - 1) / ks : 0.0, (unsigned long long)stats[5],
-            (unsigned long long)stats[4]);
-  FILE* f = O.out.empty() ? stdout : fopen(O.out.c_str(), "w");
-  if (!f) die("cannot open " + O.out);
-  char desc[256] = {0};
-  tsa_describe(ctx, desc, sizeof desc);
-  // summary words per label set in the reference's 32-bit count (one bit per 16-byte chunk)
-  const char* sp = strstr(desc, " sums=");
-  const int nsum = (sp && atoi(sp + 6) > 0) ? (lay.W / 2 + 31) / 32 : 0;
-  fprintf(f, "{\"tc\": %.6f, \"sc\": %d, \"gpu_time\": %s, \"h100_time\": %s, \"valid\": %s, \"labels_ok\": %s, \"best_chain\": %d,\n",
-          HE.tc, HE.sc, jnum(HE.time).c_str(), jnum(HE.time2).c_str(), valid ? "true" : "false",
-          labels_ok ? "true" : "false", best_chain);
-  fprintf(f, " \"slicing\": %s, \"nsliced\": %d, \"n_repair\": %d, \"tc_total\": %.6f, \"gpu_time_total\": %s, \"h100_time_total\": %s, \"sliced\": [",
-          O.slicing ? "true" : "false", HE.ns, n_repair, HE.tc + HE.ns, jnum(HE.time * std::exp2((double)HE.ns)).c_str(),
-          jnum(HE.time2 * std::exp2((double)HE.ns)).c_str());
-  {
-    int k = 0;
-    const uint64_t* S = best.data() + lay.s_off;
-    for (int l = 0; l < I.nlab; l++)
-      if (O.slicing && (S[l >> 6] >> (l & 63) & 1u)) fprintf(f, "%s%d", k++ ? "," : "", l);
+            "best: tc %.4f sc %d |S| %d (+%d repaired), gpu model %.4e s, h100 model %.4e s per slice\n"
+            "time: anneal %.3f s, set-up %.3f s, sweep kernels %.3f s: %.3e proposals/s, %.3e node visits/s; "
+            "slice moves %llu of %llu accepted\n",
+            HE.tc, HE.sc, HE.ns, n_repair, HE.time, HE.time2, t_anneal, t_init, ks, ks > 0 ? st[0] / ks : 0.0,
+            ks > 0 ? (double)total_sweeps * O_.nchains * (N_.m - 1) / ks : 0.0, (unsigned long long)st[5],
+            (unsigned long long)st[4]);
+
+  const std::string desc = dev_->describe();
+  const size_t sp = desc.find(" sums=");
+  const int nsum = (sp != std::string::npos && atoi(desc.c_str() + sp + 6) > 0) ? (lay_.W / 2 + 31) / 32 : 0;
+  int W32 = 0, nw32 = 0;
+  reference_widths(N_.nlab, lay_.runtime_width != 0, &W32, &nw32);
+  std::string sliced = "[";
+  for (int l = 0; l < N_.nlab && O_.slicing; l++)
+    if (best.p[lay_.s_off + (l >> 6)] >> (l & 63) & 1u) sliced += (sliced.size() > 1 ? "," : "") + std::to_string(l);
+  sliced += "]";
+  std::string tree = "[";
+  for (int i = 0; i < lay_.nint; i++)
+    tree += (i ? ",[" : "[") + std::to_string(bch[i] & 0xFFFFu) + "," + std::to_string(bch[i] >> 16) + "]";
+  tree += "]";
+
+  Json j;
+  j.fixed6("tc", HE.tc);
+  j.integer("sc", HE.sc);
+  j.sci6("gpu_time", HE.time);
+  j.sci6("h100_time", HE.time2);
+  j.boolean("valid", valid);
+  j.boolean("labels_ok", labels_ok);
+  j.integer("best_chain", best_chain);
+  j.boolean("slicing", O_.slicing);
+  j.integer("nsliced", HE.ns);
+  j.integer("n_repair", n_repair);
+  j.fixed6("tc_total", HE.tc + HE.ns);
+  j.sci6("gpu_time_total", HE.time * std::exp2((double)HE.ns));
+  j.sci6("h100_time_total", HE.time2 * std::exp2((double)HE.ns));
+  j.raw("sliced", sliced);
+  j.fixed6("t_anneal", t_anneal);
+  j.fixed6("t_init", t_init);
+  j.fixed6("kernel_s", ks);
+  static const char* counter_keys[7] = {"proposals",       "accepts",       "warp_steps", "node_visits",
+                                        "slice_proposals", "slice_accepts", "busy_lanes"};
+  for (int k = 0; k < 7; k++) j.integer(counter_keys[k], (long long)st[k]);
+  j.integer("coop_max", 1);
+  j.integer("coop_min", 1);
+  j.integer("coop_full", 1);
+  j.integer("par_follow", O_.par_follow);
+  j.integer("par_band", O_.par_band);
+  j.integer("nsum", nsum);
+  j.integer("wpc", 1);
+  j.text("order", order_ == TSA_ORDER_PAR ? "par" : "preorder");
+  j.integer("nchains", O_.nchains);
+  j.integer("niters", O_.niters);
+  j.integer("nlevels", (long long)sched_.size());
+  j.integer("total_sweeps", total_sweeps);
+  j.integer("W", W32);
+  j.integer("nw", nw32);
+  j.integer("W64", lay_.W);
+  j.integer("word_bits", 64);
+  j.integer("lpc", 64);
+  j.text("kernel", kernel_label());
+  j.text("hip_kernel", desc);
+  j.text("scheme", O_.scheme);
+  j.integer("mode", O_.mode);
+  j.integer("nresample", nresample);
+  j.integer("sum_chunks", (long long)chunks[0]);
+  j.integer("sum_xchunks", (long long)chunks[1]);
+  if (!init_tcs_.empty()) {
+    j.text("init", O_.init);
+    j.fixed6("t_start_trees", t_trees_);
+    std::string v = "[";
+    for (size_t i = 0; i < init_tcs_.size(); i++) {
+      char b[32];
+      snprintf(b, sizeof b, "%s%.4f", i ? ", " : "", init_tcs_[i]);
+      v += b;
+    }
+    j.raw("init_tcs", v + "]");
   }
-  fprintf(f, "],\n \"t_anneal\": %.6f, \"t_init\": %.6f, \"kernel_s\": %.6f, \"proposals\": %llu, \"accepts\": %llu, \"warp_steps\": %llu, \"node_visits\": %llu, \"slice_proposals\": %llu, \"slice_accepts\": %llu, \"busy_lanes\": %llu, \"coop_max\": %d, \"coop_min\": %d, \"coop_full\": %d, \"par_follow\": %d, \"par_band\": %d, \"nsum\": %d, \"wpc\": %d, \"order\": \"%s\",\n",
-          t_anneal, t_init, ks, (unsigned long long)stats[0], (unsigned long long)stats[1], (unsigned long long)stats[2],
-          (unsigned long long)stats[3], (unsigned long long)stats[4], (unsigned long long)stats[5],
-          (unsigned long long)stats[6], 1, 1, 1, O.par_follow, O.par_band, nsum, 1,
-          order == TSA_ORDER_PAR ? "par" : "preorder");
-  fprintf(f, " \"nchains\": %d, \"niters\": %d, \"nlevels\": %zu, \"total_sweeps\": %u, \"W\": %d, \"nw\": %d, \"word_bits\": 64, \"lpc\": 64, \"kernel\": \"%s\", \"hip_kernel\": \"%s\", \"scheme\": \"%s\", \"mode\": %d, \"nresample\": %d,\n",
-          nc, O.niters, betas.size(), sweep_ctr, lay.runtime_width ? 0 : lay.W, lay.W, kernel_name().c_str(), desc,
-          O.scheme.c_str(), O.mode, nresample);
-  fprintf(f, " \"sum_chunks\": %llu, \"sum_xchunks\": %llu,\n", (unsigned long long)chunks[0],
-          (unsigned long long)chunks[1]);
-  if (!init_tcs.empty()) {
-    fprintf(f, " \"init\": \"%s\", \"t_start_trees\": %.6f, \"init_tcs\": [", O.init.c_str(), t_trees);
-    for (size_t i = 0; i < init_tcs.size(); i++) fprintf(f, "%s%.4f", i ? ", " : "", init_tcs[i]);
-    fprintf(f, "],\n");
+  if (staged) {
+    j.fixed6("stage1_tc", h1.tc);
+    j.integer("stage1_sc", h1.sc);
+    j.integer("stage1_nsliced", h1.ns);
+    j.sci6("stage1_gpu_time", h1.time);
+    j.sci6("stage1_h100_time", h1.time2);
+    j.sci6("stage1_h100_time_total", h1.time2 * std::exp2((double)h1.ns));
   }
-  if (staged)
-    fprintf(f, " \"stage1_tc\": %.6f, \"stage1_sc\": %d, \"stage1_nsliced\": %d, \"stage1_gpu_time\": %s, \"stage1_h100_time\": %s, \"stage1_h100_time_total\": %s,\n",
-            H1.tc, H1.sc, H1.ns, jnum(H1.time).c_str(), jnum(H1.time2).c_str(),
-            jnum(H1.time2 * std::exp2((double)H1.ns)).c_str());
-  fprintf(f, " \"trace_cols\": [\"t\", \"level\", \"beta\", \"best_lcost_per_slice\", \"best_sc\", \"mean_E\", \"families\", \"mode\", \"best_nsliced\", \"mean_nsliced\"],\n");
-  fprintf(f, " \"trace\": [%s],\n \"tree\": [", trace.c_str());
-  for (int i = 0; i < lay.nint; i++) fprintf(f, "%s[%u,%u]", i ? "," : "", bch[i] & 0xFFFFu, bch[i] >> 16);
-  fprintf(f, "]}\n");
+  j.raw("trace_cols",
+        "[\"t\", \"level\", \"beta\", \"best_lcost_per_slice\", \"best_sc\", \"mean_E\", \"families\", \"mode\", "
+        "\"best_nsliced\", \"mean_nsliced\"]");
+  j.raw("trace", "[" + trace_ + "]");
+  j.raw("tree", tree);
+  const std::string text = j.finish();
+  FILE* f = O_.out_file.empty() ? stdout : fopen(O_.out_file.c_str(), "w");
+  if (!f) throw InputError("cannot open " + O_.out_file);
+  fputs(text.c_str(), f);
   if (f != stdout) fclose(f);
   return valid && labels_ok ? 0 : 2;
 }
 
-// Validation on the device (csrc/treesa_gpu.cu:1940-2061): [1] every chain is a valid tree whose labels
-// equal the topology's, [2] the energy kernel agrees with the host double computation, [3] the other
-// kernel mapping (chain in LDS vs in HBM) is bit-identical.  The CPU-reference comparison [4] needs the
-// oracle, which this binary does not link; the test suite runs it through the C ABI.
-int Runner::run_check() {
-  std::vector<float> betas = parse_betas(O.betas);
-  if (O.max_levels > 0 && (int)betas.size() > O.max_levels) betas.resize(O.max_levels);
-  const std::vector<uint64_t> init = init_population();
-  create(&ctx, cfg.kernel);
-  ck(tsa_upload(ctx, init.data()));
-  for (size_t lev = 0; lev < betas.size(); lev++)
-    ck(tsa_sweeps(ctx, order, betas[lev], (uint32_t)(lev * O.niters), O.niters));
+// --check (csrc/treesa_gpu.cu:1940-2061): sweeps of every level, then [1] every chain is a valid tree whose
+// label sets equal its topology's, [2] the energy kernel agrees with the host double computation, [3] the
+// other kernel mapping (chain in LDS or wide vs one wave in HBM) is bit-identical.  The CPU-reference
+// comparison [4] needs the oracle, which this binary does not link; the test suite runs it through the C ABI.
+int Run::check() {
+  build_schedule();
+  sched_.resize(std::min(sched_.size(), parse_schedule(O_.betas).size()));  // stage 1 only
+  const std::vector<uint64_t> init = start_population();
+  dev_ = std::make_unique<Device>(lay_, leaf_, N_.largest_tensor(), cfg_, O_.nchains);
+  tsa_ctx* c = dev_->get();
+  auto sweep_all = [&](tsa_ctx* x) {
+    for (size_t lev = 0; lev < sched_.size(); lev++)
+      dev_->ok(tsa_sweeps(x, order_, sched_[lev].beta, (uint32_t)(lev * O_.niters), O_.niters));
+  };
+  dev_->ok(tsa_upload(c, init.data()));
+  sweep_all(c);
   std::vector<uint64_t> fin(init.size());
-  ck(tsa_download(ctx, 0, O.nchains, fin.data()));
-  uint64_t stats[7];
-  ck(tsa_stats(ctx, stats));
-  char desc[256] = {0};
-  tsa_describe(ctx, desc, sizeof desc);
+  dev_->ok(tsa_download(c, 0, O_.nchains, fin.data()));
+  uint64_t st[7], ch[2];
+  dev_->counters(st, ch);
+  const std::string desc = dev_->describe();
   printf("check: %d chains, %zu levels x %d sweeps, kernel %s (%s), mode %d, W=%d (64-bit words), slicing %d (moves %d): "
          "%llu proposals, %llu accepted, %llu/%llu slice moves accepted\n",
-         O.nchains, betas.size(), O.niters, kernel_name().c_str(), desc, O.mode, lay.W, cfg.slicing, cfg.slice_moves,
-         (unsigned long long)stats[0], (unsigned long long)stats[1], (unsigned long long)stats[5],
-         (unsigned long long)stats[4]);
-  int bad_tree = 0, bad_lab = 0, changed = 0, Schanged = 0;
-  std::vector<uint64_t> lab2((size_t)lay.nint * lay.W);
-  for (int c = 0; c < O.nchains; c++) {
-    const uint64_t* base = &fin[(size_t)c * lay.chain_words];
-    const uint64_t* b0 = &init[(size_t)c * lay.chain_words];
-    if (!labels_from_topology(I, lay.W, chCh(base), lab2.data())) {
+         O_.nchains, sched_.size(), O_.niters, kernel_label().c_str(), desc.c_str(), O_.mode, lay_.W, cfg_.slicing,
+         cfg_.slice_moves, (unsigned long long)st[0], (unsigned long long)st[1], (unsigned long long)st[5],
+         (unsigned long long)st[4]);
+  int bad_tree = 0, bad_lab = 0, changed = 0, s_changed = 0;
+  std::vector<uint64_t> lab((size_t)lay_.nint * lay_.W);
+  for (int k = 0; k < O_.nchains; k++) {
+    const uint64_t* r = &fin[(size_t)k * lay_.chain_words];
+    const uint64_t* r0 = &init[(size_t)k * lay_.chain_words];
+    if (!topology_labels(N_, lay_.W, children(r), lab.data())) {
       bad_tree++;
       continue;
     }
-    if (!std::equal(lab2.begin(), lab2.end(), base)) bad_lab++;
-    if (!std::equal(base, base + lay.s_off, b0)) changed++;
-    if (!std::equal(base + lay.s_off, base + lay.s_off + lay.W, b0 + lay.s_off)) Schanged++;
+    bad_lab += !std::equal(lab.begin(), lab.end(), r);
+    changed += !std::equal(r, r + lay_.s_off, r0);
+    s_changed += !std::equal(r + lay_.s_off, r + lay_.s_off + lay_.W, r0 + lay_.s_off);
   }
   printf("  [1] invalid trees: %d, chains with label mismatch vs recomputation: %d (chains changed by SA: %d/%d, "
          "slice set changed: %d)\n",
-         bad_tree, bad_lab, changed, O.nchains, Schanged);
-  std::vector<float> lc(O.nchains);
-  std::vector<int> sc(O.nchains), ns(O.nchains);
-  ck(tsa_energy(ctx, lc.data(), sc.data(), ns.data()));
-  double maxd = 0;
-  int scbad = 0;
-  for (int c = 0; c < O.nchains; c++) {
-    const uint64_t* base = &fin[(size_t)c * lay.chain_words];
-    const HostEnergy HE = host_energy(I, lay.W, ML, base, chCh(base), leaf, chS(base));
-    const double ref = O.mode == 0 ? HE.tc : std::log2(O.mode == 1 ? HE.time : HE.time2);
-    maxd = std::max(maxd, std::fabs(ref - (double)lc[c]));
-    if (HE.sc != sc[c] || HE.ns != ns[c]) scbad++;
+         bad_tree, bad_lab, changed, O_.nchains, s_changed);
+  Energies e(O_.nchains);
+  dev_->ok(tsa_energy(c, e.lc.data(), e.sc.data(), e.ns.data()));
+  double worst = 0;
+  int sc_bad = 0;
+  for (int k = 0; k < O_.nchains; k++) {
+    const uint64_t* r = &fin[(size_t)k * lay_.chain_words];
+    const HostEnergy H = host_energy(N_, lay_.W, model_, r, children(r), leaf_, slices(r));
+    const double want = O_.mode == 0 ? H.tc : std::log2(O_.mode == 1 ? H.time : H.time2);
+    worst = std::max(worst, std::fabs(want - (double)e.lc[k]));
+    sc_bad += H.sc != e.sc[k] || H.ns != e.ns[k];
   }
-  printf("  [2] GPU energy kernel vs host double: max |dlog2cost| = %.3g, sc/|S| mismatches %d\n", maxd, scbad);
+  printf("  [2] GPU energy kernel vs host double: max |dlog2cost| = %.3g, sc/|S| mismatches %d\n", worst, sc_bad);
   int xdiff = -1;
-  const bool is_lds = strncmp(desc, "lds", 3) == 0, is_wide = strncmp(desc, "wide", 4) == 0;
-  if (O.cross && cfg.slice_moves == 0 && (is_lds || (is_wide && order == TSA_ORDER_PAR))) {
-    tsa_ctx* c2 = nullptr;
-    create(&c2, TSA_KERNEL_GLOBAL);
-    ck(tsa_upload(c2, init.data()));
-    for (size_t lev = 0; lev < betas.size(); lev++)
-      ck(tsa_sweeps(c2, order, betas[lev], (uint32_t)(lev * O.niters), O.niters));
+  const bool is_lds = desc.compare(0, 3, "lds") == 0, is_wide = desc.compare(0, 4, "wide") == 0;
+  if (O_.cross && cfg_.slice_moves == 0 && (is_lds || (is_wide && order_ == TSA_ORDER_PAR))) {
+    tsa_config_t c2 = cfg_;
+    c2.kernel = TSA_KERNEL_GLOBAL;
+    Device other(lay_, leaf_, N_.largest_tensor(), c2, O_.nchains);
+    other.ok(tsa_upload(other.get(), init.data()));
+    for (size_t lev = 0; lev < sched_.size(); lev++)
+      other.ok(tsa_sweeps(other.get(), order_, sched_[lev].beta, (uint32_t)(lev * O_.niters), O_.niters));
     std::vector<uint64_t> fin2(fin.size());
-    ck(tsa_download(c2, 0, O.nchains, fin2.data()));
-    tsa_destroy(c2);
+    other.ok(tsa_download(other.get(), 0, O_.nchains, fin2.data()));
     xdiff = 0;
-    for (int c = 0; c < O.nchains; c++)
-      if (!std::equal(fin.begin() + (size_t)c * lay.chain_words, fin.begin() + (size_t)(c + 1) * lay.chain_words,
-                      fin2.begin() + (size_t)c * lay.chain_words))
-        xdiff++;
-    printf("  [3] kernel %s vs global: chains differing: %d/%d\n", is_lds ? "lds" : "wide", xdiff, O.nchains);
+    for (int k = 0; k < O_.nchains; k++)
+      xdiff += !std::equal(fin.begin() + (size_t)k * lay_.chain_words, fin.begin() + (size_t)(k + 1) * lay_.chain_words,
+                           fin2.begin() + (size_t)k * lay_.chain_words);
+    printf("  [3] kernel %s vs global: chains differing: %d/%d\n", is_lds ? "lds" : "wide", xdiff, O_.nchains);
   }
   printf("  [4] CPU reference: not linked into this binary\n");
-  const bool ok = bad_tree == 0 && bad_lab == 0 && scbad == 0 && maxd < 1e-3 && xdiff <= 0;
+  const bool ok = bad_tree == 0 && bad_lab == 0 && sc_bad == 0 && worst < 1e-3 && xdiff <= 0;
   printf("CHECK %s\n", ok ? "PASSED" : "FAILED");
   return ok ? 0 : 3;
 }
@@ -727,14 +751,25 @@ int Runner::run_check() {
 }  // namespace
 
 int main(int argc, char** argv) {
-  const Opts O = parse(argc, argv);
+  Options O;
   try {
-    const Inst I = read_instance(O.inst);
-    if (I.m < 3) die("need at least 3 tensors");
-    if (2 * I.m - 1 > 65535) die("too many tensors (node ids are 16-bit)");
-    Runner R(I, O);
-    return O.check ? R.run_check() : R.run_anneal();
-  } catch (const InputError& e) {
-    die(e.what());
+    O = parse_options(argc, argv);
+  } catch (const UsageError& e) {
+    fprintf(stderr, "%s\n%s", e.what(), usage_text().c_str());
+    return 1;
   }
+  try {
+    const Network N = read_network(O.instance);
+    if (N.m < 3) throw InputError("need at least 3 tensors");
+    if (2 * N.m - 1 > 65535) throw InputError("too many tensors (node ids are 16-bit)");
+    Run R(N, O);
+    return O.check ? R.check() : R.anneal();
+  } catch (const InputError& e) {
+    fprintf(stderr, "%s\n", e.what());
+  } catch (const DeviceError& e) {
+    fprintf(stderr, "%s\n", e.what());
+  } catch (const std::bad_alloc&) {
+    fprintf(stderr, "out of host memory\n");
+  }
+  return 1;
 }

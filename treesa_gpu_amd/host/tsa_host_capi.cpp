@@ -21,7 +21,7 @@ extern "C" {
 
 void* tsh_instance_load(const char* path, char* err, int errlen) {
   try {
-    return new Inst(read_instance(path));
+    return new Network(read_network(path));
   } catch (const std::exception& e) {
     put_err(err, errlen, e.what());
     return nullptr;
@@ -34,25 +34,25 @@ void* tsh_instance_make(int m, int nlab, const int* offs, const int* labels, int
   try {
     std::vector<std::vector<int>> ixs(m);
     for (int i = 0; i < m; i++) ixs[i].assign(labels + offs[i], labels + offs[i + 1]);
-    return new Inst(make_instance(m, nlab, ixs, std::vector<int>(iy, iy + ny)));
+    return new Network(make_network(m, nlab, ixs, std::vector<int>(iy, iy + ny)));
   } catch (const std::exception& e) {
     put_err(err, errlen, e.what());
     return nullptr;
   }
 }
 
-void tsh_instance_free(void* h) { delete static_cast<Inst*>(h); }
+void tsh_instance_free(void* h) { delete static_cast<Network*>(h); }
 
 int tsh_instance_info(void* h, int* m, int* nlab, int* lsc) {
-  const Inst& I = *static_cast<Inst*>(h);
+  const Network& I = *static_cast<Network*>(h);
   *m = I.m;
   *nlab = I.nlab;
-  *lsc = leaf_sc(I);
+  *lsc = I.largest_tensor();
   return 0;
 }
 
 int tsh_instance_leaf(void* h, int W, uint64_t* out) {
-  const Inst& I = *static_cast<Inst*>(h);
+  const Network& I = *static_cast<Network*>(h);
   const std::vector<uint64_t> lf = leaf_sets(I, W);
   memcpy(out, lf.data(), lf.size() * 8);
   return 0;
@@ -61,7 +61,7 @@ int tsh_instance_leaf(void* h, int W, uint64_t* out) {
 // Up to maxk trees into out (maxk * (m-1) words); returns K or -1.
 int tsh_read_trees(const char* path, int m, uint32_t* out, int maxk, char* err, int errlen) {
   try {
-    const auto t = read_trees(path, m);
+    const auto t = read_tree_file(path, m);
     const int K = (int)t.size() < maxk ? (int)t.size() : maxk;
     for (int k = 0; k < K; k++) memcpy(out + (size_t)k * (m - 1), t[k].data(), (size_t)(m - 1) * 4);
     return (int)t.size();
@@ -74,7 +74,7 @@ int tsh_read_trees(const char* path, int m, uint32_t* out, int maxk, char* err, 
 // Returns the number of betas (only the first maxn are written) or -1.
 int tsh_parse_betas(const char* spec, float* out, int maxn, char* err, int errlen) {
   try {
-    const auto b = parse_betas(spec);
+    const auto b = parse_schedule(spec);
     for (int i = 0; i < (int)b.size() && i < maxn; i++) out[i] = b[i];
     return (int)b.size();
   } catch (const std::exception& e) {
@@ -91,14 +91,14 @@ void tsh_random_tree(int m, uint64_t seed, uint32_t* out) {
 }
 
 int tsh_labels(void* h, int W, const uint32_t* ch, uint64_t* lab) {
-  return labels_from_topology(*static_cast<Inst*>(h), W, ch, lab) ? 0 : 1;
+  return topology_labels(*static_cast<Network*>(h), W, ch, lab) ? 0 : 1;
 }
 
 int tsh_build_population(void* h, int W, int ch_off, int s_off, int chain_words, const uint32_t* trees, int K,
                          int nchains, uint64_t seed, const uint64_t* S0, int random_slices, uint64_t* pop, char* err,
                          int errlen) {
   try {
-    const Inst& I = *static_cast<Inst*>(h);
+    const Network& I = *static_cast<Network*>(h);
     std::vector<std::vector<uint32_t>> t(K);
     for (int k = 0; k < K; k++) t[k].assign(trees + (size_t)k * (I.m - 1), trees + (size_t)(k + 1) * (I.m - 1));
     std::vector<uint64_t> s0(S0 ? S0 : nullptr, S0 ? S0 + W : nullptr);
@@ -115,7 +115,7 @@ int tsh_build_population(void* h, int W, int ch_off, int s_off, int chain_words,
 // out = {tc, sc, gpu_time, h100_time, |S|}; S may be null (no slicing).
 int tsh_host_energy(void* h, int W, const double* gm, const double* h100, const uint64_t* lab, const uint32_t* ch,
                     const uint64_t* S, double* out) {
-  const Inst& I = *static_cast<Inst*>(h);
+  const Network& I = *static_cast<Network*>(h);
   ModelConsts C;
   if (gm) memcpy(C.gm, gm, sizeof C.gm);
   if (h100) memcpy(C.h100, h100, sizeof C.h100);
@@ -129,13 +129,35 @@ int tsh_host_energy(void* h, int W, const double* gm, const double* h100, const 
 }
 
 int tsh_greedy_repair(void* h, int W, const uint64_t* lab, uint64_t* S, double sc_target) {
-  const Inst& I = *static_cast<Inst*>(h);
+  const Network& I = *static_cast<Network*>(h);
   return greedy_repair(I, W, lab, leaf_sets(I, W), S, sc_target);
+}
+
+// The level loop's host arithmetic (tsa_population.cpp) for tests.  scoring: {mode, slicing, select_sc};
+// which: 0 selection score, 1 population energy.
+double tsh_score(const int* scoring, double sc_target, double sc_weight, float lc, int sc, int ns, int which) {
+  Scoring S;
+  S.mode = scoring[0];
+  S.slicing = scoring[1] != 0;
+  S.select_sc = scoring[2] != 0;
+  S.sc_target = sc_target;
+  S.sc_weight = sc_weight;
+  return which ? population_energy(S, lc, sc, ns) : selection_score(S, lc, sc, ns);
+}
+
+void tsh_systematic(const double* E, int n, double db, double u, int* anc) {
+  const std::vector<int> a = systematic_ancestors(std::vector<double>(E, E + n), db, u);
+  memcpy(anc, a.data(), (size_t)n * 4);
+}
+
+void tsh_truncation(const double* E, int n, double frac, int* anc) {
+  const std::vector<int> a = truncation_ancestors(std::vector<double>(E, E + n), frac);
+  memcpy(anc, a.data(), (size_t)n * 4);
 }
 
 // path_cost of an ordering: out = {tc, sc}.
 int tsh_path_cost(void* h, const int* order, int m, double* out) {
-  const Inst& I = *static_cast<Inst*>(h);
+  const Network& I = *static_cast<Network*>(h);
   if (m != I.m) return -1;
   const auto r = path_cost(I, std::vector<int>(order, order + m));
   out[0] = r.first;
@@ -145,7 +167,7 @@ int tsh_path_cost(void* h, const int* order, int m, double* out) {
 
 // Up to k spectral orderings: orders (k * m ints), tc[k], sc[k]; returns how many were written.
 int tsh_spectral_orders(void* h, int k, int nangles, int nrandom, uint64_t seed, int* orders, double* tc, int* sc) {
-  const Inst& I = *static_cast<Inst*>(h);
+  const Network& I = *static_cast<Network*>(h);
   const auto so = spectral_orders(I, k, nangles, nrandom, seed);
   for (size_t i = 0; i < so.size(); i++) {
     memcpy(orders + i * (size_t)I.m, so[i].order.data(), (size_t)I.m * 4);
@@ -158,7 +180,7 @@ int tsh_spectral_orders(void* h, int k, int nangles, int nrandom, uint64_t seed,
 // spectral_search over caller-given eigenvectors (m x d) and random directions (ndirs x d); as above.
 int tsh_spectral_search(void* h, const double* V, int d, const double* dirs, int ndirs, int k, int nangles,
                         int* orders, double* tc, int* sc) {
-  const Inst& I = *static_cast<Inst*>(h);
+  const Network& I = *static_cast<Network*>(h);
   const auto so = spectral_search(I, std::vector<double>(V, V + (size_t)I.m * d), d,
                                   std::vector<double>(dirs, dirs + (size_t)ndirs * d), k, nangles);
   for (size_t i = 0; i < so.size(); i++) {
@@ -171,7 +193,7 @@ int tsh_spectral_search(void* h, const double* V, int d, const double* dirs, int
 
 // Laplacian eigenvectors 1..k (m * k doubles, row-major) and eigenvalues (k); returns the k computed.
 int tsh_laplacian_vectors(void* h, int k, uint64_t seed, double* vecs, double* vals) {
-  const Inst& I = *static_cast<Inst*>(h);
+  const Network& I = *static_cast<Network*>(h);
   std::vector<double> ev;
   const auto V = laplacian_vectors(I, k, seed, &ev);
   const int kk = (int)ev.size();
@@ -182,7 +204,7 @@ int tsh_laplacian_vectors(void* h, int k, uint64_t seed, double* vecs, double* v
 
 // Greedy tree into out (m - 1 children words); tc receives its tc.
 int tsh_greedy_tree(void* h, int nrepeat, uint64_t seed, uint32_t* out, double* tc) {
-  const Inst& I = *static_cast<Inst*>(h);
+  const Network& I = *static_cast<Network*>(h);
   const auto ch = greedy_tree(I, nrepeat, seed, tc);
   memcpy(out, ch.data(), ch.size() * 4);
   return 0;

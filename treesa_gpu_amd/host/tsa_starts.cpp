@@ -47,12 +47,12 @@ struct Graph {
   std::vector<double> w, deg;
 };
 
-Graph tensor_graph(const Inst& I) {
+Graph tensor_graph(const Network& I) {
   Graph G;
   G.n = I.m;
   std::vector<std::vector<int>> holders(I.nlab);
   for (int t = 0; t < I.m; t++)
-    for (int l : I.ixs[t]) holders[l].push_back(t);
+    for (int l : I.tensors[t]) holders[l].push_back(t);
   std::vector<std::pair<uint64_t, double>> acc;
   for (const auto& ts : holders) {
     const int k = (int)ts.size();
@@ -201,7 +201,7 @@ struct Normal {
 
 }  // namespace
 
-std::vector<double> laplacian_vectors(const Inst& I, int k, uint64_t seed, std::vector<double>* evals) {
+std::vector<double> laplacian_vectors(const Network& I, int k, uint64_t seed, std::vector<double>* evals) {
   const Graph G = tensor_graph(I);
   const int n = G.n;
   k = std::min(k, std::max(1, n - 2));
@@ -291,14 +291,14 @@ std::vector<double> laplacian_vectors(const Inst& I, int k, uint64_t seed, std::
   return V;
 }
 
-std::pair<double, int> path_cost(const Inst& I, const std::vector<int>& order) {
+std::pair<double, int> path_cost(const Network& I, const std::vector<int>& order) {
   const int m = (int)order.size();
-  if (m < 2) return {0.0, leaf_sc(I)};
+  if (m < 2) return {0.0, I.largest_tensor()};
   std::vector<int> pos(m);
   for (int i = 0; i < m; i++) pos[order[i]] = i;
   std::vector<int> first(I.nlab, -1), last(I.nlab, -1);
   for (int t = 0; t < m; t++)
-    for (int l : I.ixs[t]) {
+    for (int l : I.tensors[t]) {
       const int p = pos[t];
       if (first[l] < 0 || p < first[l]) first[l] = p;
       if (last[l] < 0 || p > last[l]) last[l] = p;
@@ -307,7 +307,7 @@ std::pair<double, int> path_cost(const Inst& I, const std::vector<int>& order) {
   std::vector<long long> diff(m + 2, 0), newc(m, 0);
   for (int l = 0; l < I.nlab; l++) {
     if (first[l] < 0) continue;
-    const int f = first[l], la = I.in_iy[l] ? m : last[l];
+    const int f = first[l], la = I.is_open[l] ? m : last[l];
     newc[f]++;
     diff[f + 1]++;
     diff[la + 1]--;
@@ -322,13 +322,13 @@ std::pair<double, int> path_cost(const Inst& I, const std::vector<int>& order) {
   // dimension-2 indices its cost is the size of the union of the two label sets
   std::vector<long long> cost(m - 1);
   {
-    std::vector<int> u(I.ixs[order[0]]);
-    u.insert(u.end(), I.ixs[order[1]].begin(), I.ixs[order[1]].end());
+    std::vector<int> u(I.tensors[order[0]]);
+    u.insert(u.end(), I.tensors[order[1]].begin(), I.tensors[order[1]].end());
     std::sort(u.begin(), u.end());
     cost[0] = std::unique(u.begin(), u.end()) - u.begin();
   }
   for (int i = 2; i < m; i++) cost[i - 1] = alive[i] + newc[i];
-  long long sc = leaf_sc(I);
+  long long sc = I.largest_tensor();
   for (int i = 2; i <= m; i++) sc = std::max(sc, alive[i]);
   const long long cm = *std::max_element(cost.begin(), cost.end());
   double s = 0.0;
@@ -346,14 +346,14 @@ std::vector<uint32_t> path_tree(const std::vector<int>& order) {
   return ch;
 }
 
-std::vector<SpectralOrder> spectral_search(const Inst& I, const std::vector<double>& V, int d,
+std::vector<SpectralOrder> spectral_search(const Network& I, const std::vector<double>& V, int d,
                                            const std::vector<double>& rdirs, int k, int nangles) {
   const int n = I.m;
   std::vector<SpectralOrder> out;
   if (n < 3) {
     std::vector<int> o(n);
     std::iota(o.begin(), o.end(), 0);
-    out.push_back({0.0, leaf_sc(I), o});
+    out.push_back({0.0, I.largest_tensor(), o});
     return out;
   }
   struct Cand {
@@ -435,7 +435,7 @@ std::vector<SpectralOrder> spectral_search(const Inst& I, const std::vector<doub
   return out;
 }
 
-std::vector<SpectralOrder> spectral_orders(const Inst& I, int k, int nangles, int nrandom, uint64_t seed) {
+std::vector<SpectralOrder> spectral_orders(const Network& I, int k, int nangles, int nrandom, uint64_t seed) {
   const int n = I.m;
   if (n < 3) return spectral_search(I, {}, 0, {}, k, nangles);
   const int d = std::min(3, std::max(1, n - 2));
@@ -465,11 +465,12 @@ struct GreedyRun {
   double tc;
 };
 
-GreedyRun greedy_once(const Inst& I, uint64_t seed, bool random_ties) {
+GreedyRun greedy_once(const Network& I, uint64_t seed, bool random_ties) {
   const int m = I.m;
   std::vector<std::vector<int>> sets(2 * m - 1);
-  for (int t = 0; t < m; t++) sets[t] = I.ixs[t];
-  std::vector<int> cnt(I.total.begin(), I.total.end());
+  for (int t = 0; t < m; t++) sets[t] = I.tensors[t];
+  std::vector<int> cnt(I.nlab);
+  for (int l = 0; l < I.nlab; l++) cnt[l] = I.occurrences(l);
   std::vector<std::set<int>> holders(I.nlab);
   for (int t = 0; t < m; t++)
     for (int l : sets[t]) holders[l].insert(t);
@@ -480,7 +481,7 @@ GreedyRun greedy_once(const Inst& I, uint64_t seed, bool random_ties) {
     for (int l : u) {
       const int inside = (int)std::binary_search(sets[a].begin(), sets[a].end(), l) +
                          (int)std::binary_search(sets[b].begin(), sets[b].end(), l);
-      if (I.in_iy[l] || cnt[l] - inside > 0) o.push_back(l);
+      if (I.is_open[l] || cnt[l] - inside > 0) o.push_back(l);
     }
     return o;
   };
@@ -571,7 +572,7 @@ GreedyRun greedy_once(const Inst& I, uint64_t seed, bool random_ties) {
 
 }  // namespace
 
-std::vector<uint32_t> greedy_tree(const Inst& I, int nrepeat, uint64_t seed, double* tc) {
+std::vector<uint32_t> greedy_tree(const Network& I, int nrepeat, uint64_t seed, double* tc) {
   GreedyRun best{{}, INFINITY};
   for (int r = 0; r < std::max(1, nrepeat); r++) {
     GreedyRun g = greedy_once(I, splitmix64(seed * 1000003ull + (uint64_t)r), r > 0);
