@@ -200,6 +200,25 @@ int tsa_describe(tsa_ctx* ctx, char* buf, int32_t len);
 void* tsa_host_alloc(size_t bytes);
 void tsa_host_free(void* p);
 
+/* Allocation-free sweeps for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the reference.  It runs what tsa_sweeps
+ * + tsa_energy + tsa_stats do on a context, on buffers the caller owns, and allocates nothing: no context, no
+ * hipMalloc / hipFree, no events.  The caller passes device pointers: leaf_dev (m * W words, the layout's leaf
+ * table), population_dev (nchains records, swept in place; every record must hold a valid tree, as written by
+ * tsa_download or an earlier call: nothing is checked on the host), and optionally lc_dev / sc_dev / ns_dev
+ * (all or none: the energies after the last sweep) and stats_dev (7 words: the call's counters, as tsa_stats).
+ * Register-width layouts only (at most 512 labels, no --wide).  stream: a hipStream_t (NULL: the null stream);
+ * everything is enqueued on it and the call returns without waiting.
+ * Its working memory is one static device buffer of 32 MiB per GPU (held until the process ends): the
+ * counters plus, when energies are asked for, 6 bytes per internal node per chain; a call that would need more
+ * fails with TSA_ERR_ARG.  The first call on a device fills the library's log2f table there with one
+ * synchronous copy (make it before any graph capture).  Calls on one GPU share that buffer: calls that overlap
+ * in time on one GPU (several host threads or streams) race and must be serialized by the caller. */
+int tsa_sweeps_noalloc(const tsa_layout_t* lay, const tsa_config_t* cfg, int32_t leaf_sc, const uint64_t* leaf_dev,
+                       uint64_t* population_dev, int32_t nchains, int32_t order, float beta, uint32_t sweep0,
+                       int32_t nsweeps, float* lc_dev, int32_t* sc_dev, int32_t* ns_dev, uint64_t* stats_dev,
+                       void* stream);
+
 /* Release everything.  Replaces Runner::release, csrc/treesa_gpu.cu:1579-1582. */
 int tsa_destroy(tsa_ctx* ctx);
 

@@ -25,7 +25,8 @@ DEFAULT_H100 = (4e-6, 1.23e13, 5.44e-14, 7.68e-15, 6.37e-14, 2.02e-16, 1.77e-13,
 
 EXPORTS = ("tsa_layout", "tsa_create", "tsa_upload", "tsa_download", "tsa_sweeps", "tsa_sweeps_ms", "tsa_energy",
            "tsa_resample", "tsa_set_mode", "tsa_stats", "tsa_chunk_stats", "tsa_describe", "tsa_destroy", "tsa_last_error",
-           "tsa_host_math", "tsa_host_alloc", "tsa_host_free")
+           "tsa_host_math", "tsa_host_alloc", "tsa_host_free", "tsa_track_begin", "tsa_track", "tsa_track_end",
+           "tsa_sweeps_noalloc")
 
 
 class Layout(ctypes.Structure):
@@ -83,6 +84,8 @@ def load():
     lib.tsa_host_alloc.restype = P
     lib.tsa_host_free.argtypes = [P]
     lib.tsa_host_free.restype = None
+    lib.tsa_sweeps_noalloc.argtypes = [ctypes.POINTER(Layout), ctypes.POINTER(Config), I32, P, P, I32, I32, F32, U32,
+                                       I32, P, P, P, P, P]
     _lib = lib
     return lib
 
@@ -230,3 +233,13 @@ class Context:
             self.close()
         except Exception:
             pass
+
+
+def sweeps_noalloc(lay, cfg, leaf_sc, leaf_dev, pop_dev, nchains, order, beta, sweep0, nsweeps, lc_dev=None, sc_dev=None,
+                   ns_dev=None, stats_dev=None, stream=None):
+    """tsa_sweeps_noalloc on device pointers (ints); raises TsaError on a refused call."""
+    lib = load()
+    rc = lib.tsa_sweeps_noalloc(ctypes.byref(lay), ctypes.byref(cfg), leaf_sc, leaf_dev, pop_dev, nchains, order, beta,
+                                sweep0, nsweeps, lc_dev, sc_dev, ns_dev, stats_dev, stream)
+    if rc != 0:
+        raise TsaError(rc, lib.tsa_last_error(None).decode())

@@ -265,21 +265,19 @@ static void free_ctx(tsa_ctx* c) {
   delete c;
 }
 
-static void fill_params(tsa_ctx* c, int32_t leaf_sc) {
-  TsaKParams& P = c->P;
+static void fill_params(const tsa_layout_t& lay, const tsa_config_t& C, int32_t leaf_sc, TsaKParams& P) {
   memset(&P, 0, sizeof P);
-  P.m = c->lay.m;
-  P.nint = c->lay.nint;
-  P.W = c->lay.W;
-  P.ch_off = c->lay.ch_off;
-  P.s_off = c->lay.s_off;
-  P.chain_words = c->lay.chain_words;
+  P.m = lay.m;
+  P.nint = lay.nint;
+  P.W = lay.W;
+  P.ch_off = lay.ch_off;
+  P.s_off = lay.s_off;
+  P.chain_words = lay.chain_words;
   P.leaf_sc = leaf_sc;
-  const tsa_config_t& C = c->cfg;
   P.slicing = C.slicing ? 1 : 0;
   P.slice_moves = C.slicing ? C.slice_moves : 0;
   P.slice_every = C.slice_every > 0 ? C.slice_every : 1;
-  P.max_slices = C.max_slices > 0 ? C.max_slices : c->lay.nlab;
+  P.max_slices = C.max_slices > 0 ? C.max_slices : lay.nlab;
   P.par_follow = C.par_follow;
   P.par_band = C.par_band;
   P.key0 = C.key0;
@@ -305,24 +303,21 @@ static void fill_params(tsa_ctx* c, int32_t leaf_sc) {
   build_lse(P.lse);
 }
 
-extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t leaf_sc, const tsa_config_t* cfg,
-                          int32_t nchains, tsa_ctx** out) {
-  if (!lay || !leaf || !cfg || !out) return fail(nullptr, TSA_ERR_ARG, "tsa_create: null argument");
-  *out = nullptr;
+// Arguments every context-free entry shares with tsa_create: a layout from tsa_layout and a valid config.
+static int check_layout_config(const tsa_layout_t* lay, const tsa_config_t* cfg, const char* who) {
   tsa_layout_t chk;
   if (tsa_layout(lay->m, lay->nlab, lay->runtime_width, &chk) != TSA_OK) return TSA_ERR_ARG;
-  if (memcmp(&chk, lay, sizeof chk) != 0) return fail(nullptr, TSA_ERR_ARG, "tsa_create: layout not from tsa_layout");
-  if (nchains < 1 || nchains > (1 << 24)) return fail(nullptr, TSA_ERR_ARG, "tsa_create: nchains out of range");
-  if (cfg->mode < 0 || cfg->mode > 2) return fail(nullptr, TSA_ERR_ARG, "tsa_create: mode must be 0, 1 or 2");
+  if (memcmp(&chk, lay, sizeof chk) != 0) return fail(nullptr, TSA_ERR_ARG, std::string(who) + ": layout not from tsa_layout");
+  if (cfg->mode < 0 || cfg->mode > 2) return fail(nullptr, TSA_ERR_ARG, std::string(who) + ": mode must be 0, 1 or 2");
   if (cfg->par_band == 1 || cfg->par_band < 0 || cfg->par_band > 16)
     return fail(nullptr, TSA_ERR_ARG, "--par-band L: 0 (off) or 2..16");
-  if (cfg->slicing && cfg->slice_moves < 0) return fail(nullptr, TSA_ERR_ARG, "tsa_create: slice_moves < 0");
-  for (size_t i = 0; i < (size_t)lay->m * lay->W; i++) {
-    const int used = lay->nlab - 64 * (int)(i % lay->W);  // labels that word i may hold
-    if (used <= 0 ? leaf[i] != 0 : (used < 64 && (leaf[i] >> used) != 0))
-      return fail(nullptr, TSA_ERR_ARG, "tsa_create: leaf label out of range");
-  }
+  if (cfg->slicing && cfg->slice_moves < 0) return fail(nullptr, TSA_ERR_ARG, std::string(who) + ": slice_moves < 0");
+  return TSA_OK;
+}
 
+// The host libm must be the one the restated expf / exp2f / log2f were checked against (the log2f correction
+// table is built from it); built and checked once per process.
+static int check_host_math() {
   std::call_once(g_fix_once, build_log2_fix);
   if (g_fix_far != 0)
     return fail(nullptr, TSA_ERR_LIBM, "host libm log2f is more than 1 ulp from the restated log2f on [1, 2]");
@@ -333,13 +328,71 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
     if (selftest < 0) selftest = libm_selftest();
   }
   if (selftest != 0) return fail(nullptr, TSA_ERR_LIBM, "host libm expf/exp2f differ from the restated algorithm");
+  return TSA_OK;
+}
+
+// The one-wave-per-chain plan: the chain and the leaf table staged in LDS when they fit and the width is a
+// register width (or kernel forces it), else the record in HBM with only the node arrays in LDS; up to four
+// chains per workgroup, fewer when there are fewer chains than full workgroups on every compute unit (then
+// they spread over all units and share each unit's LDS, scalar unit and issue with fewer others).
+static int plan_one_wave(const tsa_layout_t* lay, const tsa_config_t* cfg, int nchains, int lds_max, int ncu,
+                         TsaLaunch* L, bool* use_lds_out) {
+  const int nodew = tsa_node_words(lay->nint) + (cfg->par_band > 0 ? ((lay->nint + 3) & ~3) / 2 : 0);
+  const int nodew2 = (nodew + 1) & ~1;
+  const int leafw = (lay->m * lay->W + 1) & ~1;
+  const int per_wave_lds = lay->chain_words + nodew2;
+  const int ldsw = (lds_max - 1024) / 8;  // less room for the kernel's static LDS (under 1 KB)
+  const bool lds_fits = !lay->runtime_width && leafw + per_wave_lds <= ldsw;
+  bool use_lds;
+  if (cfg->kernel == TSA_KERNEL_LDS) {
+    if (!lds_fits)
+      return fail(nullptr, TSA_ERR_FIT, "chain does not fit in LDS (or the label width is not a register width)");
+    use_lds = true;
+  } else {
+    use_lds = cfg->kernel == TSA_KERNEL_GLOBAL ? false : lds_fits;
+  }
+  if (use_lds) {
+    L->W = lay->W;
+    L->lds = 1;
+    L->lds_words = per_wave_lds;
+    const int wpb = (ldsw - leafw) / per_wave_lds;
+    L->wpb = wpb < 1 ? 1 : (wpb > 4 ? 4 : wpb);
+  } else {
+    if (nodew2 > ldsw) return fail(nullptr, TSA_ERR_FIT, "par: node arrays do not fit in LDS");
+    L->W = 0;
+    L->lds = 0;
+    L->lds_words = nodew2;
+    const int wpb = ldsw / nodew2;
+    L->wpb = wpb < 1 ? 1 : (wpb > 4 ? 4 : wpb);
+  }
+  if (ncu > 0 && (long long)nchains < (long long)ncu * L->wpb) {
+    const int spread = (nchains + ncu - 1) / ncu;
+    L->wpb = spread < 1 ? 1 : spread;
+  }
+  *use_lds_out = use_lds;
+  return TSA_OK;
+}
+
+extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t leaf_sc, const tsa_config_t* cfg,
+                          int32_t nchains, tsa_ctx** out) {
+  if (!lay || !leaf || !cfg || !out) return fail(nullptr, TSA_ERR_ARG, "tsa_create: null argument");
+  *out = nullptr;
+  if (check_layout_config(lay, cfg, "tsa_create") != TSA_OK) return TSA_ERR_ARG;
+  if (nchains < 1 || nchains > (1 << 24)) return fail(nullptr, TSA_ERR_ARG, "tsa_create: nchains out of range");
+  for (size_t i = 0; i < (size_t)lay->m * lay->W; i++) {
+    const int used = lay->nlab - 64 * (int)(i % lay->W);  // labels that word i may hold
+    if (used <= 0 ? leaf[i] != 0 : (used < 64 && (leaf[i] >> used) != 0))
+      return fail(nullptr, TSA_ERR_ARG, "tsa_create: leaf label out of range");
+  }
+
+  if (check_host_math() != TSA_OK) return TSA_ERR_LIBM;
 
   tsa_ctx* c = new tsa_ctx();
   c->lay = *lay;
   c->cfg = *cfg;
   c->mode = cfg->mode;
   c->nchains = nchains;
-  fill_params(c, leaf_sc);
+  fill_params(c->lay, c->cfg, leaf_sc, c->P);
 
   int dev = 0;
   int lds_max = 0, ncu = 0, lds_cu = 0;
@@ -354,51 +407,13 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   }
   c->ncu = ncu;
 
-  // kernel choice: chain + leaf table in LDS when it fits and the width is a register width
-  const int nodew = tsa_node_words(lay->nint) + (cfg->par_band > 0 ? ((lay->nint + 3) & ~3) / 2 : 0);
-  const int nodew2 = (nodew + 1) & ~1;
+  bool use_lds = false;
+  if (plan_one_wave(lay, cfg, nchains, lds_max, ncu, &c->L, &use_lds) != TSA_OK) {
+    free_ctx(c);
+    return TSA_ERR_FIT;
+  }
+  c->Wt = c->L.W;
   const int leafw = (lay->m * lay->W + 1) & ~1;
-  const int per_wave_lds = lay->chain_words + nodew2;
-  const int ldsw = (lds_max - 1024) / 8;  // less room for the kernel's static LDS (under 1 KB)
-  const bool reg = !lay->runtime_width;
-  const bool lds_fits = reg && leafw + per_wave_lds <= ldsw;
-  bool use_lds;
-  if (cfg->kernel == TSA_KERNEL_LDS) {
-    if (!lds_fits) {
-      free_ctx(c);
-      return fail(nullptr, TSA_ERR_FIT, "chain does not fit in LDS (or the label width is not a register width)");
-    }
-    use_lds = true;
-  } else if (cfg->kernel == TSA_KERNEL_GLOBAL) {
-    use_lds = false;
-  } else {
-    use_lds = lds_fits;
-  }
-  if (use_lds) {
-    c->Wt = lay->W;
-    c->L.W = lay->W;
-    c->L.lds = 1;
-    c->L.lds_words = per_wave_lds;
-    int wpb = (ldsw - leafw) / per_wave_lds;
-    c->L.wpb = wpb < 1 ? 1 : (wpb > 4 ? 4 : wpb);
-  } else {
-    if (nodew2 > ldsw) {
-      free_ctx(c);
-      return fail(nullptr, TSA_ERR_FIT, "par: node arrays do not fit in LDS");
-    }
-    c->Wt = 0;
-    c->L.W = 0;
-    c->L.lds = 0;
-    c->L.lds_words = nodew2;
-    int wpb = ldsw / nodew2;
-    c->L.wpb = wpb < 1 ? 1 : (wpb > 4 ? 4 : wpb);
-  }
-  // fewer chains than full workgroups on every compute unit: smaller workgroups spread them over all units,
-  // so that a wave shares its unit's LDS, scalar unit and instruction issue with fewer others
-  if (ncu > 0 && (long long)nchains < (long long)ncu * c->L.wpb) {
-    const int spread = (nchains + ncu - 1) / ncu;
-    c->L.wpb = spread < 1 ? 1 : spread;
-  }
   if (cfg->fused_energy) {
     // chains resident at once: workgroups of wpb chains, as many per compute unit as its LDS holds
     const long long smem = ((long long)(use_lds ? leafw : 0) + (long long)c->L.wpb * c->L.lds_words) * 8;
@@ -952,4 +967,111 @@ extern "C" float tsa_host_math(int32_t which, float x) {
   std::call_once(g_fix_once, build_log2_fix);
   const TsaMathTabs T{tsa_exp2_tab_h, g_fix.data(), g_fix.data() + TSA_LOG2FIX_WORDS, tsa_log2_tab_h};
   return tsa_log2f_12(x, T);
+}
+
+// ---------------------------------------------------------------------------------------------------
+// The allocation-free entry point: sweeps (and energies) of a population the caller holds in device memory
+// ---------------------------------------------------------------------------------------------------
+// Scratch of tsa_sweeps_noalloc: the statistic counters (TSA_NSTAT_ALL x TSA_STAT_SLOTS words), then the node
+// costs (float) and masked sizes (uint16) the sweep kernel leaves for the fold kernel, nint4 per chain each.
+// Every GPU the library runs on holds its own copy until the process ends; every call on a GPU shares it.
+#define TSA_SCRATCH_BYTES (32u << 20)
+static __device__ __align__(256) unsigned char scratch[TSA_SCRATCH_BYTES];
+// The log2f correction table and its summary bitmap (what tsa_create copies into every context), filled once
+// per device by the first call there.
+static __device__ __align__(256) uint32_t log2_fix_table[TSA_LOG2FIX_WORDS + TSA_LOG2MAP_WORDS];
+
+namespace {
+struct StaticDevice {
+  bool ready = false;
+  unsigned char* scratch = nullptr;  // device address of `scratch` on this device
+  uint32_t* fix = nullptr;           // device address of `log2_fix_table` on this device
+  int lds_max = 0, ncu = 0;
+};
+constexpr int kMaxDevices = 64;
+StaticDevice g_static[kMaxDevices];
+std::mutex g_static_mu;
+constexpr size_t kCounterBytes = ((size_t)TSA_NSTAT_ALL * TSA_STAT_SLOTS * 8 + 255) & ~(size_t)255;
+}  // namespace
+
+// First call on the current device: the device addresses of the two static arrays (the arrays' names are
+// host-side stand-ins, never passed to a kernel), the correction table copied in, the device's LDS and
+// compute-unit counts.
+static int static_device(StaticDevice** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(nullptr, TSA_ERR_HIP, std::string("no HIP device: ") + hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(nullptr, TSA_ERR_ARG, "tsa_sweeps_noalloc: device index too large");
+  std::lock_guard<std::mutex> g(g_static_mu);
+  StaticDevice& d = g_static[dev];
+  if (!d.ready) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return fail(nullptr, TSA_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+    void* f = nullptr;
+    e = hipGetSymbolAddress(&f, HIP_SYMBOL(log2_fix_table));
+    if (e != hipSuccess)
+      return fail(nullptr, TSA_ERR_HIP, std::string("hipGetSymbolAddress(log2_fix_table): ") + hipGetErrorString(e));
+    static_assert(sizeof(log2_fix_table) == (TSA_LOG2FIX_WORDS + TSA_LOG2MAP_WORDS) * 4, "table size");
+    if (g_fix.size() * 4 != sizeof(log2_fix_table)) return fail(nullptr, TSA_ERR_ARG, "log2f table size");
+    e = hipMemcpy(f, g_fix.data(), g_fix.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&d.lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&d.ncu, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return fail(nullptr, TSA_ERR_HIP, std::string("tsa_sweeps_noalloc set-up: ") + hipGetErrorString(e));
+    d.scratch = static_cast<unsigned char*>(p);
+    d.fix = static_cast<uint32_t*>(f);
+    d.ready = true;
+  }
+  *out = &d;
+  return TSA_OK;
+}
+
+extern "C" int tsa_sweeps_noalloc(const tsa_layout_t* lay, const tsa_config_t* cfg, int32_t leaf_sc,
+                                  const uint64_t* leaf_dev, uint64_t* population_dev, int32_t nchains, int32_t order,
+                                  float beta, uint32_t sweep0, int32_t nsweeps, float* lc_dev, int32_t* sc_dev,
+                                  int32_t* ns_dev, uint64_t* stats_dev, void* stream) {
+  if (!lay || !cfg || !leaf_dev || !population_dev)
+    return fail(nullptr, TSA_ERR_ARG, "tsa_sweeps_noalloc: null argument");
+  if ((lc_dev == nullptr) != (sc_dev == nullptr) || (lc_dev == nullptr) != (ns_dev == nullptr))
+    return fail(nullptr, TSA_ERR_ARG, "tsa_sweeps_noalloc: lc, sc and ns are all given or all null");
+  if (check_layout_config(lay, cfg, "tsa_sweeps_noalloc") != TSA_OK) return TSA_ERR_ARG;
+  if (lay->runtime_width)
+    return fail(nullptr, TSA_ERR_ARG, "tsa_sweeps_noalloc: register-width layouts only (at most 512 labels, not wide)");
+  if (order != TSA_ORDER_PAR && order != TSA_ORDER_PREORDER) return fail(nullptr, TSA_ERR_ARG, "--order par|preorder");
+  if (nsweeps < 0) return fail(nullptr, TSA_ERR_ARG, "tsa_sweeps_noalloc: nsweeps < 0");
+  if (nchains < 1 || nchains > (1 << 24)) return fail(nullptr, TSA_ERR_ARG, "tsa_sweeps_noalloc: nchains out of range");
+  const size_t nint4 = (size_t)((lay->nint + 3) & ~3);
+  const size_t need = kCounterBytes + (lc_dev ? (size_t)nchains * nint4 * 6 : 0);
+  if (need > TSA_SCRATCH_BYTES)
+    return fail(nullptr, TSA_ERR_ARG,
+                "tsa_sweeps_noalloc: " + std::to_string(nchains) + " chains x " + std::to_string(lay->nint) +
+                    " nodes need " + std::to_string(need) + " bytes of scratch, more than its " +
+                    std::to_string(TSA_SCRATCH_BYTES) + " (fewer chains per call, or no energies)");
+  if (check_host_math() != TSA_OK) return TSA_ERR_LIBM;
+  StaticDevice* d = nullptr;
+  if (static_device(&d) != TSA_OK) return TSA_ERR_HIP;
+  TsaLaunch L{};
+  bool in_lds = false;
+  if (plan_one_wave(lay, cfg, nchains, d->lds_max, d->ncu, &L, &in_lds) != TSA_OK) return TSA_ERR_FIT;
+  TsaKParams P;
+  fill_params(*lay, *cfg, leaf_sc, P);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  unsigned long long* counters = reinterpret_cast<unsigned long long*>(d->scratch);
+  float* cost = reinterpret_cast<float*>(d->scratch + kCounterBytes);
+  uint16_t* z = reinterpret_cast<uint16_t*>(d->scratch + kCounterBytes + (size_t)nchains * nint4 * 4);
+  // the counters start at zero on every call (the scratch keeps the last call's contents)
+  hipError_t e = tsa_launch_zero(counters, TSA_NSTAT_ALL * TSA_STAT_SLOTS, st);
+  if (e == hipSuccess && nsweeps > 0) {
+    const TsaEnergyOut eo{nullptr, nullptr, nullptr, lc_dev ? cost : nullptr, lc_dev ? z : nullptr, nullptr};
+    e = tsa_launch_sweeps(L, cfg->mode, order, P, population_dev, leaf_dev, d->fix, nchains, beta, sweep0, nsweeps,
+                          counters, eo, st);
+    if (e == hipSuccess && lc_dev)
+      e = tsa_launch_fold(P, population_dev, leaf_dev, d->fix, cost, z, nchains, lc_dev, sc_dev, ns_dev, st);
+  } else if (e == hipSuccess && lc_dev) {
+    // no sweeps: the energies of the population as it stands
+    e = tsa_launch_energy(L.W, cfg->mode, P, population_dev, leaf_dev, d->fix, nchains, lc_dev, sc_dev, ns_dev, st);
+  }
+  if (e == hipSuccess && stats_dev) e = tsa_launch_sum_stats(counters, reinterpret_cast<unsigned long long*>(stats_dev), st);
+  if (e != hipSuccess) return fail(nullptr, TSA_ERR_HIP, std::string("tsa_sweeps_noalloc launch: ") + hipGetErrorString(e));
+  return TSA_OK;
 }

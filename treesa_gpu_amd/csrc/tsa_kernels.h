@@ -110,6 +110,10 @@ hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int n
 hipError_t tsa_launch_track_init(TsaTrackState* st, unsigned long long* ticks0, hipStream_t stream);
 hipError_t tsa_launch_copy(const uint64_t* src, uint64_t* dst, const int* anc, int nchains, int chain_words,
                            hipStream_t st);
+// n zeroed 64-bit words, by a kernel.
+hipError_t tsa_launch_zero(unsigned long long* p, int n, hipStream_t st);
+// out[k] = the sum of counter k's TSA_STAT_SLOTS slots, k < TSA_NSTAT.
+hipError_t tsa_launch_sum_stats(const unsigned long long* slots, unsigned long long* out, hipStream_t st);
 
 // ---------------------------------------------------------------------------------------------------
 // Wide path (tsa_wide.hip): par-order sweeps and energies of runtime-width chains, label sets streamed

@@ -866,6 +866,32 @@ hipError_t tsa_launch_track_init(TsaTrackState* stt, unsigned long long* ticks0,
   return hipGetLastError();
 }
 
+// Clears n 64-bit words (a kernel rather than hipMemsetAsync, so that the call can sit in a captured graph).
+__global__ void k_zero_u64(unsigned long long* __restrict__ p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0ull;
+}
+
+// out[k] = sum of the TSA_STAT_SLOTS slots of counter k, k < TSA_NSTAT (one wave).
+__global__ void k_sum_stats(const unsigned long long* __restrict__ slots, unsigned long long* __restrict__ out) {
+  const int k = threadIdx.x;
+  if (k >= TSA_NSTAT) return;
+  unsigned long long s = 0;
+  for (int j = 0; j < TSA_STAT_SLOTS; j++) s += slots[k * TSA_STAT_SLOTS + j];
+  out[k] = s;
+}
+
+hipError_t tsa_launch_zero(unsigned long long* p, int n, hipStream_t st) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(k_zero_u64, dim3((n + 255) / 256), dim3(256), 0, st, p, n);
+  return hipGetLastError();
+}
+
+hipError_t tsa_launch_sum_stats(const unsigned long long* slots, unsigned long long* out, hipStream_t st) {
+  hipLaunchKernelGGL(k_sum_stats, dim3(1), dim3(64), 0, st, slots, out);
+  return hipGetLastError();
+}
+
 hipError_t tsa_launch_copy(const uint64_t* src, uint64_t* dst, const int* anc, int nchains, int chain_words,
                            hipStream_t st) {
   hipLaunchKernelGGL(k_copy, dim3(nchains), dim3(256), 0, st, reinterpret_cast<const uint4*>(src),
