@@ -16,17 +16,33 @@ resident in HBM, until the last level's energies are back), after --bench-warmup
 value = K * nchains * (m - 1) / that wall time (whole job), of the median of R runs (default 5; their results are
 identical, their spread is reported as "repetitions").
 kernel_visits_per_s = the reference's own definition (bench/throughput.py:64-70): node visits over the
-event-timed sweep kernels only.  roofline: algorithmic bytes of the sweep kernel per launch (5 label sets of
-W words + 8 B of children per proposal, W words + 8 B written per accept, 4 B per visit without a rule, from
-the kernel's own counters) over its average event-timed launch duration, against the 8 TB/s HBM peak.
-cpu_baseline: the reference's own CPU port (csrc/cpu_ref.h, oracle/_ref/ref_harness) on one core, over a
-bounded sample of the same workload (a subset of the chains, every level).
+event-timed sweep kernels only.
+
+roofline: of the sweep kernel, per launch, with the resource that bounds it.  Chains staged in LDS (c1-c3):
+bound "lds", achieved = the algorithmic bytes of the proposals (5 label sets of W words + 8 B of children per
+proposal, W words + 8 B written per accept, 4 B per visit without a rule, plus the slice steps' tree passes;
+from the kernel's own counters), all served from LDS, over the average event-timed launch, against the LDS read
+peak measured on this GPU by bin/lds_peak; beside it the same kernel's measured HBM traffic against 8 TB/s and
+its VALUBusy from the committed rocprof summary.  Label sets streamed from HBM (c4, c5 --no-sum): bound "hbm",
+the algorithmic bytes against 8 TB/s.  The chunk-summary kernel (c5 default) reads only the nonzero 16-byte
+chunks: achieved = the bytes it loaded (its chunk counters), never the dense per-proposal figure.
+cpu_baseline: the reference's own CPU port (csrc/cpu_ref.h, oracle/_ref/ref_harness) under OpenMP on the host's
+cores (up to 16, the GPU's share of the host), over a bounded sample of the same workload (a subset of the
+chains, every level); the one-core rate beside it.  Slicing runs (c3) time the oracle port (the reference's CPU
+port has no slice moves).
+full_schedule (when --steps is shorter than the workload's schedule): the whole schedule, once.
+quality: best log2 tc at fixed wall time on random 3-SAT n=100 against the reference's published figure
+(docs/REPORT.md:399-400: population annealing, 576 chains x 200 sweeps per level, tc 66.51 in 2.1 s, sc target
+30, Quadro RTX 6000): the same instance, start tree (its omeco greedy tree), schedule (0.01:0.05:15, 300 levels)
+and sc target, 8192 chains with as many sweeps per level as fit in 2.1 s of end-to-end wall time (the binary's
+whole process, as the reference's figure includes its process start and I/O).
 long_variant (c1 and c5, whose literal runs are 1.1e7 and 5.9e6 node visits): the same workload with its schedule
 repeated ten times, so that the level loop's fixed costs are spread over more levels; reported beside value.
 """
 import argparse
 import json
 import os
+import platform
 import subprocess
 import sys
 import tempfile
@@ -145,6 +161,52 @@ def measured_traffic(cfgname, path="dense"):
     return None
 
 
+def profile_value(cfgname, key, path="dense"):
+    """A "key: value" line of the committed rocprof summary of this workload and path (None when absent)."""
+    f = PROFILES.get((cfgname, path))
+    if not f or not os.path.exists(os.path.join(ROOT, "profiles", f)):
+        return None
+    with open(os.path.join(ROOT, "profiles", f)) as fh:
+        for line in fh:
+            if line.strip().startswith(key + ":"):
+                return float(line.split(":")[1])
+    return None
+
+
+_lds_peak = None
+
+
+def lds_peak_gbs():
+    """LDS read bandwidth of this GPU, measured once per run by bin/lds_peak (ds_read_b128 on every compute
+    unit)."""
+    global _lds_peak
+    if _lds_peak is None:
+        p = subprocess.run([os.path.join(ROOT, "treesa_gpu_amd", "bin", "lds_peak")], check=True, capture_output=True,
+                           text=True)
+        _lds_peak = json.loads(p.stdout.strip().splitlines()[-1])
+    return _lds_peak
+
+
+def host_facts():
+    """CPU model, logical CPUs and the C library of this host."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    libc = " ".join(platform.libc_ver()) or "unknown"
+    return {"cpu_model": model, "nproc": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0)), "libc": libc}
+
+
+def cpu_threads():
+    """Threads for the CPU baseline: the CPUs this process may use, at most 16 (one GPU's share of its host)."""
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
 def cpu_port_worker(cfgname, nsample):
     """One-thread timing of the oracle port (slice moves included) on nsample chains; prints seconds."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
@@ -162,9 +224,8 @@ def cpu_port_worker(cfgname, nsample):
     print(time.perf_counter() - t0)
 
 
-def cpu_baseline(cfgname, C, inst, trees, betas, nsample):
-    """The reference's own CPU port (oracle/_ref, csrc/cpu_ref.h) on one core over nsample chains and every
-    level; configurations with slice moves (which the reference's CPU port lacks) time the oracle port."""
+def cpu_time(cfgname, C, inst, trees, betas, nsample, threads):
+    """Seconds the CPU port takes for nsample chains over every level on `threads` cores, and its kind."""
     ref = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
     if os.path.exists(ref) and not C["slicing"]:
         with tempfile.TemporaryDirectory() as td:
@@ -176,18 +237,30 @@ def cpu_baseline(cfgname, C, inst, trees, betas, nsample):
             bs = ",".join(repr(b) for b in betas)
             args = [ref, "-i", os.path.join(DATA, C["inst"] + ".txt"), "--tree", tf, "--chains", str(nsample),
                     "--niters", str(C["niters"]), "--betas", bs, "--order", C["order"], "--mode", "tc",
-                    "--sc-target", str(C["sc_target"]), "--seed", "1", "--timing"]
+                    "--sc-target", str(C["sc_target"]), "--seed", "1", "--timing", "--threads", str(threads)]
             out = json.loads(subprocess.run(args, check=True, capture_output=True, text=True).stdout)
-            secs, kind = out["seconds"], "reference"
-    else:
-        env = dict(os.environ, OMP_NUM_THREADS="1")
-        p = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-port-worker", cfgname, "--cpu-chains",
-                            str(nsample)], check=True, capture_output=True, text=True, env=env)
-        secs, kind = float(p.stdout.strip().splitlines()[-1]), "port"
-    visits = nsample * len(betas) * C["niters"] * (inst.m - 1)
-    return dict(value=visits / secs, unit="node visits/s", cores=1, kind=kind,
-                sample=f"{nsample} of {C['nchains']} chains x {len(betas) * C['niters']} sweeps "
-                       f"({visits:.3e} visits, {secs:.1f} s)")
+            return out["seconds"], "reference"
+    env = dict(os.environ, OMP_NUM_THREADS=str(threads))
+    p = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-port-worker", cfgname, "--cpu-chains",
+                        str(nsample)], check=True, capture_output=True, text=True, env=env)
+    return float(p.stdout.strip().splitlines()[-1]), "port"
+
+
+def cpu_baseline(cfgname, C, inst, trees, betas, nsample):
+    """The reference's own CPU port (oracle/_ref, csrc/cpu_ref.h) over a sample of the workload's chains and every
+    level: under OpenMP on every usable core (up to 16) with nsample chains per core, and on one core with nsample
+    chains; configurations with slice moves (which the reference's CPU port lacks) time the oracle port."""
+    threads = cpu_threads()
+    per_level = len(betas) * C["niters"] * (inst.m - 1)
+    n_all = min(C["nchains"], nsample * threads)
+    secs, kind = cpu_time(cfgname, C, inst, trees, betas, n_all, threads)
+    secs1, _ = cpu_time(cfgname, C, inst, trees, betas, nsample, 1)
+    return dict(value=n_all * per_level / secs, unit="node visits/s", cores=threads, kind=kind,
+                sample=f"{n_all} chains (chain slots 0..{n_all - 1} of this workload's start) x "
+                       f"{len(betas) * C['niters']} sweeps on {threads} threads: {n_all * per_level:.3e} visits in "
+                       f"{secs:.1f} s",
+                one_core={"value": nsample * per_level / secs1, "sample": f"{nsample} chains, {secs1:.1f} s"},
+                host=host_facts())
 
 
 def copy_calibration(cfgname, reps=10):
@@ -240,6 +313,38 @@ def run_binary(C, trees, betas, steps, warmup, scheme=None, extra=()):
             return json.load(f)
 
 
+def quality_at_wall(budget_s, visits_per_s):
+    """Best log2 tc reached within budget_s of end-to-end wall time on random 3-SAT n=100 (population annealing,
+    sc target 30, the omeco greedy start, the 300-level schedule 0.01:0.05:15), with 8192 chains and as many
+    sweeps per level as fit; the reference's published figure for the same instance and settings beside it."""
+    inst = host.Instance(os.path.join(DATA, "sat100.txt"))
+    nchains, nlev = 8192, 300
+    betas = [float(np.float32(0.01 + i * 0.05)) for i in range(nlev)]
+    C = dict(inst="sat100", nchains=nchains, niters=1, sc_target=30.0, order="par", scheme="pa", slicing=False)
+    trees = inst.read_trees(os.path.join(DATA, "sat100.tree"))
+    # sweeps per level from the measured sweep rate, leaving about 0.7 s for the process, the device set-up and
+    # the population steps; fewer while a run does not fit
+    niters = max(1, int((budget_s - 0.7) * visits_per_s / (nchains * nlev * (inst.m - 1))))
+    tries = []
+    while True:
+        C["niters"] = niters
+        t0 = time.perf_counter()
+        r = run_binary(C, trees, betas, nlev, 0, "pa")
+        wall = time.perf_counter() - t0
+        tries.append({"niters": niters, "wall_s": wall, "tc": r["tc"]})
+        if wall <= budget_s or niters == 1 or len(tries) == 4:
+            break
+        niters = max(1, int(niters * budget_s / wall * 0.95))
+    return {"metric": "best log2 tc at fixed wall time", "instance": "random 3-SAT n=100 (sat100.txt)",
+            "budget_s": budget_s, "wall_s": wall, "within_budget": wall <= budget_s, "tc": r["tc"], "sc": r["sc"],
+            "config": f"population annealing, {nchains} chains x {niters} sweeps per level, 300 levels "
+                      f"0.01:0.05:15, sc target 30, omeco greedy start, seed 1 (end-to-end wall of the binary)",
+            "tries": tries,
+            "reference": {"tc": 66.51, "sc": 62, "wall_s": 2.1, "hardware": "Quadro RTX 6000",
+                          "config": "population annealing, 576 chains x 200 sweeps per level, same schedule, "
+                                    "sc target and start", "source": "docs/REPORT.md:399-400"}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -263,6 +368,8 @@ def main():
                          "c5, none otherwise; 0 or 1: none)")
     ap.add_argument("--no-overlap", action="store_true",
                     help="fold and selection of a level on the sweep's stream, not beside the next sweep")
+    ap.add_argument("--no-full", action="store_true", help="no full-schedule record when --steps is shorter")
+    ap.add_argument("--no-quality", action="store_true", help="no best-tc-at-fixed-wall-time run (c2)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run identity population copies of the workload (counter calibration)")
     a = ap.parse_args()
@@ -300,14 +407,31 @@ def main():
         B = algorithmic_bytes(st, lay.W, inst.m - 1, C["slicing"], slice_steps) / steps
         dur = r["kernel_s"] / steps
         desc = r.get("hip_kernel") or ""
-        roof = {"bound": "hbm", "achieved": B / dur / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": B / dur / 1e9 / HBM_PEAK_GBS, "traffic": measured_traffic(a.config, label_path(desc)),
-                "kernel": kernel_label(desc, order), "bytes_per_launch": B, "avg_launch_ms": dur * 1e3}
-        if r.get("sum_chunks", 0) > 0:
-            # the chunk-summary kernel loads only nonzero chunks: its algorithmic bytes (the same per-proposal
-            # figure as every kernel) exceed what it moves, so achieved can pass the HBM peak; traffic is the
-            # measured HBM bytes per launch
-            roof["loaded_bytes_per_launch"] = loaded_bytes(st, (r["sum_chunks"], r["sum_xchunks"])) / steps
+        path = label_path(desc)
+        traffic = measured_traffic(a.config, path)
+        roof = {"kernel": kernel_label(desc, order), "algorithmic_bytes_per_launch": B, "avg_launch_ms": dur * 1e3,
+                "traffic": traffic}
+        if desc.startswith("lds"):
+            # label sets served from LDS: the LDS read peak of this GPU bounds the proposals' reads; HBM carries
+            # only the staging of the records, and VALU issue is the resource the kernel actually saturates
+            peak = lds_peak_gbs()
+            roof.update(bound="lds", achieved=B / dur / 1e9, peak=peak["lds_read_GBps"], unit="GB/s",
+                        frac=B / dur / 1e9 / peak["lds_read_GBps"],
+                        peak_source="bin/lds_peak on this GPU: ds_read_b128 from every wave of every compute unit")
+            if traffic is not None:
+                roof["hbm"] = {"achieved": traffic / dur / 1e9, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                               "frac": traffic / dur / 1e9 / HBM_PEAK_GBS}
+            vb = profile_value(a.config, "valu_busy", path)
+            if vb is not None:
+                roof["valu_busy"] = vb / 100.0
+        elif r.get("sum_chunks", 0) > 0:
+            # the chunk-summary kernel reads only the nonzero chunks of its sets: what it loaded, from its counters
+            L = loaded_bytes(st, (r["sum_chunks"], r["sum_xchunks"])) / steps
+            roof.update(bound="hbm", achieved=L / dur / 1e9, peak=HBM_PEAK_GBS, unit="GB/s",
+                        frac=L / dur / 1e9 / HBM_PEAK_GBS, loaded_bytes_per_launch=L)
+        else:
+            roof.update(bound="hbm", achieved=B / dur / 1e9, peak=HBM_PEAK_GBS, unit="GB/s",
+                        frac=B / dur / 1e9 / HBM_PEAK_GBS)
         return r, roof
 
     r, roof = measure(extra)
@@ -344,6 +468,15 @@ def main():
         res["long_variant"] = {"levels": lsteps, "value": lv / lr["t_anneal"], "ms_per_step": lr["t_anneal"] * 1e3 / lsteps,
                                "kernel_visits_per_s": lv / lr["kernel_s"], "best_tc": lr["tc"],
                                "note": f"the same workload with its {steps}-level schedule run {long_k} times in a row"}
+    if steps < C["levels"] and not a.no_full:
+        # the timed steps are the first levels of the schedule: the whole schedule, once, beside them
+        fsteps = C["levels"]
+        fv = fsteps * C["niters"] * nchains * (inst.m - 1)
+        fr = run_binary(C, trees, betas, fsteps, a.warmup, a.scheme, extra)
+        res["full_schedule"] = {"levels": fsteps, "value": fv / fr["t_anneal"], "ms_per_step": fr["t_anneal"] * 1e3 / fsteps,
+                                "kernel_visits_per_s": fv / fr["kernel_s"], "best_tc": fr["tc"], "best_sc": fr["sc"]}
+    if a.config == "c2" and not a.no_quality:
+        res["quality"] = quality_at_wall(2.1, res["kernel_visits_per_s"])
     if not a.no_cpu:
         res["cpu_baseline"] = cpu_baseline(a.config, C, inst, trees, betas, min(a.cpu_chains or C["cpu_chains"], nchains))
     print(json.dumps(res))

@@ -78,7 +78,7 @@ static void rand_tree(int m, uint64_t seed, std::vector<int>& L, std::vector<int
 
 int main(int argc, char** argv) {
   std::string inst, tree, betas = "0.2:0.7:7", order = "par";
-  int chains = 4, niters = 4, mode = 0, random_slices = 0, par_follow = 0, par_band = 0, timing = 0;
+  int chains = 4, niters = 4, mode = 0, random_slices = 0, par_follow = 0, par_band = 0, timing = 0, threads = 1;
   bool random_trees = false;
   double sc_target = 24, sc_weight = 1;
   uint64_t seed = 7;
@@ -105,6 +105,7 @@ int main(int argc, char** argv) {
     else if (a == "--par-follow") par_follow = 1;
     else if (a == "--par-band") par_band = std::stoi(nx());
     else if (a == "--timing") timing = 1;
+    else if (a == "--threads") threads = std::max(1, std::stoi(nx()));
     else { fprintf(stderr, "unknown argument %s\n", a.c_str()); return 1; }
   }
   for (int d = 0; d < 64; d++) h_lse_tab[d] = (float)std::log2(1.0 + std::exp2(-(double)d));
@@ -183,11 +184,13 @@ int main(int argc, char** argv) {
   P.v2_small_rank = (int)hm[7];
   P.v2_lsmall_cell = (float)std::log2(hm[8]);
 
-  printf("{\"chains\": [");
-  double secs = 0;
-  long long tot_prop = 0;
+  // chains are independent: with --threads N their records are built and swept under OpenMP, and --timing
+  // reports the wall time of the sweep phase of all of them (one thread: the sum over chains)
+  std::vector<RefTree> trees(chains);
+  std::vector<long long> nprop(chains, 0), nacc(chains, 0);
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
   for (int c = 0; c < chains; c++) {
-    RefTree T;
+    RefTree& T = trees[c];
     T.m = m;
     T.left.assign(2 * m - 1, -1);
     T.right.assign(2 * m - 1, -1);
@@ -221,8 +224,12 @@ int main(int argc, char** argv) {
       for (int l = 0; l < nlab; l++)
         if (cnt[v][l] > 0 && (cnt[v][l] < total[l] || open[l])) T.labels[v].push_back(l);
     }
+  }
+  const auto t0 = std::chrono::steady_clock::now();
+#pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
+  for (int c = 0; c < chains; c++) {
+    RefTree& T = trees[c];
     long long np = 0, na = 0;
-    const auto t0 = std::chrono::steady_clock::now();
     for (size_t lev = 0; lev < bs.size(); lev++)
       for (int it = 0; it < niters; it++) {
         const uint32_t sw = (uint32_t)(lev * niters + it);
@@ -236,8 +243,15 @@ int main(int argc, char** argv) {
           else ref_optimize_subtree<2>(T, 2 * m - 2, bs[lev], sw, (uint32_t)c, P, np, na);
         }
       }
-    secs += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
-    tot_prop += np;
+    nprop[c] = np;
+    nacc[c] = na;
+  }
+  const double secs = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  long long tot_prop = 0;
+  printf("{\"chains\": [");
+  for (int c = 0; c < chains; c++) {
+    const RefTree& T = trees[c];
+    tot_prop += nprop[c];
     // FNV-1a over the internal label sets as 64-bit words (W = ceil(nlab / 64)), node by node
     const int W = (nlab + 63) / 64;
     uint64_t h = 1469598103934665603ULL;
@@ -251,12 +265,12 @@ int main(int argc, char** argv) {
         }
     }
     printf("%s{\"chain\": %d, \"nprop\": %lld, \"nacc\": %lld, \"labels_fnv\": \"%016" PRIx64 "\", \"children\": [",
-           c ? ", " : "", c, np, na, h);
+           c ? ", " : "", c, nprop[c], nacc[c], h);
     for (int v = m; v < 2 * m - 1; v++) printf("%s%d,%d", v > m ? "," : "", T.left[v], T.right[v]);
     printf("]}");
   }
   printf("]");
-  if (timing) printf(", \"seconds\": %.6f, \"proposals\": %lld", secs, tot_prop);
+  if (timing) printf(", \"seconds\": %.6f, \"proposals\": %lld, \"threads\": %d", secs, tot_prop, threads);
   printf("}\n");
   return 0;
 }
