@@ -368,6 +368,8 @@ def main():
                          "c5, none otherwise; 0 or 1: none)")
     ap.add_argument("--no-overlap", action="store_true",
                     help="fold and selection of a level on the sweep's stream, not beside the next sweep")
+    ap.add_argument("--draw-waves", type=int, default=0, choices=(-1, 0, 1),
+                    help="pre-order: helper waves draw ahead (1), each visit draws (-1), automatic (0)")
     ap.add_argument("--no-full", action="store_true", help="no full-schedule record when --steps is shorter")
     ap.add_argument("--no-quality", action="store_true", help="no best-tc-at-fixed-wall-time run (c2)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -388,7 +390,8 @@ def main():
     extra = (["--wpc", str(2 * a.wide_waves)] if a.wide_waves else []) + \
         (["--wide-wgs", str(a.wide_wgs)] if a.wide_wgs else []) + \
         (["--wide-lanes", str(a.wide_lanes)] if a.wide_lanes else []) + \
-        {"auto": [], "on": ["--sums"], "off": ["--no-sum"]}[a.sums] + (["--no-overlap"] if a.no_overlap else [])
+        {"auto": [], "on": ["--sums"], "off": ["--no-sum"]}[a.sums] + (["--no-overlap"] if a.no_overlap else []) + \
+        (["--draw-waves", str(a.draw_waves)] if a.draw_waves else [])
     visits = steps * C["niters"] * nchains * (inst.m - 1)
 
     def measure(extra_args):

@@ -94,6 +94,11 @@ typedef struct tsa_config_t {
    * kernel, without slice moves): 0 = automatic, the fold and the selection of that sweep's snapshot run on
    * a second stream beside the next sweep; -1 = never, they run on the sweep's stream.  Results do not change */
   int32_t track_overlap;
+  /* pre-order sweeps: one chain per workgroup, whose three helper waves draw every internal node's random
+   * numbers (the rule word and the Metropolis threshold) for the next sweep while the first wave sweeps, instead
+   * of each visit drawing its own: 0 = automatic (on for at most one chain per compute unit, where the sweeping
+   * wave's dependent steps bound the sweep and three SIMDs idle), 1 = on, -1 = off.  Results do not change */
+  int32_t draw_waves;
 } tsa_config_t;
 
 typedef struct tsa_ctx tsa_ctx;

@@ -29,7 +29,7 @@ def leaf_sets(m, ixs, W):
 class Case:
     def __init__(self, inst, order, mode, init="greedy", random_slices=0, par_follow=False, par_band=0, slicing=False,
                  slice_moves=1, slice_every=1, nchains=NCHAINS, kernel=capi.KERNEL_AUTO, wide=False, seed=None,
-                 sc_target=None, wide_waves=0, wide_wgs=0, sums=0, lanes=0, data=None):
+                 sc_target=None, wide_waves=0, wide_wgs=0, sums=0, lanes=0, data=None, draw_waves=0):
         """inst names a fixture; data = (m, nlab, ixs, iy) gives an instance directly (then init must be a
         start-tree kind without fixture, e.g. "random")."""
         self.inst, self.order = inst, order
@@ -45,7 +45,8 @@ class Case:
         self.cfg = capi.make_config(mode=mode, sc_target=common.CHECK_SC_TARGET if sc_target is None else sc_target,
                                     seed=seed, slicing=sl, slice_moves=slice_moves if slicing else 0,
                                     slice_every=slice_every, par_follow=par_follow, par_band=par_band, kernel=kernel,
-                                    wide_waves=wide_waves, wide_wgs=wide_wgs, sums=sums, wide_lanes=lanes)
+                                    wide_waves=wide_waves, wide_wgs=wide_wgs, sums=sums, wide_lanes=lanes,
+                                    draw_waves=draw_waves)
         self.leaf_sc = max(len(x) for x in ixs)
         self.P = orc.params_from_config(self.cfg, self.leaf_sc, nlab)
         self.leaf = leaf_sets(m, ixs, self.lay.W)
@@ -55,7 +56,8 @@ class Case:
     def run_gpu(self, betas=common.CHECK_BETAS, niters=common.CHECK_NITERS):
         print(f"[gpu] {self.inst} {self.order} mode={self.cfg.mode} slicing={self.cfg.slicing} "
               f"kernel={self.cfg.kernel} W={self.lay.W} chains={self.nchains} wide_waves={self.cfg.wide_waves} "
-              f"wide_wgs={self.cfg.wide_wgs} sums={self.cfg.sums} lanes={self.cfg.wide_lanes}", flush=True)
+              f"wide_wgs={self.cfg.wide_wgs} sums={self.cfg.sums} lanes={self.cfg.wide_lanes} "
+              f"draw_waves={self.cfg.draw_waves}", flush=True)
         with capi.Context(self.lay, self.leaf, self.leaf_sc, self.cfg, self.nchains) as ctx:
             ctx.upload(self.pop0)
             for lev, b in enumerate(betas):
@@ -111,6 +113,21 @@ def test_lds_and_global_kernels_agree(inst, order, mode):
     assert ga[3].startswith("lds") and gb[3].startswith("global")
     assert np.array_equal(ga[0], gb[0])
     compare(a, ga, a.run_oracle())
+
+
+# Pre-order sweeps with helper waves drawing each sweep's Philox words and Metropolis thresholds ahead
+# (accept iff -beta*dE >= threshold) against each visit drawing its own and evaluating expf: both equal the
+# oracle bit for bit, with the helpers forced on beyond one chain per compute unit and off below it, in every
+# energy mode, on LDS and global-memory records, with slice moves.
+@pytest.mark.parametrize("inst,mode,nchains,draw,kernel,slicing", [
+    ("sat100", "tc", 300, 1, capi.KERNEL_AUTO, False), ("sat100", "tc", 300, -1, capi.KERNEL_AUTO, False),
+    ("sat100", "gpu", 40, -1, capi.KERNEL_AUTO, False), ("lat14", "h100", 40, 1, capi.KERNEL_AUTO, False),
+    ("reg3_250", "tc", 40, 1, capi.KERNEL_GLOBAL, False), ("sat60", "tc", 40, 1, capi.KERNEL_AUTO, True)])
+def test_draw_waves_match_oracle(inst, mode, nchains, draw, kernel, slicing):
+    case = Case(inst, "preorder", mode, nchains=nchains, kernel=kernel, draw_waves=draw, slicing=slicing,
+                sc_target=20 if slicing else None)
+    gpu = case.run_gpu()
+    compare(case, gpu, case.run_oracle())
 
 
 @pytest.mark.parametrize("inst,order,mode,moves,every", [("sat100", "par", "tc", 1, 1), ("sat100", "preorder", "tc", 2, 1),

@@ -28,6 +28,18 @@ def test_restated_expf_exp2f_log2_core_exhaustive(tmp_path):
     assert 0 < fixed < (1 << 23) // 20  # the correction table is sparse: about 1 % of [1, 2)
 
 
+def test_metropolis_threshold_exhaustive(tmp_path):
+    """Pre-order sweeps with their random numbers drawn ahead test x >= T(u) instead of u < expf(x): the same
+    decision for every x when the restated expf is non-decreasing over all 2^32 floats and T(u) is the least float
+    whose expf exceeds u, for every uniform u = k * 2^-24 the kernels draw (tests/threshold_check.cpp)."""
+    exe = str(tmp_path / "threshold_check")
+    subprocess.run(["g++", "-O2", "-fopenmp", "-ffp-contract=off", "-I", os.path.join(ROOT, "treesa_gpu_amd", "csrc"),
+                    os.path.join(HERE, "threshold_check.cpp"), "-o", exe], check=True)
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=600)
+    drops, bad, nans = map(int, r.stdout.split())
+    assert (drops, bad, nans) == (0, 0, 0), r.stdout
+
+
 def test_library_host_math_equals_libm():
     lib = capi.load()
     libm = ctypes.CDLL("libm.so.6")

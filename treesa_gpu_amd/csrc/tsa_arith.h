@@ -199,6 +199,64 @@ TSA_HD bool tsa_metropolis(uint32_t r, float beta, float dE, const uint64_t* exp
   return u < tsa_expf_t(-beta * dE, exp2tab);
 }
 
+// The Metropolis test as a threshold on x = -beta * dE: tsa_expf is non-decreasing over the floats (checked on
+// every float), so {x : expf(x) > u} is every float from its least element T(u) up and u < expf(x) exactly when
+// x >= T(u).  For u = (r >> 8) * 2^-24 > 0 the set's least element lies below zero, where a float's bit pattern
+// grows as the float falls.  The search starts at the float nearest log(u + ulp(u) / 2) (where a correctly
+// rounded expf would first exceed u), doubles its step in bit patterns until it brackets the boundary, then
+// halves the bracket: one or two expf evaluations for most u, about 2 log2 of the distance in ulps near u = 1
+// (where t is much finer than expf's output).  NaN for u = 0 or a search that does not settle within its
+// bound: the caller then evaluates expf itself.
+TSA_HD float tsa_accept_threshold(uint32_t r, const uint64_t* exp2tab) {
+  const float nan = tsa_ffrom(0x7fc00000u);
+  const uint32_t k = r >> 8;
+  if (k == 0) return nan;
+  const float u = (float)k * (1.0f / 16777216.0f);
+  const double half = 0.5 * ((double)tsa_ffrom(tsa_fbits(u) + 1u) - (double)u);
+  const float t0 = (float)log((double)u + half);
+  if (!(t0 < 0.0f)) return nan;
+  // in(b): the float with bit pattern b (below zero) has expf above u
+  const uint32_t neg_zero = 0x80000000u, neg_inf = 0xff800000u;
+  uint32_t b = tsa_fbits(t0);
+  int evals = 0;
+  auto in = [&](uint32_t bits) { evals++; return tsa_expf_t(tsa_ffrom(bits), exp2tab) > u; };
+  uint32_t inside, outside;  // a pattern in the set and one below it (larger pattern) outside it
+  if (in(b)) {
+    inside = b;
+    uint32_t step = 1u;
+    for (;;) {
+      const uint32_t probe = inside + step < neg_inf && inside + step > inside ? inside + step : neg_inf;
+      if (!in(probe)) {
+        outside = probe;
+        break;
+      }
+      if (probe == neg_inf || evals > 40) return nan;
+      inside = probe;
+      step <<= 1;
+    }
+  } else {
+    outside = b;
+    uint32_t step = 1u;
+    for (;;) {
+      const uint32_t probe = outside - step > neg_zero && outside - step < outside ? outside - step : neg_zero + 1u;
+      if (in(probe)) {
+        inside = probe;
+        break;
+      }
+      if (probe == neg_zero + 1u || evals > 40) return nan;
+      outside = probe;
+      step <<= 1;
+    }
+  }
+  while (outside - inside > 1u) {  // inside < outside as patterns; the least float in the set is the largest
+    const uint32_t mid = inside + (outside - inside) / 2u;  // pattern inside it
+    if (in(mid)) inside = mid;
+    else outside = mid;
+    if (evals > 80) return nan;
+  }
+  return tsa_ffrom(inside);
+}
+
 // Slots of rule r (reference comment csrc/treesa_gpu.cu:137-144): the pivot P is the left child
 // (slotP 0) for rules 0, 1 and the right child for rules 2, 3; M, the grandchild under P that moves
 // up, is P's left child (slotM 0) for rules 1, 2 and its right child for rules 0, 3.  Every rule swaps

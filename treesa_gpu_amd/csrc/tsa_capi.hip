@@ -369,6 +369,10 @@ static int plan_one_wave(const tsa_layout_t* lay, const tsa_config_t* cfg, int n
     const int spread = (nchains + ncu - 1) / ncu;
     L->wpb = spread < 1 ? 1 : spread;
   }
+  L->lds_max = ldsw * 8;
+  // pre-order sweeps of at most one chain per compute unit are bound by the sweeping wave's chain of
+  // dependent steps while three SIMDs idle: there helper waves draw the next sweep's random numbers
+  L->draw_waves = cfg->draw_waves > 0 || (cfg->draw_waves == 0 && ncu > 0 && (long long)nchains <= ncu);
   *use_lds_out = use_lds;
   return TSA_OK;
 }
@@ -449,9 +453,10 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
              "fold_stage=%d",
              lay->W, c->wide.G, c->wide.nsw, c->wide.nt / 64, c->wide.K, c->wide.smem, c->wide.eK, c->wide.fold_stage);
   else
-    snprintf(kb, sizeof kb, "%s W=%d waves/block=%d lds_bytes/wave=%d%s", use_lds ? "lds" : "global",
+    snprintf(kb, sizeof kb, "%s W=%d waves/block=%d lds_bytes/wave=%d%s%s", use_lds ? "lds" : "global",
              use_lds ? c->Wt : lay->W, c->L.wpb, c->L.lds_words * 8,
-             cfg->fused_energy && c->fold_apart ? " fold=apart" : "");
+             cfg->fused_energy && c->fold_apart ? " fold=apart" : "",
+             c->L.draw_waves ? " preorder_draw_waves=3" : "");
   c->kname = kb;
 
   const size_t recb = (size_t)nchains * lay->chain_words * 8;

@@ -14,6 +14,8 @@ struct TsaKParams {
   int leaf_sc;
   int slicing, slice_moves, slice_every, max_slices;
   int par_follow, par_band;
+  int helpers;                 // pre-order, one chain per workgroup: waves after the first draw the next sweep's
+                               // Philox words and Metropolis thresholds while the first sweeps (0: none)
   uint32_t key0, key1;
   TsaModel model;
   float lse[64];               // lse[d] = (float)log2(1 + 2^-d), 0 for d >= 53
@@ -36,7 +38,15 @@ struct TsaLaunch {
   int lds;           // 1: chain staged in LDS
   int wpb;           // waves (= chains) per workgroup
   int lds_words;     // LDS words per wave
+  int draw_waves;    // 1: pre-order sweeps run one chain per workgroup with helper waves that draw ahead
+  int lds_max;       // dynamic LDS bytes a workgroup may have, less the kernel's static LDS
 };
+
+// Helper waves per workgroup of a pre-order sweep with draws made ahead (the workgroup fills a compute unit's
+// four SIMDs), and the LDS words they add: two buffers (this sweep's and the next) of one Philox word and one
+// threshold per internal node.
+#define TSA_DRAW_HELPERS 3
+static inline int tsa_draw_words(int nint) { return 2 * ((nint + 3) & ~3); }
 
 // Per-chain energies a sweep launch also writes (lc == nullptr: none): the chain is evaluated by the sweep
 // kernel right after its last sweep, while it is still staged, exactly as the energy kernel would.

@@ -46,6 +46,28 @@ __device__ __forceinline__ int tsa_nth_label(const uint64_t* A, const uint64_t* 
   return -1;
 }
 
+// Metropolis of a visit: with draws made ahead, x = -beta * dE against the node's threshold (a NaN threshold,
+// u = 0 or an unsettled search, draws the uniform again and evaluates expf); else u < expf(x).
+__device__ __forceinline__ bool tsa_visit_accept(const TsaKParams& P, int v, uint32_t sw, uint32_t chain, bool pre,
+                                                 uint32_t ry, float thr, float beta, float dE, const TsaMathTabs& T) {
+  if (pre) {
+    if (thr == thr) return -beta * dE >= thr;
+    ry = tsa_philox(TsaU4{(uint32_t)v, sw, chain, 0u}, P.key0, P.key1).y;
+  }
+  return tsa_metropolis(ry, beta, dE, T.exp2);
+}
+
+// Draws of one sweep made ahead: internal node i's first Philox word and Metropolis threshold, threads
+// t0, t0 + ts, ... of the workgroup.
+__device__ __forceinline__ void tsa_draw_ahead(const TsaKParams& P, uint32_t* dx, float* dt, uint32_t sw,
+                                               uint32_t chain, int t0, int ts, const uint64_t* exp2tab) {
+  for (int i = t0; i < P.nint; i += ts) {
+    const TsaU4 r = tsa_philox(TsaU4{(uint32_t)(P.m + i), sw, chain, 0u}, P.key0, P.key1);
+    dx[i] = r.x;
+    dt[i] = tsa_accept_threshold(r.y, exp2tab);
+  }
+}
+
 struct TsaVisit {
   uint32_t cw;  // the visited node's children word after the visit
   int Pn, On, Mn;
@@ -55,11 +77,13 @@ struct TsaVisit {
 // One proposal at internal node v by one lane (csrc/treesa_gpu.cu:156-235; CPU twin
 // csrc/cpu_ref.h:87-126).  lf: leaf sets (m*NW words), lab: internal sets, ch: children words, Sm: slice
 // set or null.  With P the pivot child, O the other child, M the grandchild under P that moves up and K
-// the one that stays, every rule swaps M and O, and P gets X = (K|O)&(M|d).
+// the one that stays, every rule swaps M and O, and P gets X = (K|O)&(M|d).  pre_x / pre_t (null: drawn
+// here): every internal node's first Philox word and Metropolis threshold for this sweep, drawn ahead.
 template <int W, int MODE>
 __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab, uint32_t* ch, const uint64_t* Sm,
                                               const uint64_t* lf, const float* lse, const TsaMathTabs& T, int v,
-                                              float beta, uint32_t sw, uint32_t chain) {
+                                              float beta, uint32_t sw, uint32_t chain,
+                                              const uint32_t* pre_x = nullptr, const float* pre_t = nullptr) {
   const int m = P.m;
   const int NW = W > 0 ? W : P.W;
   TsaVisit o;
@@ -71,8 +95,17 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
   const int l = (int)(chv & 0xFFFFu), r = (int)(chv >> 16);
   const bool li = l >= m, ri = r >= m;
   if (!li && !ri) return o;
-  const TsaU4 rnd = tsa_philox(TsaU4{(uint32_t)v, sw, chain, 0u}, P.key0, P.key1);
-  const int rule = tsa_pick_rule(li, ri, rnd.x);
+  uint32_t rx, ry = 0u;
+  float thr = 0.0f;
+  if (pre_x) {
+    rx = pre_x[v - m];
+    thr = pre_t[v - m];
+  } else {
+    const TsaU4 rnd = tsa_philox(TsaU4{(uint32_t)v, sw, chain, 0u}, P.key0, P.key1);
+    rx = rnd.x;
+    ry = rnd.y;
+  }
+  const int rule = tsa_pick_rule(li, ri, rx);
   const int slotP = tsa_slot_p(rule), slotM = tsa_slot_m(rule);
   const int Pn = slotP ? r : l, On = slotP ? l : r;
   const uint32_t chp = ch[Pn - m];
@@ -97,7 +130,7 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
       tsa_acc<MODE>(cnt, k & nm, mm & nm, p & nm, oo & nm, d & nm, x & nm);
     }
     const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, lse, T);
-    acc = tsa_metropolis(rnd.y, beta, dE, T.exp2);
+    acc = tsa_visit_accept(P, v, sw, chain, pre_x != nullptr, ry, thr, beta, dE, T);
     if (acc) {
 #pragma unroll
       for (int i = 0; i < W; i++) pP[i] = X[i];
@@ -110,7 +143,7 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
       tsa_acc<MODE>(cnt, k & nm, mm & nm, p & nm, oo & nm, d & nm, x & nm);
     }
     const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, lse, T);
-    acc = tsa_metropolis(rnd.y, beta, dE, T.exp2);
+    acc = tsa_visit_accept(P, v, sw, chain, pre_x != nullptr, ry, thr, beta, dE, T);
     if (acc)
       for (int i = 0; i < NW; i++) pP[i] = (pK[i] | pO[i]) & (pM[i] | pD[i]);
   }
@@ -302,17 +335,31 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
     lf = tsa_smem;
   }
   __syncthreads();
-  const int c = blockIdx.x * wpb + wv;
-  if (c >= nchains) return;  // whole waves; no workgroup barrier below this point
+  // with helper waves the workgroup holds one chain, swept by wave 0; else wave wv holds chain wpb*block + wv
+  const bool helped = ORDER == 1 && P.helpers > 0;
+  const int c = helped ? (int)blockIdx.x : (int)blockIdx.x * wpb + wv;
+  if (c >= nchains) return;  // whole waves (whole workgroups with helpers); every barrier below is the
+                             // helper mode's, reached by all of its waves
   uint64_t* const g = rec + (size_t)c * P.chain_words;
-  uint64_t* const wbase = tsa_smem + leafw + (size_t)wv * lds_words;
+  uint64_t* const wbase = tsa_smem + leafw + (size_t)(helped ? 0 : wv) * lds_words;
   uint64_t* base;
   uint16_t* nodes;
   if constexpr (LDS) {
     base = wbase;
-    const uint4* src = reinterpret_cast<const uint4*>(g);
-    uint4* dst = reinterpret_cast<uint4*>(base);
-    for (int i = lane; i < P.chain_words / 2; i += 64) dst[i] = src[i];
+    if (!helped || wv == 0) {  // with helpers wave 0 copies while the others draw the first sweep's numbers
+      const uint4* src = reinterpret_cast<const uint4*>(g);
+      uint4* dst = reinterpret_cast<uint4*>(base);
+      const int n16 = P.chain_words / 2;
+      int i = lane;
+      for (; i + 192 < n16; i += 256) {  // four loads in flight per lane
+        const uint4 a = src[i], b = src[i + 64], d = src[i + 128], e = src[i + 192];
+        dst[i] = a;
+        dst[i + 64] = b;
+        dst[i + 128] = d;
+        dst[i + 192] = e;
+      }
+      for (; i < n16; i += 64) dst[i] = src[i];
+    }
     nodes = reinterpret_cast<uint16_t*>(base + P.chain_words);
   } else {
     base = g;
@@ -481,8 +528,30 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
     }
   } else {
     const int root = 2 * m - 2;
+    // helper waves: every internal node's Philox word x and Metropolis threshold of sweep s sit in buffer s & 1
+    // (after the wave's node arrays) before sweep s starts, so that no visit of a sweep's dependent chain of
+    // steps waits on Philox or expf.  The helpers draw sweep 0 while wave 0 copies the record, and sweep s + 1
+    // during sweep s; a workgroup barrier closes each of these.
+    uint32_t* const dbuf = helped ? reinterpret_cast<uint32_t*>(wbase + lds_words) : nullptr;
+    if (helped) {
+      if (wv > 0)
+        tsa_draw_ahead(P, dbuf, reinterpret_cast<float*>(dbuf + nint4), sweep0, (uint32_t)c, (int)threadIdx.x - 64,
+                       (int)blockDim.x - 64, T.exp2);
+      __syncthreads();
+    }
     for (int s = 0; s < nsweeps; s++) {
       const uint32_t sw = sweep0 + (uint32_t)s;
+      if (helped && wv > 0) {  // helper waves
+        if (s + 1 < nsweeps) {
+          uint32_t* const nx = dbuf + (size_t)((s + 1) & 1) * 2 * nint4;
+          tsa_draw_ahead(P, nx, reinterpret_cast<float*>(nx + nint4), sw + 1u, (uint32_t)c, (int)threadIdx.x - 64,
+                         (int)blockDim.x - 64, T.exp2);
+        }
+        __syncthreads();
+        continue;
+      }
+      const uint32_t* const pre_x = helped ? dbuf + (size_t)(s & 1) * 2 * nint4 : nullptr;
+      const float* const pre_t = helped ? reinterpret_cast<const float*>(pre_x + nint4) : nullptr;
       if (lane == 0) wl[0] = (uint16_t)root;
       int sp = 1;
       tsa_wave_sync();
@@ -492,7 +561,7 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
         tsa_wave_sync();  // every lane has read its node before pushes overwrite the list
         uint32_t cw = 0;
         if (lane < k) {
-          const TsaVisit o = tsa_visit<W, MODE>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c);
+          const TsaVisit o = tsa_visit<W, MODE>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t);
           cw = o.cw;
           nv++;
           nbusy++;
@@ -513,46 +582,57 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
         tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
         tsa_wave_sync();
       }
+      if (helped) __syncthreads();
     }
   }
 
+  // with helper waves the whole workgroup evaluates the node costs, then the helpers write the snapshot and
+  // the record back while wave 0 folds the energy
+  const int e0 = helped ? (int)threadIdx.x : lane, es = helped ? (int)blockDim.x : 64;
   if (eo.cost) {
-    // node costs and masked sizes by all 64 lanes, for k_fold
+    // node costs and masked sizes, for k_fold
     float* const gc = eo.cost + (size_t)c * nint4;
     uint16_t* const gz = eo.z + (size_t)c * nint4;
-    for (int i = lane; i < nint; i += 64) {
+    for (int i = e0; i < nint; i += es) {
       int Z;
       gc[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
       gz[i] = (uint16_t)Z;
     }
   } else if (eo.lc) {
-    // the chain's energy, as k_energy computes it: node costs by all 64 lanes into the node arrays (free
-    // after the sweeps: pri and par hold nint4 floats, wl nint4 sizes), then the 32-lane fold
+    // the chain's energy, as k_energy computes it: node costs into the node arrays (free after the sweeps:
+    // pri and par hold nint4 floats, wl nint4 sizes), then the 32-lane fold
     tsa_wave_sync();
     float* const ncost = reinterpret_cast<float*>(pri);
-    for (int i = lane; i < nint; i += 64) {
+    for (int i = e0; i < nint; i += es) {
       int Z;
       ncost[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
       wl[i] = (uint16_t)Z;
     }
-    tsa_wave_sync();
-    const TsaEvalOut e = tsa_fold32(P, ncost, wl, Sm, lf, NW, T, lane & 31);
-    if (lane == 0) {
-      eo.lc[c] = e.lcost;
-      eo.sc[c] = e.sc;
-      eo.ns[c] = e.ns;
+    if (helped) __syncthreads();
+    else tsa_wave_sync();
+    if (!helped || wv == 0) {
+      const TsaEvalOut e = tsa_fold32(P, ncost, wl, Sm, lf, NW, T, lane & 31);
+      if (lane == 0) {
+        eo.lc[c] = e.lcost;
+        eo.sc[c] = e.sc;
+        eo.ns[c] = e.ns;
+      }
     }
   }
-  if (eo.ch) {
-    uint32_t* const gch = eo.ch + (size_t)c * nint;
-    for (int i = lane; i < nint; i += 64) gch[i] = ch[i];
+  if (!helped || wv > 0) {
+    const int u0 = helped ? (int)threadIdx.x - 64 : lane, us = helped ? (int)blockDim.x - 64 : 64;
+    if (eo.ch) {
+      uint32_t* const gch = eo.ch + (size_t)c * nint;
+      for (int i = u0; i < nint; i += us) gch[i] = ch[i];
+    }
+    if constexpr (LDS) {
+      tsa_wave_sync();
+      const uint4* src = reinterpret_cast<const uint4*>(base);
+      uint4* dst = reinterpret_cast<uint4*>(g);
+      for (int i = u0; i < P.chain_words / 2; i += us) dst[i] = src[i];
+    }
   }
-  if constexpr (LDS) {
-    tsa_wave_sync();
-    const uint4* src = reinterpret_cast<const uint4*>(base);
-    uint4* dst = reinterpret_cast<uint4*>(g);
-    for (int i = lane; i < P.chain_words / 2; i += 64) dst[i] = src[i];
-  }
+  if (helped && wv > 0) return;
   const long long sp_ = tsa_wave_sum(np), sa_ = tsa_wave_sum(na), sv_ = tsa_wave_sum(nv), sb_ = tsa_wave_sum(nbusy);
   if (lane == 0) {  // counters spread over TSA_STAT_SLOTS addresses each, summed by the host
     unsigned long long* st = stats + (c & (TSA_STAT_SLOTS - 1));
@@ -767,7 +847,21 @@ static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64
                                  hipEvent_t e1) {
   const int NW = W > 0 ? W : P.W;
   const size_t leafw = LDS ? (size_t)((P.m * NW + 1) & ~1) : 0;
-  const size_t smem = (leafw + (size_t)L.wpb * L.lds_words) * 8;
+  // pre-order sweeps with helper waves: one chain per workgroup of 1 + TSA_DRAW_HELPERS waves, with two draw
+  // buffers after the chain's words, when they fit
+  TsaKParams P2 = P;
+  P2.helpers = 0;
+  int wpb = L.wpb, threads = 64 * L.wpb;
+  size_t smem = (leafw + (size_t)L.wpb * L.lds_words) * 8;
+  if (ORDER == 1 && L.draw_waves) {
+    const size_t hs = (leafw + (size_t)L.lds_words + tsa_draw_words(P.nint)) * 8;
+    if (hs <= (size_t)L.lds_max) {
+      P2.helpers = TSA_DRAW_HELPERS;
+      wpb = 1;
+      threads = 64 * (1 + TSA_DRAW_HELPERS);
+      smem = hs;
+    }
+  }
   static size_t attr_set = 0;
   if (smem > 65536 && smem > attr_set) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_sweep<W, MODE, ORDER, LDS>),
@@ -775,10 +869,10 @@ static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64
     if (e != hipSuccess) return e;
     attr_set = smem;
   }
-  const int grid = (nchains + L.wpb - 1) / L.wpb;
+  const int grid = (nchains + wpb - 1) / wpb;
   // e0 / e1 (null: none) take the kernel's start and stop times in the dispatch itself
-  hipExtLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS>), dim3(grid), dim3(64 * L.wpb), (uint32_t)smem, st, e0, e1, 0u,
-                        P, rec, leaf, fix, nchains, L.lds_words, beta, sweep0, nsweeps, stats, eo);
+  hipExtLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS>), dim3(grid), dim3(threads), (uint32_t)smem, st, e0, e1, 0u,
+                        P2, rec, leaf, fix, nchains, L.lds_words, beta, sweep0, nsweeps, stats, eo);
   return hipGetLastError();
 }
 

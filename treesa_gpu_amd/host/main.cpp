@@ -284,6 +284,7 @@ void Run::fill_config() {
   cfg_.fused_energy = O_.eval_every == 1 ? 1 : 0;  // every level evaluated: the sweep kernel evaluates too
   cfg_.sums = O_.no_sum ? -1 : (O_.force_sum ? 1 : 0);
   cfg_.track_overlap = O_.no_overlap ? -1 : 0;
+  cfg_.draw_waves = O_.draw_waves;
 }
 
 const std::vector<std::vector<uint32_t>>& Run::start_trees() {

@@ -123,6 +123,9 @@ const std::vector<Flag>& flags() {
       {"--wpc", "n", "wide kernel: 32-lane warps per workgroup (waves = n / 2)", INT_FIELD(wpc)},
       {"--wide-wgs", "K", "wide kernel: workgroups per chain", INT_FIELD(wide_wgs)},
       {"--wide-lanes", "G", "wide kernel: lanes per proposal", INT_FIELD(wide_lanes)},
+      {"--draw-waves", "1|-1|0",
+       "pre-order: helper waves draw the next sweep's random numbers (1), each visit draws its own (-1), automatic (0)",
+       INT_FIELD(draw_waves)},
       {"--lpc", "32|16|8", "lanes per chain of the reference's warp kernels (not 32: pre-order)", INT_FIELD(lpc)},
       {"--wpb", "W", "accepted, no effect here", INT_FIELD(wpb)},
       {"--block", "B", "accepted, no effect here", INT_FIELD(block)},

@@ -38,6 +38,7 @@ struct Options {
   int par_follow = 0, par_band = 0;
   bool wide = false, no_sum = false, force_sum = false;
   int wpc = 0, wide_wgs = 0, wide_lanes = 0;
+  int draw_waves = 0;  // pre-order: 1 helper waves draw the next sweep's random numbers, -1 each visit, 0 automatic
   int lpc = 32, wpb = 0, block = 0, coop_max = 0, coop_min_units = -1, coop_min = 1, coop_full = 0, coop_chunks = 2;
   // validation mode
   bool check = false, cross = true;
