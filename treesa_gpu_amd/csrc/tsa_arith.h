@@ -143,11 +143,47 @@ TSA_HD void tsa_counts_zero(TsaCounts& c) {
   for (int q = 0; q < 4; q++) c.B[q] = c.M[q] = c.N[q] = c.K[q] = 0;
 }
 
+// Three-input bitwise functions by truth table: bit i of f is the result for the operand bits
+// (a, b, c) = (i >> 2 & 1, i >> 1 & 1, i & 1), i.e. f = g(0xF0, 0xCC, 0xAA) for the function g.  On the device
+// one v_bitop3_b32 per 32-bit half; on the host the same table bit by bit.
+#define TSA_F_AB_NC 0x40u   // a & b & ~c
+#define TSA_F_ABC 0x80u     // a & b & c
+#define TSA_F_A_NB_C 0x20u  // a & ~b & c
+#define TSA_F_NA_BC 0x08u   // ~a & b & c
+#define TSA_F_A_BORC 0xE0u  // a & (b | c)
+template <uint32_t F>
+TSA_HD uint32_t tsa_bitop3(uint32_t a, uint32_t b, uint32_t c) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  return __builtin_amdgcn_bitop3_b32(a, b, c, F);
+#else
+  uint32_t r = 0;
+  for (int i = 0; i < 8; i++)
+    if ((F >> i) & 1u) r |= ((i & 4) ? a : ~a) & ((i & 2) ? b : ~b) & ((i & 1) ? c : ~c);
+  return r;
+#endif
+}
+
+// popcount of g(a, b, c) over a 64-bit word, as two 32-bit halves
+template <uint32_t F>
+TSA_HD int tsa_popc3(uint64_t a, uint64_t b, uint64_t c) {
+  const uint32_t lo = tsa_bitop3<F>((uint32_t)a, (uint32_t)b, (uint32_t)c);
+  const uint32_t hi = tsa_bitop3<F>((uint32_t)(a >> 32), (uint32_t)(b >> 32), (uint32_t)(c >> 32));
+  return tsa_popc64(((uint64_t)hi << 32) | lo);
+}
+
+// x = (k|o)&(m|d), P's label set after a move
+TSA_HD uint64_t tsa_xset(uint64_t k, uint64_t o, uint64_t m, uint64_t d) {
+  const uint64_t t = k | o;
+  const uint32_t lo = tsa_bitop3<TSA_F_A_BORC>((uint32_t)t, (uint32_t)m, (uint32_t)d);
+  const uint32_t hi = tsa_bitop3<TSA_F_A_BORC>((uint32_t)(t >> 32), (uint32_t)(m >> 32), (uint32_t)(d >> 32));
+  return ((uint64_t)hi << 32) | lo;
+}
+
 TSA_HD void tsa_count3(uint64_t x, uint64_t y, uint64_t z, int& B, int& M, int& N, int& K) {
-  B += tsa_popc64(x & y & z);
-  M += tsa_popc64(x & ~y & z);
-  N += tsa_popc64(~x & y & z);
-  K += tsa_popc64(x & y & ~z);
+  B += tsa_popc3<TSA_F_ABC>(x, y, z);
+  M += tsa_popc3<TSA_F_A_NB_C>(x, y, z);
+  N += tsa_popc3<TSA_F_NA_BC>(x, y, z);
+  K += tsa_popc3<TSA_F_AB_NC>(x, y, z);
 }
 
 // One 64-bit word of the masked sets k, m, p, o, d and x = (k|o)&(m|d).  common.h:180-196.
@@ -157,10 +193,10 @@ TSA_HD void tsa_acc(TsaCounts& c, uint64_t k, uint64_t m, uint64_t p, uint64_t o
   c.sp += tsa_popc64(p);
   c.sx += tsa_popc64(x);
   if (MODE == 0) {
-    c.K[0] += tsa_popc64(k & m & ~p);
-    c.K[1] += tsa_popc64(p & o & ~d);
-    c.K[2] += tsa_popc64(k & o & ~x);
-    c.K[3] += tsa_popc64(x & m & ~d);
+    c.K[0] += tsa_popc3<TSA_F_AB_NC>(k, m, p);
+    c.K[1] += tsa_popc3<TSA_F_AB_NC>(p, o, d);
+    c.K[2] += tsa_popc3<TSA_F_AB_NC>(k, o, x);
+    c.K[3] += tsa_popc3<TSA_F_AB_NC>(x, m, d);
   } else {
     tsa_count3(k, m, p, c.B[0], c.M[0], c.N[0], c.K[0]);
     tsa_count3(p, o, d, c.B[1], c.M[1], c.N[1], c.K[1]);

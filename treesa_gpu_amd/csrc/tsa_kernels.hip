@@ -76,10 +76,13 @@ struct TsaVisit {
 
 // One proposal at internal node v by one lane (csrc/treesa_gpu.cu:156-235; CPU twin
 // csrc/cpu_ref.h:87-126).  lf: leaf sets (m*NW words), lab: internal sets, ch: children words, Sm: slice
-// set or null.  With P the pivot child, O the other child, M the grandchild under P that moves up and K
-// the one that stays, every rule swaps M and O, and P gets X = (K|O)&(M|d).  pre_x / pre_t (null: drawn
-// here): every internal node's first Philox word and Metropolis threshold for this sweep, drawn ahead.
-template <int W, int MODE>
+// set (SL: slicing on; else unused and no masking).  UNI: the leaf sets sit right below the internal ones
+// (lab == lf + m*NW), so that any node's set is at lf + node*NW without a select.  With P the pivot child,
+// O the other child, M the grandchild under P that moves up and K the one that stays, every rule swaps M and
+// O, and P gets X = (K|O)&(M|d).  pre_x / pre_t (null: drawn here): every internal node's first Philox word
+// and Metropolis threshold for this sweep, drawn ahead; they are read beside the children word, so that the
+// rule is known when that word arrives.
+template <int W, int MODE, bool SL, bool UNI>
 __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab, uint32_t* ch, const uint64_t* Sm,
                                               const uint64_t* lf, const float* lse, const TsaMathTabs& T, int v,
                                               float beta, uint32_t sw, uint32_t chain,
@@ -91,16 +94,17 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
   o.acc = false;
   o.Pn = o.On = o.Mn = 0;
   const uint32_t chv = ch[v - m];
-  o.cw = chv;
-  const int l = (int)(chv & 0xFFFFu), r = (int)(chv >> 16);
-  const bool li = l >= m, ri = r >= m;
-  if (!li && !ri) return o;
-  uint32_t rx, ry = 0u;
+  uint32_t rx = 0u, ry = 0u;
   float thr = 0.0f;
   if (pre_x) {
     rx = pre_x[v - m];
     thr = pre_t[v - m];
-  } else {
+  }
+  o.cw = chv;
+  const int l = (int)(chv & 0xFFFFu), r = (int)(chv >> 16);
+  const bool li = l >= m, ri = r >= m;
+  if (!li && !ri) return o;
+  if (!pre_x) {
     const TsaU4 rnd = tsa_philox(TsaU4{(uint32_t)v, sw, chain, 0u}, P.key0, P.key1);
     rx = rnd.x;
     ry = rnd.y;
@@ -111,11 +115,12 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
   const uint32_t chp = ch[Pn - m];
   const int Mn = slotM ? (int)(chp >> 16) : (int)(chp & 0xFFFFu);
   const int Kn = slotM ? (int)(chp & 0xFFFFu) : (int)(chp >> 16);
+  const uint64_t* const U = lab - (size_t)m * NW;  // UNI: every node's set at U + node * NW
   uint64_t* pP = lab + (size_t)(Pn - m) * NW;
   const uint64_t* pD = lab + (size_t)(v - m) * NW;
-  const uint64_t* pO = On >= m ? lab + (size_t)(On - m) * NW : lf + (size_t)On * NW;
-  const uint64_t* pK = Kn >= m ? lab + (size_t)(Kn - m) * NW : lf + (size_t)Kn * NW;
-  const uint64_t* pM = Mn >= m ? lab + (size_t)(Mn - m) * NW : lf + (size_t)Mn * NW;
+  const uint64_t* pO = UNI ? U + (size_t)On * NW : (On >= m ? lab + (size_t)(On - m) * NW : lf + (size_t)On * NW);
+  const uint64_t* pK = UNI ? U + (size_t)Kn * NW : (Kn >= m ? lab + (size_t)(Kn - m) * NW : lf + (size_t)Kn * NW);
+  const uint64_t* pM = UNI ? U + (size_t)Mn * NW : (Mn >= m ? lab + (size_t)(Mn - m) * NW : lf + (size_t)Mn * NW);
   TsaCounts cnt;
   tsa_counts_zero(cnt);
   bool acc;
@@ -124,10 +129,14 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
 #pragma unroll
     for (int i = 0; i < W; i++) {
       const uint64_t d = pD[i], p = pP[i], oo = pO[i], k = pK[i], mm = pM[i];
-      const uint64_t x = (k | oo) & (mm | d);
+      const uint64_t x = tsa_xset(k, oo, mm, d);
       X[i] = x;
-      const uint64_t nm = Sm ? ~Sm[i] : ~0ull;
-      tsa_acc<MODE>(cnt, k & nm, mm & nm, p & nm, oo & nm, d & nm, x & nm);
+      if constexpr (SL) {
+        const uint64_t nm = ~Sm[i];
+        tsa_acc<MODE>(cnt, k & nm, mm & nm, p & nm, oo & nm, d & nm, x & nm);
+      } else {
+        tsa_acc<MODE>(cnt, k, mm, p, oo, d, x);
+      }
     }
     const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, lse, T);
     acc = tsa_visit_accept(P, v, sw, chain, pre_x != nullptr, ry, thr, beta, dE, T);
@@ -138,9 +147,13 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
   } else {
     for (int i = 0; i < NW; i++) {
       const uint64_t d = pD[i], p = pP[i], oo = pO[i], k = pK[i], mm = pM[i];
-      const uint64_t x = (k | oo) & (mm | d);
-      const uint64_t nm = Sm ? ~Sm[i] : ~0ull;
-      tsa_acc<MODE>(cnt, k & nm, mm & nm, p & nm, oo & nm, d & nm, x & nm);
+      const uint64_t x = tsa_xset(k, oo, mm, d);
+      if constexpr (SL) {
+        const uint64_t nm = ~Sm[i];
+        tsa_acc<MODE>(cnt, k & nm, mm & nm, p & nm, oo & nm, d & nm, x & nm);
+      } else {
+        tsa_acc<MODE>(cnt, k, mm, p, oo, d, x);
+      }
     }
     const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, lse, T);
     acc = tsa_visit_accept(P, v, sw, chain, pre_x != nullptr, ry, thr, beta, dE, T);
@@ -330,9 +343,11 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
   const uint64_t* lf = leaf;
   int leafw = 0;
   if constexpr (LDS) {
+    // the leaf sets end where the first wave's chain begins (their rounding gap below them)
     leafw = (m * NW + 1) & ~1;
-    for (int i = threadIdx.x; i < m * NW; i += blockDim.x) tsa_smem[i] = leaf[i];
-    lf = tsa_smem;
+    uint64_t* const sl = tsa_smem + (leafw - m * NW);
+    for (int i = threadIdx.x; i < m * NW; i += blockDim.x) sl[i] = leaf[i];
+    lf = sl;
   }
   __syncthreads();
   // with helper waves the workgroup holds one chain, swept by wave 0; else wave wv holds chain wpb*block + wv
@@ -502,7 +517,9 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
             const int v = wl[j];
             const bool rev = (pri[v - m] & 1u) == 0;  // a follow-up visit draws its own numbers
             const uint32_t swv = sw | (rev ? 0x80000000u : 0u);
-            const TsaVisit o = tsa_visit<W, MODE>(P, lab, ch, Sm, lf, s_lse, T, v, beta, swv, (uint32_t)c);
+            const TsaVisit o = P.slicing
+                                   ? tsa_visit<W, MODE, true, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, swv, (uint32_t)c)
+                                   : tsa_visit<W, MODE, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, swv, (uint32_t)c);
             nv++;
             nbusy++;
             np += o.prop;
@@ -533,6 +550,7 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
     // steps waits on Philox or expf.  The helpers draw sweep 0 while wave 0 copies the record, and sweep s + 1
     // during sweep s; a workgroup barrier closes each of these.
     uint32_t* const dbuf = helped ? reinterpret_cast<uint32_t*>(wbase + lds_words) : nullptr;
+    const bool uni = LDS && helped;  // one chain in the workgroup's LDS, right above the leaf sets
     if (helped) {
       if (wv > 0)
         tsa_draw_ahead(P, dbuf, reinterpret_cast<float*>(dbuf + nint4), sweep0, (uint32_t)c, (int)threadIdx.x - 64,
@@ -561,7 +579,12 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
         tsa_wave_sync();  // every lane has read its node before pushes overwrite the list
         uint32_t cw = 0;
         if (lane < k) {
-          const TsaVisit o = tsa_visit<W, MODE>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t);
+          // with helpers (one chain per workgroup) the staged leaf sets end where the chain's internal sets begin
+          const TsaVisit o =
+              P.slicing ? (uni ? tsa_visit<W, MODE, true, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
+                               : tsa_visit<W, MODE, true, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t))
+                        : (uni ? tsa_visit<W, MODE, false, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
+                               : tsa_visit<W, MODE, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t));
           cw = o.cw;
           nv++;
           nbusy++;

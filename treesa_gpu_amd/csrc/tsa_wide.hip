@@ -467,8 +467,8 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
 #pragma unroll
                 for (int q = 0; q < SC; q++) {
                   TsaW2 x;
-                  x.a = (kk[q].a | oo[q].a) & (mm[q].a | dd[q].a);
-                  x.b = (kk[q].b | oo[q].b) & (mm[q].b | dd[q].b);
+                  x.a = tsa_xset(kk[q].a, oo[q].a, mm[q].a, dd[q].a);
+                  x.b = tsa_xset(kk[q].b, oo[q].b, mm[q].b, dd[q].b);
                   tsa_acc<MODE>(cn, kk[q].a, mm[q].a, pp[q].a, oo[q].a, dd[q].a, x.a);
                   tsa_acc<MODE>(cn, kk[q].b, mm[q].b, pp[q].b, oo[q].b, dd[q].b, x.b);
                   if (r0 == 0) {
@@ -494,8 +494,8 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
               }
 #pragma unroll
               for (int q = 0; q < TSA_WIDE_CPL; q++) {
-                xx[q].a = (kk[q].a | oo[q].a) & (mm[q].a | dd[q].a);
-                xx[q].b = (kk[q].b | oo[q].b) & (mm[q].b | dd[q].b);
+                xx[q].a = tsa_xset(kk[q].a, oo[q].a, mm[q].a, dd[q].a);
+                xx[q].b = tsa_xset(kk[q].b, oo[q].b, mm[q].b, dd[q].b);
                 tsa_acc<MODE>(cn, kk[q].a, mm[q].a, pp[q].a, oo[q].a, dd[q].a, xx[q].a);
                 tsa_acc<MODE>(cn, kk[q].b, mm[q].b, pp[q].b, oo[q].b, dd[q].b, xx[q].b);
               }
