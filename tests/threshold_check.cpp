@@ -3,7 +3,7 @@
 // is the same decision for every x exactly when (1) the restated expf is non-decreasing over the floats, so that
 // {x : expf(x) > u} is every float from some least one up, and (2) T(u) is that least float: expf(T) > u and
 // expf(next float below T) <= u.  (1) is checked over all 2^32 floats in value order, (2) for every uniform the
-// kernels draw, u = k * 2^-24 for k = 1 .. 2^24 - 1 (k = 0 yields NaN and the kernels evaluate expf).
+// kernels draw, u = k * 2^-24 for k = 0 .. 2^24 - 1.
 // Build: g++ -O2 -fopenmp -ffp-contract=off -I treesa_gpu_amd/csrc tests/threshold_check.cpp
 // Prints "drops bad_thresholds nan_thresholds" and exits 0 iff all three are 0.
 #include <cmath>
@@ -26,7 +26,7 @@ int main() {
     if (tsa_expf(by_value(i)) < tsa_expf(by_value(i - 1))) drops++;
   long long bad = 0, nans = 0;
 #pragma omp parallel for reduction(+ : bad, nans) schedule(static)
-  for (int64_t k = 1; k < (1 << 24); k++) {
+  for (int64_t k = 0; k < (1 << 24); k++) {
     const uint32_t r = (uint32_t)k << 8;
     const float u = (float)k * (1.0f / 16777216.0f);
     const float T = tsa_accept_threshold(r, TSA_EXP2_TABLE);

@@ -241,12 +241,12 @@ TSA_HD bool tsa_metropolis(uint32_t r, float beta, float dE, const uint64_t* exp
 // grows as the float falls.  The search starts at the float nearest log(u + ulp(u) / 2) (where a correctly
 // rounded expf would first exceed u), doubles its step in bit patterns until it brackets the boundary, then
 // halves the bracket: one or two expf evaluations for most u, about 2 log2 of the distance in ulps near u = 1
-// (where t is much finer than expf's output).  NaN for u = 0 or a search that does not settle within its
-// bound: the caller then evaluates expf itself.
+// (where t is much finer than expf's output).  u = 0 takes the same search (its boundary lies where expf
+// stops underflowing to zero).  NaN for a search that does not settle within its bound, which no u of the
+// 2^24 the kernels draw reaches (checked for every one of them, on the host and on the device).
 TSA_HD float tsa_accept_threshold(uint32_t r, const uint64_t* exp2tab) {
   const float nan = tsa_ffrom(0x7fc00000u);
   const uint32_t k = r >> 8;
-  if (k == 0) return nan;
   const float u = (float)k * (1.0f / 16777216.0f);
   const double half = 0.5 * ((double)tsa_ffrom(tsa_fbits(u) + 1u) - (double)u);
   const float t0 = (float)log((double)u + half);

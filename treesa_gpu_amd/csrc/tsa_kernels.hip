@@ -46,15 +46,12 @@ __device__ __forceinline__ int tsa_nth_label(const uint64_t* A, const uint64_t* 
   return -1;
 }
 
-// Metropolis of a visit: with draws made ahead, x = -beta * dE against the node's threshold (a NaN threshold,
-// u = 0 or an unsettled search, draws the uniform again and evaluates expf); else u < expf(x).
-__device__ __forceinline__ bool tsa_visit_accept(const TsaKParams& P, int v, uint32_t sw, uint32_t chain, bool pre,
-                                                 uint32_t ry, float thr, float beta, float dE, const TsaMathTabs& T) {
-  if (pre) {
-    if (thr == thr) return -beta * dE >= thr;
-    ry = tsa_philox(TsaU4{(uint32_t)v, sw, chain, 0u}, P.key0, P.key1).y;
-  }
-  return tsa_metropolis(ry, beta, dE, T.exp2);
+// Metropolis of a visit: with draws made ahead (PRE), x = -beta * dE against the node's threshold T(u), the
+// least float whose expf exceeds u (a number for every u the kernels draw, u = 0 included); else u < expf(x).
+template <bool PRE>
+__device__ __forceinline__ bool tsa_visit_accept(uint32_t ry, float thr, float beta, float dE, const TsaMathTabs& T) {
+  if constexpr (PRE) return -beta * dE >= thr;
+  else return tsa_metropolis(ry, beta, dE, T.exp2);
 }
 
 // Draws of one sweep made ahead: internal node i's first Philox word and Metropolis threshold, threads
@@ -79,10 +76,10 @@ struct TsaVisit {
 // set (SL: slicing on; else unused and no masking).  UNI: the leaf sets sit right below the internal ones
 // (lab == lf + m*NW), so that any node's set is at lf + node*NW without a select.  With P the pivot child,
 // O the other child, M the grandchild under P that moves up and K the one that stays, every rule swaps M and
-// O, and P gets X = (K|O)&(M|d).  pre_x / pre_t (null: drawn here): every internal node's first Philox word
-// and Metropolis threshold for this sweep, drawn ahead; they are read beside the children word, so that the
-// rule is known when that word arrives.
-template <int W, int MODE, bool SL, bool UNI>
+// O, and P gets X = (K|O)&(M|d).  PRE: pre_x / pre_t hold every internal node's first Philox word and
+// Metropolis threshold for this sweep, drawn ahead; they are read beside the children word, so that the rule
+// is known when that word arrives.  Else the visit draws its own.
+template <int W, int MODE, bool SL, bool UNI, bool PRE>
 __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab, uint32_t* ch, const uint64_t* Sm,
                                               const uint64_t* lf, const float* lse, const TsaMathTabs& T, int v,
                                               float beta, uint32_t sw, uint32_t chain,
@@ -96,7 +93,7 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
   const uint32_t chv = ch[v - m];
   uint32_t rx = 0u, ry = 0u;
   float thr = 0.0f;
-  if (pre_x) {
+  if constexpr (PRE) {
     rx = pre_x[v - m];
     thr = pre_t[v - m];
   }
@@ -104,7 +101,7 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
   const int l = (int)(chv & 0xFFFFu), r = (int)(chv >> 16);
   const bool li = l >= m, ri = r >= m;
   if (!li && !ri) return o;
-  if (!pre_x) {
+  if constexpr (!PRE) {
     const TsaU4 rnd = tsa_philox(TsaU4{(uint32_t)v, sw, chain, 0u}, P.key0, P.key1);
     rx = rnd.x;
     ry = rnd.y;
@@ -139,7 +136,7 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
       }
     }
     const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, lse, T);
-    acc = tsa_visit_accept(P, v, sw, chain, pre_x != nullptr, ry, thr, beta, dE, T);
+    acc = tsa_visit_accept<PRE>(ry, thr, beta, dE, T);
     if (acc) {
 #pragma unroll
       for (int i = 0; i < W; i++) pP[i] = X[i];
@@ -156,7 +153,7 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
       }
     }
     const float dE = tsa_energy_from_counts<MODE>(cnt, P.model, lse, T);
-    acc = tsa_visit_accept(P, v, sw, chain, pre_x != nullptr, ry, thr, beta, dE, T);
+    acc = tsa_visit_accept<PRE>(ry, thr, beta, dE, T);
     if (acc)
       for (int i = 0; i < NW; i++) pP[i] = (pK[i] | pO[i]) & (pM[i] | pD[i]);
   }
@@ -518,8 +515,8 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
             const bool rev = (pri[v - m] & 1u) == 0;  // a follow-up visit draws its own numbers
             const uint32_t swv = sw | (rev ? 0x80000000u : 0u);
             const TsaVisit o = P.slicing
-                                   ? tsa_visit<W, MODE, true, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, swv, (uint32_t)c)
-                                   : tsa_visit<W, MODE, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, swv, (uint32_t)c);
+                                   ? tsa_visit<W, MODE, true, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, swv, (uint32_t)c)
+                                   : tsa_visit<W, MODE, false, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, swv, (uint32_t)c);
             nv++;
             nbusy++;
             np += o.prop;
@@ -550,7 +547,6 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
     // steps waits on Philox or expf.  The helpers draw sweep 0 while wave 0 copies the record, and sweep s + 1
     // during sweep s; a workgroup barrier closes each of these.
     uint32_t* const dbuf = helped ? reinterpret_cast<uint32_t*>(wbase + lds_words) : nullptr;
-    const bool uni = LDS && helped;  // one chain in the workgroup's LDS, right above the leaf sets
     if (helped) {
       if (wv > 0)
         tsa_draw_ahead(P, dbuf, reinterpret_cast<float*>(dbuf + nint4), sweep0, (uint32_t)c, (int)threadIdx.x - 64,
@@ -580,11 +576,12 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
         uint32_t cw = 0;
         if (lane < k) {
           // with helpers (one chain per workgroup) the staged leaf sets end where the chain's internal sets begin
+          // (LDS records) and the draws are made ahead
           const TsaVisit o =
-              P.slicing ? (uni ? tsa_visit<W, MODE, true, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
-                               : tsa_visit<W, MODE, true, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t))
-                        : (uni ? tsa_visit<W, MODE, false, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
-                               : tsa_visit<W, MODE, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t));
+              P.slicing ? (helped ? tsa_visit<W, MODE, true, LDS, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
+                                  : tsa_visit<W, MODE, true, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c))
+                        : (helped ? tsa_visit<W, MODE, false, LDS, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
+                                  : tsa_visit<W, MODE, false, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c));
           cw = o.cw;
           nv++;
           nbusy++;
