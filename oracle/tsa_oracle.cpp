@@ -99,16 +99,38 @@ float lse_flt(float a, float b) {
 }
 // Rounding variants for perturbation experiments (oracle_set_variant): bit 0 evaluates the energy fold's lse
 // in double and rounds once (an equally accurate float lse whose last bit differs from the libm form now and
-// then, as another device's log2f / exp2f would), bit 1 does the same in the float energy models of the
-// sweeps.  0 (the default) is the reference's arithmetic on this host.
+// then), bit 1 does the same in the float energy models of the sweeps; bits 2 and 3 instead move the
+// results of exp2f and log2f in the fold (bit 2) or in the models (bit 3) by one ulp up or down, each with
+// probability 1/4 by a hash of the operand and g_noise_seed: a device whose exp2f / log2f stay within one ulp
+// but round differently from libm; bit 4 moves the Metropolis expf result by -2..2 ulp the same way (accept()).
+// 0 (the default) is the reference's arithmetic on this host.
 int g_variant = 0;
+uint32_t g_noise_seed = 0;
 float lse_dbl(float a, float b) {
   const float hi = a > b ? a : b, lo = a > b ? b : a;
   if (hi == -INFINITY) return hi;
   return (float)((double)hi + std::log2(1.0 + std::exp2((double)lo - (double)hi)));
 }
-float lse_fold(float a, float b) { return (g_variant & 1) ? lse_dbl(a, b) : lse_flt(a, b); }
-float lse_model(float a, float b) { return (g_variant & 2) ? lse_dbl(a, b) : lse_flt(a, b); }
+float nudge(float x, float operand, uint32_t salt) {
+  uint32_t u;
+  std::memcpy(&u, &operand, 4);
+  const uint32_t h = fmix(u ^ (g_noise_seed * 0x9E3779B9u) ^ salt);
+  if ((h & 3u) == 1u) return std::nextafter(x, INFINITY);
+  if ((h & 3u) == 2u) return std::nextafter(x, -INFINITY);
+  return x;
+}
+float lse_noisy(float a, float b) {
+  const float hi = a > b ? a : b, lo = a > b ? b : a;
+  if (hi == -INFINITY) return hi;
+  const float d = lo - hi, e = nudge(exp2f(d), d, 0x51u), s = 1.0f + e;
+  return hi + nudge(log2f(s), s, 0xA7u);
+}
+float lse_fold(float a, float b) {
+  return (g_variant & 4) ? lse_noisy(a, b) : (g_variant & 1) ? lse_dbl(a, b) : lse_flt(a, b);
+}
+float lse_model(float a, float b) {
+  return (g_variant & 8) ? lse_noisy(a, b) : (g_variant & 2) ? lse_dbl(a, b) : lse_flt(a, b);
+}
 float model_lt(int mode, int B, int M, int N, int K, const OParams& P) {
   if (mode == 1) {
     const float lops = (float)(1 + B + std::max(M, P.m0) + std::max(N, P.n0) + std::max(K, P.k0)) - P.lpeak;
@@ -127,9 +149,26 @@ float model_lt(int mode, int B, int M, int N, int K, const OParams& P) {
   }
   return lse_model(lse_model(P.v2_l3launch, P.v2_lperm2 + lab), best);
 }
-bool accept(uint32_t r, float beta, float dE) {
+// Metropolis with the 24-bit uniform of r (csrc/common.h:224-229).  near (optional) is set when u lies within
+// two ulp of expf(-beta dE): a decision that an expf rounding differently by up to two ulp could flip.  Variant
+// bit 4 moves the expf result by up to two ulp at hash-chosen operands (perturbation experiments only).
+bool accept(uint32_t r, float beta, float dE, bool* near = nullptr) {
   const float u = (float)(r >> 8) * (1.0f / 16777216.0f);
-  return u < expf(-beta * dE);
+  const float x = -beta * dE;
+  float e = expf(x);
+  if (near && e > 0.0f && e < 1.0f) {
+    const float lo = std::nextafter(std::nextafter(e, 0.0f), 0.0f), hi = std::nextafter(std::nextafter(e, 2.0f), 2.0f);
+    if (u >= lo && u < hi) *near = true;
+  }
+  if (g_variant & 16) {
+    uint32_t ux;
+    std::memcpy(&ux, &x, 4);
+    const uint32_t h = fmix(ux ^ (g_noise_seed * 0x85EBCA77u) ^ 0x3C6EF372u);
+    const int k = (int)(h % 5u) - 2;  // -2 .. 2 ulp
+    for (int i = 0; i < k; i++) e = std::nextafter(e, INFINITY);
+    for (int i = 0; i > k; i--) e = std::nextafter(e, -INFINITY);
+  }
+  return u < e;
 }
 
 // ---- sets --------------------------------------------------------------------------------------------
@@ -179,6 +218,7 @@ struct Tree {
 
 struct Counter {
   long long prop = 0, acc = 0, visits = 0, phases = 0, sprop = 0, sacc = 0;
+  bool near = false;  // a Metropolis decision within two ulp of expf happened
 };
 
 // One proposal at internal node v (csrc/cpu_ref.h:87-121).  Julia rules 1..4: pivot = left child for
@@ -221,7 +261,7 @@ void propose(Tree& T, int v, float beta, uint32_t sweep, uint32_t chain, const O
   const float w = ((float)std::max(sc0, sc1) > P.sc_target) ? P.sc_weight : 0.0f;
   const float dE = w * (float)(sc1 - sc0) + dtc;
   C.prop++;
-  if (!accept(rn.b, beta, dE)) return;
+  if (!accept(rn.b, beta, dE, &C.near)) return;
   C.acc++;
   // b and c trade places, keeping slots
   if (rule == 1) { T.R[piv] = oth; T.R[v] = b; }
@@ -357,39 +397,49 @@ int kth_label(const Set& s, const std::vector<char>& cut, int k) {
   return -1;
 }
 
+// The proposal of one slice move from the chain's evaluation cur and the word r1 (csrc/treesa_gpu.cu:
+// 455-478): type 0 add, 1 remove, 2 swap, -1 no move; ladd / lrem the labels added / removed (-1: none).
+int propose_slice(const Tree& T, const Eval& cur, const R4& r1, const OParams& P, int& ladd, int& lrem) {
+  const int m = T.m, nint = m - 1;
+  int type;
+  if (cur.ns == 0) type = 0;
+  else if (cur.ns >= P.max_slices) type = (r1.a >> 31) ? 1 : 2;
+  else type = r1.a < 0x80000000u ? 0 : (r1.a < 0xC0000000u ? 1 : 2);
+  ladd = -1;
+  lrem = -1;
+  if (type != 1 && cur.ncand > 0 && cur.sc_int > 0) {
+    int rr = (int)(r1.b % (uint32_t)cur.ncand), node = -1;
+    for (int i = 0; i < nint && node < 0; i++)
+      if (live_size(T.lab[m + i], T.cut) == cur.sc_int && rr-- == 0) node = m + i;
+    if (node >= 0) ladd = kth_label(T.lab[node], T.cut, (int)(r1.c % (uint32_t)cur.sc_int));
+  }
+  if (type != 0) {
+    int k = (int)(r1.d % (uint32_t)cur.ns);
+    for (int l = 0; l < T.nlab; l++)
+      if (T.cut[l] && k-- == 0) { lrem = l; break; }
+  }
+  if (type == 2 && ladd < 0) type = 1;
+  if (type == 0 && ladd < 0) return -1;
+  return type;
+}
+
 // Slice moves after a sweep (mirror of csrc/treesa_gpu.cu:445-502): add a label of a largest internal
 // tensor, remove a sliced label, or swap, Metropolis on E = |S| + lcost + sc penalty.
 void slice_step(Tree& T, float beta, uint32_t sweep, uint32_t chain, const OParams& P, int mode, Counter& C) {
-  const int m = T.m, nint = m - 1;
   Eval cur = eval_chain(T, P, mode);
   float Ecur = slice_energy(cur, P);
   for (int j = 0; j < P.slice_moves; j++) {
     const R4 r1 = philox10(R4{0x10000u + 2u * (uint32_t)j, sweep, chain, 0u}, P.key0, P.key1);
     const R4 r2 = philox10(R4{0x10001u + 2u * (uint32_t)j, sweep, chain, 0u}, P.key0, P.key1);
-    int type;  // 0 add, 1 remove, 2 swap
-    if (cur.ns == 0) type = 0;
-    else if (cur.ns >= P.max_slices) type = (r1.a >> 31) ? 1 : 2;
-    else type = r1.a < 0x80000000u ? 0 : (r1.a < 0xC0000000u ? 1 : 2);
-    int ladd = -1, lrem = -1;
-    if (type != 1 && cur.ncand > 0 && cur.sc_int > 0) {
-      int rr = (int)(r1.b % (uint32_t)cur.ncand), node = -1;
-      for (int i = 0; i < nint && node < 0; i++)
-        if (live_size(T.lab[m + i], T.cut) == cur.sc_int && rr-- == 0) node = m + i;
-      if (node >= 0) ladd = kth_label(T.lab[node], T.cut, (int)(r1.c % (uint32_t)cur.sc_int));
-    }
-    if (type != 0) {
-      int k = (int)(r1.d % (uint32_t)cur.ns);
-      for (int l = 0; l < T.nlab; l++)
-        if (T.cut[l] && k-- == 0) { lrem = l; break; }
-    }
-    if (type == 2 && ladd < 0) type = 1;
-    if (type == 0 && ladd < 0) continue;
+    int ladd, lrem;
+    const int type = propose_slice(T, cur, r1, P, ladd, lrem);
+    if (type < 0) continue;
     if (type != 1) T.cut[ladd] = 1;
     if (type != 0) T.cut[lrem] = 0;
     const Eval nxt = eval_chain(T, P, mode);
     const float Enew = slice_energy(nxt, P);
     C.sprop++;
-    if (accept(r2.a, beta, Enew - Ecur)) {
+    if (accept(r2.a, beta, Enew - Ecur, &C.near)) {
       C.sacc++;
       cur = nxt;
       Ecur = Enew;
@@ -666,7 +716,10 @@ void oracle_free(void* h) { delete static_cast<Inst*>(h); }
 uint64_t oracle_splitmix64(uint64_t x) { return smix64(x); }
 
 // Perturbation experiments only: see g_variant (0 restores the reference's arithmetic).
-void oracle_set_variant(int v) { g_variant = v; }
+void oracle_set_variant(int v, uint32_t noise_seed) {
+  g_variant = v;
+  g_noise_seed = noise_seed;
+}
 
 void oracle_philox(const uint32_t* ctr, uint32_t k0, uint32_t k1, uint32_t* out) {
   const R4 r = philox10(R4{ctr[0], ctr[1], ctr[2], ctr[3]}, k0, k1);
@@ -784,6 +837,26 @@ int oracle_energy(void* h, const OParams* P, int W, int ch_off, int s_off, int c
   return 0;
 }
 
+// One record's chain evaluation (the fold the sweep kernels run) and the slice proposal the words r1 make
+// from it: out = {type, ladd, lrem, sc_int, ncand, ns, sc}, *lcost the folded log2 cost.
+int oracle_slice_propose(void* h, const OParams* P, int W, int ch_off, int s_off, int chain_words,
+                         const uint64_t* rec, const uint32_t* r1, int* out, float* lcost) {
+  const Inst& I = *static_cast<Inst*>(h);
+  const Layout Lo{W, ch_off, s_off, chain_words};
+  const Tree T = from_record(I, Lo, rec, P->slicing != 0);
+  const Eval e = eval_chain(T, *P, P->mode);
+  int ladd, lrem;
+  out[0] = propose_slice(T, e, R4{r1[0], r1[1], r1[2], r1[3]}, *P, ladd, lrem);
+  out[1] = ladd;
+  out[2] = lrem;
+  out[3] = e.sc_int;
+  out[4] = e.ncand;
+  out[5] = e.ns;
+  out[6] = e.sc;
+  *lcost = e.lcost;
+  return 0;
+}
+
 // Host double-precision complexities of one record (csrc/treesa_gpu.cu:1206-1244): out = {tc, sc,
 // gpu_time, h100_time, |S|}.  gm / hm: the model constants as given on the command line.
 void oracle_host_energy(void* h, const double* gm, const double* hm, int W, int ch_off, int s_off, int chain_words,
@@ -809,6 +882,13 @@ struct OAnnealIn {
   const int32_t* lniters;  // nlev: sweeps of every level
   const double* gm;        // model constants as given on the command line (6 and 9 values)
   const double* hm;
+  // near-tie record (diagnostics; near_cap 0: off): every evaluated level's best chain whose score lies within
+  // near_tol of the incumbent's after the level, as {level, chain, score, lc, host tc, host sc}
+  double near_tol;
+  int32_t near_cap;
+  int32_t pad2;
+  double* near_out;        // near_cap x 6 doubles
+  int32_t* near_count;     // entries written (at most near_cap)
 };
 
 // What one level left (field order matches tests/oracle.py).
@@ -818,6 +898,8 @@ struct OLevel {
   double score, meanE, meanNs;
   double sel_margin;  // smallest gap between the level's best score and another tree's score, or the incumbent's
   double pop_margin;  // resampling: smallest |cumulative - pointer| (pa) or E gap between ranked neighbours (trunc)
+  int32_t metropolis_near;  // chains with a Metropolis decision within two ulp of expf in this level's sweeps
+  int32_t pad;
 };
 
 // The reference's run_anneal (csrc/treesa_gpu.cu:1756-1877) over the population pop (nc records, chain c in
@@ -869,11 +951,14 @@ int oracle_anneal(void* h, const OParams* P0, int W, int ch_off, int s_off, int 
     P.mode = mode;
     const float beta = in->betas[L];
     const int nsw = in->lniters[L];
-#pragma omp parallel for schedule(dynamic, 1)
+    int near_here = 0;
+#pragma omp parallel for schedule(dynamic, 1) reduction(+ : near_here)
     for (int c = 0; c < nc; c++) {
       Counter C;
       run_chain(trees[c], P, in->order, beta, sweeps, nsw, (uint32_t)c, C);
+      near_here += C.near ? 1 : 0;
     }
+    o.metropolis_near = near_here;
     sweeps += (uint32_t)nsw;
     const bool last = L + 1 == in->nlev;
     const bool switching = !last && in->lmode[L + 1] != mode;
@@ -906,6 +991,17 @@ int oracle_anneal(void* h, const OParams* P0, int W, int ch_off, int s_off, int 
       best_chain = bi;
       best = trees[bi];
       have_best = true;
+    }
+    if (in->near_cap > 0 && std::fabs(s[bi] - best_score) <= in->near_tol && *in->near_count < in->near_cap) {
+      double e[5];
+      tree_host_energy(trees[bi], in->gm, in->hm, e);
+      double* q = in->near_out + 6 * (size_t)(*in->near_count)++;
+      q[0] = L;
+      q[1] = bi;
+      q[2] = s[bi];
+      q[3] = lc[bi];
+      q[4] = e[0];
+      q[5] = e[1];
     }
     std::vector<int> seen(nc, 0);
     int nf = 0;

@@ -34,13 +34,16 @@ class OAnnealIn(ctypes.Structure):
                 ("eval_every", ctypes.c_int32), ("select_sc", ctypes.c_int32), ("pad", ctypes.c_int32),
                 ("trunc_frac", ctypes.c_double), ("sc_target", ctypes.c_double), ("sc_weight", ctypes.c_double),
                 ("seed", ctypes.c_uint64), ("betas", ctypes.c_void_p), ("lmode", ctypes.c_void_p),
-                ("lniters", ctypes.c_void_p), ("gm", ctypes.c_void_p), ("hm", ctypes.c_void_p)]
+                ("lniters", ctypes.c_void_p), ("gm", ctypes.c_void_p), ("hm", ctypes.c_void_p),
+                ("near_tol", ctypes.c_double), ("near_cap", ctypes.c_int32), ("pad2", ctypes.c_int32),
+                ("near_out", ctypes.c_void_p), ("near_count", ctypes.c_void_p)]
 
 
 # one level of oracle_anneal (struct OLevel)
 LEVEL_DTYPE = np.dtype([("evaluated", "<i4"), ("best", "<i4"), ("sc", "<i4"), ("ns", "<i4"), ("families", "<i4"),
                         ("mode", "<i4"), ("resampled", "<i4"), ("lc", "<f4"), ("score", "<f8"), ("meanE", "<f8"),
-                        ("meanNs", "<f8"), ("sel_margin", "<f8"), ("pop_margin", "<f8")])
+                        ("meanNs", "<f8"), ("sel_margin", "<f8"), ("pop_margin", "<f8"), ("metropolis_near", "<i4"),
+                        ("pad", "<i4")])
 
 SCHEMES = {"indep": 0, "pa": 1, "trunc": 2}
 
@@ -74,6 +77,7 @@ def load():
     lib.oracle_random_slices.argtypes = [I, U64, I, I, I, P]
     lib.oracle_sweeps.argtypes = [P, ctypes.POINTER(OParams), I, I, I, I, P, I, I, I, F, U32, I, P]
     lib.oracle_energy.argtypes = [P, ctypes.POINTER(OParams), I, I, I, I, P, I, P, P, P]
+    lib.oracle_slice_propose.argtypes = [P, ctypes.POINTER(OParams), I, I, I, I, P, P, P, P]
     lib.oracle_host_energy.argtypes = [P, P, P, I, I, I, I, P, I, P]
     lib.oracle_anneal.argtypes = [P, ctypes.POINTER(OParams), I, I, I, I, P, I, ctypes.POINTER(OAnnealIn), P, P, P,
                                   P, P]
@@ -83,7 +87,7 @@ def load():
     lib.oracle_score.argtypes = [I, I, I, ctypes.c_double, ctypes.c_double, F, I, I, I]
     lib.oracle_score.restype = ctypes.c_double
     lib.oracle_pa_uniforms.argtypes = [U64, I, P]
-    lib.oracle_set_variant.argtypes = [I]
+    lib.oracle_set_variant.argtypes = [I, U32]
     _lib = lib
     return lib
 
@@ -139,6 +143,18 @@ class Oracle:
                                pop.ctypes.data, n, lc.ctypes.data, sc.ctypes.data, ns.ctypes.data)
         return lc, sc, ns
 
+    def slice_propose(self, params, lay, rec, r1):
+        """The chain evaluation of one record and the slice proposal words r1 make from it: dict(type, ladd, lrem,
+        sc_int, ncand, ns, sc, lcost); type 0 add, 1 remove, 2 swap, -1 no move."""
+        rec = np.ascontiguousarray(rec, np.uint64)
+        w = np.array(r1, np.uint32)
+        out = np.zeros(7, np.int32)
+        lc = np.zeros(1, np.float32)
+        self.lib.oracle_slice_propose(self.h, ctypes.byref(params), lay.W, lay.ch_off, lay.s_off, lay.chain_words,
+                                      rec.ctypes.data, w.ctypes.data, out.ctypes.data, lc.ctypes.data)
+        keys = ("type", "ladd", "lrem", "sc_int", "ncand", "ns", "sc")
+        return dict(zip(keys, (int(x) for x in out)), lcost=float(lc[0]))
+
     def host_energy(self, lay, rec, slicing, gm, h100):
         rec = np.ascontiguousarray(rec, np.uint64)
         g = np.array(gm, np.float64)
@@ -149,7 +165,8 @@ class Oracle:
         return float(out[0]), int(out[1]), float(out[2]), float(out[3]), int(out[4])
 
     def anneal(self, params, lay, pop, betas, lmode, lniters, order, scheme="indep", eval_every=1, select_sc=False,
-               trunc_frac=0.25, sc_target=20.0, sc_weight=1.0, seed=1, gm=DEFAULT_GM, h100=DEFAULT_H100):
+               trunc_frac=0.25, sc_target=20.0, sc_weight=1.0, seed=1, gm=DEFAULT_GM, h100=DEFAULT_H100,
+               near_tol=0.0, near_cap=0):
         """The reference's level loop over a (nc, chain_words) population, in place (oracle_anneal).  Returns
         a dict: levels (LEVEL_DTYPE per level), anc (nlev x nc), best_rec, best_chain, nresample, staged,
         total_sweeps, h1 (the stage-1 incumbent's host energy when staged)."""
@@ -160,8 +177,11 @@ class Oracle:
         ln = np.array(lniters, np.int32)
         g = np.array(gm, np.float64)
         hm = np.array(h100, np.float64)
+        near = np.zeros((max(1, near_cap), 6), np.float64)
+        nnear = np.zeros(1, np.int32)
         a = OAnnealIn(nlev, order, SCHEMES[scheme], eval_every, 1 if select_sc else 0, 0, trunc_frac, sc_target,
-                      sc_weight, seed, b.ctypes.data, lm.ctypes.data, ln.ctypes.data, g.ctypes.data, hm.ctypes.data)
+                      sc_weight, seed, b.ctypes.data, lm.ctypes.data, ln.ctypes.data, g.ctypes.data, hm.ctypes.data,
+                      near_tol, near_cap, 0, near.ctypes.data, nnear.ctypes.data)
         levels = np.zeros(nlev, LEVEL_DTYPE)
         anc = np.zeros((nlev, nc), np.int32)
         best = np.zeros(lay.chain_words, np.uint64)
@@ -171,7 +191,7 @@ class Oracle:
                                pop.ctypes.data, nc, ctypes.byref(a), levels.ctypes.data, anc.ctypes.data,
                                best.ctypes.data, iout.ctypes.data, h1.ctypes.data)
         return {"levels": levels, "anc": anc, "best_rec": best, "best_chain": int(iout[0]), "nresample": int(iout[1]),
-                "staged": bool(iout[2]), "total_sweeps": int(iout[3]), "h1": h1}
+                "staged": bool(iout[2]), "total_sweeps": int(iout[3]), "h1": h1, "near": near[:int(nnear[0])]}
 
     def repair(self, lay, rec, sc_target):
         """Final greedy slice repair of rec's tree, S updated in place; returns the labels added."""
@@ -262,6 +282,6 @@ def pa_uniforms(seed, n):
     return out
 
 
-def set_variant(v):
+def set_variant(v, noise_seed=0):
     """Rounding variant of the oracle's float lse (0: the reference's arithmetic; see oracle_set_variant)."""
-    load().oracle_set_variant(int(v))
+    load().oracle_set_variant(int(v), int(noise_seed))

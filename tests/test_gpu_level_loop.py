@@ -23,7 +23,7 @@ import pytest
 
 import common
 import oracle as orc
-from treesa_gpu_amd import capi
+from treesa_gpu_amd import capi, formats
 
 pytestmark = pytest.mark.gpu
 
@@ -198,4 +198,30 @@ def test_level_loop_matches_oracle(c, tmp_path):
         assert r["staged"]
         assert abs(res["stage1_tc"] - r["h1"][0]) < 5e-6 and res["stage1_sc"] == int(r["h1"][1])
     print("[ok]", c.name, f"tc {res['tc']:.4f} sc {res['sc']} |S| {res['nsliced']} resampled {res['nresample']}",
+          flush=True)
+
+
+def test_c3_full_size_properties(tmp_path):
+    """The sat70 slicing workload at its benchmark size -- 2048 chains, 20 levels of 10 sweeps, one slice move
+    per sweep, population annealing after every level -- beyond what the oracle replays in test time: the
+    returned tree is valid over the sliced network, its label sets are the ones its topology gives, the tc / sc
+    / |S| the binary reports equal the driver's recomputation in Python from the tree and the sliced labels,
+    population annealing resampled after every level but the last (between 1 and 2048 families per level), and
+    the repaired result meets the sc target."""
+    c = Case("c3-full", "sat70", nchains=2048, niters=10, betas=linear_betas(0.01, 15.0, 20), sc_target=24.0,
+             slicing=True)
+    res, blev = run_binary(c, tmp_path)
+    assert res["valid"] and res["labels_ok"]
+    assert res["total_sweeps"] == 200 and res["nchains"] == 2048
+    m, nlab, ixs, iy = common.load_instance("sat70")
+    tree, info = formats.result_tree(res, ixs, iy)
+    assert abs(info["tc_py"] - res["tc"]) < 1e-4 and info["sc_py"] == res["sc"]
+    assert res["nsliced"] == len(res["sliced"]) == len(set(res["sliced"]))
+    assert abs(info["tc_total_py"] - (res["tc"] + res["nsliced"])) < 1e-4
+    assert res["sc"] <= c.sc_target
+    assert [b["level"] for b in blev] == list(range(20))
+    assert all(1 <= b["families"] <= 2048 for b in blev)
+    assert [b["resampled"] for b in blev] == [True] * 19 + [False]
+    assert res["slice_proposals"] > 0
+    print("[ok] c3 full size", f"tc {res['tc']:.4f} sc {res['sc']} |S| {res['nsliced']} resampled {res['nresample']}",
           flush=True)
