@@ -99,6 +99,10 @@ typedef struct tsa_config_t {
    * of each visit drawing its own: 0 = automatic (on for at most one chain per compute unit, where the sweeping
    * wave's dependent steps bound the sweep and three SIMDs idle), 1 = on, -1 = off.  Results do not change */
   int32_t draw_waves;
+  /* wide kernel with several workgroups per chain: polls a workgroup waits at the chain's check-in for the
+   * others before it sweeps the chain alone (0 = default, about a millisecond; -1 = at once, every chain swept
+   * by one workgroup -- for tests).  Results do not change */
+  int32_t wide_join;
 } tsa_config_t;
 
 typedef struct tsa_ctx tsa_ctx;

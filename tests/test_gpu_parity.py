@@ -29,7 +29,7 @@ def leaf_sets(m, ixs, W):
 class Case:
     def __init__(self, inst, order, mode, init="greedy", random_slices=0, par_follow=False, par_band=0, slicing=False,
                  slice_moves=1, slice_every=1, nchains=NCHAINS, kernel=capi.KERNEL_AUTO, wide=False, seed=None,
-                 sc_target=None, wide_waves=0, wide_wgs=0, sums=0, lanes=0, data=None, draw_waves=0):
+                 sc_target=None, wide_waves=0, wide_wgs=0, sums=0, lanes=0, data=None, draw_waves=0, wide_join=0):
         """inst names a fixture; data = (m, nlab, ixs, iy) gives an instance directly (then init must be a
         start-tree kind without fixture, e.g. "random")."""
         self.inst, self.order = inst, order
@@ -46,7 +46,7 @@ class Case:
                                     seed=seed, slicing=sl, slice_moves=slice_moves if slicing else 0,
                                     slice_every=slice_every, par_follow=par_follow, par_band=par_band, kernel=kernel,
                                     wide_waves=wide_waves, wide_wgs=wide_wgs, sums=sums, wide_lanes=lanes,
-                                    draw_waves=draw_waves)
+                                    draw_waves=draw_waves, wide_join=wide_join)
         self.leaf_sc = max(len(x) for x in ixs)
         self.P = orc.params_from_config(self.cfg, self.leaf_sc, nlab)
         self.leaf = leaf_sets(m, ixs, self.lay.W)
@@ -57,7 +57,7 @@ class Case:
         print(f"[gpu] {self.inst} {self.order} mode={self.cfg.mode} slicing={self.cfg.slicing} "
               f"kernel={self.cfg.kernel} W={self.lay.W} chains={self.nchains} wide_waves={self.cfg.wide_waves} "
               f"wide_wgs={self.cfg.wide_wgs} sums={self.cfg.sums} lanes={self.cfg.wide_lanes} "
-              f"draw_waves={self.cfg.draw_waves}", flush=True)
+              f"draw_waves={self.cfg.draw_waves} wide_join={self.cfg.wide_join}", flush=True)
         with capi.Context(self.lay, self.leaf, self.leaf_sc, self.cfg, self.nchains) as ctx:
             ctx.upload(self.pop0)
             for lev, b in enumerate(betas):
@@ -163,6 +163,21 @@ def test_wide_kernel_matches_oracle(inst, mode, waves, wgs, follow, band, sums, 
         assert (" sums=0 " in gpu[3]) == (sums < 0), gpu[3]
     if lanes:
         assert f" G={lanes} " in gpu[3], gpu[3]
+    compare(case, gpu, case.run_oracle())
+
+
+# Several workgroups per chain check in before they sweep it; a chain whose check-in runs out of polls is swept
+# by one of its workgroups alone.  Forced: every chain claimed at once (-1), or after a single poll (1, a mix of
+# claimed and shared chains): the result is the oracle's bit for bit either way, and the next launch (whose
+# check-in words the last workgroup of each chain reset) is too.
+@pytest.mark.parametrize("inst,mode,waves,wgs,join", [("sq46", "tc", 8, 3, -1), ("sq46", "gpu", 16, 5, 1),
+                                                      ("grid45", "tc", 16, 4, -1), ("grid24", "h100", 8, 2, 1),
+                                                      ("lat14", "tc", 2, 2, 1)])
+def test_wide_check_in_and_lone_sweeps_match_oracle(inst, mode, waves, wgs, join):
+    case = Case(inst, "par", mode, wide=True, kernel=capi.KERNEL_WIDE, wide_waves=waves, wide_wgs=wgs,
+                wide_join=join)
+    gpu = case.run_gpu()
+    assert f"blocks/chain={wgs}" in gpu[3], gpu[3]
     compare(case, gpu, case.run_oracle())
 
 

@@ -450,8 +450,9 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   if (c->wide.on)
     snprintf(kb, sizeof kb,
              "wide W=%d G=%d sums=%d waves/block=%d blocks/chain=%d lds_bytes/block=%d energy_blocks/chain=%d "
-             "fold_stage=%d",
-             lay->W, c->wide.G, c->wide.nsw, c->wide.nt / 64, c->wide.K, c->wide.smem, c->wide.eK, c->wide.fold_stage);
+             "fold_stage=%d xcds=%d",
+             lay->W, c->wide.G, c->wide.nsw, c->wide.nt / 64, c->wide.K, c->wide.smem, c->wide.eK, c->wide.fold_stage,
+             c->wide.nxcd);
   else
     snprintf(kb, sizeof kb, "%s W=%d waves/block=%d lds_bytes/wave=%d%s%s", use_lds ? "lds" : "global",
              use_lds ? c->Wt : lay->W, c->L.wpb, c->L.lds_words * 8,
@@ -495,10 +496,13 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   }
   if (c->wide.on) {
     const size_t nint4 = (size_t)((lay->nint + 3) & ~3);
-    TSA_CREATE_HIP(hipMalloc(&c->d_wsync, (size_t)nchains * 8));
-    TSA_CREATE_HIP(hipMemsetAsync(c->d_wsync, 0, (size_t)nchains * 8, c->st));
+    TSA_CREATE_HIP(hipMalloc(&c->d_wsync, (size_t)nchains * 12));
+    TSA_CREATE_HIP(hipMemsetAsync(c->d_wsync, 0, (size_t)nchains * 12, c->st));
     c->wsync.bar = c->d_wsync;
     c->wsync.done = c->d_wsync + nchains;
+    c->wsync.join = c->d_wsync + 2 * (size_t)nchains;
+    c->wsync.nxcd = c->wide.nxcd;
+    c->wsync.join_polls = cfg->wide_join;
     c->wsync.err = reinterpret_cast<unsigned*>(c->d_lc) + 3 * (size_t)nchains;
     if (c->wide.K > 1) TSA_CREATE_HIP(hipMalloc(&c->wsync.out, (size_t)nchains * 2 * nint4));
     TSA_CREATE_HIP(hipMalloc(&c->d_ncost, (size_t)nchains * nint4 * 4));
@@ -575,14 +579,18 @@ static hipError_t launch_energy(tsa_ctx* c) {
 }
 
 // The wide path's error word (set when a chain barrier gave up, leaving the population undefined):
-// reported once by the next synchronizing call, then cleared.
+// reported once by the next synchronizing call, then cleared.  A workgroup the device never started cannot
+// cause it (a chain's workgroups check in before its first barrier, and a chain whose check-in times out is
+// swept by one workgroup alone); only one of a chain's running workgroups descheduled for seconds could.
 static int wide_error(tsa_ctx* c, uint32_t word) {
   if (word == 0) return TSA_OK;
   c->costs_valid = false;
   c->sums_valid = false;
   (void)hipMemsetAsync(c->wsync.err, 0, 4, c->st);
   (void)hipStreamSynchronize(c->st);
-  return fail(c, TSA_ERR_HIP, "wide sweep kernel: a chain barrier timed out; the population is undefined");
+  return fail(c, TSA_ERR_HIP,
+              "wide sweep kernel: a chain barrier timed out after its workgroups had all started; the population is "
+              "undefined");
 }
 
 extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {

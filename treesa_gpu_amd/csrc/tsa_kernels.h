@@ -132,6 +132,7 @@ hipError_t tsa_launch_sum_stats(const unsigned long long* slots, unsigned long l
 #define TSA_WIDE_CPL 2        // 16-byte chunks per lane and label set (so W <= 2 * TSA_WIDE_CPL * 64 = 256)
 #define TSA_WIDE_MAX_K 16     // workgroups per chain
 #define TSA_WIDE_SPIN (1u << 22)  // polls of a chain barrier before the launch gives up (seconds)
+#define TSA_WIDE_JOIN (1u << 16)  // default polls of the check-in (milliseconds)
 
 struct TsaWide {
   int on;     // 1: par-order sweeps of this context run k_wide
@@ -145,10 +146,11 @@ struct TsaWide {
   int fold_smem_map;  // LDS bytes of stage 2
   int nsw;            // 64-bit words of a chunk summary per label set (0: no summaries; dense streaming)
   int lsum_lds;       // summaries: the input tensors' summaries are staged in LDS too
+  int nxcd;           // XCDs of the device (hipDeviceAttributeNumberOfXccs): workgroups are dealt to them in turn
 };
 
-// Device state of the wide sweep kernel: the chain barrier words bar[nchains], done[nchains], err[1] (all
-// zero between launches); outcome bytes of the visits of the last two phases, out[nchains][2][nint4]
+// Device state of the wide sweep kernel: the chain barrier words bar[nchains], done[nchains], join[nchains],
+// err[1] (all zero between launches); outcome bytes of the visits of the last two phases, out[nchains][2][nint4]
 // (K > 1 only); the per-node cost cache ncost / nz [nchains][nint4] (cost and masked size of every internal
 // node), which the sweep kernel keeps current on every accepted rotation and the energy kernel folds.
 // With chunk summaries (nsw > 0): sum[nchains][nint4][nsw] holds, for every internal node, bit c set iff
@@ -157,7 +159,10 @@ struct TsaWide {
 struct TsaWideSync {
   unsigned* bar;
   unsigned* done;
+  unsigned* join;  // K > 1: the chain's workgroups check in before they sweep it (see k_wide)
   unsigned* err;
+  int nxcd;        // XCDs of the device
+  int join_polls;  // polls of the check-in before a workgroup sweeps its chain alone; < 0: at once (tests)
   uint8_t* out;
   float* ncost;
   uint16_t* nz;

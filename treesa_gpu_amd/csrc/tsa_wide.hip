@@ -25,11 +25,21 @@
 // and the replays, of one phase commute.  Every proposal draws Philox((v, sweep, chain)), so the result is
 // the CPU phase-by-phase sweep bit for bit, whatever K and G.
 //
-// Chain barrier: all K * nchains workgroups are co-resident (the plan checks occupancy).  Thread 0 of each
-// workgroup releases at agent scope, adds 1 to the chain's counter and polls it until K * (barriers so far)
-// with a bounded number of polls; a workgroup that runs out of polls sets the error word, and every
-// workgroup that sees the error word stops, so every wave reaches the end of the kernel.  The last
-// workgroup of a chain to finish resets the chain's counters to zero for the next launch.
+// Check-in (K > 1): before it changes anything of its chain, each workgroup adds 1 to the chain's join word
+// and waits, with a bounded number of polls, until all K have arrived.  All K arrived means all K are
+// resident, and they stay resident until they leave, so the chain barriers below cannot wait on a workgroup
+// that the device has not started.  A workgroup that runs out of polls first (another one is not resident:
+// the device is shared with other work, or the plan's occupancy was wrong) claims the chain by setting the
+// join word's top bit with a compare-and-swap that fails if anyone arrived meanwhile; it then sweeps the
+// chain alone (K = 1 within the same kernel: the result is the same bit for bit), and every workgroup of the
+// chain that arrives later sees the bit and leaves at once.
+//
+// Chain barrier: thread 0 of each workgroup releases at agent scope, adds 1 to the chain's counter and polls
+// it until K * (barriers so far) with a bounded number of polls (seconds: only a workgroup descheduled for
+// that long could make a checked-in barrier wait); a workgroup that runs out of polls sets the error word, and
+// every workgroup that sees the error word stops, so every wave reaches the end of the kernel.  The last
+// workgroup of a chain to leave (all K of them leave, including those that only checked in) resets the
+// chain's words to zero for the next launch.
 #include "tsa_kernels.h"
 #include "tsa_fold.h"
 
@@ -106,6 +116,38 @@ __device__ __forceinline__ void group_sum(uint32_t (&a)[N]) {
   for (int o = G / 2; o > 0; o >>= 1) {
 #pragma unroll
     for (int i = 0; i < N; i++) a[i] += (uint32_t)__shfl_xor((int)a[i], o, G);
+  }
+}
+
+// Check-in of thread 0 (see the file comment): 0 sweep with the other K - 1, 1 sweep the chain alone, 2 leave.
+#define TSA_JOIN_CLAIMED 0x80000000u
+__device__ int chain_join(const TsaWideSync& sy, int c, int K) {
+  const unsigned old = __hip_atomic_fetch_add(sy.join + c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old & TSA_JOIN_CLAIMED) return 2;
+  const unsigned limit = sy.join_polls > 0 ? (unsigned)sy.join_polls : TSA_WIDE_JOIN;
+  unsigned polls = 0;
+  for (;;) {
+    unsigned v = __hip_atomic_load(sy.join + c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (v & TSA_JOIN_CLAIMED) return 2;
+    if (v >= (unsigned)K) return 0;
+    if (sy.join_polls < 0 || ++polls >= limit) {
+      if (__hip_atomic_compare_exchange_strong(sy.join + c, &v, v | TSA_JOIN_CLAIMED, __ATOMIC_RELAXED,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))
+        return 1;
+      continue;  // someone arrived (or claimed) meanwhile: look again
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// The last of the chain's K workgroups to leave resets its words for the next launch (thread 0).
+__device__ void chain_leave(const TsaWideSync& sy, int c, int K) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  const unsigned old = __hip_atomic_fetch_add(sy.done + c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (old == (unsigned)(K - 1)) {  // every workgroup of the chain has left
+    __hip_atomic_store(sy.bar + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(sy.join + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(sy.done + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -225,18 +267,19 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
   extern __shared__ __align__(16) unsigned char tsa_wsm[];
   __shared__ float s_lse[64];
   __shared__ uint64_t s_mt[TSA_MT_WORDS];
-  __shared__ int s_cnt, s_ok, s_next;
+  __shared__ int s_cnt, s_ok, s_next, s_role;
   const int NT = blockDim.x, nwv = NT >> 6, lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
   const int m = P.m, nint = P.nint, nint4 = (nint + 3) & ~3, ngrp = (nint + 63) >> 6;
   const int NW = P.W, nch = NW >> 1;
-  // Workgroups are dealt to the 8 XCDs of the device in turn (workgroup b to XCD b % 8), each XCD with its
-  // own L2.  With K > 1 the K workgroups of a chain are taken from one XCD -- b = 8 (K (c / 8) + k) + c % 8
-  // -- so that they share that L2 for the chain's label sets; the grid is K * nchains rounded up to a
-  // multiple of 8 chains, and workgroups past the last chain leave at once.
+  // Workgroups are dealt to the X = sy.nxcd XCDs of the device in turn (workgroup b to XCD b % X), each XCD
+  // with its own L2.  With K > 1 the K workgroups of a chain are taken from one XCD -- b = X (K (c / X) + k) +
+  // c % X -- so that they share that L2 for the chain's label sets; the grid is K * nchains rounded up to a
+  // multiple of X chains, and workgroups past the last chain leave at once.
   int c, k;
   if constexpr (COOP) {
-    const int x = (int)(blockIdx.x & 7u), sl = (int)(blockIdx.x >> 3);
-    c = (sl / K) * 8 + x;
+    const int X = sy.nxcd;
+    const int x = (int)(blockIdx.x % (unsigned)X), sl = (int)(blockIdx.x / (unsigned)X);
+    c = (sl / K) * X + x;
     k = sl - (sl / K) * K;
   } else {
     c = (int)blockIdx.x;
@@ -275,6 +318,22 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
   }
   if (threadIdx.x == 0) par[nint - 1] = 0xFFFFu;
   __syncthreads();
+
+  // K > 1: check in (see the file comment); a chain claimed by one workgroup is swept by it alone (Ke = 1)
+  int Ke = K, ke = k;
+  if constexpr (COOP) {
+    if (threadIdx.x == 0) s_role = chain_join(sy, c, K);
+    __syncthreads();
+    const int role = s_role;
+    if (role == 2) {
+      if (threadIdx.x == 0) chain_leave(sy, c, K);
+      return;
+    }
+    if (role == 1) {
+      Ke = 1;
+      ke = 0;
+    }
+  }
 
   constexpr int gpw = 64 / G;
   const int ngr = nwv * gpw;
@@ -396,13 +455,13 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
       // 2. visits: this workgroup's share of the work list -- entries k, k + K, k + 2K, ... (interleaved, so
       // that neighbouring entries, which cost alike, spread over the workgroups) -- handed out gpw at a time
       // to whichever wave asks next (an LDS counter), so that waves that run ahead take more
-      const int nk = (cnt - k + K - 1) / K;
+      const int nk = (cnt - ke + Ke - 1) / Ke;
       for (;;) {
         int i0 = 0;
         if (lane == 0) i0 = atomicAdd(&s_next, gpw);
         i0 = __shfl(i0, 0, 64);
         if (i0 >= nk) break;  // uniform within the wave
-        const int j = k + K * (i0 + gsub);
+        const int j = ke + Ke * (i0 + gsub);
         if (i0 + gsub < nk) {  // uniform within a lane group
           const int v = wl[j];
           const uint32_t chv = ch[v - m];
@@ -611,7 +670,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
       // 3. barrier
       if constexpr (COOP) {
         nb++;
-        if (!chain_barrier(sy, c, nb * (unsigned)K, &s_ok)) {
+        if (!chain_barrier(sy, c, nb * (unsigned)Ke, &s_ok)) {
           ok = false;
           break;
         }
@@ -640,7 +699,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
           if (On >= m) par[On - m] = (uint16_t)Pn;
           if (Mn >= m) par[Mn - m] = (uint16_t)v;
           if (P.par_follow && (pv & 1u) && pri[Pn - m] == 0) pri[Pn - m] = (uint16_t)tsa_follow_pri((uint32_t)Pn, hs);
-          if (SUMS && j % K != k)  // P's new summary, written by another workgroup's visit
+          if (SUMS && j % Ke != ke)  // P's new summary, written by another workgroup's visit
             for (int q = 0; q < nsw; q++) ssum[(size_t)(Pn - m) * nsw + q] = gsum[(size_t)(Pn - m) * nsw + q];
         }
         pri[v - m] = 0;
@@ -649,7 +708,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
     }
   }
 
-  if (ok && k == 0) {
+  if (ok && ke == 0) {
     for (int i = threadIdx.x; i < nint; i += NT) gch[i] = ch[i];
     if (sy.snap_ch) {  // the level's snapshot: tree from LDS, node costs (final after the last barrier)
       uint32_t* const sch = sy.snap_ch + (size_t)c * nint;
@@ -667,7 +726,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
     atomicAdd(&st[TSA_ST_ACC * TSA_STAT_SLOTS], (unsigned long long)sa_);
     atomicAdd(&st[TSA_ST_VISITS * TSA_STAT_SLOTS], (unsigned long long)sv_);
     atomicAdd(&st[TSA_ST_BUSY * TSA_STAT_SLOTS], (unsigned long long)sv_);
-    if (k == 0 && wv == 0) atomicAdd(&st[TSA_ST_STEPS * TSA_STAT_SLOTS], (unsigned long long)nst);
+    if (ke == 0 && wv == 0) atomicAdd(&st[TSA_ST_STEPS * TSA_STAT_SLOTS], (unsigned long long)nst);
     if (SUMS) {
       atomicAdd(&st[TSA_ST_CHUNKS * TSA_STAT_SLOTS], (unsigned long long)sk_);
       atomicAdd(&st[TSA_ST_XCHUNKS * TSA_STAT_SLOTS], (unsigned long long)sx_);
@@ -675,14 +734,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
   }
   if constexpr (COOP) {
     __syncthreads();
-    if (threadIdx.x == 0) {
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-      const unsigned old = __hip_atomic_fetch_add(sy.done + c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (old == (unsigned)(K - 1)) {  // every workgroup of the chain has left its last barrier
-        __hip_atomic_store(sy.bar + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(sy.done + c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
-    }
+    if (threadIdx.x == 0) chain_leave(sy, c, K);
   }
 }
 
@@ -801,8 +853,8 @@ hipError_t launch_wide_gms(const TsaWide& X, const TsaKParams& P, uint64_t* rec,
     // once, so on an idle device they are all resident together (the cooperative launch API gives the same
     // guarantee but costs tens of microseconds per launch on the host side); if they ever are not, a chain
     // barrier runs out of polls, sets the error word and every workgroup leaves
-    const int nchains8 = (nchains + 7) & ~7;  // (chains grouped by XCD, see k_wide)
-    hipExtLaunchKernelGGL((k_wide<G, MODE, true, SUMS>), dim3(nchains8 * X.K), dim3(X.nt), (uint32_t)X.smem, st, e0,
+    const int nchainsx = (nchains + X.nxcd - 1) / X.nxcd * X.nxcd;  // (chains grouped by XCD, see k_wide)
+    hipExtLaunchKernelGGL((k_wide<G, MODE, true, SUMS>), dim3(nchainsx * X.K), dim3(X.nt), (uint32_t)X.smem, st, e0,
                           e1, 0u, P, rec, leaf, fix, nchains, X.K, beta, sweep0, nsweeps, stats, sy);
     return hipGetLastError();
   }
@@ -952,11 +1004,17 @@ hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int w
   int G = want_g > 0 ? want_g : (X.nsw ? 1 : Gd);
   if (X.nsw ? (G < 1 || G > 16 || (G & (G - 1))) : (G < Gd || G > 64 || (G & (G - 1)))) return hipErrorInvalidValue;
   X.G = G;
-  int dev = 0, ncu = 0, lds_max = 0;
+  int dev = 0, ncu = 0, lds_max = 0, nxcd = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev);
   if (e == hipSuccess) e = hipDeviceGetAttribute(&lds_max, hipDeviceAttributeMaxSharedMemoryPerBlock, dev);
   if (e != hipSuccess) return e;
+  // XCDs of the device (8 on MI355X in its single-partition mode, 1 per partition otherwise)
+  if (hipDeviceGetAttribute(&nxcd, hipDeviceAttributeNumberOfXccs, dev) != hipSuccess || nxcd < 1 || nxcd > ncu) {
+    (void)hipGetLastError();
+    nxcd = 1;
+  }
+  X.nxcd = nxcd;
   // measured on MI355X: with at least one chain per CU, one 8-wave workgroup per chain streams best; with
   // fewer chains, 16-wave workgroups, as many per chain as stay co-resident
   // (the summary path is compiled for at most 8 waves per workgroup: its visit needs more registers)
@@ -991,9 +1049,10 @@ hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int w
   if (e == hipSuccess) e = wcost_lds_cap_g(Gd, lds_cap);
   if (e != hipSuccess) return e;
   if (per_cu < 1) return hipErrorInvalidValue;
-  // with K > 1 a chain's workgroups share one XCD (8 per device, see k_wide): the chains of the fullest XCD
-  // times K must be resident on its ncu / 8 compute units at once
-  const int kmax = per_cu * (ncu / 8) / ((nchains + 7) / 8);
+  // with K > 1 a chain's workgroups share one XCD (see k_wide): the chains of the fullest XCD times K must
+  // be resident on its ncu / nxcd compute units at once (when they are not -- the device is shared with other
+  // work -- a chain's check-in times out and one of its workgroups sweeps it alone)
+  const int kmax = per_cu * (ncu / nxcd) / ((nchains + nxcd - 1) / nxcd);
   int K = want_k > 0 ? want_k : (X.nsw ? 1 : kmax);
   K = K < 1 ? 1 : (K > TSA_WIDE_MAX_K ? TSA_WIDE_MAX_K : K);
   if (K > 1 && K > kmax) return hipErrorCooperativeLaunchTooLarge;
