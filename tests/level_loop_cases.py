@@ -152,19 +152,39 @@ def spectral_trees(inst, k, seed, nangles=24, nrandom=24):
     return np.array([S.path_tree(o) for _, _, o in so], np.uint32)
 
 
+SPECTRAL_DIR = os.path.join(HERE, "golden", "spectral_starts")
+
+
+def spectral_tree_path(inst, k, seed):
+    """The committed spectral start trees of a case: computed once, here, by spectral_trees.  numpy's eigh on
+    another machine may return other vectors for the degenerate eigenvalues of the lattices, hence other
+    start trees, so every run of a case reads these."""
+    return os.path.join(SPECTRAL_DIR, f"{inst}_k{k}_seed{seed}.tree")
+
+
+def write_spectral_starts(cases):
+    os.makedirs(SPECTRAL_DIR, exist_ok=True)
+    for c in cases:
+        if c["init"] != "spectral":
+            continue
+        p = spectral_tree_path(c["inst"], c["spectral_k"], c["seed"])
+        if os.path.exists(p):
+            continue
+        trees = spectral_trees(c["inst"], c["spectral_k"], c["seed"])
+        assert trees.shape[1] + 1 == common.load_instance(c["inst"])[0]
+        with open(p, "w") as f:
+            for t in trees:
+                for w in t:
+                    f.write(f"{int(w) & 0xFFFF} {int(w) >> 16}\n")
+
+
 def tree_file_for(c, tmpdir):
     """Path of the case's start-tree file (None: random trees)."""
     if c["init"] == "greedy":
         return common.tree_file(c["inst"], "greedy")
     if c["init"] == "spectral":
-        trees = spectral_trees(c["inst"], c["spectral_k"], c["seed"])
-        p = os.path.join(tmpdir, "spectral.tree")
-        m = trees.shape[1] + 1
-        with open(p, "w") as f:
-            for t in trees:
-                for w in t:
-                    f.write(f"{int(w) & 0xFFFF} {int(w) >> 16}\n")
-        assert m == common.load_instance(c["inst"])[0]
+        p = spectral_tree_path(c["inst"], c["spectral_k"], c["seed"])
+        assert os.path.exists(p), f"{p} missing (tests/golden/make_level_loop_answers.py writes it)"
         return p
     return None
 
