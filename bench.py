@@ -404,6 +404,9 @@ def main():
                     help="fold and selection of a level on the sweep's stream, not beside the next sweep")
     ap.add_argument("--draw-waves", type=int, default=0, choices=(-1, 0, 1),
                     help="pre-order: helper waves draw ahead (1), each visit draws (-1), automatic (0)")
+    ap.add_argument("--level-launches", action="store_true",
+                    help="scheme indep: one sweep launch and one selection per level instead of the level loop in one "
+                         "launch")
     ap.add_argument("--no-full", action="store_true", help="no full-schedule record when --steps is shorter")
     ap.add_argument("--no-quality", action="store_true", help="no best-tc-at-fixed-wall-time run (c2)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -425,7 +428,8 @@ def main():
         (["--wide-wgs", str(a.wide_wgs)] if a.wide_wgs else []) + \
         (["--wide-lanes", str(a.wide_lanes)] if a.wide_lanes else []) + \
         {"auto": [], "on": ["--sums"], "off": ["--no-sum"]}[a.sums] + (["--no-overlap"] if a.no_overlap else []) + \
-        (["--draw-waves", str(a.draw_waves)] if a.draw_waves else [])
+        (["--draw-waves", str(a.draw_waves)] if a.draw_waves else []) + \
+        (["--level-launches"] if a.level_launches else [])
     visits = steps * C["niters"] * nchains * (inst.m - 1)
 
     def measure(extra_args):

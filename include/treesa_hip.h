@@ -103,6 +103,10 @@ typedef struct tsa_config_t {
    * others before it sweeps the chain alone (0 = default, about a millisecond; -1 = at once, every chain swept
    * by one workgroup -- for tests).  Results do not change */
   int32_t wide_join;
+  /* tsa_anneal: 0 = automatic (the level loop in one launch when every chain of it is resident on the device
+   * at once, else one sweep launch and one selection per level), 1 = the level loop in one launch whenever the
+   * context's kernels run it, -1 = per-level launches.  Results do not change */
+  int32_t level_loop;
 } tsa_config_t;
 
 typedef struct tsa_ctx tsa_ctx;
@@ -198,6 +202,23 @@ int tsa_track(tsa_ctx* ctx, int32_t level);
  * wall-clock rate in Hz; ticks0 = device wall clock at tsa_track_begin. */
 int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_level, double* best_score, uint64_t* best_record,
                   tsa_trace_row_t* rows, uint64_t* ticks0, double* tick_hz);
+
+/* The level loop of a run without population steps (scheme indep), levels level0 .. level0 + nlevels - 1:
+ * niters[l] >= 1 sweeps at betas[l], the sweep counter running on from sweep0, and after every level with
+ * evaluated[l] != 0 the energies and selection of tsa_track.  Exactly tsa_sweeps for each level followed by
+ * tsa_track at the evaluated ones: the same population, statistics, trace rows and, at tsa_track_end, the
+ * same best chain, level, score and tree.  It replaces the level loop of run_anneal
+ * (csrc/treesa_gpu.cu:1788-1832), which the reference runs as one sweep launch and one host-side selection per
+ * level.  On the LDS kernels with every chain resident at once (tsa_config_t.level_loop) the call is ONE
+ * launch: each chain stays staged from its first level to its last, folds its energy and keeps its own best
+ * tree after every evaluated level, and the last chain to finish a level selects while the others sweep on, so
+ * no level waits for the host or for a launch (the trace row's ticks: the device clock of that selection).
+ * Else it runs those per-level launches itself.  Needs tsa_track_begin (max_levels >= level0 + nlevels); a
+ * session that has called tsa_track runs per-level launches, and tsa_track after a one-launch tsa_anneal in the
+ * same session fails.  tsa_describe names the way the last call ran.  The kernel time counts in
+ * tsa_sweeps_ms.  Asynchronous. */
+int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t nlevels, const float* betas,
+               const int32_t* niters, const uint8_t* evaluated, uint32_t sweep0);
 
 /* Human-readable description of the kernels this context launches (name, lanes, LDS bytes). */
 int tsa_describe(tsa_ctx* ctx, char* buf, int32_t len);

@@ -26,13 +26,22 @@ DEFAULT_H100 = (4e-6, 1.23e13, 5.44e-14, 7.68e-15, 6.37e-14, 2.02e-16, 1.77e-13,
 EXPORTS = ("tsa_layout", "tsa_create", "tsa_upload", "tsa_download", "tsa_sweeps", "tsa_sweeps_ms", "tsa_energy",
            "tsa_resample", "tsa_set_mode", "tsa_stats", "tsa_chunk_stats", "tsa_describe", "tsa_destroy", "tsa_last_error",
            "tsa_host_math", "tsa_host_alloc", "tsa_host_free", "tsa_track_begin", "tsa_track", "tsa_track_end",
-           "tsa_sweeps_noalloc")
+           "tsa_sweeps_noalloc", "tsa_anneal")
 
 
 class Layout(ctypes.Structure):
     _fields_ = [("m", ctypes.c_int32), ("nint", ctypes.c_int32), ("nlab", ctypes.c_int32), ("W", ctypes.c_int32),
                 ("runtime_width", ctypes.c_int32), ("ch_off", ctypes.c_int32), ("s_off", ctypes.c_int32),
                 ("chain_words", ctypes.c_int32)]
+
+
+class Select(ctypes.Structure):
+    _fields_ = [("mode", ctypes.c_int32), ("slicing", ctypes.c_int32), ("select_sc", ctypes.c_int32),
+                ("sc_target", ctypes.c_double), ("sc_weight", ctypes.c_double)]
+
+
+TRACE_ROW = np.dtype([("lc", "<f4"), ("sc", "<i4"), ("ns", "<i4"), ("chain", "<i4"), ("score", "<f8"),
+                      ("meanE", "<f8"), ("meanNs", "<f8"), ("ticks", "<u8")])
 
 
 class Config(ctypes.Structure):
@@ -47,7 +56,8 @@ class Config(ctypes.Structure):
                 ("v2_ltc_out", ctypes.c_float), ("v2_lsmall_cell", ctypes.c_float), ("v2_small_rank", ctypes.c_int32),
                 ("wide_waves", ctypes.c_int32), ("wide_wgs", ctypes.c_int32), ("fused_energy", ctypes.c_int32),
                 ("sums", ctypes.c_int32), ("wide_lanes", ctypes.c_int32),
-                ("track_overlap", ctypes.c_int32), ("draw_waves", ctypes.c_int32), ("wide_join", ctypes.c_int32)]
+                ("track_overlap", ctypes.c_int32), ("draw_waves", ctypes.c_int32), ("wide_join", ctypes.c_int32),
+                ("level_loop", ctypes.c_int32)]
 
 
 _lib = None
@@ -84,6 +94,10 @@ def load():
     lib.tsa_host_alloc.restype = P
     lib.tsa_host_free.argtypes = [P]
     lib.tsa_host_free.restype = None
+    lib.tsa_track_begin.argtypes = [P, ctypes.POINTER(Select), I32]
+    lib.tsa_track.argtypes = [P, I32]
+    lib.tsa_track_end.argtypes = [P, P, P, P, P, P, P, P]
+    lib.tsa_anneal.argtypes = [P, I32, I32, I32, P, P, P, U32]
     lib.tsa_sweeps_noalloc.argtypes = [ctypes.POINTER(Layout), ctypes.POINTER(Config), I32, P, P, I32, I32, F32, U32,
                                        I32, P, P, P, P, P]
     _lib = lib
@@ -120,7 +134,8 @@ def layout(m, nlab, wide=False):
 
 def make_config(mode="tc", sc_target=20.0, sc_weight=1.0, seed=1, slicing=False, slice_moves=1, slice_every=1,
                 max_slices=0, par_follow=False, par_band=0, kernel=KERNEL_AUTO, gm=DEFAULT_GM, h100=DEFAULT_H100,
-                wide_waves=0, wide_wgs=0, fused_energy=False, sums=0, wide_lanes=0, track_overlap=0, draw_waves=0, wide_join=0):
+                wide_waves=0, wide_wgs=0, fused_energy=False, sums=0, wide_lanes=0, track_overlap=0, draw_waves=0, wide_join=0,
+                level_loop=0):
     """Config with the fields the reference's Runner derives from its options (csrc/treesa_gpu.cu:1449-1474)."""
     k = splitmix64(seed)
     c = Config()
@@ -149,6 +164,7 @@ def make_config(mode="tc", sc_target=20.0, sc_weight=1.0, seed=1, slicing=False,
     c.track_overlap = int(track_overlap)  # 0: automatic, -1: fold and selection on the sweep's stream
     c.draw_waves = int(draw_waves)  # pre-order: 0 automatic, 1 helper waves draw ahead, -1 each visit draws
     c.wide_join = int(wide_join)  # wide kernel, K > 1: check-in polls (0 default, -1 every chain swept alone)
+    c.level_loop = int(level_loop)  # tsa_anneal: 0 automatic, 1 one launch whenever possible, -1 per-level launches
     return c
 
 
@@ -213,6 +229,37 @@ class Context:
         out = np.zeros(2, np.uint64)
         self._check(self.lib.tsa_chunk_stats(self.h, out.ctypes.data))
         return [int(x) for x in out]
+
+    def track_begin(self, mode="tc", slicing=False, select_sc=False, sc_target=20.0, sc_weight=1.0, max_levels=1):
+        s = Select()
+        s.mode = MODES[mode] if isinstance(mode, str) else int(mode)
+        s.slicing, s.select_sc = int(bool(slicing)), int(bool(select_sc))
+        s.sc_target, s.sc_weight = float(sc_target), float(sc_weight)
+        self._max_levels = max_levels
+        self._check(self.lib.tsa_track_begin(self.h, ctypes.byref(s), max_levels))
+
+    def track(self, level):
+        self._check(self.lib.tsa_track(self.h, level))
+
+    def anneal(self, order, betas, niters, evaluated, level0=0, sweep0=0):
+        """tsa_anneal over len(betas) levels."""
+        b = np.ascontiguousarray(betas, dtype=np.float32)
+        it = np.ascontiguousarray(niters, dtype=np.int32)
+        ev = np.ascontiguousarray(evaluated, dtype=np.uint8)
+        assert len(b) == len(it) == len(ev)
+        self._check(self.lib.tsa_anneal(self.h, order, level0, len(b), b.ctypes.data, it.ctypes.data, ev.ctypes.data,
+                                        sweep0))
+
+    def track_end(self):
+        """(best_chain, best_level, best_score, best_record, rows, ticks0, tick_hz)."""
+        bc, bl = ctypes.c_int32(), ctypes.c_int32()
+        bs, hz = ctypes.c_double(), ctypes.c_double()
+        t0 = ctypes.c_uint64()
+        rec = np.zeros(self.lay.chain_words, np.uint64)
+        rows = np.zeros(self._max_levels, TRACE_ROW)
+        self._check(self.lib.tsa_track_end(self.h, ctypes.byref(bc), ctypes.byref(bl), ctypes.byref(bs), rec.ctypes.data,
+                                           rows.ctypes.data, ctypes.byref(t0), ctypes.byref(hz)))
+        return bc.value, bl.value, bs.value, rec, rows, t0.value, hz.value
 
     def describe(self):
         buf = ctypes.create_string_buffer(256)

@@ -85,8 +85,29 @@ struct tsa_ctx {
   uint16_t* d_snap_nz[2] = {nullptr, nullptr};
   uint32_t* d_snap_en[2] = {nullptr, nullptr};  // energies folded by the sweep kernel: lc, sc, ns per chain
   int snap_kind[2] = {0, 0};  // what the sweep that filled a slot left there: a SNAP_* value
+  // The level loop on the device (tsa_anneal, TsaLevels): the tracking session's kind (0: nothing tracked
+  // yet, TRACK_LEVELS: tsa_track, TRACK_ANNEAL: tsa_anneal), whether the per-chain best still has to be
+  // reset, the levels evaluated so far in the session, and the buffers, grown on demand.
+  int track_kind = 0;
+  bool lv_reset = false;
+  int lv_resident[6] = {-1, -1, -1, -1, -1, -1};  // level-loop chains resident per compute unit, per mode and order
+  int lv_used = -1;                               // whether the last tsa_anneal ran the level loop (-1: none yet)
+  std::vector<char> lv_evaluated;
+  int lv_cap_levels = 0, lv_cap_evals = 0;
+  int* d_lv = nullptr;               // per level: beta (as bits), sweeps, evaluated index (-1: not evaluated)
+  int* h_lv = nullptr;               // pinned staging of d_lv
+  hipEvent_t ev_lv = nullptr;        // recorded after the upload that read h_lv last
+  bool lv_pending = false;
+  uint32_t* d_lv_en = nullptr;       // lc | sc | ns per evaluated level and chain
+  unsigned* d_lv_cnt = nullptr;      // arrival counters, (ngroups + 1) per evaluated level
+  TsaTrackPart* d_lv_part = nullptr; // group results, ngroups per evaluated level
+  uint64_t* d_cand = nullptr;        // two candidate trees per chain
+  double* d_own = nullptr;           // per chain: best score and the slot of its tree
+  int* d_bslot = nullptr;
   std::string err;
 };
+
+enum { TRACK_LEVELS = 1, TRACK_ANNEAL = 2 };
 
 static thread_local std::string g_err;
 
@@ -261,6 +282,15 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_trace) (void)hipFree(c->d_trace);
   if (c->d_best) (void)hipFree(c->d_best);
   if (c->d_ticks0) (void)hipFree(c->d_ticks0);
+  if (c->d_lv) (void)hipFree(c->d_lv);
+  if (c->h_lv) (void)hipHostFree(c->h_lv);
+  if (c->ev_lv) (void)hipEventDestroy(c->ev_lv);
+  if (c->d_lv_en) (void)hipFree(c->d_lv_en);
+  if (c->d_lv_cnt) (void)hipFree(c->d_lv_cnt);
+  if (c->d_lv_part) (void)hipFree(c->d_lv_part);
+  if (c->d_cand) (void)hipFree(c->d_cand);
+  if (c->d_own) (void)hipFree(c->d_own);
+  if (c->d_bslot) (void)hipFree(c->d_bslot);
   if (c->st) (void)hipStreamDestroy(c->st);
   delete c;
 }
@@ -793,6 +823,9 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   }
   ctx->overlap = want_overlap;
   ctx->slot = 0;
+  ctx->track_kind = 0;
+  ctx->lv_reset = true;
+  ctx->lv_evaluated.assign((size_t)max_levels, 0);
   TSA_HIP(ctx, hipMemsetAsync(ctx->d_trace, 0, (size_t)max_levels * sizeof(TsaTraceRowD), ctx->st));
   TSA_HIP(ctx, hipMemsetAsync(ctx->d_best, 0, (size_t)ctx->lay.chain_words * 8, ctx->st));
   TSA_HIP(ctx, tsa_launch_track_init(ctx->d_track, ctx->d_ticks0, ctx->st));
@@ -803,6 +836,9 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_track: null context");
   if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_track: no tsa_track_begin");
   if (level < 0 || level >= ctx->track_levels) return fail(ctx, TSA_ERR_ARG, "tsa_track: level out of range");
+  if (ctx->track_kind == TRACK_ANNEAL)
+    return fail(ctx, TSA_ERR_ARG, "tsa_track: this tracking session runs its levels with tsa_anneal");
+  ctx->track_kind = TRACK_LEVELS;
   TsaSelect S = ctx->sel;
   S.mode = ctx->mode;
   const tsa_layout_t& L = ctx->lay;
@@ -860,6 +896,27 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
   TSA_HIP(ctx, quiesce_track(ctx));
   if (wide_error(ctx, werr) != TSA_OK) return TSA_ERR_HIP;
+  if (ctx->track_kind == TRACK_ANNEAL) {
+    // the device level loop wrote the rows; the best is the lowest score over the evaluated levels' rows
+    // (first level on ties, as k_track keeps it), and that chain's tree is the one its best slot holds: a chain
+    // whose score equals the lowest at an earlier level would have been chosen at that level
+    h.best_score = INFINITY;
+    h.best_chain = h.best_level = -1;
+    for (int l = 0; l < ctx->track_levels; l++)
+      if (ctx->lv_evaluated[l] && rows[l].chain >= 0 && rows[l].score < h.best_score) {
+        h.best_score = rows[l].score;
+        h.best_chain = rows[l].chain;
+        h.best_level = l;
+      }
+    if (h.best_chain >= 0) {
+      int bs = -1;
+      TSA_HIP(ctx, hipMemcpy(&bs, ctx->d_bslot + h.best_chain, 4, hipMemcpyDeviceToHost));
+      if (bs < 0 || bs > 1) return fail(ctx, TSA_ERR_HIP, "tsa_track_end: the best chain has no kept tree");
+      const int cw = L.s_off + L.W - L.ch_off;
+      TSA_HIP(ctx, hipMemcpy(best_record + L.ch_off, ctx->d_cand + ((size_t)bs * ctx->nchains + h.best_chain) * cw,
+                             (size_t)cw * 8, hipMemcpyDeviceToHost));
+    }
+  }
   int dev = 0, khz = 0;
   TSA_HIP(ctx, hipGetDevice(&dev));
   TSA_HIP(ctx, hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
@@ -868,6 +925,149 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
   *best_score = h.best_score;
   *ticks0 = t0;
   *tick_hz = (double)khz * 1e3;
+  return TSA_OK;
+}
+
+// Grow the level loop's buffers to nlev levels with nev evaluated ones (the sizes only grow).
+static int levels_alloc(tsa_ctx* ctx, int nlev, int nev) {
+  const int n = ctx->nchains, ng = (n + 255) / 256;
+  const tsa_layout_t& L = ctx->lay;
+  if (!ctx->d_cand) {
+    const size_t cw = (size_t)(L.s_off + L.W - L.ch_off);
+    TSA_HIP(ctx, hipMalloc(&ctx->d_cand, 2 * (size_t)n * cw * 8));
+    TSA_HIP(ctx, hipMalloc(&ctx->d_own, (size_t)n * 8));
+    TSA_HIP(ctx, hipMalloc(&ctx->d_bslot, (size_t)n * 4));
+    TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_lv, hipEventDisableTiming));
+  }
+  if (nlev > ctx->lv_cap_levels) {
+    if (ctx->lv_pending) TSA_HIP(ctx, hipEventSynchronize(ctx->ev_lv));
+    ctx->lv_pending = false;
+    if (ctx->d_lv) TSA_HIP(ctx, hipFree(ctx->d_lv));
+    if (ctx->h_lv) TSA_HIP(ctx, hipHostFree(ctx->h_lv));
+    ctx->d_lv = nullptr;
+    ctx->h_lv = nullptr;
+    TSA_HIP(ctx, hipMalloc(&ctx->d_lv, (size_t)nlev * 3 * 4));
+    TSA_HIP(ctx, hipHostMalloc(&ctx->h_lv, (size_t)nlev * 3 * 4, hipHostMallocDefault));
+    ctx->lv_cap_levels = nlev;
+  }
+  if (nev > ctx->lv_cap_evals) {
+    TSA_HIP(ctx, hipStreamSynchronize(ctx->st));  // a running level loop may still use the old buffers
+    if (ctx->d_lv_en) TSA_HIP(ctx, hipFree(ctx->d_lv_en));
+    if (ctx->d_lv_cnt) TSA_HIP(ctx, hipFree(ctx->d_lv_cnt));
+    if (ctx->d_lv_part) TSA_HIP(ctx, hipFree(ctx->d_lv_part));
+    ctx->d_lv_en = nullptr;
+    ctx->d_lv_cnt = nullptr;
+    ctx->d_lv_part = nullptr;
+    TSA_HIP(ctx, hipMalloc(&ctx->d_lv_en, (size_t)nev * n * 3 * 4));
+    TSA_HIP(ctx, hipMalloc(&ctx->d_lv_cnt, ((size_t)nev * (ng + 1) + 1) / 2 * 8));  // cleared as 64-bit words
+    TSA_HIP(ctx, hipMalloc(&ctx->d_lv_part, (size_t)nev * ng * sizeof(TsaTrackPart)));
+    ctx->lv_cap_evals = nev;
+  }
+  return TSA_OK;
+}
+
+extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t nlevels, const float* betas,
+                          const int32_t* niters, const uint8_t* evaluated, uint32_t sweep0) {
+  if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_anneal: null context");
+  if (order != TSA_ORDER_PAR && order != TSA_ORDER_PREORDER) return fail(ctx, TSA_ERR_ARG, "--order par|preorder");
+  if (!betas || !niters || !evaluated || nlevels < 1) return fail(ctx, TSA_ERR_ARG, "tsa_anneal: no levels");
+  if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_anneal: no tsa_track_begin");
+  if (level0 < 0 || nlevels > ctx->track_levels - level0)
+    return fail(ctx, TSA_ERR_ARG, "tsa_anneal: levels beyond tsa_track_begin's max_levels");
+  long long total = 0;
+  int nev = 0;
+  for (int l = 0; l < nlevels; l++) {
+    if (niters[l] < 1) return fail(ctx, TSA_ERR_ARG, "tsa_anneal: a level with no sweep");
+    total += niters[l];
+    nev += evaluated[l] != 0;
+  }
+  if (total > INT32_MAX) return fail(ctx, TSA_ERR_ARG, "tsa_anneal: more than 2^31 - 1 sweeps in one call");
+  // One launch for the whole call when the context's kernels run the level loop (the LDS kernels), it is not
+  // turned off, and either it is asked for or every chain of it is resident at once: with more chains than
+  // that, a chain resident only after others have run all their levels would leave the per-level launches'
+  // fold of every chain in one round and their occupancy for nothing.  A session that began with one kind
+  // stays with it (the best is tracked per chain by the level loop, per level by tsa_track).
+  bool loop = ctx->track_kind == TRACK_ANNEAL;
+  if (ctx->track_kind == 0 && !ctx->wide.on && ctx->L.lds && ctx->cfg.level_loop >= 0) {
+    loop = ctx->cfg.level_loop > 0;
+    if (!loop) {
+      int& r = ctx->lv_resident[ctx->mode * 2 + order];
+      if (r < 0) {
+        TsaLevels q{};
+        const TsaEnergyOut eo{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+        TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
+                                       ctx->nchains, 0.0f, 0u, 0, ctx->d_stats, eo, ctx->st, nullptr, nullptr, &q, &r));
+      }
+      loop = (long long)r * ctx->ncu >= ctx->nchains;
+    }
+  }
+  ctx->lv_used = loop ? 1 : 0;
+  if (!loop) {  // one sweep launch per level, a selection at each evaluated one
+    uint32_t sw = sweep0;
+    for (int l = 0; l < nlevels; l++) {
+      int rc = tsa_sweeps(ctx, order, betas[l], sw, niters[l]);
+      sw += (uint32_t)niters[l];
+      if (rc == TSA_OK && evaluated[l]) rc = tsa_track(ctx, level0 + l);
+      if (rc != TSA_OK) return rc;
+    }
+    return TSA_OK;
+  }
+  if (levels_alloc(ctx, nlevels, nev > 0 ? nev : 1) != TSA_OK) return TSA_ERR_HIP;
+  ctx->track_kind = TRACK_ANNEAL;
+  const int n = ctx->nchains, ng = (n + 255) / 256;
+  // the schedule, through pinned staging the previous call's upload has finished reading
+  if (ctx->lv_pending) TSA_HIP(ctx, hipEventSynchronize(ctx->ev_lv));
+  int* h = ctx->h_lv;
+  for (int l = 0, e = 0; l < nlevels; l++) {
+    memcpy(&h[l], &betas[l], 4);
+    h[nlevels + l] = niters[l];
+    h[2 * nlevels + l] = evaluated[l] ? e++ : -1;
+    if (evaluated[l]) ctx->lv_evaluated[level0 + l] = 1;
+  }
+  join_track(ctx);
+  ctx->last_slot = -1;
+  ctx->energy_fresh = ctx->energy_host = false;
+  ctx->costs_valid = ctx->sums_valid = false;
+  TSA_HIP(ctx, hipMemcpyAsync(ctx->d_lv, h, (size_t)nlevels * 3 * 4, hipMemcpyHostToDevice, ctx->st));
+  TSA_HIP(ctx, hipEventRecord(ctx->ev_lv, ctx->st));
+  ctx->lv_pending = true;
+  if (ctx->lv_reset) {
+    TSA_HIP(ctx, tsa_launch_levels_init(ctx->d_own, ctx->d_bslot, n, ctx->st));
+    ctx->lv_reset = false;
+  }
+  // the arrival counters start at zero (each launch also leaves them so, unless it was cut short)
+  const size_t cnt_words = (size_t)(nev > 0 ? nev : 1) * (ng + 1);
+  TSA_HIP(ctx, tsa_launch_zero(reinterpret_cast<unsigned long long*>(ctx->d_lv_cnt), (int)((cnt_words + 1) / 2),
+                               ctx->st));
+  while ((int)ctx->ev.size() < 2 * (ctx->npending + 1)) {
+    hipEvent_t e;
+    TSA_HIP(ctx, hipEventCreate(&e));
+    ctx->ev.push_back(e);
+  }
+  hipEvent_t e0 = ctx->ev[2 * ctx->npending], e1 = ctx->ev[2 * ctx->npending + 1];
+  TsaLevels lv{};
+  lv.beta = reinterpret_cast<const float*>(ctx->d_lv);
+  lv.niters = ctx->d_lv + nlevels;
+  lv.eval = ctx->d_lv + 2 * nlevels;
+  lv.nlev = nlevels;
+  lv.total = (int)total;
+  lv.level0 = level0;
+  lv.en_lc = reinterpret_cast<float*>(ctx->d_lv_en);
+  lv.en_sc = reinterpret_cast<int*>(ctx->d_lv_en) + (size_t)ctx->lv_cap_evals * n;
+  lv.en_ns = reinterpret_cast<int*>(ctx->d_lv_en) + 2 * (size_t)ctx->lv_cap_evals * n;
+  lv.cnt = ctx->d_lv_cnt;
+  lv.part = ctx->d_lv_part;
+  lv.cand = ctx->d_cand;
+  lv.cand_words = ctx->lay.s_off + ctx->lay.W - ctx->lay.ch_off;
+  lv.own = ctx->d_own;
+  lv.bslot = ctx->d_bslot;
+  lv.trace = ctx->d_trace;
+  lv.S = ctx->sel;
+  lv.S.mode = ctx->mode;
+  const TsaEnergyOut eo{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, n, 0.0f,
+                                 sweep0, 0, ctx->d_stats, eo, ctx->st, e0, e1, &lv));
+  ctx->npending++;
   return TSA_OK;
 }
 
@@ -948,7 +1148,8 @@ extern "C" int tsa_chunk_stats(tsa_ctx* ctx, uint64_t out[2]) {
 
 extern "C" int tsa_describe(tsa_ctx* ctx, char* buf, int32_t len) {
   if (!ctx || !buf || len < 1) return fail(ctx, TSA_ERR_ARG, "tsa_describe: null argument");
-  snprintf(buf, (size_t)len, "%s", ctx->kname.c_str());
+  snprintf(buf, (size_t)len, "%s%s", ctx->kname.c_str(),
+           ctx->lv_used < 0 ? "" : (ctx->lv_used ? " anneal=level_loop" : " anneal=level_launches"));
   return TSA_OK;
 }
 

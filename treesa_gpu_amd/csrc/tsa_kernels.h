@@ -63,6 +63,36 @@ struct TsaEnergyOut {
   uint32_t* ch;
 };
 
+struct TsaTrackPart;
+struct TsaTraceRowD;
+
+// The level loop of independent chains run by one sweep launch (nlev > 0; nlev == 0: the launch's single
+// beta and nsweeps).  Level l sweeps niters[l] >= 1 times at beta[l], the sweep counter running on across
+// levels from sweep0.  After an evaluated level (eval[l] = e >= 0, its index among the launch's evaluated
+// levels) every chain folds its energy into en_* [e * nchains + c], writes its tree (the record's words
+// [ch_off, s_off + W)) into one of its two candidate slots (cand + (slot * nchains + c) * cand_words) and
+// keeps that slot when its score beats the best it has had (own / bslot, per chain, read at the start of
+// the launch and written at its end).  The last of a group of 256 chains to arrive reduces the group into
+// part [e * ngroups + g], the last group the level, into trace[level0 + l], in the order k_track reduces.
+// cnt: (ngroups + 1) arrival counters per evaluated level, zero before the launch and left zero after it.
+struct TsaLevels {
+  const float* beta;
+  const int* niters;
+  const int* eval;
+  int nlev, total, level0;   // levels; sweeps over all of them; the trace row of level 0
+  float* en_lc;
+  int* en_sc;
+  int* en_ns;
+  unsigned* cnt;
+  TsaTrackPart* part;
+  uint64_t* cand;
+  int cand_words;
+  double* own;
+  int* bslot;
+  TsaTraceRowD* trace;
+  TsaSelect S;
+};
+
 // Copy n elements with nthr threads (this one is tid), U loads per thread in flight at once: a loop that
 // stores each element before it loads the next waits a memory latency per element.
 template <typename T, int U>
@@ -86,7 +116,10 @@ __device__ __forceinline__ void tsa_copy_inflight(T* dst, const T* __restrict__ 
 hipError_t tsa_launch_sweeps(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
                              const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
                              int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st,
-                             hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
+                             hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr, const TsaLevels* lv = nullptr,
+                             int* res = nullptr);
+// With res set nothing is launched: *res = chains of the launch's kernel (the level loop's with lv set) that
+// are resident on one compute unit at once.
 hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
                              const uint32_t* fix, int nchains, float* lc, int* sc, int* ns, hipStream_t st);
 // The fold of node costs a sweep launch left in cost / z (nchains * nint4 each) into lc / sc / ns.
@@ -118,6 +151,8 @@ hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int n
                             const uint32_t* ch_snap, TsaTrackState* st, TsaTraceRowD* trace, uint64_t* best_rec,
                             TsaTrackPart* part, unsigned* done, hipStream_t stream);
 hipError_t tsa_launch_track_init(TsaTrackState* st, unsigned long long* ticks0, hipStream_t stream);
+// The level loop's per-chain best (TsaLevels.own / bslot) of n chains reset: +inf, no slot.
+hipError_t tsa_launch_levels_init(double* own, int* bslot, int n, hipStream_t stream);
 hipError_t tsa_launch_copy(const uint64_t* src, uint64_t* dst, const int* anc, int nchains, int chain_words,
                            hipStream_t st);
 // n zeroed 64-bit words, by a kernel.

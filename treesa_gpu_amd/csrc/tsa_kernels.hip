@@ -317,18 +317,229 @@ __device__ __forceinline__ long long tsa_wave_sum(long long x) {
 // 64-node groups per batch of the par scan.
 #define TSA_SCAN_GROUPS 8
 
-// Sweep kernel.  ORDER 0: par, 1: pre-order.  LDS: chain and leaf table staged in LDS.
+// ---------------------------------------------------------------------------------------------------
+// The level loop on the device (TsaLevels): the selection of an evaluated level, by the last chain to
+// arrive, in the order k_track reduces (csrc/treesa_gpu.cu:1810-1832 is the loop it replaces).
+// ---------------------------------------------------------------------------------------------------
+
+// One entry of the selection's reduction: best score and its chain, sums of E and |S|.
+struct TsaRed {
+  double s, e, n;
+  int i;
+};
+
+// k_track's combination of entries a (lower position) and b: the lower score, the lower chain on ties.
+__device__ __forceinline__ void tsa_red_merge(TsaRed& a, const TsaRed& b) {
+  if (b.s < a.s || (b.s == a.s && b.i < a.i)) {
+    a.s = b.s;
+    a.i = b.i;
+  }
+  a.e += b.e;
+  a.n += b.n;
+}
+
+// k_track's 256-entry tree (strides 128, 64, ..., 1, entry t combined with t + stride) by one wave: entry
+// t = lane + 64 j sits in v[j]; the result is lane 0's.
+__device__ __forceinline__ TsaRed tsa_red_tree256(TsaRed* v) {
+  tsa_red_merge(v[0], v[2]);
+  tsa_red_merge(v[1], v[3]);
+  tsa_red_merge(v[0], v[1]);
+  TsaRed a = v[0];
+  for (int o = 32; o > 0; o >>= 1) {
+    TsaRed b;
+    b.s = __shfl_down(a.s, o, 64);
+    b.e = __shfl_down(a.e, o, 64);
+    b.n = __shfl_down(a.n, o, 64);
+    b.i = __shfl_down(a.i, o, 64);
+    tsa_red_merge(a, b);
+  }
+  return a;
+}
+
+// A chain's best score over the levels evaluated so far and the candidate slot holding that tree (-1: none).
+struct TsaOwn {
+  double s;
+  int slot;
+};
+
+// Chain c's arrival at evaluated level (ev, its index among the launch's evaluated levels; level, its trace
+// row), by one whole wave; lc / sc / ns (lane 0's count) are the chain's energies, o its best so far, cslot
+// the slot this level's tree was just written to; returns the chain's best (uniform over the wave).  The
+// last chain of the group of 256 reduces the group as a k_track workgroup does; the last group reduces the
+// groups as k_track's last workgroup does and writes the trace row.  Not inlined, here and in the level
+// functions below: the sweep loop's registers stay as they are without the level loop, and this runs
+// once per evaluated level.
+__device__ __noinline__ TsaOwn tsa_level_arrive(const TsaLevels& Lv, int n, int c, int ev, int level, float lc, int sc,
+                                                int ns, TsaOwn o, int cslot, int lane) {
+  double own = o.s;
+  int bslot = o.slot;
+  const int ng = (n + 255) >> 8, g = c >> 8;
+  unsigned* const cnt = Lv.cnt + (size_t)ev * (ng + 1);
+  const size_t e0 = (size_t)ev * n;
+  int last = 0;
+  if (lane == 0) {
+    Lv.en_lc[e0 + c] = lc;
+    Lv.en_sc[e0 + c] = sc;
+    Lv.en_ns[e0 + c] = ns;
+    const double s = tsa_score(lc, sc, ns, Lv.S);
+    if (s < own) {
+      own = s;
+      bslot = cslot;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const int gsize = n - (g << 8) < 256 ? n - (g << 8) : 256;
+    const unsigned old = __hip_atomic_fetch_add(cnt + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == (unsigned)gsize - 1u;
+  }
+  own = __shfl(own, 0, 64);
+  bslot = __shfl(bslot, 0, 64);
+  const TsaOwn res{own, bslot};
+  if (!__shfl(last, 0, 64)) return res;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  TsaRed v[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int cc = (g << 8) + lane + 64 * j;
+    v[j] = TsaRed{INFINITY, 0.0, 0.0, n};
+    if (cc < n) {
+      const float l = Lv.en_lc[e0 + cc];
+      const int s = Lv.en_sc[e0 + cc], z = Lv.en_ns[e0 + cc];
+      v[j].s = tsa_score(l, s, z, Lv.S);
+      v[j].i = v[j].s < INFINITY ? cc : n;
+      v[j].e = tsa_energyE(l, s, z, Lv.S);
+      v[j].n = (double)z;
+    }
+  }
+  TsaRed r = tsa_red_tree256(v);
+  int top = 0;
+  if (lane == 0) {
+    __hip_atomic_store(cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    Lv.part[(size_t)ev * ng + g] = TsaTrackPart{r.s, r.e, r.n, r.i};
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const unsigned old = __hip_atomic_fetch_add(cnt + ng, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    top = old == (unsigned)ng - 1u;
+  }
+  if (!__shfl(top, 0, 64)) return res;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // the groups' results, in group order: entry t folds groups t, t + 256, ... then the tree
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    v[j] = TsaRed{INFINITY, 0.0, 0.0, n};
+    for (int k = lane + 64 * j; k < ng; k += 256) {
+      const TsaTrackPart q = Lv.part[(size_t)ev * ng + k];
+      tsa_red_merge(v[j], TsaRed{q.score, q.sumE, q.sumNs, q.idx});
+    }
+  }
+  r = tsa_red_tree256(v);
+  if (lane == 0) {
+    __hip_atomic_store(cnt + ng, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int b = r.i;
+    TsaTraceRowD row;
+    row.chain = b < n ? b : -1;
+    row.lc = b < n ? Lv.en_lc[e0 + b] : 0.0f;
+    row.sc = b < n ? Lv.en_sc[e0 + b] : 0;
+    row.ns = b < n ? Lv.en_ns[e0 + b] : 0;
+    row.score = r.s;
+    row.meanE = r.e / n;
+    row.meanNs = r.n / n;
+    row.ticks = wall_clock64();
+    Lv.trace[Lv.level0 + level] = row;
+  }
+  return res;
+}
+
+// The record words [ch_off, s_off + W) (children words and S) of the chain at base into its candidate slot
+// cslot, by nthr threads (this one tid).
+__device__ __forceinline__ void tsa_level_keep(const TsaLevels& Lv, const TsaKParams& P, const uint64_t* base, int n,
+                                               int c, int cslot, int tid, int nthr) {
+  uint64_t* const d = Lv.cand + ((size_t)cslot * n + c) * Lv.cand_words;
+  const uint64_t* const s = base + P.ch_off;
+  for (int i = tid; i < Lv.cand_words; i += nthr) d[i] = s[i];
+}
+
+// Parent of every internal node from the children words (the root's is 0xFFFF), by one wave.
+__device__ __forceinline__ void tsa_par_from_children(const uint32_t* ch, uint16_t* par, int nint, int m, int lane) {
+  for (int i = lane; i < nint; i += 64) {
+    const uint32_t cw = ch[i];
+    const int l = (int)(cw & 0xFFFFu), r = (int)(cw >> 16);
+    if (l >= m) par[l - m] = (uint16_t)(m + i);
+    if (r >= m) par[r - m] = (uint16_t)(m + i);
+  }
+  if (lane == 0) par[nint - 1] = 0xFFFFu;
+}
+
+// An evaluated level's end for a chain swept by one wave: node costs into the node arrays (pri and par hold
+// nint4 floats, wl nint4 sizes; their sweep contents are rebuilt by the next sweep, par by the caller), the
+// 32-lane fold as k_energy's, the tree into a candidate slot, then the chain's arrival.
+template <int W, int MODE>
+__device__ __noinline__ TsaOwn tsa_level_wave(const TsaKParams& P, const TsaLevels& Lv, const uint64_t* base,
+                                              const uint64_t* lab, const uint32_t* ch, const uint64_t* Sm,
+                                              const uint64_t* lf, TsaMathTabs T, uint16_t* pri, uint16_t* wl, int n,
+                                              int c, int ev, int level, TsaOwn o, int lane) {
+  const int NW = W > 0 ? W : P.W;
+  tsa_wave_sync();
+  float* const ncost = reinterpret_cast<float*>(pri);
+  for (int i = lane; i < P.nint; i += 64) {
+    int Z;
+    ncost[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
+    wl[i] = (uint16_t)Z;
+  }
+  tsa_wave_sync();
+  const TsaEvalOut e = tsa_fold32(P, ncost, wl, Sm, lf, NW, T, lane & 31);
+  const int cslot = o.slot < 0 ? 0 : o.slot ^ 1;
+  tsa_level_keep(Lv, P, base, n, c, cslot, lane, 64);
+  o = tsa_level_arrive(Lv, n, c, ev, level, e.lcost, e.sc, e.ns, o, cslot, lane);
+  tsa_wave_sync();
+  return o;
+}
+
+// An evaluated level's end for a chain swept by wave 0 of a workgroup with helper waves: the whole workgroup
+// evaluates the node costs; wave 0 folds while wave 1 keeps the tree, then wave 0 returns to its sweeps while
+// wave 1 arrives (and selects when it is the last chain).  en: three LDS words for the energies from wave 0
+// to wave 1.  Returns the chain's best in wave 1.
+template <int W, int MODE>
+__device__ __noinline__ TsaOwn tsa_level_helped(const TsaKParams& P, const TsaLevels& Lv, const uint64_t* base,
+                                                const uint64_t* lab, const uint32_t* ch, const uint64_t* Sm,
+                                                const uint64_t* lf, TsaMathTabs T, uint16_t* pri, uint16_t* wl, int n,
+                                                int c, int ev, int level, TsaOwn o, int wv, int lane, uint32_t* en) {
+  const int NW = W > 0 ? W : P.W;
+  float* const ncost = reinterpret_cast<float*>(pri);
+  for (int i = threadIdx.x; i < P.nint; i += blockDim.x) {
+    int Z;
+    ncost[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
+    wl[i] = (uint16_t)Z;
+  }
+  __syncthreads();
+  const int cslot = o.slot < 0 ? 0 : o.slot ^ 1;
+  if (wv == 0) {
+    const TsaEvalOut e = tsa_fold32(P, ncost, wl, Sm, lf, NW, T, lane & 31);
+    if (lane == 0) {
+      en[0] = __float_as_uint(e.lcost);
+      en[1] = (uint32_t)e.sc;
+      en[2] = (uint32_t)e.ns;
+    }
+  } else if (wv == 1) {
+    tsa_level_keep(Lv, P, base, n, c, cslot, lane, 64);
+  }
+  __syncthreads();
+  if (wv == 1) o = tsa_level_arrive(Lv, n, c, ev, level, __uint_as_float(en[0]), (int)en[1], (int)en[2], o, cslot, lane);
+  return o;
+}
+
+// Sweep kernel.  ORDER 0: par, 1: pre-order.  LDS: chain and leaf table staged in LDS.  LVL: the level loop
+// (TsaLevels) of independent chains in one launch, the chain staying staged from its first level to its last.
 // LDS layout (words): [leaf table (LDS variant only), rounded to even] then per wave lds_words:
 // [chain record (LDS variant only)][pri u16 x nint4][par u16 x nint4][work list u16 x nint4]
 // [band words u32 x nint4 when par_band > 0].
-template <int W, int MODE, int ORDER, bool LDS>
+template <int W, int MODE, int ORDER, bool LDS, bool LVL>
 __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restrict__ rec,
                                                const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
-                                               int nchains, int lds_words, float beta, uint32_t sweep0, int nsweeps,
-                                               unsigned long long* __restrict__ stats, TsaEnergyOut eo) {
+                                               int nchains, int lds_words, float beta1, uint32_t sweep0, int nsweeps,
+                                               unsigned long long* __restrict__ stats, TsaEnergyOut eo, TsaLevels Lv) {
   extern __shared__ uint64_t tsa_smem[];
   __shared__ float s_lse[64];
   __shared__ uint64_t s_exp2[32];
+  __shared__ uint32_t s_en[3];  // helper mode, level loop: the chain's energies from wave 0 to wave 1
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, wpb = blockDim.x >> 6;
   const int NW = W > 0 ? W : P.W;
   const int m = P.m, nint = P.nint, nint4 = (nint + 3) & ~3;
@@ -386,18 +597,21 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
   uint16_t* const wl = par + nint4;
   uint32_t* const dw = reinterpret_cast<uint32_t*>(wl + nint4);
   int np = 0, na = 0, nst = 0, nv = 0, nsp = 0, nsa = 0, nbusy = 0;
+  // the level loop (Lv.nlev > 0) or the launch's one level: sweeps in all, the current level, its sweeps left
+  // and beta; the chain's best score and the candidate slot of its tree, kept by the wave that tracks the chain
+  // (wave 1 with helpers, else the chain's wave)
+  const int nsw = LVL ? Lv.total : nsweeps;
+  int lv = 0, left = LVL ? Lv.niters[0] : nsweeps;
+  float beta = LVL ? Lv.beta[0] : beta1;
+  const bool tracker = LVL && (!helped || wv == 1);
+  TsaOwn own{INFINITY, -1};
+  if (tracker) own = TsaOwn{Lv.own[c], Lv.bslot[c]};
   tsa_wave_sync();
 
   if constexpr (ORDER == 0) {
-    for (int i = lane; i < nint; i += 64) {
-      const uint32_t cw = ch[i];
-      const int l = (int)(cw & 0xFFFFu), r = (int)(cw >> 16);
-      if (l >= m) par[l - m] = (uint16_t)(m + i);
-      if (r >= m) par[r - m] = (uint16_t)(m + i);
-    }
-    if (lane == 0) par[nint - 1] = 0xFFFFu;
+    tsa_par_from_children(ch, par, nint, m, lane);
     tsa_wave_sync();
-    for (int s = 0; s < nsweeps; s++) {
+    for (int s = 0; s < nsw; s++) {
       const uint32_t sw = sweep0 + (uint32_t)s;
       const uint32_t hs = tsa_sweep_hash(sw, (uint32_t)c, P.key0);
       for (int i = lane; i < nint; i += 64) pri[i] = (uint16_t)tsa_par_pri((uint32_t)(m + i), hs);
@@ -539,6 +753,20 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
         tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
         tsa_wave_sync();
       }
+      if constexpr (LVL) {
+        if (--left == 0) {  // the level's last sweep
+          const int ev = Lv.eval[lv];
+          if (ev >= 0) {
+            own = tsa_level_wave<W, MODE>(P, Lv, base, lab, ch, Sm, lf, T, pri, wl, nchains, c, ev, lv, own, lane);
+            tsa_par_from_children(ch, par, nint, m, lane);  // the evaluation overwrote par
+            tsa_wave_sync();
+          }
+          if (++lv < Lv.nlev) {
+            beta = Lv.beta[lv];
+            left = Lv.niters[lv];
+          }
+        }
+      }
     }
   } else {
     const int root = 2 * m - 2;
@@ -553,56 +781,78 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
                        (int)blockDim.x - 64, T.exp2);
       __syncthreads();
     }
-    for (int s = 0; s < nsweeps; s++) {
+    for (int s = 0; s < nsw; s++) {
       const uint32_t sw = sweep0 + (uint32_t)s;
       if (helped && wv > 0) {  // helper waves
-        if (s + 1 < nsweeps) {
+        if (s + 1 < nsw) {
           uint32_t* const nx = dbuf + (size_t)((s + 1) & 1) * 2 * nint4;
           tsa_draw_ahead(P, nx, reinterpret_cast<float*>(nx + nint4), sw + 1u, (uint32_t)c, (int)threadIdx.x - 64,
                          (int)blockDim.x - 64, T.exp2);
         }
         __syncthreads();
-        continue;
-      }
-      const uint32_t* const pre_x = helped ? dbuf + (size_t)(s & 1) * 2 * nint4 : nullptr;
-      const float* const pre_t = helped ? reinterpret_cast<const float*>(pre_x + nint4) : nullptr;
-      if (lane == 0) wl[0] = (uint16_t)root;
-      int sp = 1;
-      tsa_wave_sync();
-      while (sp > 0) {
-        const int k = sp < 64 ? sp : 64, b0 = sp - k;
-        const int v = lane < k ? (int)wl[b0 + lane] : 0;
-        tsa_wave_sync();  // every lane has read its node before pushes overwrite the list
-        uint32_t cw = 0;
-        if (lane < k) {
-          // with helpers (one chain per workgroup) the staged leaf sets end where the chain's internal sets begin
-          // (LDS records) and the draws are made ahead
-          const TsaVisit o =
-              P.slicing ? (helped ? tsa_visit<W, MODE, true, LDS, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
-                                  : tsa_visit<W, MODE, true, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c))
-                        : (helped ? tsa_visit<W, MODE, false, LDS, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
-                                  : tsa_visit<W, MODE, false, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c));
-          cw = o.cw;
-          nv++;
-          nbusy++;
-          np += o.prop;
-          na += o.acc;
+      } else {
+        const uint32_t* const pre_x = helped ? dbuf + (size_t)(s & 1) * 2 * nint4 : nullptr;
+        const float* const pre_t = helped ? reinterpret_cast<const float*>(pre_x + nint4) : nullptr;
+        if (lane == 0) wl[0] = (uint16_t)root;
+        int sp = 1;
+        tsa_wave_sync();
+        while (sp > 0) {
+          const int k = sp < 64 ? sp : 64, b0 = sp - k;
+          const int v = lane < k ? (int)wl[b0 + lane] : 0;
+          tsa_wave_sync();  // every lane has read its node before pushes overwrite the list
+          uint32_t cw = 0;
+          if (lane < k) {
+            // with helpers (one chain per workgroup) the staged leaf sets end where the chain's internal sets begin
+            // (LDS records) and the draws are made ahead
+            const TsaVisit o =
+                P.slicing ? (helped ? tsa_visit<W, MODE, true, LDS, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
+                                    : tsa_visit<W, MODE, true, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c))
+                          : (helped ? tsa_visit<W, MODE, false, LDS, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
+                                    : tsa_visit<W, MODE, false, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c));
+            cw = o.cw;
+            nv++;
+            nbusy++;
+            np += o.prop;
+            na += o.acc;
+          }
+          nst++;
+          const bool c1 = lane < k && (int)(cw & 0xFFFFu) >= m;
+          const bool c2 = lane < k && (int)(cw >> 16) >= m;
+          const uint64_t b1 = __ballot(c1), b2 = __ballot(c2);
+          int pos = b0 + __popcll(b1 & tsa_lt_mask(lane)) + __popcll(b2 & tsa_lt_mask(lane));
+          if (c2) wl[pos++] = (uint16_t)(cw >> 16);
+          if (c1) wl[pos] = (uint16_t)(cw & 0xFFFFu);
+          sp = b0 + __popcll(b1) + __popcll(b2);
+          tsa_wave_sync();
         }
-        nst++;
-        const bool c1 = lane < k && (int)(cw & 0xFFFFu) >= m;
-        const bool c2 = lane < k && (int)(cw >> 16) >= m;
-        const uint64_t b1 = __ballot(c1), b2 = __ballot(c2);
-        int pos = b0 + __popcll(b1 & tsa_lt_mask(lane)) + __popcll(b2 & tsa_lt_mask(lane));
-        if (c2) wl[pos++] = (uint16_t)(cw >> 16);
-        if (c1) wl[pos] = (uint16_t)(cw & 0xFFFFu);
-        sp = b0 + __popcll(b1) + __popcll(b2);
-        tsa_wave_sync();
+        if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
+          tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
+          tsa_wave_sync();
+        }
+        if (helped) __syncthreads();
       }
-      if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
-        tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
-        tsa_wave_sync();
+      if constexpr (LVL) {
+        if (--left == 0) {  // the level's last sweep
+          const int ev = Lv.eval[lv];
+          if (ev >= 0) {
+            if (helped)
+              own = tsa_level_helped<W, MODE>(P, Lv, base, lab, ch, Sm, lf, T, pri, wl, nchains, c, ev, lv, own, wv,
+                                              lane, s_en);
+            else
+              own = tsa_level_wave<W, MODE>(P, Lv, base, lab, ch, Sm, lf, T, pri, wl, nchains, c, ev, lv, own, lane);
+          }
+          if (++lv < Lv.nlev) {
+            beta = Lv.beta[lv];
+            left = Lv.niters[lv];
+          }
+        }
       }
-      if (helped) __syncthreads();
+    }
+  }
+  if constexpr (LVL) {
+    if (tracker && lane == 0) {
+      Lv.own[c] = own.s;
+      Lv.bslot[c] = own.slot;
     }
   }
 
@@ -860,11 +1110,11 @@ __global__ void k_track_init(TsaTrackState* st, unsigned long long* ticks0) {
 // ---------------------------------------------------------------------------------------------------
 // Host-side launchers
 // ---------------------------------------------------------------------------------------------------
-template <int W, int MODE, int ORDER, bool LDS>
+template <int W, int MODE, int ORDER, bool LDS, bool LVL>
 static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
                                  const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
                                  unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st, hipEvent_t e0,
-                                 hipEvent_t e1) {
+                                 hipEvent_t e1, const TsaLevels* lv, int* res) {
   const int NW = W > 0 ? W : P.W;
   const size_t leafw = LDS ? (size_t)((P.m * NW + 1) & ~1) : 0;
   // pre-order sweeps with helper waves: one chain per workgroup of 1 + TSA_DRAW_HELPERS waves, with two draw
@@ -884,15 +1134,23 @@ static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64
   }
   static size_t attr_set = 0;
   if (smem > 65536 && smem > attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_sweep<W, MODE, ORDER, LDS>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_sweep<W, MODE, ORDER, LDS, LVL>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess) return e;
     attr_set = smem;
   }
+  if (res) {  // a query: chains resident per compute unit, no launch
+    int nb = 0;
+    const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+        &nb, reinterpret_cast<const void*>(&k_sweep<W, MODE, ORDER, LDS, LVL>), threads, smem);
+    *res = nb * wpb;
+    return e;
+  }
   const int grid = (nchains + wpb - 1) / wpb;
   // e0 / e1 (null: none) take the kernel's start and stop times in the dispatch itself
-  hipExtLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS>), dim3(grid), dim3(threads), (uint32_t)smem, st, e0, e1, 0u,
-                        P2, rec, leaf, fix, nchains, L.lds_words, beta, sweep0, nsweeps, stats, eo);
+  hipExtLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS, LVL>), dim3(grid), dim3(threads), (uint32_t)smem, st, e0, e1, 0u,
+                        P2, rec, leaf, fix, nchains, L.lds_words, beta, sweep0, nsweeps, stats, eo,
+                        lv ? *lv : TsaLevels{});
   return hipGetLastError();
 }
 
@@ -900,17 +1158,23 @@ template <int W, int MODE>
 static hipError_t launch_sweep_wm(const TsaLaunch& L, int order, const TsaKParams& P, uint64_t* rec,
                                   const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
                                   int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st,
-                                  hipEvent_t e0, hipEvent_t e1) {
+                                  hipEvent_t e0, hipEvent_t e1, const TsaLevels* lv, int* res) {
   if constexpr (W > 0) {
     if (L.lds) {
-      if (order == 0) return launch_sweep_t<W, MODE, 0, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
-      return launch_sweep_t<W, MODE, 1, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+      // the level loop (lv set) is a kernel of its own: its level functions are calls the plain sweep kernel
+      // does not carry
+      if (lv) {
+        if (order == 0) return launch_sweep_t<W, MODE, 0, true, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+        return launch_sweep_t<W, MODE, 1, true, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+      }
+      if (order == 0) return launch_sweep_t<W, MODE, 0, true, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+      return launch_sweep_t<W, MODE, 1, true, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
     }
     return hipErrorInvalidValue;  // the register-width kernels exist only in the LDS variant
   } else {
-    if (L.lds) return hipErrorInvalidValue;
-    if (order == 0) return launch_sweep_t<0, MODE, 0, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
-    return launch_sweep_t<0, MODE, 1, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+    if (L.lds || lv) return hipErrorInvalidValue;  // the level loop runs on the register-width kernels only
+    if (order == 0) return launch_sweep_t<0, MODE, 0, false, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, nullptr, res);
+    return launch_sweep_t<0, MODE, 1, false, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, nullptr, res);
   }
 }
 
@@ -918,22 +1182,22 @@ template <int W>
 static hipError_t launch_sweep_w(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
                                  const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
                                  int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st,
-                                 hipEvent_t e0, hipEvent_t e1) {
-  if (mode == 0) return launch_sweep_wm<W, 0>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
-  if (mode == 1) return launch_sweep_wm<W, 1>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
-  return launch_sweep_wm<W, 2>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+                                 hipEvent_t e0, hipEvent_t e1, const TsaLevels* lv, int* res) {
+  if (mode == 0) return launch_sweep_wm<W, 0>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+  if (mode == 1) return launch_sweep_wm<W, 1>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+  return launch_sweep_wm<W, 2>(L, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
 }
 
 hipError_t tsa_launch_sweeps(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
                              const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
                              int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st,
-                             hipEvent_t e0, hipEvent_t e1) {
+                             hipEvent_t e0, hipEvent_t e1, const TsaLevels* lv, int* res) {
   switch (L.W) {
-    case 1: return launch_sweep_w<1>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
-    case 2: return launch_sweep_w<2>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
-    case 4: return launch_sweep_w<4>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
-    case 8: return launch_sweep_w<8>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
-    case 0: return launch_sweep_w<0>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1);
+    case 1: return launch_sweep_w<1>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+    case 2: return launch_sweep_w<2>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+    case 4: return launch_sweep_w<4>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+    case 8: return launch_sweep_w<8>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+    case 0: return launch_sweep_w<0>(L, mode, order, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
     default: return hipErrorInvalidValue;
   }
 }
@@ -977,6 +1241,20 @@ hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int n
 
 hipError_t tsa_launch_track_init(TsaTrackState* stt, unsigned long long* ticks0, hipStream_t stream) {
   hipLaunchKernelGGL(k_track_init, dim3(1), dim3(1), 0, stream, stt, ticks0);
+  return hipGetLastError();
+}
+
+// The level loop's per-chain best: score +inf, no candidate slot.
+__global__ void k_levels_init(double* __restrict__ own, int* __restrict__ bslot, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) {
+    own[i] = INFINITY;
+    bslot[i] = -1;
+  }
+}
+
+hipError_t tsa_launch_levels_init(double* own, int* bslot, int n, hipStream_t stream) {
+  hipLaunchKernelGGL(k_levels_init, dim3((n + 255) / 256), dim3(256), 0, stream, own, bslot, n);
   return hipGetLastError();
 }
 

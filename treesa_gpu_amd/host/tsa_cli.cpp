@@ -149,6 +149,8 @@ const std::vector<Flag>& flags() {
       {"--host-select", nullptr, "select on the host at every level, also for --scheme indep",
        SWITCH(host_select, true)},
       {"--no-overlap", nullptr, "device-side selection on the sweep's stream", SWITCH(no_overlap, true)},
+      {"--level-launches", nullptr, "scheme indep: one sweep launch and one selection per level, not the level loop "
+       "in one launch", SWITCH(level_launches, true)},
       {"--level-log", "FILE", "one JSON line per evaluated level: best chain, score, energies, ancestors",
        TEXT_FIELD(level_log)},
   };
