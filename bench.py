@@ -18,7 +18,9 @@ identical, their spread is reported as "repetitions").
 kernel_visits_per_s = the reference's own definition (bench/throughput.py:64-70): node visits over the
 event-timed sweep kernels only.
 
-roofline: of the sweep kernel, per launch, with the resource that bounds it.  Chains staged in LDS (c1-c3):
+roofline: of the sweep kernel, per launch, with the resource that bounds it.  Where the binary runs the level
+loop in one launch (scheme indep with every chain resident at once: c1) a launch is the whole schedule
+(levels_per_launch), else one level.  Chains staged in LDS (c1-c3):
 bound "lds", achieved = the algorithmic bytes of the proposals (5 label sets of W words + 8 B of children per
 proposal, W words + 8 B written per accept, 4 B per visit without a rule, plus the slice steps' tree passes;
 from the kernel's own counters), all served from LDS, over the average event-timed launch, against the LDS read
@@ -288,7 +290,8 @@ def kernel_label(desc, order):
     if desc.startswith("wide") and order == capi.ORDER_PAR:
         how = "nonzero 16-byte chunks only (chunk summaries)" if " sums=0 " not in desc else "dense streaming"
         return f"k_wide par, label sets in HBM, {how}, " + desc.split(" ", 1)[1]
-    return f"k_sweep {o}, " + ("chain in LDS" if desc.startswith("lds") else "chain in HBM")
+    loop = ", the whole level loop in one launch" if desc.endswith("anneal=level_loop") else ""
+    return f"k_sweep {o}, " + ("chain in LDS" if desc.startswith("lds") else "chain in HBM") + loop
 
 
 def run_binary(C, trees, betas, steps, warmup, scheme=None, extra=()):
@@ -445,13 +448,15 @@ def main():
         assert r["node_visits"] == visits, (r["node_visits"], visits)
         st = [r["proposals"], r["accepts"], r["warp_steps"], r["node_visits"], r["slice_proposals"]]
         slice_steps = steps * C["niters"] * nchains if C["slicing"] else 0
-        B = algorithmic_bytes(st, lay.W, inst.m - 1, C["slicing"], slice_steps) / steps
-        dur = r["kernel_s"] / steps
         desc = r.get("hip_kernel") or ""
+        # the level loop in one launch runs every level of the schedule; else one sweep launch per level
+        launches = 1 if desc.endswith("anneal=level_loop") else steps
+        B = algorithmic_bytes(st, lay.W, inst.m - 1, C["slicing"], slice_steps) / launches
+        dur = r["kernel_s"] / launches
         path = label_path(desc)
         traffic = measured_traffic(a.config, path)
-        roof = {"kernel": kernel_label(desc, order), "algorithmic_bytes_per_launch": B, "avg_launch_ms": dur * 1e3,
-                "traffic": traffic}
+        roof = {"kernel": kernel_label(desc, order), "levels_per_launch": steps // launches,
+                "algorithmic_bytes_per_launch": B, "avg_launch_ms": dur * 1e3, "traffic": traffic}
         if desc.startswith("lds"):
             # label sets served from LDS: the LDS read peak of this GPU bounds the proposals' reads; HBM carries
             # only the staging of the records, and VALU issue is the resource the kernel actually saturates
@@ -467,7 +472,7 @@ def main():
                 roof["valu_busy"] = vb / 100.0
         elif r.get("sum_chunks", 0) > 0:
             # the chunk-summary kernel reads only the nonzero chunks of its sets: what it loaded, from its counters
-            L = loaded_bytes(st, (r["sum_chunks"], r["sum_xchunks"])) / steps
+            L = loaded_bytes(st, (r["sum_chunks"], r["sum_xchunks"])) / launches
             roof.update(bound="hbm", achieved=L / dur / 1e9, peak=HBM_PEAK_GBS, unit="GB/s",
                         frac=L / dur / 1e9 / HBM_PEAK_GBS, loaded_bytes_per_launch=L)
         else:

@@ -7,8 +7,9 @@ order, so the means agree to the last bit) and the best chain, level, score and 
 cases cover both sweep orders, pre-order with and without helper waves, one group of 256 chains and several
 with a ragged last one, every energy mode, slicing, the sc-first selection, sparse evaluation, a schedule
 split over two calls, the one-launch loop forced on more chains than are resident at once, and the per-level
-launches tsa_anneal runs itself (too many chains, a session begun with tsa_track, the wide path).  That the selection itself is the reference's is covered by the level-loop tests, which
-run the binary (whose indep loop is this launch) against the oracle's level loop.
+launches tsa_anneal runs itself (too many chains, a session begun with tsa_track, the wide path).  That the
+selection itself is the reference's is covered by the level-loop tests, which run the binary (whose indep loop
+is this launch) against the oracle's level loop.
 """
 import numpy as np
 import pytest

@@ -493,37 +493,17 @@ __device__ __noinline__ TsaOwn tsa_level_wave(const TsaKParams& P, const TsaLeve
   return o;
 }
 
-// An evaluated level's end for a chain swept by wave 0 of a workgroup with helper waves: the whole workgroup
-// evaluates the node costs; wave 0 folds while wave 1 keeps the tree, then wave 0 returns to its sweeps while
-// wave 1 arrives (and selects when it is the last chain).  en: three LDS words for the energies from wave 0
-// to wave 1.  Returns the chain's best in wave 1.
-template <int W, int MODE>
-__device__ __noinline__ TsaOwn tsa_level_helped(const TsaKParams& P, const TsaLevels& Lv, const uint64_t* base,
-                                                const uint64_t* lab, const uint32_t* ch, const uint64_t* Sm,
-                                                const uint64_t* lf, TsaMathTabs T, uint16_t* pri, uint16_t* wl, int n,
-                                                int c, int ev, int level, TsaOwn o, int wv, int lane, uint32_t* en) {
+// The rest of an evaluated level's end for a chain swept by wave 0 of a workgroup with helper waves, by wave 1
+// while wave 0 sweeps on: the fold of the node costs and sizes the workgroup left in cost / z (S: a copy of
+// the slice set as it was then), then the chain's arrival.  Returns the chain's best.
+template <int W>
+__device__ __noinline__ TsaOwn tsa_level_fold_arrive(const TsaKParams& P, const TsaLevels& Lv, const float* cost,
+                                                     const uint16_t* z, const uint64_t* S, const uint64_t* lf,
+                                                     TsaMathTabs T, int n, int c, int ev, int level, TsaOwn o,
+                                                     int cslot, int lane) {
   const int NW = W > 0 ? W : P.W;
-  float* const ncost = reinterpret_cast<float*>(pri);
-  for (int i = threadIdx.x; i < P.nint; i += blockDim.x) {
-    int Z;
-    ncost[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
-    wl[i] = (uint16_t)Z;
-  }
-  __syncthreads();
-  const int cslot = o.slot < 0 ? 0 : o.slot ^ 1;
-  if (wv == 0) {
-    const TsaEvalOut e = tsa_fold32(P, ncost, wl, Sm, lf, NW, T, lane & 31);
-    if (lane == 0) {
-      en[0] = __float_as_uint(e.lcost);
-      en[1] = (uint32_t)e.sc;
-      en[2] = (uint32_t)e.ns;
-    }
-  } else if (wv == 1) {
-    tsa_level_keep(Lv, P, base, n, c, cslot, lane, 64);
-  }
-  __syncthreads();
-  if (wv == 1) o = tsa_level_arrive(Lv, n, c, ev, level, __uint_as_float(en[0]), (int)en[1], (int)en[2], o, cslot, lane);
-  return o;
+  const TsaEvalOut e = tsa_fold32(P, cost, z, S, lf, NW, T, lane & 31);
+  return tsa_level_arrive(Lv, n, c, ev, level, e.lcost, e.sc, e.ns, o, cslot, lane);
 }
 
 // Sweep kernel.  ORDER 0: par, 1: pre-order.  LDS: chain and leaf table staged in LDS.  LVL: the level loop
@@ -539,7 +519,7 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
   extern __shared__ uint64_t tsa_smem[];
   __shared__ float s_lse[64];
   __shared__ uint64_t s_exp2[32];
-  __shared__ uint32_t s_en[3];  // helper mode, level loop: the chain's energies from wave 0 to wave 1
+  __shared__ uint64_t s_S[8];  // helper mode, level loop: the slice set at a level's end, for wave 1's fold
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, wpb = blockDim.x >> 6;
   const int NW = W > 0 ? W : P.W;
   const int m = P.m, nint = P.nint, nint4 = (nint + 3) & ~3;
@@ -775,6 +755,8 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
     // steps waits on Philox or expf.  The helpers draw sweep 0 while wave 0 copies the record, and sweep s + 1
     // during sweep s; a workgroup barrier closes each of these.
     uint32_t* const dbuf = helped ? reinterpret_cast<uint32_t*>(wbase + lds_words) : nullptr;
+    // level loop with helpers: the node sizes of an evaluated level, after the draw buffers
+    uint16_t* const lz = LVL && helped ? reinterpret_cast<uint16_t*>(dbuf + 4 * nint4) : nullptr;
     if (helped) {
       if (wv > 0)
         tsa_draw_ahead(P, dbuf, reinterpret_cast<float*>(dbuf + nint4), sweep0, (uint32_t)c, (int)threadIdx.x - 64,
@@ -835,11 +817,28 @@ __global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restric
         if (--left == 0) {  // the level's last sweep
           const int ev = Lv.eval[lv];
           if (ev >= 0) {
-            if (helped)
-              own = tsa_level_helped<W, MODE>(P, Lv, base, lab, ch, Sm, lf, T, pri, wl, nchains, c, ev, lv, own, wv,
-                                              lane, s_en);
-            else
+            if (helped) {
+              // the whole workgroup evaluates the node costs into pri / par (free in pre-order sweeps) and the
+              // sizes into lz, wave 1 keeps the tree and S; then wave 0 returns to its sweeps at once and wave 1
+              // folds, arrives (and selects when it is the last chain) beside them
+              float* const ncost = reinterpret_cast<float*>(pri);
+              for (int i = threadIdx.x; i < nint; i += blockDim.x) {
+                int Z;
+                ncost[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
+                lz[i] = (uint16_t)Z;
+              }
+              const int cslot = own.slot < 0 ? 0 : own.slot ^ 1;
+              if (wv == 1) {
+                tsa_level_keep(Lv, P, base, nchains, c, cslot, lane, 64);
+                if (P.slicing && lane < NW) s_S[lane] = S[lane];
+              }
+              __syncthreads();
+              if (wv == 1)
+                own = tsa_level_fold_arrive<W>(P, Lv, ncost, lz, P.slicing ? s_S : nullptr, lf, T, nchains, c, ev,
+                                               lv, own, cslot, lane);
+            } else {
               own = tsa_level_wave<W, MODE>(P, Lv, base, lab, ch, Sm, lf, T, pri, wl, nchains, c, ev, lv, own, lane);
+            }
           }
           if (++lv < Lv.nlev) {
             beta = Lv.beta[lv];
@@ -1124,7 +1123,9 @@ static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64
   int wpb = L.wpb, threads = 64 * L.wpb;
   size_t smem = (leafw + (size_t)L.wpb * L.lds_words) * 8;
   if (ORDER == 1 && L.draw_waves) {
-    const size_t hs = (leafw + (size_t)L.lds_words + tsa_draw_words(P.nint)) * 8;
+    // (the level loop adds a node-size array after the draw buffers)
+    const size_t zw = LVL ? (size_t)(((P.nint + 3) & ~3) * 2 + 7) / 8 : 0;
+    const size_t hs = (leafw + (size_t)L.lds_words + tsa_draw_words(P.nint) + zw) * 8;
     if (hs <= (size_t)L.lds_max) {
       P2.helpers = TSA_DRAW_HELPERS;
       wpb = 1;
