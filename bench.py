@@ -410,6 +410,8 @@ def main():
     ap.add_argument("--level-launches", action="store_true",
                     help="scheme indep: one sweep launch and one selection per level instead of the level loop in one "
                          "launch")
+    ap.add_argument("--level-loop", action="store_true",
+                    help="scheme indep: the level loop in one launch also with more chains than are resident at once")
     ap.add_argument("--no-full", action="store_true", help="no full-schedule record when --steps is shorter")
     ap.add_argument("--no-quality", action="store_true", help="no best-tc-at-fixed-wall-time run (c2)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -432,7 +434,7 @@ def main():
         (["--wide-lanes", str(a.wide_lanes)] if a.wide_lanes else []) + \
         {"auto": [], "on": ["--sums"], "off": ["--no-sum"]}[a.sums] + (["--no-overlap"] if a.no_overlap else []) + \
         (["--draw-waves", str(a.draw_waves)] if a.draw_waves else []) + \
-        (["--level-launches"] if a.level_launches else [])
+        (["--level-launches"] if a.level_launches else []) + (["--level-loop"] if a.level_loop else [])
     visits = steps * C["niters"] * nchains * (inst.m - 1)
 
     def measure(extra_args):

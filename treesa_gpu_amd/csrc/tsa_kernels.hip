@@ -366,10 +366,10 @@ struct TsaOwn {
 // row), by one whole wave; lc / sc / ns (lane 0's count) are the chain's energies, o its best so far, cslot
 // the slot this level's tree was just written to; returns the chain's best (uniform over the wave).  The
 // last chain of the group of 256 reduces the group as a k_track workgroup does; the last group reduces the
-// groups as k_track's last workgroup does and writes the trace row.  Not inlined, here and in the level
-// functions below: the sweep loop's registers stay as they are without the level loop, and this runs
-// once per evaluated level.
-__device__ __noinline__ TsaOwn tsa_level_arrive(const TsaLevels& Lv, int n, int c, int ev, int level, float lc, int sc,
+// groups as k_track's last workgroup does and writes the trace row.  Inlined into the chain's own wave (a call
+// there saves some 160 registers to scratch per lane at every evaluated level of every chain); with helper
+// waves, wave 1 calls it through tsa_level_fold_arrive, whose registers then stay out of the sweeping wave's.
+__device__ __forceinline__ TsaOwn tsa_level_arrive(const TsaLevels& Lv, int n, int c, int ev, int level, float lc, int sc,
                                                 int ns, TsaOwn o, int cslot, int lane) {
   double own = o.s;
   int bslot = o.slot;
@@ -472,7 +472,7 @@ __device__ __forceinline__ void tsa_par_from_children(const uint32_t* ch, uint16
 // nint4 floats, wl nint4 sizes; their sweep contents are rebuilt by the next sweep, par by the caller), the
 // 32-lane fold as k_energy's, the tree into a candidate slot, then the chain's arrival.
 template <int W, int MODE>
-__device__ __noinline__ TsaOwn tsa_level_wave(const TsaKParams& P, const TsaLevels& Lv, const uint64_t* base,
+__device__ __forceinline__ TsaOwn tsa_level_wave(const TsaKParams& P, const TsaLevels& Lv, const uint64_t* base,
                                               const uint64_t* lab, const uint32_t* ch, const uint64_t* Sm,
                                               const uint64_t* lf, TsaMathTabs T, uint16_t* pri, uint16_t* wl, int n,
                                               int c, int ev, int level, TsaOwn o, int lane) {
@@ -511,8 +511,10 @@ __device__ __noinline__ TsaOwn tsa_level_fold_arrive(const TsaKParams& P, const 
 // LDS layout (words): [leaf table (LDS variant only), rounded to even] then per wave lds_words:
 // [chain record (LDS variant only)][pri u16 x nint4][par u16 x nint4][work list u16 x nint4]
 // [band words u32 x nint4 when par_band > 0].
+// (The par level loop keeps three waves per SIMD, as many as the chains' LDS allows: its level functions'
+// registers would otherwise take one of them.)
 template <int W, int MODE, int ORDER, bool LDS, bool LVL>
-__global__ void __launch_bounds__(256) k_sweep(TsaKParams P, uint64_t* __restrict__ rec,
+__global__ void __launch_bounds__(256, (LVL && ORDER == 0) ? 3 : 1) k_sweep(TsaKParams P, uint64_t* __restrict__ rec,
                                                const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
                                                int nchains, int lds_words, float beta1, uint32_t sweep0, int nsweeps,
                                                unsigned long long* __restrict__ stats, TsaEnergyOut eo, TsaLevels Lv) {

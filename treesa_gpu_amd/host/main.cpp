@@ -286,6 +286,7 @@ void Run::fill_config() {
   cfg_.sums = O_.no_sum ? -1 : (O_.force_sum ? 1 : 0);
   cfg_.track_overlap = O_.no_overlap ? -1 : 0;
   cfg_.draw_waves = O_.draw_waves;
+  cfg_.level_loop = O_.level_loop ? 1 : 0;
 }
 
 const std::vector<std::vector<uint32_t>>& Run::start_trees() {

@@ -151,6 +151,8 @@ const std::vector<Flag>& flags() {
       {"--no-overlap", nullptr, "device-side selection on the sweep's stream", SWITCH(no_overlap, true)},
       {"--level-launches", nullptr, "scheme indep: one sweep launch and one selection per level, not the level loop "
        "in one launch", SWITCH(level_launches, true)},
+      {"--level-loop", nullptr, "scheme indep: the level loop in one launch also with more chains than are resident "
+       "at once", SWITCH(level_loop, true)},
       {"--level-log", "FILE", "one JSON line per evaluated level: best chain, score, energies, ancestors",
        TEXT_FIELD(level_log)},
   };

@@ -44,7 +44,7 @@ struct Options {
   bool check = false, cross = true;
   int ref_chains = 8;
   // diagnostics of this build
-  bool quiet = false, host_select = false, no_overlap = false, level_launches = false;
+  bool quiet = false, host_select = false, no_overlap = false, level_launches = false, level_loop = false;
   int bench_warmup = 0;
   std::string level_log;
 };
