@@ -129,6 +129,15 @@ int tsa_upload(tsa_ctx* ctx, const uint64_t* population);
 /* Download count chain records starting at chain c0.  Replaces the best-chain and --check copies,
  * csrc/treesa_gpu.cu:1823, 1948-1949. */
 int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* out);
+/* tsa_download enqueued on the context's stream without waiting: out (page-locked, tsa_host_alloc) holds the
+ * records, as they are at this point of the stream, once a later synchronizing call returns (tsa_download,
+ * tsa_energy, tsa_track_end, tsa_wait).  No counterpart in the reference (its best-chain copy waits,
+ * csrc/treesa_gpu.cu:1823); for a host-side level loop that keeps the best chain's record without stopping
+ * the device for it. */
+int tsa_download_async(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* out);
+/* Wait until everything enqueued on the context has run.  No counterpart in the reference (its calls are
+ * synchronous); pairs with tsa_download_async. */
+int tsa_wait(tsa_ctx* ctx);
 
 /* Enqueue nsweeps sweeps of every chain at inverse temperature beta, global sweep counter sweep0
  * (the RNG counter), in TSA_ORDER_*; slice moves follow every sweep s with (sweep0+s+1) % slice_every

@@ -26,7 +26,7 @@ DEFAULT_H100 = (4e-6, 1.23e13, 5.44e-14, 7.68e-15, 6.37e-14, 2.02e-16, 1.77e-13,
 EXPORTS = ("tsa_layout", "tsa_create", "tsa_upload", "tsa_download", "tsa_sweeps", "tsa_sweeps_ms", "tsa_energy",
            "tsa_resample", "tsa_set_mode", "tsa_stats", "tsa_chunk_stats", "tsa_describe", "tsa_destroy", "tsa_last_error",
            "tsa_host_math", "tsa_host_alloc", "tsa_host_free", "tsa_track_begin", "tsa_track", "tsa_track_end",
-           "tsa_sweeps_noalloc", "tsa_anneal")
+           "tsa_sweeps_noalloc", "tsa_anneal", "tsa_download_async", "tsa_wait")
 
 
 class Layout(ctypes.Structure):
@@ -77,6 +77,8 @@ def load():
     lib.tsa_create.argtypes = [ctypes.POINTER(Layout), P, I32, ctypes.POINTER(Config), I32, ctypes.POINTER(P)]
     lib.tsa_upload.argtypes = [P, P]
     lib.tsa_download.argtypes = [P, I32, I32, P]
+    lib.tsa_download_async.argtypes = [P, I32, I32, P]
+    lib.tsa_wait.argtypes = [P]
     lib.tsa_sweeps.argtypes = [P, I32, F32, U32, I32]
     lib.tsa_sweeps_ms.argtypes = [P, ctypes.POINTER(ctypes.c_double)]
     lib.tsa_energy.argtypes = [P, P, P, P]

@@ -653,6 +653,22 @@ extern "C" int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* o
   return TSA_OK;
 }
 
+extern "C" int tsa_download_async(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* out) {
+  if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_download_async: null argument");
+  if (c0 < 0 || count < 0 || c0 + count > ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_download_async: range");
+  const size_t cw = ctx->lay.chain_words;
+  TSA_HIP(ctx, hipMemcpyAsync(out, ctx->d_rec + (size_t)c0 * cw, (size_t)count * cw * 8, hipMemcpyDeviceToHost,
+                              ctx->st));
+  return TSA_OK;
+}
+
+extern "C" int tsa_wait(tsa_ctx* ctx) {
+  if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_wait: null context");
+  if (ctx->st2) TSA_HIP(ctx, hipStreamSynchronize(ctx->st2));
+  TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  return TSA_OK;
+}
+
 extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0, int32_t nsweeps) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps: null context");
   if (order != TSA_ORDER_PAR && order != TSA_ORDER_PREORDER) return fail(ctx, TSA_ERR_ARG, "--order par|preorder");

@@ -511,10 +511,10 @@ __device__ __noinline__ TsaOwn tsa_level_fold_arrive(const TsaKParams& P, const 
 // LDS layout (words): [leaf table (LDS variant only), rounded to even] then per wave lds_words:
 // [chain record (LDS variant only)][pri u16 x nint4][par u16 x nint4][work list u16 x nint4]
 // [band words u32 x nint4 when par_band > 0].
-// (The par level loop keeps three waves per SIMD, as many as the chains' LDS allows: its level functions'
-// registers would otherwise take one of them.)
+// (The par level loop in tc mode keeps three waves per SIMD, as many as the chains' LDS allows: its level
+// functions' registers would otherwise take one of them; the float modes need more registers than that.)
 template <int W, int MODE, int ORDER, bool LDS, bool LVL>
-__global__ void __launch_bounds__(256, (LVL && ORDER == 0) ? 3 : 1) k_sweep(TsaKParams P, uint64_t* __restrict__ rec,
+__global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1) k_sweep(TsaKParams P, uint64_t* __restrict__ rec,
                                                const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
                                                int nchains, int lds_words, float beta1, uint32_t sweep0, int nsweeps,
                                                unsigned long long* __restrict__ stats, TsaEnergyOut eo, TsaLevels Lv) {

@@ -472,10 +472,13 @@ int Run::loop_on_host(PinnedWords& best, double t0, HostEnergy& h1, bool& staged
   double incumbent = INFINITY;
   int best_chain = -1;
   uint32_t sweep = 0;
+  bool enqueued = false;  // this level's sweeps were enqueued at the end of the previous level
   for (int lev = 0; lev < n; lev++) {
     const Level& L = sched_[lev];
     if (L.mode != mode_) {
-      // stage switch: the stage-1 incumbent stays, scored in the new energy by its host double energy
+      // stage switch: the stage-1 incumbent stays, scored in the new energy by its host double energy (its
+      // record arrives with the copies enqueued so far)
+      dev_->ok(tsa_wait(c));
       h1 = host_energy(N_, lay_.W, model_, best.p, children(best.p), leaf_, slices(best.p));
       staged = true;
       mode_ = L.mode;
@@ -483,12 +486,10 @@ int Run::loop_on_host(PinnedWords& best, double t0, HostEnergy& h1, bool& staged
       incumbent = selection_score(scoring(mode_), (float)std::log2(mode_ == 1 ? h1.time : h1.time2), h1.sc, h1.ns);
       beta_resampled = L.beta;
     }
-    dev_->ok(tsa_sweeps(c, order_, L.beta, sweep, L.niters));
+    if (!enqueued) dev_->ok(tsa_sweeps(c, order_, L.beta, sweep, L.niters));
+    enqueued = false;
     sweep += (uint32_t)L.niters;
-    if (!evaluated_level(lev)) {
-      kernel_ms_ += dev_->take_kernel_ms();
-      continue;
-    }
+    if (!evaluated_level(lev)) continue;
     dev_->ok(tsa_energy(c, e.lc.data(), e.sc.data(), e.ns.data()));
     kernel_ms_ += dev_->take_kernel_ms();
     const Scoring S = scoring(mode_);
@@ -504,21 +505,16 @@ int Run::loop_on_host(PinnedWords& best, double t0, HostEnergy& h1, bool& staged
       sumE += E[k];
       sumNs += e.ns[k];
     }
-    if (bs < incumbent) {
+    if (bs < incumbent) {  // the record as it is now, copied behind the device's work
       incumbent = bs;
       best_chain = bi;
-      dev_->ok(tsa_download(c, bi, 1, best.p));
+      dev_->ok(tsa_download_async(c, bi, 1, best.p));
     }
-    std::fill(mark.begin(), mark.end(), 0);
-    int families = 0;
-    for (int k = 0; k < nc; k++) families += mark[family[k]]++ == 0;
-    const double t = wall_seconds() - t0;
-    add_trace(t, lev, e.lc[bi], e.sc[bi], sumE / nc, families, e.ns[bi], sumNs / nc);
-    progress(lev, e.lc[bi], e.sc[bi], e.ns[bi], sumE / nc, sumNs / nc, families, t);
     // population step, not at the last level nor across an energy change
     const bool last = lev + 1 == n;
+    const bool next_same = !last && sched_[lev + 1].mode == mode_;
     std::vector<int> anc;
-    if (!last && sched_[lev + 1].mode == mode_) {
+    if (next_same) {
       if (O_.scheme == "pa") {
         const double db = (double)(sched_[lev + 1].beta - beta_resampled);  // a float difference, as the reference
         beta_resampled = sched_[lev + 1].beta;
@@ -528,6 +524,19 @@ int Run::loop_on_host(PinnedWords& best, double t0, HostEnergy& h1, bool& staged
         anc = truncation_ancestors(E, O_.trunc_frac);
       }
     }
+    if (!anc.empty()) dev_->ok(tsa_resample(c, anc.data()));
+    // the next level's sweeps go to the device before this level's bookkeeping (not across an energy change,
+    // whose incumbent needs the host first)
+    if (next_same) {
+      dev_->ok(tsa_sweeps(c, order_, sched_[lev + 1].beta, sweep, sched_[lev + 1].niters));
+      enqueued = true;
+    }
+    std::fill(mark.begin(), mark.end(), 0);
+    int families = 0;
+    for (int k = 0; k < nc; k++) families += mark[family[k]]++ == 0;
+    const double t = wall_seconds() - t0;
+    add_trace(t, lev, e.lc[bi], e.sc[bi], sumE / nc, families, e.ns[bi], sumNs / nc);
+    progress(lev, e.lc[bi], e.sc[bi], e.ns[bi], sumE / nc, sumNs / nc, families, t);
     if (level_log_) {
       uint32_t bits;
       std::memcpy(&bits, &e.lc[bi], 4);
@@ -543,13 +552,14 @@ int Run::loop_on_host(PinnedWords& best, double t0, HostEnergy& h1, bool& staged
       fprintf(level_log_, "}\n");
     }
     if (!anc.empty()) {
-      dev_->ok(tsa_resample(c, anc.data()));
       std::vector<int> f2(nc);
       for (int k = 0; k < nc; k++) f2[k] = family[anc[k]];
       family.swap(f2);
       nresample++;
     }
   }
+  dev_->ok(tsa_wait(c));  // the best record's last copy
+  kernel_ms_ += dev_->take_kernel_ms();
   return best_chain;
 }
 
