@@ -88,6 +88,10 @@ struct tsa_ctx {
   // The level loop on the device (tsa_anneal, TsaLevels): the tracking session's kind (0: nothing tracked
   // yet, TRACK_LEVELS: tsa_track, TRACK_ANNEAL: tsa_anneal), whether the per-chain best still has to be
   // reset, the levels evaluated so far in the session, and the buffers, grown on demand.
+  // The host waited for the stream since the last sweep launch (tsa_energy, tsa_download, tsa_wait): the device
+  // idles until the next launch, so that launch records its timing events as stream markers around a plain
+  // dispatch (about 6 us of host time) rather than in the dispatch itself (about 20 us).
+  bool host_waited = false;
   int track_kind = 0;
   bool lv_reset = false;
   int lv_resident[6] = {-1, -1, -1, -1, -1, -1};  // level-loop chains resident per compute unit, per mode and order
@@ -650,6 +654,7 @@ extern "C" int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* o
   TSA_HIP(ctx, hipMemcpyAsync(out, ctx->d_rec + (size_t)c0 * cw, (size_t)count * cw * 8, hipMemcpyDeviceToHost,
                               ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  ctx->host_waited = true;
   return TSA_OK;
 }
 
@@ -666,6 +671,7 @@ extern "C" int tsa_wait(tsa_ctx* ctx) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_wait: null context");
   if (ctx->st2) TSA_HIP(ctx, hipStreamSynchronize(ctx->st2));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  ctx->host_waited = true;
   return TSA_OK;
 }
 
@@ -680,8 +686,12 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     ctx->ev.push_back(e);
   }
   // e0 / e1 take the start and stop times of the sweep kernel alone, recorded by its dispatch (no marker
-  // packets between the kernels of a level)
+  // packets between the kernels of a level), or, after a host wait, by markers around it (d0 / d1: the events
+  // the dispatch records itself, if any)
   hipEvent_t e0 = ctx->ev[2 * ctx->npending], e1 = ctx->ev[2 * ctx->npending + 1];
+  const bool markers = ctx->host_waited;
+  ctx->host_waited = false;
+  hipEvent_t d0 = markers ? nullptr : e0, d1 = markers ? nullptr : e1;
   ctx->energy_fresh = ctx->energy_host = false;
   if (ctx->wide.on && order == TSA_ORDER_PAR) {
     // energies stay a separate fold of the node-cost cache: every chain ends its sweep at about the same
@@ -708,8 +718,10 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
       sy.snap_nz = ctx->d_snap_nz[s];
       ctx->snap_kind[s] = SNAP_WIDE;
     }
+    if (markers) TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
     TSA_HIP(ctx, tsa_launch_wide(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains, beta,
-                                 sweep0, nsweeps, ctx->d_stats, sy, ctx->st, e0, e1));
+                                 sweep0, nsweeps, ctx->d_stats, sy, ctx->st, d0, d1));
+    if (markers) TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
     if (s >= 0) {
       ctx->ev_sweep[s] = e1;  // the selection of this snapshot waits for the sweep's stop event
       ctx->last_slot = s;
@@ -750,8 +762,10 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
         ctx->energy_host = true;
       }
     }
+    if (markers) TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
     TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
-                                   ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st, e0, e1));
+                                   ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st, d0, d1));
+    if (markers) TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
     if (s >= 0) {
       ctx->ev_sweep[s] = e1;
       ctx->last_slot = s;
@@ -1101,6 +1115,7 @@ extern "C" int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns) {
   memcpy(lc, ctx->h_en, b);
   memcpy(sc, ctx->h_en + ctx->nchains, b);
   memcpy(ns, ctx->h_en + 2 * (size_t)ctx->nchains, b);
+  ctx->host_waited = true;
   return TSA_OK;
 }
 
