@@ -201,3 +201,31 @@ def test_wide_path_runs_level_launches():
     (a, b) = out
     assert a[:3] == b[:3] and np.array_equal(a[3], b[3]) and np.array_equal(a[5], b[5])
     assert a[4] == b[4]
+
+
+def test_async_download_keeps_the_record_of_its_point_in_the_stream():
+    """tsa_download_async copies the record as it is at its place in the stream, into page-locked memory, and
+    tsa_wait completes it: the copy enqueued between two sweep launches equals a waiting download made at the
+    same point, not the record after the later sweep."""
+    import ctypes
+    s = Setup("sat100", "par", "tc", 64)
+    lib = capi.load()
+    words = s.lay.chain_words
+    with s.context() as a:
+        a.sweeps(s.ord, 2.0, 0, 2)
+        ref = a.download(5, 1)[0]
+    buf = lib.tsa_host_alloc(words * 8)
+    assert buf
+    try:
+        with s.context() as b:
+            b.sweeps(s.ord, 2.0, 0, 2)
+            b._check(lib.tsa_download_async(b.h, 5, 1, buf))
+            b.sweeps(s.ord, 4.0, 2, 3)
+            b._check(lib.tsa_wait(b.h))
+            got = np.ctypeslib.as_array((ctypes.c_uint64 * words).from_address(buf)).copy()
+            after = b.download(5, 1)[0]
+            b.sweeps_ms()
+    finally:
+        lib.tsa_host_free(buf)
+    assert np.array_equal(got, ref)
+    assert not np.array_equal(after, ref)  # the later sweeps moved the chain
