@@ -136,11 +136,20 @@ def algorithmic_bytes(st, W, nint, slicing=False, slice_steps=0):
 
 
 def loaded_bytes(st, chunks):
-    """What a chunk-summary kernel had to move: per proposal only the 16-byte chunks of its five sets that lie
-    in their union's summary (chunks[0] positions, 80 B each) and 8 B of children, per accept only P's nonzero
-    chunks (chunks[1] x 16 B) and 8 B, per visit without a rule 4 B."""
+    """What a chunk-summary kernel moves in tc mode: per proposal only the 16-byte chunks of D, O, K and M that
+    lie in their union's summary (chunks[0] positions, 64 B each; P's set is not read, its cost and size before
+    the move come from the node-cost cache), 8 B of children and 10 B of cache, per accept only P's nonzero
+    chunks (chunks[1] x 16 B), 8 B of children and 10 B of cache, per visit without a rule 4 B."""
     prop, acc, visits = st[0], st[1], st[3]
-    return chunks[0] * 80 + prop * 8 + chunks[1] * 16 + acc * 8 + (visits - prop) * 4
+    return chunks[0] * 64 + prop * (8 + 10) + chunks[1] * 16 + acc * (8 + 10) + (visits - prop) * 4
+
+
+def cached_loaded_bytes(st, W):
+    """What the dense wide kernel moves in tc mode, where a visit takes P's cost and size before the move from the
+    node-cost cache instead of counting P's set: per proposal 4 label sets, 8 B of children and 10 B of cache
+    (two costs, one size), per accept P's set, 8 B of children and 10 B of cache, per visit without a rule 4 B."""
+    prop, acc, visits = st[0], st[1], st[3]
+    return prop * (32 * W + 8 + 10) + acc * (8 * W + 8 + 10) + (visits - prop) * 4
 
 
 # committed rocprofv3 summaries by (workload, label-set path: "dense" streaming or chunk "sums")
@@ -475,6 +484,11 @@ def main():
         elif r.get("sum_chunks", 0) > 0:
             # the chunk-summary kernel reads only the nonzero chunks of its sets: what it loaded, from its counters
             L = loaded_bytes(st, (r["sum_chunks"], r["sum_xchunks"])) / launches
+            roof.update(bound="hbm", achieved=L / dur / 1e9, peak=HBM_PEAK_GBS, unit="GB/s",
+                        frac=L / dur / 1e9 / HBM_PEAK_GBS, loaded_bytes_per_launch=L)
+        elif desc.startswith("wide"):
+            # dense streaming in tc mode: P's set is never read (its cost and size come from the node-cost cache)
+            L = cached_loaded_bytes(st, lay.W) / launches
             roof.update(bound="hbm", achieved=L / dur / 1e9, peak=HBM_PEAK_GBS, unit="GB/s",
                         frac=L / dur / 1e9 / HBM_PEAK_GBS, loaded_bytes_per_launch=L)
         else:

@@ -205,23 +205,40 @@ TSA_HD void tsa_acc(TsaCounts& c, uint64_t k, uint64_t m, uint64_t p, uint64_t o
   }
 }
 
+// The tc-mode counts of the configuration after the move only (sd, sx, K2, K3), for callers that take the
+// configuration before it from cached node costs (tsa_energy_tc_cached).
+TSA_HD void tsa_acc_after_tc(TsaCounts& c, uint64_t k, uint64_t m, uint64_t o, uint64_t d, uint64_t x) {
+  c.sd += tsa_popc64(d);
+  c.sx += tsa_popc64(x);
+  c.K[2] += tsa_popc3<TSA_F_AB_NC>(k, o, x);
+  c.K[3] += tsa_popc3<TSA_F_AB_NC>(x, m, d);
+}
+
 // dE of the move (common.h:202-222):
 //   dtc = log2(2^c2 + 2^c3) - log2(2^c0 + 2^c1); dE = w*(sc1 - sc0) + dtc with sc0 = max(|P|,|d|),
 //   sc1 = max(|X|,|d|) and w = sc_weight if max(sc0, sc1) > sc_target else 0.
+// The tc-mode form from the two node costs before the move, costP = |P| + |K & M & ~P| and costV =
+// |d| + |P & O & ~d| (the costs of contractions (K, M) -> P and (P, O) -> d, symmetric in the two inputs),
+// the counts after it and sp = |P|: a caller that keeps every node's cost and size current gets the float
+// tsa_energy_from_counts<0> gets from the counted sets, without reading P's set.
+TSA_HD float tsa_energy_tc_cached(int costP, int costV, int sp, int sd, int sx, int K2, int K3, const TsaModel& P,
+                                  const float* lse) {
+  const float dtc = tsa_lse_i(sx + K2, sd + K3, lse) - tsa_lse_i(costP, costV, lse);
+  const int sc0 = sp > sd ? sp : sd;
+  const int sc1 = sx > sd ? sx : sd;
+  const int scmax = sc0 > sc1 ? sc0 : sc1;
+  const float w = ((float)scmax > P.sc_target) ? P.sc_weight : 0.0f;
+  return w * (float)(sc1 - sc0) + dtc;
+}
+
 template <int MODE>
 TSA_HD float tsa_energy_from_counts(const TsaCounts& c, const TsaModel& P, const float* lse, const TsaMathTabs& T) {
-  float dtc;
-  if (MODE == 0) {
-    const float tc0 = tsa_lse_i(c.sp + c.K[0], c.sd + c.K[1], lse);
-    const float tc1 = tsa_lse_i(c.sx + c.K[2], c.sd + c.K[3], lse);
-    dtc = tc1 - tc0;
-  } else {
-    const float t0 = tsa_lse_f(tsa_node_cost<MODE>(c.B[0], c.M[0], c.N[0], c.K[0], c.sp, P, T),
-                               tsa_node_cost<MODE>(c.B[1], c.M[1], c.N[1], c.K[1], c.sd, P, T), T);
-    const float t1 = tsa_lse_f(tsa_node_cost<MODE>(c.B[2], c.M[2], c.N[2], c.K[2], c.sx, P, T),
-                               tsa_node_cost<MODE>(c.B[3], c.M[3], c.N[3], c.K[3], c.sd, P, T), T);
-    dtc = t1 - t0;
-  }
+  if (MODE == 0) return tsa_energy_tc_cached(c.sp + c.K[0], c.sd + c.K[1], c.sp, c.sd, c.sx, c.K[2], c.K[3], P, lse);
+  const float t0 = tsa_lse_f(tsa_node_cost<MODE>(c.B[0], c.M[0], c.N[0], c.K[0], c.sp, P, T),
+                             tsa_node_cost<MODE>(c.B[1], c.M[1], c.N[1], c.K[1], c.sd, P, T), T);
+  const float t1 = tsa_lse_f(tsa_node_cost<MODE>(c.B[2], c.M[2], c.N[2], c.K[2], c.sx, P, T),
+                             tsa_node_cost<MODE>(c.B[3], c.M[3], c.N[3], c.K[3], c.sd, P, T), T);
+  const float dtc = t1 - t0;
   const int sc0 = c.sp > c.sd ? c.sp : c.sd;
   const int sc1 = c.sx > c.sd ? c.sx : c.sd;
   const int scmax = sc0 > sc1 ? sc0 : sc1;

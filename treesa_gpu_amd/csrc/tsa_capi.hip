@@ -702,15 +702,16 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     }
     TsaWideSync sy = ctx->wsync;
     int s = -1;
+    // the node-cost cache must be exact before the sweep when the snapshot it leaves is folded as it stands,
+    // and when the sweep reads it (tc mode: a visit takes P's old cost and size from it)
+    if ((ctx->overlap || ctx->mode == 0) && !ctx->costs_valid) {
+      join_track(ctx);
+      TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
+                                          ctx->nchains, ctx->d_ncost, ctx->d_nz, ctx->d_fcnt, ctx->d_lc, ctx->d_sc,
+                                          ctx->d_ns, 1, ctx->st));
+      ctx->costs_valid = true;
+    }
     if (ctx->overlap) {
-      // the node-cost cache must be exact before the sweep: the snapshot it leaves is folded as it stands
-      if (!ctx->costs_valid) {
-        join_track(ctx);
-        TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
-                                            ctx->nchains, ctx->d_ncost, ctx->d_nz, ctx->d_fcnt, ctx->d_lc, ctx->d_sc,
-                                            ctx->d_ns, 1, ctx->st));
-        ctx->costs_valid = true;
-      }
       s = ctx->slot;
       TSA_HIP(ctx, claim_slot(ctx, s));
       sy.snap_ch = ctx->d_snap_ch[s];

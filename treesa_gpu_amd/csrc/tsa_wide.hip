@@ -336,6 +336,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
   }
 
   constexpr int gpw = 64 / G;
+  constexpr bool CACHED = MODE == 0;  // tc-mode visits take P's old cost and size from the node-cost cache
   const int ngr = nwv * gpw;
   const int t = lane & (G - 1);
   const int gsub = lane / G;  // lane group within the wave
@@ -485,6 +486,16 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
             const TsaW2* qM = reinterpret_cast<const TsaW2*>(Mn >= m ? lab + (size_t)(Mn - m) * NW : leaf + (size_t)Mn * NW);
             TsaCounts cn;
             tsa_counts_zero(cn);
+            // tc mode: the costs of P and v before the move and P's size come from the node-cost cache
+            // (exact: every accept rewrites both costs and P's size, and a sweep starts from a full pass), so
+            // P's set is never read
+            int costP = 0, costV = 0, szP = 0;
+            if constexpr (CACHED) {
+              const size_t cb = (size_t)c * nint4;
+              costP = (int)sy.ncost[cb + (Pn - m)];
+              costV = (int)sy.ncost[cb + (v - m)];
+              szP = (int)sy.nz[cb + (Pn - m)];
+            }
             constexpr int SC = TsaSumRound<G>::SC;
             constexpr int XN = SUMS ? SC : TSA_WIDE_CPL;
             TsaW2 xx[XN];  // only X stays live across the energy evaluation
@@ -515,7 +526,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
                 for (int q = 0; q < SC; q++) {
                   if (ii[q] >= 0) {
                     dd[q] = qD[ii[q]];
-                    pp[q] = qP[ii[q]];
+                    if constexpr (!CACHED) pp[q] = qP[ii[q]];
                     oo[q] = qO[ii[q]];
                     kk[q] = qK[ii[q]];
                     mm[q] = qM[ii[q]];
@@ -528,8 +539,13 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
                   TsaW2 x;
                   x.a = tsa_xset(kk[q].a, oo[q].a, mm[q].a, dd[q].a);
                   x.b = tsa_xset(kk[q].b, oo[q].b, mm[q].b, dd[q].b);
-                  tsa_acc<MODE>(cn, kk[q].a, mm[q].a, pp[q].a, oo[q].a, dd[q].a, x.a);
-                  tsa_acc<MODE>(cn, kk[q].b, mm[q].b, pp[q].b, oo[q].b, dd[q].b, x.b);
+                  if constexpr (CACHED) {
+                    tsa_acc_after_tc(cn, kk[q].a, mm[q].a, oo[q].a, dd[q].a, x.a);
+                    tsa_acc_after_tc(cn, kk[q].b, mm[q].b, oo[q].b, dd[q].b, x.b);
+                  } else {
+                    tsa_acc<MODE>(cn, kk[q].a, mm[q].a, pp[q].a, oo[q].a, dd[q].a, x.a);
+                    tsa_acc<MODE>(cn, kk[q].b, mm[q].b, pp[q].b, oo[q].b, dd[q].b, x.b);
+                  }
                   if (r0 == 0) {
                     xx[q] = x;
                     ix[q] = ii[q];
@@ -543,7 +559,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
                 const int cc = t + q * G;
                 if (cc < nch) {
                   dd[q] = qD[cc];
-                  pp[q] = qP[cc];
+                  if constexpr (!CACHED) pp[q] = qP[cc];
                   oo[q] = qO[cc];
                   kk[q] = qK[cc];
                   mm[q] = qM[cc];
@@ -555,15 +571,31 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
               for (int q = 0; q < TSA_WIDE_CPL; q++) {
                 xx[q].a = tsa_xset(kk[q].a, oo[q].a, mm[q].a, dd[q].a);
                 xx[q].b = tsa_xset(kk[q].b, oo[q].b, mm[q].b, dd[q].b);
-                tsa_acc<MODE>(cn, kk[q].a, mm[q].a, pp[q].a, oo[q].a, dd[q].a, xx[q].a);
-                tsa_acc<MODE>(cn, kk[q].b, mm[q].b, pp[q].b, oo[q].b, dd[q].b, xx[q].b);
+                if constexpr (CACHED) {
+                  tsa_acc_after_tc(cn, kk[q].a, mm[q].a, oo[q].a, dd[q].a, xx[q].a);
+                  tsa_acc_after_tc(cn, kk[q].b, mm[q].b, oo[q].b, dd[q].b, xx[q].b);
+                } else {
+                  tsa_acc<MODE>(cn, kk[q].a, mm[q].a, pp[q].a, oo[q].a, dd[q].a, xx[q].a);
+                  tsa_acc<MODE>(cn, kk[q].b, mm[q].b, pp[q].b, oo[q].b, dd[q].b, xx[q].b);
+                }
               }
             }
-            uint32_t pk[TsaFlat<MODE>::NP];
-            counts_pack<MODE>(cn, pk);
-            group_sum<G, TsaFlat<MODE>::NP>(pk);
-            counts_unpack<MODE>(pk, cn);
-            const float dE = tsa_energy_from_counts<MODE>(cn, P.model, s_lse, T);
+            float dE;
+            if constexpr (CACHED) {
+              uint32_t pk[2] = {(uint32_t)cn.sd | ((uint32_t)cn.sx << 16), (uint32_t)cn.K[2] | ((uint32_t)cn.K[3] << 16)};
+              group_sum<G, 2>(pk);
+              cn.sd = (int)(pk[0] & 0xFFFFu);
+              cn.sx = (int)(pk[0] >> 16);
+              cn.K[2] = (int)(pk[1] & 0xFFFFu);
+              cn.K[3] = (int)(pk[1] >> 16);
+              dE = tsa_energy_tc_cached(costP, costV, szP, cn.sd, cn.sx, cn.K[2], cn.K[3], P.model, s_lse);
+            } else {
+              uint32_t pk[TsaFlat<MODE>::NP];
+              counts_pack<MODE>(cn, pk);
+              group_sum<G, TsaFlat<MODE>::NP>(pk);
+              counts_unpack<MODE>(pk, cn);
+              dE = tsa_energy_from_counts<MODE>(cn, P.model, s_lse, T);
+            }
             const bool acc = tsa_metropolis(rnd.y, beta, dE, T.exp2);
             if (acc) {
               if constexpr (SUMS) {
