@@ -78,12 +78,17 @@ struct TsaVisit {
 // O the other child, M the grandchild under P that moves up and K the one that stays, every rule swaps M and
 // O, and P gets X = (K|O)&(M|d).  PRE: pre_x / pre_t hold every internal node's first Philox word and
 // Metropolis threshold for this sweep, drawn ahead; they are read beside the children word, so that the rule
-// is known when that word arrives.  Else the visit draws its own.
-template <int W, int MODE, bool SL, bool UNI, bool PRE>
+// is known when that word arrives.  Else the visit draws its own.  CC (tc mode, no slicing, register width):
+// cc_cost / cc_size hold every internal node's cost and size, exact on entry; the costs of P and v before the
+// move and P's size come from there instead of from P's set (the same dE: tsa_energy_tc_cached), and an accept
+// rewrites the two costs and P's size.
+template <int W, int MODE, bool SL, bool UNI, bool PRE, bool CC = false>
 __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab, uint32_t* ch, const uint64_t* Sm,
                                               const uint64_t* lf, const float* lse, const TsaMathTabs& T, int v,
                                               float beta, uint32_t sw, uint32_t chain,
-                                              const uint32_t* pre_x = nullptr, const float* pre_t = nullptr) {
+                                              const uint32_t* pre_x = nullptr, const float* pre_t = nullptr,
+                                              float* cc_cost = nullptr, uint16_t* cc_size = nullptr) {
+  static_assert(!CC || (MODE == 0 && !SL && W > 0), "the cost cache serves tc-mode register-width visits");
   const int m = P.m;
   const int NW = W > 0 ? W : P.W;
   TsaVisit o;
@@ -121,7 +126,26 @@ __device__ __forceinline__ TsaVisit tsa_visit(const TsaKParams& P, uint64_t* lab
   TsaCounts cnt;
   tsa_counts_zero(cnt);
   bool acc;
-  if constexpr (W > 0) {
+  if constexpr (CC) {
+    const int costP = (int)cc_cost[Pn - m], costV = (int)cc_cost[v - m], szP = (int)cc_size[Pn - m];
+    uint64_t X[W];
+#pragma unroll
+    for (int i = 0; i < W; i++) {
+      const uint64_t d = pD[i], oo = pO[i], k = pK[i], mm = pM[i];
+      const uint64_t x = tsa_xset(k, oo, mm, d);
+      X[i] = x;
+      tsa_acc_after_tc(cnt, k, mm, oo, d, x);
+    }
+    const float dE = tsa_energy_tc_cached(costP, costV, szP, cnt.sd, cnt.sx, cnt.K[2], cnt.K[3], P.model, lse);
+    acc = tsa_visit_accept<PRE>(ry, thr, beta, dE, T);
+    if (acc) {
+#pragma unroll
+      for (int i = 0; i < W; i++) pP[i] = X[i];
+      cc_cost[Pn - m] = (float)(cnt.sx + cnt.K[2]);  // tsa_node_cost<0> of (K, O) -> P and (P, M) -> v
+      cc_cost[v - m] = (float)(cnt.sd + cnt.K[3]);
+      cc_size[Pn - m] = (uint16_t)cnt.sx;
+    }
+  } else if constexpr (W > 0) {
     uint64_t X[W];
 #pragma unroll
     for (int i = 0; i < W; i++) {
@@ -759,11 +783,23 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
     uint32_t* const dbuf = helped ? reinterpret_cast<uint32_t*>(wbase + lds_words) : nullptr;
     // level loop with helpers: the node sizes of an evaluated level, after the draw buffers
     uint16_t* const lz = LVL && helped ? reinterpret_cast<uint16_t*>(dbuf + 4 * nint4) : nullptr;
+    // tc mode with helpers, no slicing: every internal node's cost and size (the visits' cost cache), after lz
+    const bool cc = MODE == 0 && W > 0 && helped && !P.slicing;
+    float* const cc_cost = cc ? reinterpret_cast<float*>(dbuf + 4 * nint4 + (LVL ? nint4 / 2 : 0)) : nullptr;
+    uint16_t* const cc_size = cc ? reinterpret_cast<uint16_t*>(cc_cost + nint4) : nullptr;
     if (helped) {
       if (wv > 0)
         tsa_draw_ahead(P, dbuf, reinterpret_cast<float*>(dbuf + nint4), sweep0, (uint32_t)c, (int)threadIdx.x - 64,
                        (int)blockDim.x - 64, T.exp2);
       __syncthreads();
+      if (cc) {  // the cache from the record just staged
+        for (int i = threadIdx.x; i < nint; i += blockDim.x) {
+          int Z;
+          cc_cost[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
+          cc_size[i] = (uint16_t)Z;
+        }
+        __syncthreads();
+      }
     }
     for (int s = 0; s < nsw; s++) {
       const uint32_t sw = sweep0 + (uint32_t)s;
@@ -791,7 +827,8 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
             const TsaVisit o =
                 P.slicing ? (helped ? tsa_visit<W, MODE, true, LDS, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
                                     : tsa_visit<W, MODE, true, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c))
-                          : (helped ? tsa_visit<W, MODE, false, LDS, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
+                          : (helped ? tsa_visit<W, MODE, false, LDS, true, MODE == 0 && (W > 0)>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t,
+                                                                             cc_cost, cc_size)
                                     : tsa_visit<W, MODE, false, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c));
             cw = o.cw;
             nv++;
@@ -823,11 +860,17 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
               // the whole workgroup evaluates the node costs into pri / par (free in pre-order sweeps) and the
               // sizes into lz, wave 1 keeps the tree and S; then wave 0 returns to its sweeps at once and wave 1
               // folds, arrives (and selects when it is the last chain) beside them
+              // (with the cost cache: a copy of it, which the visits of the next sweep leave alone)
               float* const ncost = reinterpret_cast<float*>(pri);
               for (int i = threadIdx.x; i < nint; i += blockDim.x) {
-                int Z;
-                ncost[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
-                lz[i] = (uint16_t)Z;
+                if (cc) {
+                  ncost[i] = cc_cost[i];
+                  lz[i] = cc_size[i];
+                } else {
+                  int Z;
+                  ncost[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
+                  lz[i] = (uint16_t)Z;
+                }
               }
               const int cslot = own.slot < 0 ? 0 : own.slot ^ 1;
               if (wv == 1) {
@@ -1125,9 +1168,11 @@ static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64
   int wpb = L.wpb, threads = 64 * L.wpb;
   size_t smem = (leafw + (size_t)L.wpb * L.lds_words) * 8;
   if (ORDER == 1 && L.draw_waves) {
-    // (the level loop adds a node-size array after the draw buffers)
-    const size_t zw = LVL ? (size_t)(((P.nint + 3) & ~3) * 2 + 7) / 8 : 0;
-    const size_t hs = (leafw + (size_t)L.lds_words + tsa_draw_words(P.nint) + zw) * 8;
+    // (the level loop adds a node-size array after the draw buffers; tc mode then a node-cost cache, 4 + 2 B
+    // per node)
+    const size_t nint4 = (size_t)((P.nint + 3) & ~3);
+    const size_t zw = LVL ? (nint4 * 2 + 7) / 8 : 0, cw = MODE == 0 && W > 0 ? (nint4 * 6 + 7) / 8 : 0;
+    const size_t hs = (leafw + (size_t)L.lds_words + tsa_draw_words(P.nint) + zw + cw) * 8;
     if (hs <= (size_t)L.lds_max) {
       P2.helpers = TSA_DRAW_HELPERS;
       wpb = 1;
