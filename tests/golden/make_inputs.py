@@ -2,7 +2,7 @@
 
 * sat70.txt + sat70_greedy.tree: random 3-SAT n=70, m=round(4.26*70)=298, seed 1 (the reference's generator,
   treesa_gpu_amd/instances.py) and the native greedy start tree, best of 10 runs, seed 1
-  (treesa_gpu_amd/starts.py; the reference commits no greedy tree for this instance).
+  (treesa_gpu_amd/host.py; the reference commits no greedy tree for this instance).
 * reg3_2000.txt + reg3_2000_spectral.tree: a 3-regular graph with 2000 vertices from the seeded configuration
   model (seed 1) and its 4 best native spectral path trees (seed 1).
 * sq64.txt + sq64_row.tree: the 64 x 64 lattice and its row-major path tree.
@@ -15,7 +15,7 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 from treesa_gpu_amd import instances as I  # noqa: E402
-from treesa_gpu_amd import starts as S  # noqa: E402
+from treesa_gpu_amd import host as S  # noqa: E402
 
 DATA = os.path.join(HERE, "data")
 

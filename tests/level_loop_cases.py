@@ -17,7 +17,7 @@ treesa_gpu.optimize and the argv driver.optimize builds from them (treesa_gpu/dr
 Greedy starts are the reference's committed omeco trees (tests/golden/data/<inst>.tree).  Spectral starts are
 computed as treesa_gpu/spectral.py:136-199 computes them: the clique-expansion Laplacian (each tensor pair
 once, weight 1/(k-1) per shared label of k holders), numpy.linalg.eigh, numpy.random.default_rng(seed)
-directions, and the candidate search of treesa_gpu_amd.starts.spectral_search (pinned against the reference's
+directions, and the candidate search of treesa_gpu_amd.host.spectral_search (pinned against the reference's
 printed orders in tests/test_starts.py).
 """
 import json
@@ -139,7 +139,7 @@ def reference_laplacian(ixs):
 
 def spectral_trees(inst, k, seed, nangles=24, nrandom=24):
     """The path trees of the reference's k best spectral orderings for this seed (children words, k x (m-1))."""
-    from treesa_gpu_amd import starts as S
+    from treesa_gpu_amd import host as S
     m, nlab, ixs, iy = common.load_instance(inst)
     _, V = np.linalg.eigh(reference_laplacian(ixs))
     V = V[:, 1:4]

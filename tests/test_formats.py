@@ -18,7 +18,7 @@ import pytest
 import common
 from treesa_gpu_amd import capi, host
 from treesa_gpu_amd import formats as F
-from treesa_gpu_amd import starts as S
+from treesa_gpu_amd import host as S
 
 PAT = re.compile(r"ok   (\w+): trees == omeco complexity \(GreedyMethod: ([\d.]+)/(\d+)\)")
 

@@ -106,7 +106,7 @@ def test_result_is_valid_and_consistent(scheme, tmp_path):
 # --init spectral / greedy make the start trees natively; the run equals the same trees passed as a --tree file
 @pytest.mark.parametrize("inst,init", [("sat60", "spectral"), ("lat14", "spectral"), ("reg3_250", "greedy")])
 def test_native_start_trees_equal_tree_file(inst, init, tmp_path):
-    from treesa_gpu_amd import starts as S
+    from treesa_gpu_amd import host as S
     m, nlab, ixs, iy = common.load_instance(inst)
     if init == "spectral":
         so = S.spectral_orders(ixs, iy, k=3, seed=5)

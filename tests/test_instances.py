@@ -9,7 +9,7 @@ import pytest
 import common
 from treesa_gpu_amd import capi, host
 from treesa_gpu_amd import instances as I
-from treesa_gpu_amd import starts as S
+from treesa_gpu_amd import host as S
 
 
 def fixture(name):

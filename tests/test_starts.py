@@ -1,5 +1,5 @@
 """CPU tests of the native start-tree generators (treesa_gpu_amd/host/tsa_starts.cpp through
-treesa_gpu_amd/starts.py).
+treesa_gpu_amd/host.py).
 
 * The candidate search, given numpy's eigenvectors and numpy's random directions (the reference's inputs to
   it, treesa_gpu/spectral.py:63-67, 143-160), returns the path tc values the reference's own test run
@@ -17,7 +17,7 @@ import pytest
 
 import common
 from treesa_gpu_amd import capi, host
-from treesa_gpu_amd import starts as S
+from treesa_gpu_amd import host as S
 
 # tests/test_python_results.txt:63-66 -- spectral_orders(ixs, iy, k=3) of the reference, rounded to 3 places
 REFERENCE_ORDERS = {
