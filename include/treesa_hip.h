@@ -170,7 +170,8 @@ int tsa_set_mode(tsa_ctx* ctx, int32_t mode);
 int tsa_stats(tsa_ctx* ctx, uint64_t out[7]);
 
 /* Counters of the wide kernel with chunk summaries since creation: out[0] = 16-byte chunk positions a
- * proposal loaded (one per set bit of the union of its summaries; each is read from the five label sets),
+ * proposal loaded (one per set bit of the union of its summaries; each is read from the label sets of the
+ * visited node, the other child and the two grandchildren, and from the pivot's too in the gpu / h100 modes),
  * out[1] = chunk positions written by accepted rotations.  Both stay 0 without summaries.  No counterpart in
  * the reference: it is the measured byte count of the summary path's roofline. */
 int tsa_chunk_stats(tsa_ctx* ctx, uint64_t out[2]);

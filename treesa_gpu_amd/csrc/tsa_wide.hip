@@ -11,7 +11,8 @@
 //   2. visits: workgroup k takes the k-th of K contiguous shares of the work list, and its waves take
 //      entries from that share 64/G at a time through an LDS counter (one entry per lane group), so
 //      that faster waves take more; the G lanes of a
-//      group load the five label sets D, P, O, K, M in 16-byte chunks (chunk t, t+G, ...), count with
+//      group load the label sets D, O, K, M (and P, except in tc mode, where the costs of P and v before the
+//      move and P's size come from the node-cost cache) in 16-byte chunks (chunk t, t+G, ...), count with
 //      popcounts, sum the counters (packed two per 32-bit word) with xor shuffles inside the group, all
 //      lanes evaluate the same dE and Metropolis test, and on accept each lane stores its chunks of
 //      X = (K|O)&(M|D) into P's set.  The group leader publishes one outcome byte (accepted, pivot slot,
