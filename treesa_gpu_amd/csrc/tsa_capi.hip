@@ -598,13 +598,19 @@ static hipError_t claim_slot(tsa_ctx* c, int s) {
   return e;
 }
 
+// The chunk summaries for a full node-cost pass, when they match the population (else none: a dense pass).
+static TsaSums wide_sums(const tsa_ctx* c) {
+  if (!c->wide.nsw || !c->sums_valid) return TsaSums{nullptr, nullptr, 0};
+  return TsaSums{c->d_sum, c->d_leafsum, c->wide.nsw};
+}
+
 static hipError_t launch_energy(tsa_ctx* c) {
   join_track(c);
   if (c->energy_fresh) return hipSuccess;  // the last sweep launch left them in d_lc / d_sc / d_ns
   if (c->wide.on) {
     const hipError_t e = tsa_launch_wide_energy(c->wide, c->mode, c->P, c->d_rec, c->d_leaf, c->d_fix, c->nchains,
                                                 c->d_ncost, c->d_nz, c->d_fcnt, c->d_lc, c->d_sc, c->d_ns,
-                                                c->costs_valid ? 0 : 1, c->st);
+                                                c->costs_valid ? 0 : 1, c->st, wide_sums(c));
     c->costs_valid = e == hipSuccess;
     return e;
   }
@@ -708,7 +714,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
       join_track(ctx);
       TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
                                           ctx->nchains, ctx->d_ncost, ctx->d_nz, ctx->d_fcnt, ctx->d_lc, ctx->d_sc,
-                                          ctx->d_ns, 1, ctx->st));
+                                          ctx->d_ns, 1, ctx->st, wide_sums(ctx)));
       ctx->costs_valid = true;
     }
     if (ctx->overlap) {

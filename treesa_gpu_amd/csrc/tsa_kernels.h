@@ -251,10 +251,18 @@ hipError_t tsa_launch_wide(const TsaWide& X, int mode, const TsaKParams& P, uint
                            const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
                            unsigned long long* stats, const TsaWideSync& sy, hipStream_t st,
                            hipEvent_t e0 = nullptr, hipEvent_t e1 = nullptr);
+// Chunk summaries of the internal sets (isum[nchains][nint4][nsw]) and of the input tensors (lsum[m][nsw]) that
+// match the population; nsw = 0: none.
+struct TsaSums {
+  const uint64_t* isum;
+  const uint64_t* lsum;
+  int nsw;
+};
 // Energies through per-node costs: ncost / nz hold nchains * nint4 node costs and masked sizes, fcnt
-// nchains zeroed counters.  nodes = 1: recompute every node cost from the label sets first; nodes = 0: fold
-// the cached costs only.
+// nchains zeroed counters.  nodes = 1: recompute every node cost from the label sets first (with summaries:
+// only the chunks in the union of a node's and its children's summaries, where all their nonzero chunks lie);
+// nodes = 0: fold the cached costs only.
 hipError_t tsa_launch_wide_energy(const TsaWide& X, int mode, const TsaKParams& P, const uint64_t* rec,
                                   const uint64_t* leaf, const uint32_t* fix, int nchains, float* ncost,
                                   uint16_t* nz, unsigned* fcnt, float* lc, int* sc, int* ns, int nodes,
-                                  hipStream_t st);
+                                  hipStream_t st, TsaSums sums = TsaSums{nullptr, nullptr, 0});

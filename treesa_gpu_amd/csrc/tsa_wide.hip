@@ -782,7 +782,8 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
                                                const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
                                                int nchains, int K2, int nodes, int stage, float* __restrict__ ncost,
                                                uint16_t* __restrict__ nz, unsigned* __restrict__ fcnt,
-                                               float* __restrict__ lc, int* __restrict__ sc, int* __restrict__ ns) {
+                                               float* __restrict__ lc, int* __restrict__ sc, int* __restrict__ ns,
+                                               TsaSums sums) {
   // LDS (stage != 0): the chain's node costs f32[nint4] and sizes u16[nint4], then (stage == 2) the log2f
   // summary bitmap at the next 16-byte boundary
   extern __shared__ __align__(16) unsigned char s_dyn[];
@@ -823,11 +824,23 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
         const TsaW2* qx = reinterpret_cast<const TsaW2*>(l >= m ? lab + (size_t)(l - m) * NW : leaf + (size_t)l * NW);
         const TsaW2* qy = reinterpret_cast<const TsaW2*>(r >= m ? lab + (size_t)(r - m) * NW : leaf + (size_t)r * NW);
         const TsaW2* qz = reinterpret_cast<const TsaW2*>(lab + (size_t)i * NW);
+        // with summaries only the chunks in the union of the three sets' summaries are read (a chunk outside it
+        // is zero in all three and adds nothing to any count)
+        uint64_t u0 = ~0ull, u1 = ~0ull;
+        if (sums.nsw) {
+          const int nsw = sums.nsw;
+          const uint64_t* const is = sums.isum + (size_t)c * nint4 * nsw;
+          auto sw = [&](int n, int q) -> uint64_t {
+            return n >= m ? is[(size_t)(n - m) * nsw + q] : sums.lsum[(size_t)n * nsw + q];
+          };
+          u0 = sw(l, 0) | sw(r, 0) | is[(size_t)i * nsw];
+          u1 = nsw > 1 ? (sw(l, 1) | sw(r, 1) | is[(size_t)i * nsw + 1]) : 0ull;
+        }
         TsaW2 xx[TSA_WIDE_CPL], yy[TSA_WIDE_CPL], zv[TSA_WIDE_CPL];
 #pragma unroll
         for (int q = 0; q < TSA_WIDE_CPL; q++) {
           const int cc = t + q * G;
-          if (cc < nch) {
+          if (cc < nch && (((cc < 64 ? u0 >> cc : u1 >> (cc - 64)) & 1ull) != 0ull)) {
             xx[q] = qx[cc];
             yy[q] = qy[cc];
             zv[q] = qz[cc];
@@ -911,22 +924,22 @@ hipError_t launch_wide_g(const TsaWide& X, int mode, const TsaKParams& P, uint64
 template <int G, int MODE>
 hipError_t launch_wcost_gm(const TsaWide& X, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
                            const uint32_t* fix, int nchains, float* ncost, uint16_t* nz, unsigned* fcnt, float* lc,
-                           int* sc, int* ns, int nodes, hipStream_t st) {
+                           int* sc, int* ns, int nodes, hipStream_t st, TsaSums sums) {
   const int K2 = nodes ? X.eK : 1;
   const int stage = nodes ? (X.fold_smem > 0 ? 1 : 0) : X.fold_stage;
   const size_t smem = stage == 2 ? (size_t)X.fold_smem_map : stage == 1 ? (size_t)X.fold_smem : 0;
   hipLaunchKernelGGL((k_wcost<G, MODE>), dim3(nchains * K2), dim3(256), smem, st, P, rec, leaf, fix, nchains, K2, nodes,
-                     stage, ncost, nz, fcnt, lc, sc, ns);
+                     stage, ncost, nz, fcnt, lc, sc, ns, sums);
   return hipGetLastError();
 }
 
 template <int G>
 hipError_t launch_wcost_g(const TsaWide& X, int mode, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
                           const uint32_t* fix, int nchains, float* ncost, uint16_t* nz, unsigned* fcnt, float* lc,
-                          int* sc, int* ns, int nodes, hipStream_t st) {
-  if (mode == 0) return launch_wcost_gm<G, 0>(X, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
-  if (mode == 1) return launch_wcost_gm<G, 1>(X, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
-  return launch_wcost_gm<G, 2>(X, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
+                          int* sc, int* ns, int nodes, hipStream_t st, TsaSums sums) {
+  if (mode == 0) return launch_wcost_gm<G, 0>(X, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st, sums);
+  if (mode == 1) return launch_wcost_gm<G, 1>(X, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st, sums);
+  return launch_wcost_gm<G, 2>(X, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st, sums);
 }
 
 // Largest number of co-resident workgroups per CU of the multi-workgroup sweep kernel over the three modes,
@@ -1137,13 +1150,14 @@ hipError_t tsa_launch_wsum(const TsaWide& X, const TsaKParams& P, const uint64_t
 hipError_t tsa_launch_wide_energy(const TsaWide& X, int mode, const TsaKParams& P, const uint64_t* rec,
                                   const uint64_t* leaf, const uint32_t* fix, int nchains, float* ncost,
                                   uint16_t* nz, unsigned* fcnt, float* lc, int* sc, int* ns, int nodes,
-                                  hipStream_t st) {
+                                  hipStream_t st, TsaSums sums) {
+  if (!nodes || !sums.isum || !sums.lsum) sums.nsw = 0;
   switch (X.eG) {
-    case 4: return launch_wcost_g<4>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
-    case 8: return launch_wcost_g<8>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
-    case 16: return launch_wcost_g<16>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
-    case 32: return launch_wcost_g<32>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
-    case 64: return launch_wcost_g<64>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st);
+    case 4: return launch_wcost_g<4>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st, sums);
+    case 8: return launch_wcost_g<8>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st, sums);
+    case 16: return launch_wcost_g<16>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st, sums);
+    case 32: return launch_wcost_g<32>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st, sums);
+    case 64: return launch_wcost_g<64>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st, sums);
     default: return hipErrorInvalidValue;
   }
 }
