@@ -231,6 +231,44 @@ def test_wide_summaries_across_upload_resample_and_preorder():
     assert ck[0] > 0 and ck[1] > 0, ck
 
 
+# A tc-mode wide visit takes the costs of P and v before the move and P's size from the node-cost cache instead
+# of P's set; the cache is rebuilt before the first sweep after an upload, a resample and a switch back from
+# another energy mode (whose sweeps neither read nor keep tc costs).  Dense and summary paths, two workgroups
+# per chain, no energy call between the steps: the records after every step and the final energies equal the
+# oracle's.
+@pytest.mark.parametrize("sums", [-1, 1])
+def test_wide_cost_cache_across_resample_and_mode_switch(sums):
+    case = Case("sq46", "par", "tc", kernel=capi.KERNEL_WIDE, nchains=24, sums=sums, wide_wgs=2)
+    Pg = orc.params_from_config(case.cfg, case.leaf_sc, case.nlab)
+    Pg.mode = capi.MODES["gpu"]
+    rng = np.random.default_rng(11)
+    anc = rng.integers(0, case.nchains, case.nchains).astype(np.int32)
+    opop = case.pop0.copy()
+    print(f"[gpu] cost cache across resample / mode switch sq46 sums={sums}", flush=True)
+    with capi.Context(case.lay, case.leaf, case.leaf_sc, case.cfg, case.nchains) as ctx:
+        assert ctx.describe().startswith("wide") and (" sums=0 " in ctx.describe()) == (sums < 0)
+        ctx.upload(case.pop0)
+        ctx.sweeps(capi.ORDER_PAR, 1.0, 0, 2)
+        case.O.sweeps(case.P, case.lay, opop, capi.ORDER_PAR, 1.0, 0, 2)
+        assert np.array_equal(ctx.download(), opop), "after an upload"
+        ctx.resample(anc)
+        opop = opop[anc].copy()
+        ctx.sweeps(capi.ORDER_PAR, 2.0, 2, 1)
+        case.O.sweeps(case.P, case.lay, opop, capi.ORDER_PAR, 2.0, 2, 1)
+        assert np.array_equal(ctx.download(), opop), "after a resample"
+        ctx.set_mode("gpu")
+        ctx.sweeps(capi.ORDER_PAR, 3.0, 3, 1)
+        case.O.sweeps(Pg, case.lay, opop, capi.ORDER_PAR, 3.0, 3, 1)
+        ctx.set_mode("tc")
+        ctx.sweeps(capi.ORDER_PAR, 4.0, 4, 2)
+        case.O.sweeps(case.P, case.lay, opop, capi.ORDER_PAR, 4.0, 4, 2)
+        assert np.array_equal(ctx.download(), opop), "after a gpu-mode sweep and the switch back"
+        glc, gsc, gns = ctx.energy()
+        olc, osc, ons = case.O.energy(case.P, case.lay, opop)
+        assert np.array_equal(glc.view(np.uint32), olc.view(np.uint32))
+        assert np.array_equal(gsc, osc) and np.array_equal(gns, ons)
+
+
 # Energies from the node-cost cache the wide sweep kernel keeps: after every level the fold of the cached
 # costs equals the oracle's evaluation of the same population, in every energy mode, also with a GPU model
 # whose m0 != n0 (node costs that depend on the order of the two children).
