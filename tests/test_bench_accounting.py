@@ -9,12 +9,9 @@
 Each is checked against a count written out by hand and against the others' differences, so that a dropped term
 or a wrong set count fails.
 """
-import sys
-
 import pytest
 
-sys.argv = sys.argv[:1]
-import bench  # noqa: E402
+import bench
 
 
 @pytest.mark.parametrize("W", [1, 2, 48, 126])
