@@ -164,7 +164,12 @@ hipError_t tsa_launch_sum_stats(const unsigned long long* slots, unsigned long l
 // Wide path (tsa_wide.hip): par-order sweeps and energies of runtime-width chains, label sets streamed
 // from HBM in 16-byte chunks by groups of G lanes per proposal, node arrays in LDS, K workgroups per chain.
 // ---------------------------------------------------------------------------------------------------
-#define TSA_WIDE_CPL 2        // 16-byte chunks per lane and label set (so W <= 2 * TSA_WIDE_CPL * 64 = 256)
+#define TSA_WIDE_CPL 2        // 16-byte chunks per lane and set with 16 or more lanes (so W <= 2 * 2 * 64 = 256)
+// 16-byte chunks per lane of a set in the dense visit and the node-cost pass of G-lane groups: 4 up to 8 lanes,
+// 2 from 16 (G * chunks never falls as G grows, so a group at least as wide as the plan's holds the set).  The
+// visit's proposal-wide work (Philox, energy, Metropolis) is done once per group, so on an issue-bound kernel
+// fewer, fuller lanes per proposal pay: C4's 24 chunks take 8 lanes of 3-4 chunks, not 16 of 1-2.
+__host__ __device__ constexpr int tsa_wide_cpl(int G) { return G <= 8 ? 4 : TSA_WIDE_CPL; }
 #define TSA_WIDE_MAX_K 16     // workgroups per chain
 #define TSA_WIDE_SPIN (1u << 22)  // polls of a chain barrier before the launch gives up (seconds)
 #define TSA_WIDE_JOIN (1u << 16)  // default polls of the check-in (milliseconds)

@@ -498,7 +498,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
               szP = (int)sy.nz[cb + (Pn - m)];
             }
             constexpr int SC = TsaSumRound<G>::SC;
-            constexpr int XN = SUMS ? SC : TSA_WIDE_CPL;
+            constexpr int XN = SUMS ? SC : tsa_wide_cpl(G);
             TsaW2 xx[XN];  // only X stays live across the energy evaluation
             // SUMS: the population count of the union (uniform in the group) and the chunk positions of this
             // lane's first round
@@ -554,9 +554,10 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
                 }
               }
             } else {
-              TsaW2 dd[TSA_WIDE_CPL], pp[TSA_WIDE_CPL], oo[TSA_WIDE_CPL], kk[TSA_WIDE_CPL], mm[TSA_WIDE_CPL];
+              constexpr int CPL = tsa_wide_cpl(G);
+              TsaW2 dd[CPL], pp[CPL], oo[CPL], kk[CPL], mm[CPL];
 #pragma unroll
-              for (int q = 0; q < TSA_WIDE_CPL; q++) {
+              for (int q = 0; q < tsa_wide_cpl(G); q++) {
                 const int cc = t + q * G;
                 if (cc < nch) {
                   dd[q] = qD[cc];
@@ -569,7 +570,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
                 }
               }
 #pragma unroll
-              for (int q = 0; q < TSA_WIDE_CPL; q++) {
+              for (int q = 0; q < tsa_wide_cpl(G); q++) {
                 xx[q].a = tsa_xset(kk[q].a, oo[q].a, mm[q].a, dd[q].a);
                 xx[q].b = tsa_xset(kk[q].b, oo[q].b, mm[q].b, dd[q].b);
                 if constexpr (CACHED) {
@@ -667,7 +668,7 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
                 }
               } else {
 #pragma unroll
-                for (int q = 0; q < TSA_WIDE_CPL; q++) {
+                for (int q = 0; q < tsa_wide_cpl(G); q++) {
                   const int cc = t + q * G;
                   if (cc < nch) qP[cc] = xx[q];
                 }
@@ -805,9 +806,10 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
     const uint32_t* const ch = reinterpret_cast<const uint32_t*>(lab + P.ch_off);
     const int gpb = (int)blockDim.x / G, grp = (int)threadIdx.x / G, t = (int)threadIdx.x & (G - 1);
     const int npb = (nint + K2 - 1) / K2, i0 = k * npb, i1 = (i0 + npb < nint) ? i0 + npb : nint;
-    TsaW2 sm[TSA_WIDE_CPL];
+    constexpr int CPL = tsa_wide_cpl(G);
+    TsaW2 sm[CPL];
 #pragma unroll
-    for (int q = 0; q < TSA_WIDE_CPL; q++) {
+    for (int q = 0; q < CPL; q++) {
       const int cc = t + q * G;
       if (S && cc < nch) {
         const TsaW2 sv = reinterpret_cast<const TsaW2*>(S)[cc];
@@ -836,9 +838,9 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
           u0 = sw(l, 0) | sw(r, 0) | is[(size_t)i * nsw];
           u1 = nsw > 1 ? (sw(l, 1) | sw(r, 1) | is[(size_t)i * nsw + 1]) : 0ull;
         }
-        TsaW2 xx[TSA_WIDE_CPL], yy[TSA_WIDE_CPL], zv[TSA_WIDE_CPL];
+        TsaW2 xx[CPL], yy[CPL], zv[CPL];
 #pragma unroll
-        for (int q = 0; q < TSA_WIDE_CPL; q++) {
+        for (int q = 0; q < CPL; q++) {
           const int cc = t + q * G;
           if (cc < nch && (((cc < 64 ? u0 >> cc : u1 >> (cc - 64)) & 1ull) != 0ull)) {
             xx[q] = qx[cc];
@@ -850,7 +852,7 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
         }
         int B = 0, M = 0, N = 0, Kc = 0, Z = 0;
 #pragma unroll
-        for (int q = 0; q < TSA_WIDE_CPL; q++) {
+        for (int q = 0; q < CPL; q++) {
           const uint64_t za = zv[q].a & sm[q].a, zb = zv[q].b & sm[q].b;
           tsa_count3(xx[q].a & sm[q].a, yy[q].a & sm[q].a, za, B, M, N, Kc);
           tsa_count3(xx[q].b & sm[q].b, yy[q].b & sm[q].b, zb, B, M, N, Kc);
@@ -1040,10 +1042,10 @@ hipError_t tsa_wide_plan(const TsaKParams& P, int nchains, int want_waves, int w
                          TsaWide* out) {
   TsaWide X{};
   const int nch = P.W / 2;
-  if ((P.W & 1) || nch < 1 || nch > TSA_WIDE_CPL * 64) return hipErrorInvalidValue;
-  // dense streaming needs G * TSA_WIDE_CPL >= chunks per set; the energy kernel always streams densely
+  if ((P.W & 1) || nch < 1 || nch > tsa_wide_cpl(64) * 64) return hipErrorInvalidValue;
+  // dense streaming needs G * tsa_wide_cpl(G) >= chunks per set; the energy kernel always streams densely
   int Gd = 4;
-  while (Gd < 64 && (nch + Gd - 1) / Gd > TSA_WIDE_CPL) Gd *= 2;
+  while (Gd < 64 && (nch + Gd - 1) / Gd > tsa_wide_cpl(Gd)) Gd *= 2;
   X.nsw = (sums > 0 || (sums == 0 && P.W >= 64)) ? (nch + 63) / 64 : 0;
   // summaries: one lane per proposal (the union of a visit is a few chunks: whole-wave SIMD efficiency
   // matters more than spreading loads) and one workgroup per chain (no chain barriers)
