@@ -33,9 +33,12 @@ def run(args, tmp_path, name="out.json"):
 
 
 # sq46 runs the wide path: with chunk summaries (one workgroup per chain: the fold and selection of a level
-# run on a second stream beside the next sweep) and without (several workgroups per chain: no overlap)
+# run on a second stream beside the next sweep), without (several workgroups per chain: no overlap), and
+# without with one workgroup per chain and the selection on the sweep's stream (the sweep launch folds the
+# energies itself)
 @pytest.mark.parametrize("order", ["par", "preorder"])
-@pytest.mark.parametrize("inst,extra", [("sat60", []), ("lat14", []), ("sq46", []), ("sq46", ["--no-sum"])])
+@pytest.mark.parametrize("inst,extra", [("sat60", []), ("lat14", []), ("sq46", []), ("sq46", ["--no-sum"]),
+                                        ("sq46", ["--no-sum", "--wide-wgs", "1", "--no-overlap"])])
 def test_device_selection_equals_host_selection(inst, extra, order, tmp_path):
     args = ["-i", common.inst_path(inst), "--nchains", "96", "--niters", "2", "--betas", "0.01:0.05:15",
             "--sc-target", "30", "--order", order, "--seed", "3"] + extra

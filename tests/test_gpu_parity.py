@@ -271,18 +271,23 @@ def test_wide_cost_cache_across_resample_and_mode_switch(sums):
 
 # Energies from the node-cost cache the wide sweep kernel keeps: after every level the fold of the cached
 # costs equals the oracle's evaluation of the same population, in every energy mode, also with a GPU model
-# whose m0 != n0 (node costs that depend on the order of the two children).
-@pytest.mark.parametrize("mode,gm", [("tc", capi.DEFAULT_GM), ("h100", capi.DEFAULT_GM),
-                                     ("gpu", (11.9e15, 1.6e13, 3, 9, 8, 4e-6))])
-def test_wide_cached_energies_every_level(mode, gm):
-    case = Case("sq46", "par", mode, kernel=capi.KERNEL_WIDE, nchains=24)
+# whose m0 != n0 (node costs that depend on the order of the two children).  With one workgroup per chain
+# (wgs 1) the sweep launch folds the energies itself once the cache is exact (tc mode: from the first launch;
+# the other modes: after the first energy call's full pass); with several, the fold kernel does.
+@pytest.mark.parametrize("mode,gm,wgs", [("tc", capi.DEFAULT_GM, 0), ("h100", capi.DEFAULT_GM, 0),
+                                         ("gpu", (11.9e15, 1.6e13, 3, 9, 8, 4e-6), 0), ("tc", capi.DEFAULT_GM, 1),
+                                         ("h100", capi.DEFAULT_GM, 1), ("gpu", (11.9e15, 1.6e13, 3, 9, 8, 4e-6), 1)])
+def test_wide_cached_energies_every_level(mode, gm, wgs):
+    case = Case("sq46", "par", mode, kernel=capi.KERNEL_WIDE, nchains=24, wide_wgs=wgs, sums=-1)
     if gm is not capi.DEFAULT_GM:
         case.cfg = capi.make_config(mode=mode, sc_target=common.CHECK_SC_TARGET, seed=common.CHECK_SEED,
-                                    kernel=capi.KERNEL_WIDE, gm=gm)
+                                    kernel=capi.KERNEL_WIDE, gm=gm, wide_wgs=wgs, sums=-1)
         case.P = orc.params_from_config(case.cfg, case.leaf_sc, case.nlab)
     opop = case.pop0.copy()
-    print(f"[gpu] cached energies sq46 mode={mode} gm={gm}", flush=True)
+    print(f"[gpu] cached energies sq46 mode={mode} gm={gm} wgs={wgs}", flush=True)
     with capi.Context(case.lay, case.leaf, case.leaf_sc, case.cfg, case.nchains) as ctx:
+        desc = ctx.describe()
+        assert " sums=0 " in desc and ("blocks/chain=1 " in desc) == (wgs == 1), desc
         ctx.upload(case.pop0)
         for lev, b in enumerate([0.3, 1.0, 3.0, 10.0]):
             if lev != 1:  # level 1 runs two launches between energies

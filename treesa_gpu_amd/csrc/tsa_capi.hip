@@ -717,6 +717,16 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
                                           ctx->d_ns, 1, ctx->st, wide_sums(ctx)));
       ctx->costs_valid = true;
     }
+    // without the overlap, a dense plan of one workgroup per chain folds the energies at the end of the sweep
+    // (the sweep kernel has every chain's cost cache at hand; a fold launch after it would find the device idle
+    // but for its one lane group per chain)
+    const bool fold_here = !ctx->overlap && ctx->wide.K == 1 && ctx->wide.nsw == 0 && ctx->costs_valid;
+    if (fold_here) {
+      join_track(ctx);  // a selection still pending on st2 reads d_lc / d_sc / d_ns
+      sy.flc = ctx->d_lc;
+      sy.fsc = ctx->d_sc;
+      sy.fns = ctx->d_ns;
+    }
     if (ctx->overlap) {
       s = ctx->slot;
       TSA_HIP(ctx, claim_slot(ctx, s));
@@ -734,6 +744,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
       ctx->last_slot = s;
       ctx->slot = s ^ 1;
     }
+    ctx->energy_fresh = fold_here;
   } else {
     ctx->costs_valid = false;
     ctx->sums_valid = false;

@@ -216,6 +216,12 @@ struct TsaWideSync {
   uint32_t* snap_ch;
   float* snap_cost;
   uint16_t* snap_nz;
+  // Energies of every chain folded by the sweep kernel itself at the end of the launch, from the node-cost
+  // cache (null: none; dense plans with one workgroup per chain, and the cache exact when the launch starts):
+  // flc / fsc / fns [nchains].
+  float* flc;
+  int* fsc;
+  int* fns;
 };
 
 // LDS byte offsets of k_wide (same function on host and device).

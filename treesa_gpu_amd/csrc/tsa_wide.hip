@@ -752,6 +752,17 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
       tsa_copy_inflight<uint16_t, 8>(sy.snap_nz + cb, sy.nz + cb, nint, threadIdx.x, NT);
     }
   }
+  if constexpr (!COOP && !SUMS) {
+    // the launch's energies, folded by this workgroup rather than by a launch of their own: every accept
+    // rewrote its entries of the node-cost cache before the loop's last barrier, so the cache is the final
+    // tree's; the costs are staged in the sweep's LDS, whose last reads (the tree, above) end at the barrier
+    if (sy.flc) {
+      __syncthreads();
+      const size_t cb = (size_t)c * nint4;
+      wide_fold(P, c, sy.ncost + cb, sy.nz + cb, P.slicing ? lab + P.s_off : nullptr, leaf, fix, s_mt,
+                nint4 * 6 <= Lo.bytes ? 1 : 0, tsa_wsm, sy.flc, sy.fsc, sy.fns);
+    }
+  }
   const long long sp_ = wide_wave_sum(np), sa_ = wide_wave_sum(na), sv_ = wide_wave_sum(nv);
   const long long sk_ = SUMS ? wide_wave_sum(nck) : 0, sx_ = SUMS ? wide_wave_sum(nxk) : 0;
   if (lane == 0) {  // counters spread over TSA_STAT_SLOTS addresses each, summed by the host
