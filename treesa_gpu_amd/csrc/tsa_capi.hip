@@ -5,6 +5,7 @@
 // host-built tables the kernels read: the lse table (csrc/treesa_gpu.cu:2075) and the log2f correction
 // table of tsa_math.h, which is filled by comparing the restated log2f with this process's libm.
 #include <hip/hip_runtime.h>
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -76,6 +77,17 @@ struct tsa_ctx {
   // ev_track[s] the selection that read it (the host waits for it before a sweep overwrites the slot).
   bool overlap = false;
   hipStream_t st2 = nullptr;
+  // Split sweeps (the one-wave kernels with the overlapped selection and the fold apart, where the population
+  // is more than twice what the device holds at once): a level's chains are swept by two launches, the first
+  // part on st and the rest on st3, so that each stream's dependent dispatch and the tail of its launch are
+  // covered by the other stream's work.  st3's launch waits for what st held before the level's first launch
+  // (ev_fork); every other operation first orders st after st3 (join_split).  ev_b[s] follows the second
+  // launch of the sweep that filled slot s, when split_slot[s].
+  hipStream_t st3 = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  hipEvent_t ev_b[2] = {nullptr, nullptr};
+  bool split_slot[2] = {false, false};
+  bool split_pending = false;  // st3 holds work st is not yet ordered after
   hipEvent_t ev_sweep[2] = {nullptr, nullptr};  // (the stop events of those sweeps' timing pairs)
   hipEvent_t ev_track[2] = {nullptr, nullptr};
   bool track_pending[2] = {false, false};
@@ -272,7 +284,13 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_leafsum) (void)hipFree(c->d_leafsum);
   if (c->d_tpart) (void)hipFree(c->d_tpart);
   if (c->d_tdone) (void)hipFree(c->d_tdone);
+  if (c->st3) (void)hipStreamSynchronize(c->st3);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
+  if (c->st3) {
+    for (hipEvent_t e : {c->ev_fork, c->ev_join, c->ev_b[0], c->ev_b[1]})
+      if (e) (void)hipEventDestroy(e);
+    (void)hipStreamDestroy(c->st3);
+  }
   if (c->st2) (void)hipStreamSynchronize(c->st2);
   for (int k = 0; k < 2; k++) {
     if (c->ev_track[k]) (void)hipEventDestroy(c->ev_track[k]);
@@ -579,6 +597,14 @@ static void join_track(tsa_ctx* c) {
     if (c->track_pending[k]) (void)hipStreamWaitEvent(c->st, c->ev_track[k], 0);
 }
 
+static hipError_t join_split(tsa_ctx* c) {
+  if (!c->split_pending) return hipSuccess;
+  c->split_pending = false;
+  hipError_t e = hipEventRecord(c->ev_join, c->st3);
+  if (e == hipSuccess) e = hipStreamWaitEvent(c->st, c->ev_join, 0);
+  return e;
+}
+
 static hipError_t quiesce_track(tsa_ctx* c) {
   hipError_t e = hipSuccess;
   if (c->st2) e = hipStreamSynchronize(c->st2);
@@ -635,6 +661,7 @@ static int wide_error(tsa_ctx* c, uint32_t word) {
 
 extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
   if (!ctx || !population) return fail(ctx, TSA_ERR_ARG, "tsa_upload: null argument");
+  TSA_HIP(ctx, join_split(ctx));
   const tsa_layout_t& L = ctx->lay;
   std::vector<char> seen;
   std::vector<int> st;
@@ -655,6 +682,7 @@ extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
 
 extern "C" int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* out) {
   if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_download: null argument");
+  TSA_HIP(ctx, join_split(ctx));
   if (c0 < 0 || count < 0 || c0 + count > ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_download: range");
   const size_t cw = ctx->lay.chain_words;
   TSA_HIP(ctx, hipMemcpyAsync(out, ctx->d_rec + (size_t)c0 * cw, (size_t)count * cw * 8, hipMemcpyDeviceToHost,
@@ -666,6 +694,7 @@ extern "C" int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* o
 
 extern "C" int tsa_download_async(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* out) {
   if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_download_async: null argument");
+  TSA_HIP(ctx, join_split(ctx));
   if (c0 < 0 || count < 0 || c0 + count > ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_download_async: range");
   const size_t cw = ctx->lay.chain_words;
   TSA_HIP(ctx, hipMemcpyAsync(out, ctx->d_rec + (size_t)c0 * cw, (size_t)count * cw * 8, hipMemcpyDeviceToHost,
@@ -675,6 +704,7 @@ extern "C" int tsa_download_async(tsa_ctx* ctx, int32_t c0, int32_t count, uint6
 
 extern "C" int tsa_wait(tsa_ctx* ctx) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_wait: null context");
+  TSA_HIP(ctx, join_split(ctx));
   if (ctx->st2) TSA_HIP(ctx, hipStreamSynchronize(ctx->st2));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
   ctx->host_waited = true;
@@ -686,7 +716,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
   if (order != TSA_ORDER_PAR && order != TSA_ORDER_PREORDER) return fail(ctx, TSA_ERR_ARG, "--order par|preorder");
   if (nsweeps < 0) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps: nsweeps < 0");
   if (nsweeps == 0) return TSA_OK;
-  while ((int)ctx->ev.size() < 2 * (ctx->npending + 1)) {
+  while ((int)ctx->ev.size() < 2 * (ctx->npending + 2)) {
     hipEvent_t e;
     TSA_HIP(ctx, hipEventCreate(&e));
     ctx->ev.push_back(e);
@@ -700,6 +730,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
   hipEvent_t d0 = markers ? nullptr : e0, d1 = markers ? nullptr : e1;
   ctx->energy_fresh = ctx->energy_host = false;
   if (ctx->wide.on && order == TSA_ORDER_PAR) {
+    TSA_HIP(ctx, join_split(ctx));
     // energies stay a separate fold of the node-cost cache: every chain ends its sweep at about the same
     // time, so folding inside the sweep kernel would only lengthen it
     if (ctx->wide.nsw && !ctx->sums_valid) {
@@ -750,6 +781,10 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     ctx->sums_valid = false;
     const bool fuse = ctx->cfg.fused_energy != 0;
     const bool apart = fuse && ctx->fold_apart;
+    // a split level: chains [0, h) on st, [h, nchains) on st3 (h in whole workgroups)
+    const int h = (ctx->nchains / 2 + ctx->L.wpb - 1) / ctx->L.wpb * ctx->L.wpb;
+    const bool split = ctx->overlap && apart && h > 0 && h < ctx->nchains;
+    if (!split) TSA_HIP(ctx, join_split(ctx));
     TsaEnergyOut eo{fuse && !apart ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns, apart ? ctx->d_ncost : nullptr,
                     apart ? ctx->d_nz : nullptr, nullptr};
     int s = -1;
@@ -780,11 +815,39 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
         ctx->energy_host = true;
       }
     }
-    if (markers) TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
-    TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
-                                   ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st, d0, d1));
-    if (markers) TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
+    if (split) {
+      if (!ctx->st3) {
+        TSA_HIP(ctx, hipStreamCreateWithFlags(&ctx->st3, hipStreamNonBlocking));
+        TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_fork, hipEventDisableTiming));
+        TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_join, hipEventDisableTiming));
+        for (int k = 0; k < 2; k++) TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_b[k], hipEventDisableTiming));
+      }
+      // the second launch's timing pair follows the first's
+      hipEvent_t f0 = ctx->ev[2 * ctx->npending + 2], f1 = ctx->ev[2 * ctx->npending + 3];
+      TSA_HIP(ctx, hipEventRecord(ctx->ev_fork, ctx->st));
+      TSA_HIP(ctx, hipStreamWaitEvent(ctx->st3, ctx->ev_fork, 0));
+      if (markers) TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
+      TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, h, beta,
+                                     sweep0, nsweeps, ctx->d_stats, eo, ctx->st, d0, d1));
+      if (markers) TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
+      TsaKParams P2 = ctx->P;
+      P2.chain0 = h;
+      if (markers) TSA_HIP(ctx, hipEventRecord(f0, ctx->st3));
+      TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, P2, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
+                                     ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st3,
+                                     markers ? nullptr : f0, markers ? nullptr : f1));
+      if (markers) TSA_HIP(ctx, hipEventRecord(f1, ctx->st3));
+      TSA_HIP(ctx, hipEventRecord(ctx->ev_b[s], ctx->st3));
+      ctx->split_pending = true;
+      ctx->npending++;  // (the first launch's pair is counted below)
+    } else {
+      if (markers) TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
+      TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
+                                     ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st, d0, d1));
+      if (markers) TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
+    }
     if (s >= 0) {
+      ctx->split_slot[s] = split;
       ctx->ev_sweep[s] = e1;
       ctx->last_slot = s;
       ctx->slot = s ^ 1;
@@ -802,15 +865,31 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
 
 extern "C" int tsa_sweeps_ms(tsa_ctx* ctx, double* ms) {
   if (!ctx || !ms) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps_ms: null argument");
+  TSA_HIP(ctx, join_split(ctx));
   *ms = 0.0;
   if (ctx->npending == 0) return TSA_OK;
-  TSA_HIP(ctx, hipEventSynchronize(ctx->ev[2 * ctx->npending - 1]));
-  double sum = 0.0;
+  // the union of the launches' intervals (the two launches of a split level run at the same time), each in ms
+  // from the first launch's start
+  std::vector<std::pair<double, double>> iv((size_t)ctx->npending);
   for (int k = 0; k < ctx->npending; k++) {
-    float f = 0.f;
-    TSA_HIP(ctx, hipEventElapsedTime(&f, ctx->ev[2 * k], ctx->ev[2 * k + 1]));
-    sum += (double)f;
+    TSA_HIP(ctx, hipEventSynchronize(ctx->ev[2 * k + 1]));
+    float a = 0.f, b = 0.f;
+    if (k > 0) TSA_HIP(ctx, hipEventElapsedTime(&a, ctx->ev[0], ctx->ev[2 * k]));
+    TSA_HIP(ctx, hipEventElapsedTime(&b, ctx->ev[0], ctx->ev[2 * k + 1]));
+    iv[(size_t)k] = {(double)a, (double)b};
   }
+  std::sort(iv.begin(), iv.end());
+  double sum = 0.0, lo = 0.0, hi = 0.0;
+  for (size_t k = 0; k < iv.size(); k++) {
+    if (k == 0 || iv[k].first > hi) {
+      sum += hi - lo;
+      lo = iv[k].first;
+      hi = iv[k].second;
+    } else if (iv[k].second > hi) {
+      hi = iv[k].second;
+    }
+  }
+  sum += hi - lo;
   ctx->npending = 0;
   *ms = sum;
   return TSA_OK;
@@ -818,6 +897,7 @@ extern "C" int tsa_sweeps_ms(tsa_ctx* ctx, double* ms) {
 
 extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t max_levels) {
   if (!ctx || !sel) return fail(ctx, TSA_ERR_ARG, "tsa_track_begin: null argument");
+  TSA_HIP(ctx, join_split(ctx));
   if (max_levels < 1) return fail(ctx, TSA_ERR_ARG, "tsa_track_begin: max_levels < 1");
   ctx->sel.mode = sel->mode;
   ctx->sel.slicing = sel->slicing;
@@ -838,9 +918,9 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
     TSA_HIP(ctx, hipMalloc(&ctx->d_trace, (size_t)max_levels * sizeof(TsaTraceRowD)));
   }
   ctx->track_levels = max_levels;
-  // timing events for one sweep launch per level, created here rather than one pair per launch inside the
-  // level loop, where their creation would hold up the host's enqueueing of short levels
-  while ((int)ctx->ev.size() < 2 * (ctx->npending + max_levels)) {
+  // timing events for the sweep launches of every level (two for a split level), created here rather than
+  // inside the level loop, where their creation would hold up the host's enqueueing of short levels
+  while ((int)ctx->ev.size() < 2 * (ctx->npending + 2 * max_levels)) {
     hipEvent_t e;
     TSA_HIP(ctx, hipEventCreate(&e));
     ctx->ev.push_back(e);
@@ -894,6 +974,7 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
     // the last sweep's snapshot: fold its node costs and select on st2, beside the next sweep on st
     const int s = ctx->last_slot;
     TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_sweep[s], 0));
+    if (ctx->split_slot[s]) TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_b[s], 0));
     const int kind = ctx->snap_kind[s];
     if (kind == SNAP_WIDE)
       TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
@@ -914,6 +995,7 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
     ctx->energy_fresh = false;  // d_lc / d_sc / d_ns now hold the snapshot's energies
     return TSA_OK;
   }
+  TSA_HIP(ctx, join_split(ctx));
   TSA_HIP(ctx, launch_energy(ctx));  // (orders st after any selection pending on st2)
   TSA_HIP(ctx, tsa_launch_track(ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->nchains, S, level, ctx->d_rec, L.chain_words,
                                 L.ch_off, L.s_off, L.W, L.nint, nullptr, ctx->d_track, ctx->d_trace, ctx->d_best,
@@ -925,6 +1007,7 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
                              uint64_t* best_record, tsa_trace_row_t* rows, uint64_t* ticks0, double* tick_hz) {
   if (!ctx || !best_chain || !best_level || !best_score || !best_record || !rows || !ticks0 || !tick_hz)
     return fail(ctx, TSA_ERR_ARG, "tsa_track_end: null argument");
+  TSA_HIP(ctx, join_split(ctx));
   if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_track_end: no tsa_track_begin");
   static_assert(sizeof(TsaTraceRowD) == sizeof(tsa_trace_row_t), "trace row layout");
   TsaTrackState h;
@@ -1017,6 +1100,7 @@ static int levels_alloc(tsa_ctx* ctx, int nlev, int nev) {
 extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t nlevels, const float* betas,
                           const int32_t* niters, const uint8_t* evaluated, uint32_t sweep0) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_anneal: null context");
+  TSA_HIP(ctx, join_split(ctx));
   if (order != TSA_ORDER_PAR && order != TSA_ORDER_PREORDER) return fail(ctx, TSA_ERR_ARG, "--order par|preorder");
   if (!betas || !niters || !evaluated || nlevels < 1) return fail(ctx, TSA_ERR_ARG, "tsa_anneal: no levels");
   if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_anneal: no tsa_track_begin");
@@ -1121,6 +1205,7 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
 
 extern "C" int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns) {
   if (!ctx || !lc || !sc || !ns) return fail(ctx, TSA_ERR_ARG, "tsa_energy: null argument");
+  TSA_HIP(ctx, join_split(ctx));
   const size_t b = (size_t)ctx->nchains * 4;
   if (ctx->energy_host) {  // the last sweep launch wrote them into h_en
     TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
@@ -1139,6 +1224,7 @@ extern "C" int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns) {
 
 extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
   if (!ctx || !anc) return fail(ctx, TSA_ERR_ARG, "tsa_resample: null argument");
+  TSA_HIP(ctx, join_split(ctx));
   for (int c = 0; c < ctx->nchains; c++)
     if (anc[c] < 0 || anc[c] >= ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_resample: ancestor out of range");
   if (!ctx->d_rec2) TSA_HIP(ctx, hipMalloc(&ctx->d_rec2, (size_t)ctx->nchains * ctx->lay.chain_words * 8));
@@ -1161,6 +1247,7 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
 
 extern "C" int tsa_set_mode(tsa_ctx* ctx, int32_t mode) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: null context");
+  TSA_HIP(ctx, join_split(ctx));
   if (mode < 0 || mode > 2) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: mode must be 0, 1 or 2");
   if (mode != ctx->mode) {
     TSA_HIP(ctx, quiesce_track(ctx));
@@ -1172,6 +1259,7 @@ extern "C" int tsa_set_mode(tsa_ctx* ctx, int32_t mode) {
 
 extern "C" int tsa_stats(tsa_ctx* ctx, uint64_t out[7]) {
   if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_stats: null argument");
+  TSA_HIP(ctx, join_split(ctx));
   unsigned long long s[TSA_NSTAT * TSA_STAT_SLOTS];
   TSA_HIP(ctx, hipMemcpyAsync(s, ctx->d_stats, sizeof s, hipMemcpyDeviceToHost, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
@@ -1184,6 +1272,7 @@ extern "C" int tsa_stats(tsa_ctx* ctx, uint64_t out[7]) {
 
 extern "C" int tsa_chunk_stats(tsa_ctx* ctx, uint64_t out[2]) {
   if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_chunk_stats: null argument");
+  TSA_HIP(ctx, join_split(ctx));
   unsigned long long s[2 * TSA_STAT_SLOTS];
   TSA_HIP(ctx, hipMemcpyAsync(s, ctx->d_stats + TSA_ST_CHUNKS * TSA_STAT_SLOTS, sizeof s, hipMemcpyDeviceToHost,
                               ctx->st));

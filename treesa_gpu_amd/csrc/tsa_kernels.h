@@ -16,6 +16,7 @@ struct TsaKParams {
   int par_follow, par_band;
   int helpers;                 // pre-order, one chain per workgroup: waves after the first draw the next sweep's
                                // Philox words and Metropolis thresholds while the first sweeps (0: none)
+  int chain0;                  // k_sweep: the launch sweeps chains chain0 .. nchains - 1 (its grid covers those)
   uint32_t key0, key1;
   TsaModel model;
   float lse[64];               // lse[d] = (float)log2(1 + 2^-d), 0 for d >= 53

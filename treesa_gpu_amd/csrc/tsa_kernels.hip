@@ -565,8 +565,9 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
   }
   __syncthreads();
   // with helper waves the workgroup holds one chain, swept by wave 0; else wave wv holds chain wpb*block + wv
+  // (both counted from P.chain0)
   const bool helped = ORDER == 1 && P.helpers > 0;
-  const int c = helped ? (int)blockIdx.x : (int)blockIdx.x * wpb + wv;
+  const int c = P.chain0 + (helped ? (int)blockIdx.x : (int)blockIdx.x * wpb + wv);
   if (c >= nchains) return;  // whole waves (whole workgroups with helpers); every barrier below is the
                              // helper mode's, reached by all of its waves
   uint64_t* const g = rec + (size_t)c * P.chain_words;
@@ -1194,7 +1195,8 @@ static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64
     *res = nb * wpb;
     return e;
   }
-  const int grid = (nchains + wpb - 1) / wpb;
+  if (P.chain0 < 0 || P.chain0 >= nchains) return hipErrorInvalidValue;
+  const int grid = (nchains - P.chain0 + wpb - 1) / wpb;
   // e0 / e1 (null: none) take the kernel's start and stop times in the dispatch itself
   hipExtLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS, LVL>), dim3(grid), dim3(threads), (uint32_t)smem, st, e0, e1, 0u,
                         P2, rec, leaf, fix, nchains, L.lds_words, beta, sweep0, nsweeps, stats, eo,
