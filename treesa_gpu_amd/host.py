@@ -138,6 +138,15 @@ class Instance:
                                  S.ctypes.data if slicing else None, out.ctypes.data)
         return float(out[0]), int(out[1]), float(out[2]), float(out[3]), int(out[4])
 
+    def greedy_repair(self, lab, S, sc_target):
+        """Final slice repair (csrc/treesa_gpu.cu:1248-1274) of a tree given by its internal label sets lab
+        (nint x W words): while the largest tensor outside S (leaves included) exceeds sc_target, add the label
+        that occurs in most of the largest tensors (lowest id on ties).  S (W words) is updated in place;
+        returns the number of labels added."""
+        lab = np.ascontiguousarray(lab, np.uint64)
+        assert S.dtype == np.uint64 and S.flags.c_contiguous
+        return self.lib.tsh_greedy_repair(self.h, S.shape[-1], lab.ctypes.data, S.ctypes.data, float(sc_target))
+
     def path_cost(self, order):
         """(tc, sc) of the path tree contracting the tensors in `order` left to right."""
         o = np.ascontiguousarray(order, np.int32)
