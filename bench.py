@@ -30,8 +30,14 @@ the algorithmic bytes against 8 TB/s.  The chunk-summary kernel (c5 default) rea
 chunks: achieved = the bytes it loaded (its chunk counters), never the dense per-proposal figure.
 cpu_baseline: the reference's own CPU port (csrc/cpu_ref.h, oracle/_ref/ref_harness) under OpenMP on the host's
 cores (up to 16, the GPU's share of the host), over a bounded sample of the same workload (a subset of the
-chains, every level); the one-core rate beside it.  Slicing runs (c3) time the oracle port (the reference's CPU
-port has no slice moves).
+chains -- half from each end of the population, so that both launches of a split level are sampled -- every
+level); the one-core rate beside it.  Slicing runs (c3) time the oracle port's whole level loop (the reference's
+CPU port has no slice moves).
+parity: the same CPU runs double as the full-size check.  The binary's final population of the whole schedule
+(of the timed run, or of full_schedule when --steps is shorter; written after its timed loop) must equal the
+reference harness's final trees chain by chain -- children words and label sets of every sampled chain, and
+with the whole population sampled the proposal and accept totals -- or, for c3, every word of every record of
+the oracle port's level loop: {"chains": N, "mismatches": 0, ...}.
 full_schedule (when --steps is shorter than the workload's schedule): the whole schedule, once.
 quality: best log2 tc at fixed wall time on random 3-SAT n=100 against the reference's published figure
 (docs/REPORT.md:399-400: population annealing, 576 chains x 200 sweeps per level, tc 66.51 in 2.1 s, sc target
@@ -108,7 +114,9 @@ def score_tc(lc, sc, sc_target, sc_weight=1.0):
     return out
 
 
-def setup(cfgname):
+def setup(cfgname, population=True):
+    """The workload: its config, instance, layout, start trees, initial population (None without population),
+    sweep configuration, betas and order."""
     C = CONFIGS[cfgname]
     inst = host.Instance(os.path.join(DATA, C["inst"] + ".txt"))
     lay = capi.layout(inst.m, inst.nlab)
@@ -116,7 +124,7 @@ def setup(cfgname):
     trees = inst.read_trees(os.path.join(DATA, tf))
     if pick is not None:
         trees = trees[list(pick)]
-    pop = inst.population(lay, trees, C["nchains"], seed=1)
+    pop = inst.population(lay, trees, C["nchains"], seed=1) if population else None
     cfg = capi.make_config(mode="tc", sc_target=C["sc_target"], seed=1)
     betas = linear_betas(C["betas"][0], C["betas"][1], C["levels"])
     order = capi.ORDER_PAR if C["order"] == "par" else capi.ORDER_PREORDER
@@ -222,60 +230,152 @@ def cpu_threads():
     return max(1, min(16, len(os.sched_getaffinity(0))))
 
 
-def cpu_port_worker(cfgname, nsample):
-    """One-thread timing of the oracle port (slice moves included) on nsample chains; prints seconds."""
+def cpu_port_worker(cfgname, nsample, level_loop_out=None):
+    """Timing of the oracle port (slice moves included; threads from OMP_NUM_THREADS) on nsample chains' sweeps;
+    prints seconds.  With level_loop_out: the workload's whole level loop instead (every chain, its population
+    scheme, the oracle's restatement of csrc/treesa_gpu.cu:1756-1877), the final population saved there."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle as orc
     from common import oracle_population
-    C, inst, lay, trees, pop, cfg, betas, order = setup(cfgname)
+    C, inst, lay, trees, pop, cfg, betas, order = setup(cfgname, population=False)
     m, nlab, ixs, iy = orc.read_instance_py(os.path.join(DATA, C["inst"] + ".txt"))
     O = orc.Oracle(m, nlab, ixs, iy)
-    p0 = oracle_population(O, lay, m, nsample, 1, trees)
     ocfg = capi.make_config(mode="tc", sc_target=C["sc_target"], seed=1, slicing=C["slicing"], slice_moves=1)
     P = orc.params_from_config(ocfg, inst.leaf_sc, nlab)
+    if level_loop_out:
+        p0 = oracle_population(O, lay, m, C["nchains"], 1, trees)
+        nlev = len(betas)
+        t0 = time.perf_counter()
+        O.anneal(P, lay, p0, betas, [0] * nlev, [C["niters"]] * nlev, order, scheme=C["scheme"], eval_every=1,
+                 sc_target=C["sc_target"], seed=1)
+        secs = time.perf_counter() - t0
+        np.save(level_loop_out, p0)
+        print(secs)
+        return
+    p0 = oracle_population(O, lay, m, nsample, 1, trees)
     t0 = time.perf_counter()
     for lev, b in enumerate(betas):
         O.sweeps(P, lay, p0, order, b, lev * C["niters"], C["niters"])
     print(time.perf_counter() - t0)
 
 
-def cpu_time(cfgname, C, inst, trees, betas, nsample, threads):
-    """Seconds the CPU port takes for nsample chains over every level on `threads` cores, and its kind."""
+def sample_slots(nchains, n):
+    """Chain slots of a CPU sample of n of nchains chains: all of them, or n/2 from each end of the population
+    (the split sweep launches of a level take chains [0, h) and [h, nchains) with h about nchains / 2), as
+    (first slot, count) ranges."""
+    if n >= nchains:
+        return [(0, nchains)]
+    a = n // 2
+    return [(0, a), (nchains - (n - a), n - a)]
+
+
+def ref_harness_run(C, trees, betas, c0, count, threads):
+    """The reference's CPU port (oracle/_ref/ref_harness) on chain slots c0 .. c0 + count - 1 of the workload over
+    every level: its JSON (per chain: children, label-set hash, proposal and accept counts; sweep seconds)."""
     ref = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
-    if os.path.exists(ref) and not C["slicing"]:
-        with tempfile.TemporaryDirectory() as td:
-            tf = os.path.join(td, "trees.txt")
-            with open(tf, "w") as f:
-                for t in trees:
-                    for w in t:
-                        f.write(f"{int(w) & 0xFFFF} {int(w) >> 16}\n")
-            bs = ",".join(repr(b) for b in betas)
-            args = [ref, "-i", os.path.join(DATA, C["inst"] + ".txt"), "--tree", tf, "--chains", str(nsample),
-                    "--niters", str(C["niters"]), "--betas", bs, "--order", C["order"], "--mode", "tc",
-                    "--sc-target", str(C["sc_target"]), "--seed", "1", "--timing", "--threads", str(threads)]
-            out = json.loads(subprocess.run(args, check=True, capture_output=True, text=True).stdout)
-            return out["seconds"], "reference"
+    with tempfile.TemporaryDirectory() as td:
+        tf = os.path.join(td, "trees.txt")
+        with open(tf, "w") as f:
+            for t in trees:
+                for w in t:
+                    f.write(f"{int(w) & 0xFFFF} {int(w) >> 16}\n")
+        bs = ",".join(repr(b) for b in betas)
+        args = [ref, "-i", os.path.join(DATA, C["inst"] + ".txt"), "--tree", tf, "--chains", str(count),
+                "--chain0", str(c0), "--niters", str(C["niters"]), "--betas", bs, "--order", C["order"], "--mode",
+                "tc", "--sc-target", str(C["sc_target"]), "--seed", "1", "--timing", "--threads", str(threads)]
+        return json.loads(subprocess.run(args, check=True, capture_output=True, text=True).stdout)
+
+
+def port_run(cfgname, nsample, threads, level_loop_out=None):
+    """Seconds of the oracle port in a worker process on `threads` threads (see cpu_port_worker)."""
     env = dict(os.environ, OMP_NUM_THREADS=str(threads))
-    p = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-port-worker", cfgname, "--cpu-chains",
-                        str(nsample)], check=True, capture_output=True, text=True, env=env)
-    return float(p.stdout.strip().splitlines()[-1]), "port"
+    args = [sys.executable, os.path.abspath(__file__), "--cpu-port-worker", cfgname, "--cpu-chains", str(nsample)]
+    if level_loop_out:
+        args += ["--cpu-level-loop-out", level_loop_out]
+    p = subprocess.run(args, check=True, capture_output=True, text=True, env=env)
+    return float(p.stdout.strip().splitlines()[-1])
 
 
-def cpu_baseline(cfgname, C, inst, trees, betas, nsample):
+def load_population(path, nchains, lay):
+    """A population file the binary wrote with --dump-population."""
+    return np.fromfile(path, dtype="<u8").reshape(nchains, lay.chain_words)
+
+
+def parity_of(lay, nlab, pop, ref_chains=None, port_pop=None):
+    """A final population (nchains x chain_words: the binary's --dump-population file) against the CPU runs of
+    the same chains: per chain of the reference harness's output its children and the hash of its label sets
+    (ceil(nlab/64) words per set, as the harness hashes them), or whole records against the oracle port's level
+    loop."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import oracle as orc
+    nchains = pop.shape[0]
+    bad = []
+    if port_pop is not None:
+        bad = [c for c in range(nchains) if not np.array_equal(pop[c], port_pop[c])]
+        return {"chains": nchains, "mismatches": len(bad), "first_mismatches": bad[:8],
+                "compared": "every word of every chain's record (label sets, children, slice set)"}
+    wn = (nlab + 63) // 64
+    for ch in ref_chains:
+        c = ch["chain"]
+        words = np.ascontiguousarray(pop[c, lay.ch_off:]).view(np.uint32)[:lay.nint]
+        got = np.stack([words & 0xFFFF, words >> 16], axis=1).reshape(-1)
+        lab = pop[c, :lay.nint * lay.W].reshape(lay.nint, lay.W)[:, :wn]
+        if not np.array_equal(got, np.array(ch["children"], np.uint32)) or \
+                orc.fnv64_bytes(lab.astype("<u8")) != ch["labels_fnv"]:
+            bad.append(c)
+    return {"chains": len(ref_chains), "mismatches": len(bad), "first_mismatches": bad[:8],
+            "compared": "children words and label sets of every sampled chain"}
+
+
+def cpu_baseline(cfgname, C, inst, lay, trees, betas, nsample, dump=None, gpu=None):
     """The reference's own CPU port (oracle/_ref, csrc/cpu_ref.h) over a sample of the workload's chains and every
     level: under OpenMP on every usable core (up to 16) with nsample chains per core, and on one core with nsample
-    chains; configurations with slice moves (which the reference's CPU port lacks) time the oracle port."""
+    chains.  Its trajectories double as the parity check: with dump (the binary's final population of the same
+    schedule) every sampled chain must equal the reference's.  Configurations with slice moves (which the
+    reference's CPU port lacks) run the oracle port's whole level loop -- every chain, population annealing --
+    and compare every record."""
     threads = cpu_threads()
     per_level = len(betas) * C["niters"] * (inst.m - 1)
-    n_all = min(C["nchains"], nsample * threads)
-    secs, kind = cpu_time(cfgname, C, inst, trees, betas, n_all, threads)
-    secs1, _ = cpu_time(cfgname, C, inst, trees, betas, nsample, 1)
-    return dict(value=n_all * per_level / secs, unit="node visits/s", cores=threads, kind=kind,
-                sample=f"{n_all} chains (chain slots 0..{n_all - 1} of this workload's start) x "
-                       f"{len(betas) * C['niters']} sweeps on {threads} threads: {n_all * per_level:.3e} visits in "
-                       f"{secs:.1f} s",
-                one_core={"value": nsample * per_level / secs1, "sample": f"{nsample} chains, {secs1:.1f} s"},
-                host=host_facts())
+    ref = os.path.join(ROOT, "oracle", "_ref", "ref_harness")
+    parity = None
+    if os.path.exists(ref) and not C["slicing"]:
+        n_all = min(C["nchains"], nsample * threads)
+        ranges = sample_slots(C["nchains"], n_all)
+        outs = [ref_harness_run(C, trees, betas, c0, k, threads) for c0, k in ranges]
+        secs = sum(o["seconds"] for o in outs)
+        kind = "reference"
+        secs1 = ref_harness_run(C, trees, betas, 0, nsample, 1)["seconds"]
+        chains = [ch for o in outs for ch in o["chains"]]
+        if dump:
+            parity = parity_of(lay, inst.nlab, load_population(dump, C["nchains"], lay), ref_chains=chains)
+            if n_all == C["nchains"] and gpu is not None:
+                # the whole population: the proposal and accept counts of every chain add up to the binary's
+                parity["proposals"] = [sum(ch["nprop"] for ch in chains), gpu["proposals"]]
+                parity["accepts"] = [sum(ch["nacc"] for ch in chains), gpu["accepts"]]
+                parity["mismatches"] += (parity["proposals"][0] != parity["proposals"][1]) + \
+                    (parity["accepts"][0] != parity["accepts"][1])
+        where = " and ".join(f"{c0}..{c0 + k - 1}" for c0, k in ranges)
+        sample = (f"{n_all} chains (chain slots {where} of this workload's start) x {len(betas) * C['niters']} "
+                  f"sweeps on {threads} threads: {n_all * per_level:.3e} visits in {secs:.1f} s")
+    else:
+        kind = "port"
+        with tempfile.TemporaryDirectory() as td:
+            out = os.path.join(td, "port_pop.npy")
+            secs = port_run(cfgname, C["nchains"], threads, out if dump else None) if dump else \
+                port_run(cfgname, min(C["nchains"], nsample * threads), threads)
+            n_all = C["nchains"] if dump else min(C["nchains"], nsample * threads)
+            if dump:
+                parity = parity_of(lay, inst.nlab, load_population(dump, C["nchains"], lay), port_pop=np.load(out))
+        secs1 = port_run(cfgname, nsample, 1)
+        sample = (f"{'the whole level loop (every chain, population annealing after every level)' if dump else ''}"
+                  f" {n_all} chains x {len(betas) * C['niters']} sweeps with slice moves on {threads} threads: "
+                  f"{n_all * per_level:.3e} visits in {secs:.1f} s").strip()
+    res = dict(value=n_all * per_level / secs, unit="node visits/s", cores=threads, kind=kind, sample=sample,
+               one_core={"value": nsample * per_level / secs1, "sample": f"{nsample} chains, {secs1:.1f} s"},
+               host=host_facts())
+    if parity is not None:
+        res["parity"] = parity
+    return res
 
 
 def copy_calibration(cfgname, reps=10):
@@ -303,8 +403,9 @@ def kernel_label(desc, order):
     return f"k_sweep {o}, " + ("chain in LDS" if desc.startswith("lds") else "chain in HBM") + loop
 
 
-def run_binary(C, trees, betas, steps, warmup, scheme=None, extra=()):
-    """The drop-in binary's level loop on the workload; returns its JSON result."""
+def run_binary(C, trees, betas, steps, warmup, scheme=None, extra=(), dump=None):
+    """The drop-in binary's level loop on the workload; returns its JSON result.  With dump, the binary also
+    writes the final population there (after its timed loop)."""
     with tempfile.TemporaryDirectory() as td:
         tf = os.path.join(td, "trees.txt")
         with open(tf, "w") as f:
@@ -322,6 +423,8 @@ def run_binary(C, trees, betas, steps, warmup, scheme=None, extra=()):
         if C["slicing"]:
             args += ["--slicing", "--slice-moves", "1", "--slice-every", "1"]
         args += list(extra)
+        if dump:
+            args += ["--dump-population", dump]
         p = subprocess.run(args, capture_output=True, text=True)
         if p.returncode != 0:
             raise RuntimeError(f"treesa_gpu failed ({p.returncode}): {p.stderr[-2000:]}")
@@ -401,6 +504,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-chains", type=int, default=None, help="chains in the CPU sample (default per workload)")
     ap.add_argument("--cpu-port-worker", default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--cpu-level-loop-out", default=None, help=argparse.SUPPRESS)
     ap.add_argument("--scheme", default=None, choices=("indep", "pa", "trunc"),
                     help="population scheme (pa resamples every level: its copy kernel moves a known number of "
                          "bytes, which calibrates the FETCH_SIZE / WRITE_SIZE counters)")
@@ -430,7 +534,7 @@ def main():
         copy_calibration(a.config)
         return
     if a.cpu_port_worker:
-        cpu_port_worker(a.cpu_port_worker, a.cpu_chains or 1)
+        cpu_port_worker(a.cpu_port_worker, a.cpu_chains or 1, a.cpu_level_loop_out)
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         sys.exit("bench.py measures one GPU: chains are independent, and a multi-GPU run would shard them across "
@@ -446,11 +550,16 @@ def main():
         (["--level-launches"] if a.level_launches else []) + (["--level-loop"] if a.level_loop else [])
     visits = steps * C["niters"] * nchains * (inst.m - 1)
 
-    def measure(extra_args):
+    # the final population of one run of the whole schedule, for the parity check of the CPU baseline's leg
+    tmpdir = tempfile.TemporaryDirectory()
+    dump = os.path.join(tmpdir.name, "population.u64") if not a.no_cpu else None
+
+    def measure(extra_args, dump_to=None):
         """a.reps runs of the binary; of the run with the median wall time: its JSON, the sweep kernel's
         algorithmic bytes and mean duration per launch, and the roofline block of that kernel.  The results of
         the runs are identical (same seed); only their timings differ."""
-        runs = [run_binary(C, trees, betas, steps, a.warmup, a.scheme, extra_args) for _ in range(max(1, a.reps))]
+        runs = [run_binary(C, trees, betas, steps, a.warmup, a.scheme, extra_args, dump_to if k == 0 else None)
+                for k in range(max(1, a.reps))]
         assert all(x["tc"] == runs[0]["tc"] and x["tree"] == runs[0]["tree"] for x in runs), "runs disagree"
         runs.sort(key=lambda x: x["t_anneal"])
         r = runs[len(runs) // 2]
@@ -496,7 +605,9 @@ def main():
                         frac=B / dur / 1e9 / HBM_PEAK_GBS)
         return r, roof
 
-    r, roof = measure(extra)
+    full = steps == C["levels"]  # the timed levels are the whole schedule (else they start it)
+    r, roof = measure(extra, dump if full else None)
+    dumped = r if full else None
     wall = r["t_anneal"]
     res = {
         "metric": METRIC, "value": visits / wall, "unit": "node visits/s", "n_gpus": 1, "steps": steps,
@@ -534,7 +645,8 @@ def main():
         # the timed steps are the first levels of the schedule: the whole schedule, once, beside them
         fsteps = C["levels"]
         fv = fsteps * C["niters"] * nchains * (inst.m - 1)
-        fr = run_binary(C, trees, betas, fsteps, a.warmup, a.scheme, extra)
+        fr = run_binary(C, trees, betas, fsteps, a.warmup, a.scheme, extra, dump)
+        dumped = fr
         res["full_schedule"] = {"levels": fsteps, "value": fv / fr["t_anneal"], "ms_per_step": fr["t_anneal"] * 1e3 / fsteps,
                                 "kernel_visits_per_s": fv / fr["kernel_s"], "best_tc": fr["tc"], "best_sc": fr["sc"]}
     if a.config == "c1" and a.steps is None:
@@ -542,7 +654,14 @@ def main():
     if a.config == "c2" and not a.no_quality:
         res["quality"] = quality_at_wall(2.1, res["kernel_visits_per_s"])
     if not a.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(a.config, C, inst, trees, betas, min(a.cpu_chains or C["cpu_chains"], nchains))
+        res["cpu_baseline"] = cpu_baseline(a.config, C, inst, lay, trees, betas,
+                                           min(a.cpu_chains or C["cpu_chains"], nchains),
+                                           dump if dumped is not None else None, dumped)
+        if "parity" in res["cpu_baseline"]:
+            res["parity"] = dict(res["cpu_baseline"]["parity"],
+                                 run=("the timed run" if full else f"the full_schedule run ({C['levels']} levels)"),
+                                 against=res["cpu_baseline"]["kind"])
+    tmpdir.cleanup()
     print(json.dumps(res))
 
 

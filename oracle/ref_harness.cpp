@@ -8,7 +8,9 @@
 // from the topology, an optional fixed random slice set per chain (csrc/treesa_gpu.cu:1621-1627), then
 // runs levels x niters sweeps of ref_par_sweep or ref_optimize_subtree with the global sweep counter
 // lev * niters + it, and prints one JSON object with every chain's final children, a hash of its label
-// sets and its proposal / accept counts.
+// sets and its proposal / accept counts.  --chain0 c0 runs chain slots c0 .. c0 + chains - 1 (a slot fixes
+// the chain's start tree and its random streams), so that any part of a larger population can be sampled.
+#include <algorithm>
 #include <chrono>
 #include <cinttypes>
 #include <cstdio>
@@ -78,7 +80,7 @@ static void rand_tree(int m, uint64_t seed, std::vector<int>& L, std::vector<int
 
 int main(int argc, char** argv) {
   std::string inst, tree, betas = "0.2:0.7:7", order = "par";
-  int chains = 4, niters = 4, mode = 0, random_slices = 0, par_follow = 0, par_band = 0, timing = 0, threads = 1;
+  int chains = 4, chain0 = 0, niters = 4, mode = 0, random_slices = 0, par_follow = 0, par_band = 0, timing = 0, threads = 1;
   bool random_trees = false;
   double sc_target = 24, sc_weight = 1;
   uint64_t seed = 7;
@@ -94,6 +96,7 @@ int main(int argc, char** argv) {
     else if (a == "--tree") tree = nx();
     else if (a == "--random-trees") random_trees = true;
     else if (a == "--chains") chains = std::stoi(nx());
+    else if (a == "--chain0") chain0 = std::stoi(nx());
     else if (a == "--niters") niters = std::stoi(nx());
     else if (a == "--betas") betas = nx();
     else if (a == "--order") order = nx();
@@ -189,8 +192,9 @@ int main(int argc, char** argv) {
   std::vector<RefTree> trees(chains);
   std::vector<long long> nprop(chains, 0), nacc(chains, 0);
 #pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
-  for (int c = 0; c < chains; c++) {
-    RefTree& T = trees[c];
+  for (int k = 0; k < chains; k++) {
+    const int c = chain0 + k;
+    RefTree& T = trees[k];
     T.m = m;
     T.left.assign(2 * m - 1, -1);
     T.right.assign(2 * m - 1, -1);
@@ -203,32 +207,51 @@ int main(int argc, char** argv) {
     T.sliced.assign(nlab, 0);
     if (random_slices > 0) {
       std::mt19937_64 rng(sm64(seed * 7919ULL + c));
-      for (int k = 0; k < random_slices; k++) T.sliced[(int)(rng() % nlab)] = 1;
+      for (int j = 0; j < random_slices; j++) T.sliced[(int)(rng() % nlab)] = 1;
     }
-    // topology labels: occurrence counts bottom-up (internal ids are in post-order, children first)
-    std::vector<std::vector<int>> cnt(2 * m - 1, std::vector<int>(nlab, 0));
+    // topology labels bottom-up (internal ids are in post-order, children first): each node keeps its
+    // subtree's (label, occurrences) pairs, sorted by label, merged from its children's; a label whose every
+    // occurrence lies in the subtree (and that is not open) is dropped, and the node's set is what is left
+    std::vector<std::vector<std::pair<int, int>>> occ(2 * m - 1);
     for (int i = 0; i < m; i++) {
       T.labels[i] = ixs[i];
-      for (int l : ixs[i]) cnt[i][l]++;
+      for (int l : ixs[i]) {
+        if (!occ[i].empty() && occ[i].back().first == l) occ[i].back().second++;
+        else occ[i].push_back({l, 1});
+      }
     }
     std::vector<int> post;
-    std::function<void(int)> walk = [&](int v) {
-      if (v < m) return;
-      walk(T.left[v]);
-      walk(T.right[v]);
+    std::vector<int> stack{2 * m - 2};
+    while (!stack.empty()) {  // reverse of a right-first pre-order = post-order
+      const int v = stack.back();
+      stack.pop_back();
+      if (v < m) continue;
       post.push_back(v);
-    };
-    walk(2 * m - 2);
-    for (int v : post) {
-      for (int l = 0; l < nlab; l++) cnt[v][l] = cnt[T.left[v]][l] + cnt[T.right[v]][l];
-      for (int l = 0; l < nlab; l++)
-        if (cnt[v][l] > 0 && (cnt[v][l] < total[l] || open[l])) T.labels[v].push_back(l);
+      stack.push_back(T.left[v]);
+      stack.push_back(T.right[v]);
     }
+    std::reverse(post.begin(), post.end());
+    for (int v : post) {
+      const auto& a = occ[T.left[v]];
+      const auto& b = occ[T.right[v]];
+      auto& o = occ[v];
+      size_t i = 0, j = 0;
+      while (i < a.size() || j < b.size()) {
+        std::pair<int, int> x;
+        if (j == b.size() || (i < a.size() && a[i].first < b[j].first)) x = a[i++];
+        else if (i == a.size() || b[j].first < a[i].first) x = b[j++];
+        else x = {a[i].first, a[i++].second + b[j++].second};
+        if (x.second < total[x.first] || open[x.first]) o.push_back(x);
+      }
+      for (const auto& x : o) T.labels[v].push_back(x.first);
+    }
+    for (int v = m; v < 2 * m - 1; v++) std::vector<std::pair<int, int>>().swap(occ[v]);
   }
   const auto t0 = std::chrono::steady_clock::now();
 #pragma omp parallel for schedule(dynamic, 1) num_threads(threads)
-  for (int c = 0; c < chains; c++) {
-    RefTree& T = trees[c];
+  for (int k = 0; k < chains; k++) {
+    const int c = chain0 + k;
+    RefTree& T = trees[k];
     long long np = 0, na = 0;
     for (size_t lev = 0; lev < bs.size(); lev++)
       for (int it = 0; it < niters; it++) {
@@ -243,15 +266,15 @@ int main(int argc, char** argv) {
           else ref_optimize_subtree<2>(T, 2 * m - 2, bs[lev], sw, (uint32_t)c, P, np, na);
         }
       }
-    nprop[c] = np;
-    nacc[c] = na;
+    nprop[k] = np;
+    nacc[k] = na;
   }
   const double secs = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
   long long tot_prop = 0;
   printf("{\"chains\": [");
-  for (int c = 0; c < chains; c++) {
-    const RefTree& T = trees[c];
-    tot_prop += nprop[c];
+  for (int k = 0; k < chains; k++) {
+    const RefTree& T = trees[k];
+    tot_prop += nprop[k];
     // FNV-1a over the internal label sets as 64-bit words (W = ceil(nlab / 64)), node by node
     const int W = (nlab + 63) / 64;
     uint64_t h = 1469598103934665603ULL;
@@ -265,7 +288,7 @@ int main(int argc, char** argv) {
         }
     }
     printf("%s{\"chain\": %d, \"nprop\": %lld, \"nacc\": %lld, \"labels_fnv\": \"%016" PRIx64 "\", \"children\": [",
-           c ? ", " : "", c, nprop[c], nacc[c], h);
+           k ? ", " : "", chain0 + k, nprop[k], nacc[k], h);
     for (int v = m; v < 2 * m - 1; v++) printf("%s%d,%d", v > m ? "," : "", T.left[v], T.right[v]);
     printf("]}");
   }

@@ -1088,6 +1088,15 @@ double oracle_score(int mode, int slicing, int select_sc, double sct, double w, 
   const Selector S{slicing, select_sc, sct, w};
   return energy ? S.energy(lc, sc, ns) : S.score(mode, lc, sc, ns);
 }
+// FNV-1a (64-bit) of n bytes: the hash the reference harness prints for a chain's label sets.
+uint64_t oracle_fnv64(const uint8_t* b, size_t n) {
+  uint64_t h = 1469598103934665603ULL;
+  for (size_t i = 0; i < n; i++) {
+    h ^= b[i];
+    h *= 1099511628211ULL;
+  }
+  return h;
+}
 // The pa uniforms of a run: the first n draws of uniform_real_distribution<double>(0, 1) over
 // mt19937_64(splitmix64(seed + 777)) (csrc/treesa_gpu.cu:1786, 1846).
 void oracle_pa_uniforms(uint64_t seed, int n, double* out) {

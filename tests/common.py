@@ -35,12 +35,14 @@ def tree_file(name, init):
     return None
 
 
-def oracle_population(O, lay, m, nchains, seed, trees=None, random_slices=0):
+def oracle_population(O, lay, m, nchains, seed, trees=None, random_slices=0, first=0):
     """Initial records built by the oracle alone: chain c from trees[c % K] or from the Julia random tree
-    seeded splitmix64(seed * 1000003 + c), topology labels, optional fixed random slice sets."""
+    seeded splitmix64(seed * 1000003 + c), topology labels, optional fixed random slice sets; row k is chain
+    slot first + k."""
     pop = np.zeros((nchains, lay.chain_words), np.uint64)
     cache = {}
-    for c in range(nchains):
+    for k_row in range(nchains):
+        c = first + k_row
         if trees is not None and len(trees):
             k = c % len(trees)
             ch = trees[k]
@@ -54,12 +56,12 @@ def oracle_population(O, lay, m, nchains, seed, trees=None, random_slices=0):
                 cache[k] = lab
         else:
             lab = cache[k]
-        pop[c, :lay.nint * lay.W] = lab.reshape(-1)
-        pop[c, lay.ch_off:].view(np.uint32)[:m - 1] = ch
+        pop[k_row, :lay.nint * lay.W] = lab.reshape(-1)
+        pop[k_row, lay.ch_off:].view(np.uint32)[:m - 1] = ch
         if random_slices:
             S = np.zeros(lay.W, np.uint64)
             orc.load().oracle_random_slices(O.nlab, seed, c, random_slices, lay.W, S.ctypes.data)
-            pop[c, lay.s_off:lay.s_off + lay.W] = S
+            pop[k_row, lay.s_off:lay.s_off + lay.W] = S
     return pop
 
 

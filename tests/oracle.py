@@ -87,6 +87,8 @@ def load():
     lib.oracle_score.argtypes = [I, I, I, ctypes.c_double, ctypes.c_double, F, I, I, I]
     lib.oracle_score.restype = ctypes.c_double
     lib.oracle_pa_uniforms.argtypes = [U64, I, P]
+    lib.oracle_fnv64.argtypes = [P, ctypes.c_size_t]
+    lib.oracle_fnv64.restype = U64
     lib.oracle_set_variant.argtypes = [I, U32]
     _lib = lib
     return lib
@@ -285,3 +287,9 @@ def pa_uniforms(seed, n):
 def set_variant(v, noise_seed=0):
     """Rounding variant of the oracle's float lse (0: the reference's arithmetic; see oracle_set_variant)."""
     load().oracle_set_variant(int(v), int(noise_seed))
+
+
+def fnv64_bytes(a):
+    """FNV-1a of an array's bytes, as the reference harness hashes a chain's label sets (hex string)."""
+    a = np.ascontiguousarray(a)
+    return "%016x" % load().oracle_fnv64(a.ctypes.data, a.nbytes)

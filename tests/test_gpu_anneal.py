@@ -7,7 +7,9 @@ order, so the means agree to the last bit) and the best chain, level, score and 
 cases cover both sweep orders, pre-order with and without helper waves, one group of 256 chains and several
 with a ragged last one, every energy mode, slicing, the sc-first selection, sparse evaluation, a schedule
 split over two calls, the one-launch loop forced on more chains than are resident at once, and the per-level
-launches tsa_anneal runs itself (too many chains, a session begun with tsa_track, the wide path).  That the
+launches tsa_anneal runs itself (too many chains, a session begun with tsa_track, the wide path).  The per-level
+launches of the headline workload (8192 chains, the sweep of each level split over two streams) are compared
+with the oracle's level loop directly.  That the
 selection itself is the reference's is covered by the level-loop tests, which run the binary (whose indep loop
 is this launch) against the oracle's level loop.
 """
@@ -229,3 +231,36 @@ def test_async_download_keeps_the_record_of_its_point_in_the_stream():
         lib.tsa_host_free(buf)
     assert np.array_equal(got, ref)
     assert not np.array_equal(after, ref)  # the later sweeps moved the chain
+
+
+def test_split_sweeps_match_oracle_level_loop():
+    """The headline path as the benchmark runs it: 8192 chains of sat100 from the multi-tree starts with every
+    level evaluated, so each level's node costs are folded and the chains selected on a second stream beside the
+    next level's sweep, and each level's sweep runs as two launches on two streams (chains [0, h) and
+    [h, 8192)).  The records of all 8192 chains (both halves), every trace row and the best chain and tree equal
+    the oracle's level loop (the reference's run_anneal with scheme indep, csrc/treesa_gpu.cu:1788-1832)."""
+    s = Setup("sat100", "par", "tc", 8192, init="multi")
+    s.cfg.fused_energy = 1  # as the binary sets it when every level is evaluated
+    nlev = 6
+    betas, niters, ev = schedule(nlev, 1, 1, b0=1.0, b1=3.0)
+    a = s.per_level(betas, niters, ev)
+    assert "fold=apart" in a["desc"] and f"split_levels={nlev}" in a["desc"], a["desc"]
+    m, nlab, ixs, iy = common.load_instance("sat100")
+    O = orc.Oracle(m, nlab, ixs, iy)
+    P = orc.params_from_config(s.cfg, s.leaf_sc, nlab)
+    pop = s.pop0.copy()
+    print("[oracle] level loop, 8192 chains", flush=True)
+    r = O.anneal(P, s.lay, pop, [float(b) for b in betas], [0] * nlev, niters, capi.ORDER_PAR, scheme="indep",
+                 eval_every=1, sc_target=common.CHECK_SC_TARGET, seed=3)
+    bad = [c for c in range(s.nchains) if not np.array_equal(a["pop"][c], pop[c])]
+    assert not bad, f"{len(bad)} chains differ from the oracle (first {bad[:5]}, split at {s.nchains // 2})"
+    chain, level, score, rec, rows, _, _ = a["best"]
+    for lev in range(nlev):
+        o, g = r["levels"][lev], rows[lev]
+        assert int(g["chain"]) == int(o["best"]), lev
+        assert g["lc"].tobytes() == np.float32(o["lc"]).tobytes(), lev
+        assert (int(g["sc"]), int(g["ns"])) == (int(o["sc"]), int(o["ns"])), lev
+        assert float(g["score"]) == float(o["score"]), lev
+    assert chain == r["best_chain"]
+    span = slice(s.lay.ch_off, s.lay.s_off + s.lay.W)
+    assert np.array_equal(rec[span], r["best_rec"][span]), "best tree"

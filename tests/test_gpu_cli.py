@@ -65,6 +65,7 @@ def test_overlapped_selection(nchains, order, tmp_path):
             str(nchains), "--niters", "1", "--betas", "1:0.5:15", "--sc-target", "20", "--order", order, "--seed", "2"]
     a = run(args, tmp_path, "a.json")
     assert ("fold=apart" in a["hip_kernel"]) == (nchains == 8192), a["hip_kernel"]
+    assert ("split_levels=" in a["hip_kernel"]) == (nchains == 8192), a["hip_kernel"]
     # with the fold apart each level's sweep is two launches on two streams; the kernel time is the union of
     # their intervals, so it stays within the loop's wall time
     assert 0.0 < a["kernel_s"] <= a["t_anneal"], (a["kernel_s"], a["t_anneal"])

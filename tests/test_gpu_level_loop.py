@@ -10,8 +10,10 @@ population step; then the final tree, slice set, repair and host-energy tc / sc 
 
 Cases: pa and trunc (tc mode), two-stage tc+gpu / tc+h100, the float modes with pa, select-sc, the tc-mode
 penalty branch of the score with host-side selection, slicing with pa and the final repair, --max-slices,
---init-slices, --eval-every, and the sat70 slicing workload with population annealing after every
-10-sweep level (2048 x 200 in the benchmark; here 64 chains over all 20 levels).
+--init-slices, --eval-every, the sat70 slicing workload with population annealing after every 10-sweep level
+(2048 x 200 in the benchmark; here 64 chains over all 20 levels), and sat70 with a slice limit and a target the
+anneal cannot reach, so that the final repair adds many labels.  The final tc (tc_exact, the JSON's
+full-precision key) must equal the oracle's within 1e-9.
 """
 import json
 import math
@@ -44,7 +46,7 @@ def f32(xs):
 class Case:
     def __init__(self, name, inst, init="greedy", nchains=64, niters=4, betas=None, scheme="pa", mode="tc",
                  stage2=None, sc_target=30.0, sc_weight=1.0, seed=1, slicing=False, max_slices=0, init_slices=None,
-                 eval_every=1, select_sc=False, host_select=False, order="par", max_levels=None):
+                 eval_every=1, select_sc=False, host_select=False, order="par", max_levels=None, min_repair=0):
         self.__dict__.update(locals())
         del self.__dict__["self"]
         self.betas = betas if betas is not None else julia_betas()
@@ -71,6 +73,10 @@ CASES = [
     Case("sat40-pa-eval3", "sat40", nchains=64, eval_every=3, max_levels=150),
     Case("c3-sat70-slicing-pa", "sat70", nchains=64, niters=10, betas=linear_betas(0.01, 15.0, 20), sc_target=24.0,
          slicing=True),
+    # at most 4 slices during the anneal and a target the annealed tree does not reach: the final greedy repair
+    # (csrc/treesa_gpu.cu:1248-1274) adds dozens of labels
+    Case("sat70-slicing-repair", "sat70", nchains=64, niters=3, sc_target=18.0, slicing=True, max_slices=4,
+         max_levels=40, min_repair=3),
 ]
 
 
@@ -186,17 +192,17 @@ def test_level_loop_matches_oracle(c, tmp_path):
     assert res["nresample"] == r["nresample"]
     assert res["total_sweeps"] == r["total_sweeps"]
     assert res["valid"] and res["labels_ok"]
-    assert abs(res["tc"] - r["tc"]) < 5e-6 and res["sc"] == r["sc"]
+    assert abs(res["tc_exact"] - r["tc"]) <= 1e-9 and res["sc"] == r["sc"]
     if c.slicing:
         S = r["final"][lay.s_off:lay.s_off + lay.W]
         sliced = [l for l in range(r["nlab"]) if int(S[l >> 6]) >> (l & 63) & 1]
         assert res["sliced"] == sliced and res["nsliced"] == r["ns"] == len(sliced)
-        assert res["n_repair"] == r["n_repair"]
+        assert res["n_repair"] == r["n_repair"] >= c.min_repair
         if c.max_slices:
             assert all(b["ns"] <= c.max_slices for b in blev)
     if c.stage2:
         assert r["staged"]
-        assert abs(res["stage1_tc"] - r["h1"][0]) < 5e-6 and res["stage1_sc"] == int(r["h1"][1])
+        assert abs(res["stage1_tc_exact"] - r["h1"][0]) <= 1e-9 and res["stage1_sc"] == int(r["h1"][1])
     print("[ok]", c.name, f"tc {res['tc']:.4f} sc {res['sc']} |S| {res['nsliced']} resampled {res['nresample']}",
           flush=True)
 

@@ -3,7 +3,8 @@
 The population, the leaf table and the outputs live in device memory this test allocates through the HIP
 runtime itself; the library call allocates nothing and keeps its working memory in one static device buffer.
 Two calls in a row on the same buffer, the second smaller and in another order and energy mode, must equal a
-context's results bit for bit: every record, every chain's lc / sc / |S| and the seven counters.  A call whose
+context's results bit for bit: every record, every chain's lc / sc / |S| and the seven counters; a third call,
+a repeat of the second, leaves the device's free memory unchanged (hipMemGetInfo).  A call whose
 chains would need more than the static buffer is refused on the host, before anything reaches the device.
 """
 import ctypes
@@ -28,7 +29,14 @@ def hip():
         _hip.hipFree.argtypes = [ctypes.c_void_p]
         _hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
         _hip.hipDeviceSynchronize.argtypes = []
+        _hip.hipMemGetInfo.argtypes = [ctypes.POINTER(ctypes.c_size_t), ctypes.POINTER(ctypes.c_size_t)]
     return _hip
+
+
+def free_bytes():
+    free, total = ctypes.c_size_t(), ctypes.c_size_t()
+    assert hip().hipMemGetInfo(ctypes.byref(free), ctypes.byref(total)) == 0
+    return free.value
 
 
 H2D, D2H = 1, 2
@@ -76,7 +84,9 @@ def with_context(lay, leaf, lsc, cfg, pop, order, beta, sweep0, nsweeps):
         return ctx.download(), lc, sc, ns, ctx.stats()
 
 
-def without_allocation(lay, leaf, lsc, cfg, pop, order, beta, sweep0, nsweeps, bufs):
+def without_allocation(lay, leaf, lsc, cfg, pop, order, beta, sweep0, nsweeps, bufs, mem=None):
+    """The same through tsa_sweeps_noalloc on device buffers made here; with mem (a list), the device's free
+    bytes just before the call and after it has finished are appended to it."""
     n = pop.shape[0]
     d_leaf = DeviceArray(leaf)
     d_pop = DeviceArray(pop)
@@ -85,9 +95,14 @@ def without_allocation(lay, leaf, lsc, cfg, pop, order, beta, sweep0, nsweeps, b
                       DeviceArray(shape=n, dtype=np.int32), DeviceArray(shape=7, dtype=np.uint64))
     bufs += [lc, sc, ns, st]
     print(f"[noalloc] {n} chains, order {order}, mode {cfg.mode}", flush=True)
+    assert hip().hipDeviceSynchronize() == 0
+    if mem is not None:
+        mem.append(free_bytes())
     capi.sweeps_noalloc(lay, cfg, lsc, d_leaf.ptr.value, d_pop.ptr.value, n, order, beta, sweep0, nsweeps,
                         lc.ptr.value, sc.ptr.value, ns.ptr.value, st.ptr.value, None)
     assert hip().hipDeviceSynchronize() == 0
+    if mem is not None:
+        mem.append(free_bytes())
     return d_pop.get(), lc.get(), sc.get(), ns.get(), [int(x) for x in st.get()]
 
 
@@ -111,6 +126,14 @@ def test_noalloc_equals_context_on_two_calls():
         for k, what in enumerate(("records", "lc", "sc", "ns")):
             assert np.array_equal(got2[k], want2[k]), what
         assert got2[4] == want2[4]
+        # call 3 repeats call 2 on fresh buffers: the device's free memory is the same before and after it (the
+        # library's one-time set-up -- code objects, the symbol lookup -- happened in the calls before)
+        mem = []
+        got3 = without_allocation(lay2, leaf2, lsc2, cfg2, pop2, capi.ORDER_PREORDER, 2.0, 11, 2, bufs, mem)
+        assert mem[0] == mem[1], f"free device memory {mem[0]} before the call, {mem[1]} after"
+        for k, what in enumerate(("records", "lc", "sc", "ns")):
+            assert np.array_equal(got3[k], want2[k]), what
+        assert got3[4] == want2[4]
     finally:
         for b in bufs:
             b.free()

@@ -88,6 +88,7 @@ struct tsa_ctx {
   hipEvent_t ev_b[2] = {nullptr, nullptr};
   bool split_slot[2] = {false, false};
   bool split_pending = false;  // st3 holds work st is not yet ordered after
+  long long split_levels = 0;  // sweep calls run as two launches (reported by tsa_describe)
   hipEvent_t ev_sweep[2] = {nullptr, nullptr};  // (the stop events of those sweeps' timing pairs)
   hipEvent_t ev_track[2] = {nullptr, nullptr};
   bool track_pending[2] = {false, false};
@@ -265,6 +266,10 @@ static bool valid_tree(const uint32_t* ch, int m, std::vector<char>& seen, std::
 // ---------------------------------------------------------------------------------------------------
 static void free_ctx(tsa_ctx* c) {
   if (!c) return;
+  // every stream of the context drained before any of its buffers is released: the split sweep on st3 and the
+  // fold and selection on st2 read and write the records, the snapshots and the counters
+  for (hipStream_t s : {c->st, c->st3, c->st2})
+    if (s) (void)hipStreamSynchronize(s);
   if (c->d_rec) (void)hipFree(c->d_rec);
   if (c->d_rec2) (void)hipFree(c->d_rec2);
   if (c->d_leaf) (void)hipFree(c->d_leaf);
@@ -284,14 +289,12 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_leafsum) (void)hipFree(c->d_leafsum);
   if (c->d_tpart) (void)hipFree(c->d_tpart);
   if (c->d_tdone) (void)hipFree(c->d_tdone);
-  if (c->st3) (void)hipStreamSynchronize(c->st3);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   if (c->st3) {
     for (hipEvent_t e : {c->ev_fork, c->ev_join, c->ev_b[0], c->ev_b[1]})
       if (e) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(c->st3);
   }
-  if (c->st2) (void)hipStreamSynchronize(c->st2);
   for (int k = 0; k < 2; k++) {
     if (c->ev_track[k]) (void)hipEventDestroy(c->ev_track[k]);
     if (c->d_snap_ch[k]) (void)hipFree(c->d_snap_ch[k]);
@@ -839,6 +842,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
       if (markers) TSA_HIP(ctx, hipEventRecord(f1, ctx->st3));
       TSA_HIP(ctx, hipEventRecord(ctx->ev_b[s], ctx->st3));
       ctx->split_pending = true;
+      ctx->split_levels++;
       ctx->npending++;  // (the first launch's pair is counted below)
     } else {
       if (markers) TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
@@ -1286,15 +1290,16 @@ extern "C" int tsa_chunk_stats(tsa_ctx* ctx, uint64_t out[2]) {
 
 extern "C" int tsa_describe(tsa_ctx* ctx, char* buf, int32_t len) {
   if (!ctx || !buf || len < 1) return fail(ctx, TSA_ERR_ARG, "tsa_describe: null argument");
-  snprintf(buf, (size_t)len, "%s%s", ctx->kname.c_str(),
+  char sp[48] = "";
+  if (ctx->split_levels > 0) snprintf(sp, sizeof sp, " split_levels=%lld", ctx->split_levels);
+  snprintf(buf, (size_t)len, "%s%s%s", ctx->kname.c_str(), sp,
            ctx->lv_used < 0 ? "" : (ctx->lv_used ? " anneal=level_loop" : " anneal=level_launches"));
   return TSA_OK;
 }
 
 extern "C" int tsa_destroy(tsa_ctx* ctx) {
   if (!ctx) return TSA_OK;
-  if (ctx->st) (void)hipStreamSynchronize(ctx->st);
-  free_ctx(ctx);
+  free_ctx(ctx);  // (waits for every stream of the context first)
   return TSA_OK;
 }
 

@@ -119,6 +119,11 @@ class Json {
     if (std::isfinite(v)) put(k, "%.6e", v);
     else raw(k, "null");
   }
+  // a double that reads back to the same bits (%.17g), non-finite values as null
+  void exact(const char* k, double v) {
+    if (std::isfinite(v)) put(k, "%.17g", v);
+    else raw(k, "null");
+  }
   void integer(const char* k, long long v) { put(k, "%lld", v); }
   void boolean(const char* k, bool v) { raw(k, v ? "true" : "false"); }
   void text(const char* k, const std::string& v) { raw(k, "\"" + v + "\""); }
@@ -138,6 +143,12 @@ class Json {
   std::string out_;
   bool first_ = true;
 };
+
+// The integer after `key` in a kernel description (tsa_describe), or dflt.
+int desc_int(const std::string& desc, const char* key, int dflt) {
+  const size_t p = desc.find(key);
+  return p == std::string::npos ? dflt : atoi(desc.c_str() + p + strlen(key));
+}
 
 // Widths as the reference reports them (32-bit words): its register template width (0 on the wide path) and
 // its words per label set (csrc/treesa_gpu.cu:1439, 2078-2085).
@@ -592,6 +603,17 @@ int Run::anneal() {
   const int best_chain = on_device ? loop_on_device(best, t0) : loop_on_host(best, t0, h1, staged, nresample);
   const double t_anneal = wall_seconds() - t0;
   if (level_log_) fclose(level_log_);
+  if (!O_.dump_population.empty()) {
+    // the final population as the level loop left it (nchains records of chain_words words, in chain order)
+    std::vector<uint64_t> all((size_t)O_.nchains * lay_.chain_words);
+    dev_->ok(tsa_download(c, 0, O_.nchains, all.data()));
+    FILE* f = fopen(O_.dump_population.c_str(), "wb");
+    if (!f || fwrite(all.data(), 8, all.size(), f) != all.size()) {
+      if (f) fclose(f);
+      throw InputError("cannot write " + O_.dump_population);
+    }
+    fclose(f);
+  }
   uint32_t total_sweeps = 0;
   for (const Level& L : sched_) total_sweeps += (uint32_t)L.niters;
   uint64_t st[7], chunks[2];
@@ -641,6 +663,7 @@ int Run::anneal() {
 
   Json j;
   j.fixed6("tc", HE.tc);
+  j.exact("tc_exact", HE.tc);
   j.integer("sc", HE.sc);
   j.sci6("gpu_time", HE.time);
   j.sci6("h100_time", HE.time2);
@@ -660,13 +683,21 @@ int Run::anneal() {
   static const char* counter_keys[7] = {"proposals",       "accepts",       "warp_steps", "node_visits",
                                         "slice_proposals", "slice_accepts", "busy_lanes"};
   for (int k = 0; k < 7; k++) j.integer(counter_keys[k], (long long)st[k]);
-  j.integer("coop_max", 1);
-  j.integer("coop_min", 1);
-  j.integer("coop_full", 1);
+  // the visit mapping in the reference's terms: lanes per proposal (coop_*), waves per chain (wpc) and the
+  // proposals one round of a chain's waves holds (lpc: 64 on the one-wave kernels, waves x 64 / G on the wide
+  // kernel).  warp_steps counts what the reference's kernels count (csrc/treesa_gpu.cu:716, 990): rounds of
+  // up to lpc visits in pre-order, phases in par order; so node_visits / (lpc * warp_steps) is the lane
+  // occupancy of a pre-order sweep and the visits per phase and visit slot of a par sweep, as there
+  // (bench/throughput.py:68).
+  const int G = desc_int(desc, " G=", 1);
+  const int wpc = desc.compare(0, 5, "wide ") == 0 ? desc_int(desc, " waves/block=", 1) * desc_int(desc, " blocks/chain=", 1) : 1;
+  j.integer("coop_max", G);
+  j.integer("coop_min", G);
+  j.integer("coop_full", G);
   j.integer("par_follow", O_.par_follow);
   j.integer("par_band", O_.par_band);
   j.integer("nsum", nsum);
-  j.integer("wpc", 1);
+  j.integer("wpc", wpc);
   j.text("order", order_ == TSA_ORDER_PAR ? "par" : "preorder");
   j.integer("nchains", O_.nchains);
   j.integer("niters", O_.niters);
@@ -676,7 +707,7 @@ int Run::anneal() {
   j.integer("nw", nw32);
   j.integer("W64", lay_.W);
   j.integer("word_bits", 64);
-  j.integer("lpc", 64);
+  j.integer("lpc", wpc * 64 / G);
   j.text("kernel", kernel_label());
   j.text("hip_kernel", desc);
   j.text("scheme", O_.scheme);
@@ -697,6 +728,7 @@ int Run::anneal() {
   }
   if (staged) {
     j.fixed6("stage1_tc", h1.tc);
+    j.exact("stage1_tc_exact", h1.tc);
     j.integer("stage1_sc", h1.sc);
     j.integer("stage1_nsliced", h1.ns);
     j.sci6("stage1_gpu_time", h1.time);

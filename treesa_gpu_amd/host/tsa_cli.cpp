@@ -146,6 +146,9 @@ const std::vector<Flag>& flags() {
       {"--no-cross", nullptr, "--check: skip the comparison with the other kernel mapping", SWITCH(cross, false)},
       {"--quiet", nullptr, "no progress on stderr", SWITCH(quiet, true)},
       {"--bench-warmup", "W", "W untimed levels first, then the start population again", INT_FIELD(bench_warmup)},
+      {"--dump-population", "FILE",
+       "after the level loop (outside its timing), every chain's record as raw little-endian 64-bit words",
+       TEXT_FIELD(dump_population)},
       {"--host-select", nullptr, "select on the host at every level, also for --scheme indep",
        SWITCH(host_select, true)},
       {"--no-overlap", nullptr, "device-side selection on the sweep's stream", SWITCH(no_overlap, true)},

@@ -46,7 +46,7 @@ struct Options {
   // diagnostics of this build
   bool quiet = false, host_select = false, no_overlap = false, level_launches = false, level_loop = false;
   int bench_warmup = 0;
-  std::string level_log;
+  std::string level_log, dump_population;
 };
 
 // Parses argv; throws UsageError on an unknown flag, a missing or malformed value, or no -i.
