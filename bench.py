@@ -41,9 +41,10 @@ the oracle port's level loop: {"chains": N, "mismatches": 0, ...}.
 full_schedule (when --steps is shorter than the workload's schedule): the whole schedule, once.
 quality: best log2 tc at fixed wall time on random 3-SAT n=100 against the reference's published figure
 (docs/REPORT.md:399-400: population annealing, 576 chains x 200 sweeps per level, tc 66.51 in 2.1 s, sc target
-30, Quadro RTX 6000): the same instance, start tree (its omeco greedy tree), schedule (0.01:0.05:15, 300 levels)
-and sc target, 8192 chains with as many sweeps per level as fit in 2.1 s of end-to-end wall time (the binary's
-whole process, as the reference's figure includes its process start and I/O).
+30, Quadro RTX 6000, one run): the same instance, start tree (its omeco greedy tree), schedule (0.01:0.05:15, 300
+levels) and sc target, as mean +- sd over 5 seeds of 1152 chains with as many sweeps per level as fit in 2.1 s
+of end-to-end wall time (the binary's whole process, as the reference's figure includes its process start and
+I/O), and of the reference's own 576 x 200 configuration on this GPU.
 long_variant (c1 and c5, whose literal runs are 1.1e7 and 5.9e6 node visits): the same workload with its schedule
 repeated ten times, so that the level loop's fixed costs are spread over more levels; reported beside value.
 reference_workload (c1): the reference's own sweep-rate benchmark (bench/throughput.py:21-37: sat100, its greedy
@@ -403,7 +404,7 @@ def kernel_label(desc, order):
     return f"k_sweep {o}, " + ("chain in LDS" if desc.startswith("lds") else "chain in HBM") + loop
 
 
-def run_binary(C, trees, betas, steps, warmup, scheme=None, extra=(), dump=None):
+def run_binary(C, trees, betas, steps, warmup, scheme=None, extra=(), dump=None, seed=1):
     """The drop-in binary's level loop on the workload; returns its JSON result.  With dump, the binary also
     writes the final population there (after its timed loop)."""
     with tempfile.TemporaryDirectory() as td:
@@ -419,7 +420,7 @@ def run_binary(C, trees, betas, steps, warmup, scheme=None, extra=(), dump=None)
         args = [capi.BIN_PATH, "-i", os.path.join(DATA, C["inst"] + ".txt"), "--tree", tf, "--betas", "file:" + bf,
                 "--nchains", str(C["nchains"]), "--niters", str(C["niters"]), "--sc-target", str(C["sc_target"]),
                 "--mode", "tc", "--order", C["order"], "--kernel", "auto", "--scheme", scheme or C["scheme"],
-                "--seed", "1", "--eval-every", "1", "--bench-warmup", str(warmup), "--out", out, "--quiet"]
+                "--seed", str(seed), "--eval-every", "1", "--bench-warmup", str(warmup), "--out", out, "--quiet"]
         if C["slicing"]:
             args += ["--slicing", "--slice-moves", "1", "--slice-every", "1"]
         args += list(extra)
@@ -454,42 +455,63 @@ def reference_workload():
     return out
 
 
-def quality_at_wall(budget_s, visits_per_s):
+def quality_at_wall(budget_s, visits_per_s, seeds=(1, 2, 3, 4, 5)):
     """Best log2 tc reached within budget_s of end-to-end wall time on random 3-SAT n=100 (population annealing,
-    sc target 30, the omeco greedy start, the 300-level schedule 0.01:0.05:15), with 2304 chains and as many
-    sweeps per level as fit (measured on MI355X: 576 to 8192 chains all end within 66.7-67.5 at this budget;
-    2304 fills the GPU with the most sweeps per chain); the reference's published figure beside it."""
+    sc target 30, the omeco greedy start, the 300-level schedule 0.01:0.05:15), as a statistic over seeds:
+    * chosen: 1152 chains with as many sweeps per level as fit in the budget (calibrated on the first seed,
+      then every seed at that count).  Measured on MI355X over 5 seeds each at this budget: 1152 chains
+      66.87 +- 0.35, 2304 chains 67.04 +- 0.33, 576 chains 67.03 +- 0.59, 4608 chains 67.35 +- 0.17,
+      truncation 67.46 +- 0.49, independent chains 67.57 +- 0.17;
+    * reference_config: the reference's own configuration (576 chains x 200 sweeps per level) on this GPU;
+    beside them the reference's single published run (docs/REPORT.md:399-400)."""
     inst = host.Instance(os.path.join(DATA, "sat100.txt"))
-    nchains, nlev = 2304, 300
+    nlev = 300
     betas = [float(np.float32(0.01 + i * 0.05)) for i in range(nlev)]
-    C = dict(inst="sat100", nchains=nchains, niters=1, sc_target=30.0, order="par", scheme="pa", slicing=False)
     trees = inst.read_trees(os.path.join(DATA, "sat100.tree"))
-    # sweeps per level from the measured sweep rate, leaving about 0.5 s for the process, the device set-up and
-    # the population steps; then up to three corrections towards 90-100 % of the budget
-    niters = max(1, int((budget_s - 0.5) * visits_per_s / (nchains * nlev * (inst.m - 1))))
-    tries, best = [], None
-    for _ in range(4):
-        C["niters"] = niters
+
+    def one(nchains, niters, seed):
+        C = dict(inst="sat100", nchains=nchains, niters=niters, sc_target=30.0, order="par", scheme="pa",
+                 slicing=False)
         t0 = time.perf_counter()
-        r = run_binary(C, trees, betas, nlev, 0, "pa")
+        r = run_binary(C, trees, betas, nlev, 0, "pa", seed=seed)
         wall = time.perf_counter() - t0
-        tries.append({"niters": niters, "wall_s": round(wall, 4), "tc": r["tc"], "sc": r["sc"]})
-        if wall <= budget_s and (best is None or niters > best[0]):
-            best = (niters, wall, r)
-        if 0.9 * budget_s <= wall <= budget_s:
+        return {"seed": seed, "niters": niters, "wall_s": round(wall, 4), "tc": r["tc"], "sc": r["sc"]}
+
+    def stats(runs):
+        tcs = [x["tc"] for x in runs]
+        mean = sum(tcs) / len(tcs)
+        sd = (sum((t - mean) ** 2 for t in tcs) / (len(tcs) - 1)) ** 0.5 if len(tcs) > 1 else 0.0
+        return {"tc_mean": mean, "tc_sd": sd, "tc_min": min(tcs), "tc_max": max(tcs), "seeds": len(tcs),
+                "wall_max_s": max(x["wall_s"] for x in runs),
+                "within_budget": all(x["wall_s"] <= budget_s for x in runs), "runs": runs}
+
+    nchains = 1152
+    # sweeps per level from the measured sweep rate, leaving about 0.5 s for the process, the device set-up and
+    # the population steps; then up to three corrections towards 90-97 % of the budget
+    niters = max(1, int((budget_s - 0.5) * visits_per_s / (nchains * nlev * (inst.m - 1))))
+    tries = []
+    for _ in range(4):
+        t = one(nchains, niters, seeds[0])
+        tries.append(t)
+        if 0.9 * budget_s <= t["wall_s"] <= 0.97 * budget_s:
             break
-        niters = max(1, int(niters * 0.95 * budget_s / wall))
-        if any(t["niters"] == niters for t in tries):
+        nxt = max(1, int(niters * 0.94 * budget_s / t["wall_s"]))
+        if nxt == niters or any(x["niters"] == nxt for x in tries):
             break
-    if best is None:
-        best = (niters, wall, r)
-    niters, wall, r = best
+        niters = nxt
+    fits = [x for x in tries if x["wall_s"] <= budget_s]
+    niters = max(x["niters"] for x in fits) if fits else min(x["niters"] for x in tries)
+    chosen = [next(x for x in tries if x["niters"] == niters)] + [one(nchains, niters, sd) for sd in seeds[1:]]
+    refcfg = [one(576, 200, sd) for sd in seeds]
     return {"metric": "best log2 tc at fixed wall time", "instance": "random 3-SAT n=100 (sat100.txt)",
-            "budget_s": budget_s, "wall_s": wall, "within_budget": wall <= budget_s, "tc": r["tc"], "sc": r["sc"],
-            "config": f"population annealing, {nchains} chains x {niters} sweeps per level, 300 levels "
-                      f"0.01:0.05:15, sc target 30, omeco greedy start, seed 1 (end-to-end wall of the binary)",
-            "tries": tries,
-            "reference": {"tc": 66.51, "sc": 62, "wall_s": 2.1, "hardware": "Quadro RTX 6000",
+            "budget_s": budget_s,
+            "chosen": dict(stats(chosen), config=f"population annealing, {nchains} chains x {niters} sweeps per "
+                           "level, 300 levels 0.01:0.05:15, sc target 30, omeco greedy start (end-to-end wall of "
+                           "the binary)", calibration=tries),
+            "reference_config": dict(stats(refcfg), config="the reference's configuration on this GPU: population "
+                                     "annealing, 576 chains x 200 sweeps per level, same schedule, sc target and "
+                                     "start"),
+            "reference": {"tc": 66.51, "sc": 62, "wall_s": 2.1, "hardware": "Quadro RTX 6000", "seeds": 1,
                           "config": "population annealing, 576 chains x 200 sweeps per level, same schedule, "
                                     "sc target and start", "source": "docs/REPORT.md:399-400"}}
 
