@@ -521,7 +521,7 @@ __device__ __forceinline__ TsaOwn tsa_level_wave(const TsaKParams& P, const TsaL
 // while wave 0 sweeps on: the fold of the node costs and sizes the workgroup left in cost / z (S: a copy of
 // the slice set as it was then), then the chain's arrival.  Returns the chain's best.
 template <int W>
-__device__ __noinline__ TsaOwn tsa_level_fold_arrive(const TsaKParams& P, const TsaLevels& Lv, const float* cost,
+__device__ __forceinline__ TsaOwn tsa_level_fold_arrive(const TsaKParams& P, const TsaLevels& Lv, const float* cost,
                                                      const uint16_t* z, const uint64_t* S, const uint64_t* lf,
                                                      TsaMathTabs T, int n, int c, int ev, int level, TsaOwn o,
                                                      int cslot, int lane) {
@@ -537,7 +537,7 @@ __device__ __noinline__ TsaOwn tsa_level_fold_arrive(const TsaKParams& P, const 
 // [band words u32 x nint4 when par_band > 0].
 // (The par level loop in tc mode keeps three waves per SIMD, as many as the chains' LDS allows: its level
 // functions' registers would otherwise take one of them; the float modes need more registers than that.)
-template <int W, int MODE, int ORDER, bool LDS, bool LVL>
+template <int W, int MODE, int ORDER, bool LDS, bool LVL, bool SLICE>
 __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1) k_sweep(TsaKParams P, uint64_t* __restrict__ rec,
                                                const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
                                                int nchains, int lds_words, float beta1, uint32_t sweep0, int nsweeps,
@@ -598,7 +598,8 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
   uint64_t* const lab = base;
   uint32_t* const ch = reinterpret_cast<uint32_t*>(base + P.ch_off);
   uint64_t* const S = base + P.s_off;
-  const uint64_t* const Sm = P.slicing ? S : nullptr;
+  const bool slicing = SLICE && P.slicing;  // (launched with SLICE only when P.slicing is set)
+  const uint64_t* const Sm = slicing ? S : nullptr;
   uint16_t* const pri = nodes;
   uint16_t* const par = nodes + nint4;
   uint16_t* const wl = par + nint4;
@@ -735,7 +736,7 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
             const int v = wl[j];
             const bool rev = (pri[v - m] & 1u) == 0;  // a follow-up visit draws its own numbers
             const uint32_t swv = sw | (rev ? 0x80000000u : 0u);
-            const TsaVisit o = P.slicing
+            const TsaVisit o = slicing
                                    ? tsa_visit<W, MODE, true, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, swv, (uint32_t)c)
                                    : tsa_visit<W, MODE, false, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, swv, (uint32_t)c);
             nv++;
@@ -756,9 +757,11 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
         }
         tsa_wave_sync();
       }
-      if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
-        tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
-        tsa_wave_sync();
+      if constexpr (SLICE) {
+        if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
+          tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
+          tsa_wave_sync();
+        }
       }
       if constexpr (LVL) {
         if (--left == 0) {  // the level's last sweep
@@ -785,7 +788,7 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
     // level loop with helpers: the node sizes of an evaluated level, after the draw buffers
     uint16_t* const lz = LVL && helped ? reinterpret_cast<uint16_t*>(dbuf + 4 * nint4) : nullptr;
     // tc mode with helpers, no slicing: every internal node's cost and size (the visits' cost cache), after lz
-    const bool cc = MODE == 0 && W > 0 && helped && !P.slicing;
+    const bool cc = MODE == 0 && W > 0 && helped && !slicing;
     float* const cc_cost = cc ? reinterpret_cast<float*>(dbuf + 4 * nint4 + (LVL ? nint4 / 2 : 0)) : nullptr;
     uint16_t* const cc_size = cc ? reinterpret_cast<uint16_t*>(cc_cost + nint4) : nullptr;
     if (helped) {
@@ -802,16 +805,57 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
         __syncthreads();
       }
     }
-    for (int s = 0; s < nsw; s++) {
-      const uint32_t sw = sweep0 + (uint32_t)s;
-      if (helped && wv > 0) {  // helper waves
+    // an evaluated level's end with helpers: the whole workgroup evaluates the node costs into pri / par (free in
+    // pre-order sweeps) and the sizes into lz (with the cost cache: a copy of it, which the visits of the next
+    // sweep leave alone); then wave 0 returns to its sweeps at once and wave 1 folds, arrives (and selects when it
+    // is the last chain) beside them
+    float* const ncost = reinterpret_cast<float*>(pri);
+    auto level_costs = [&]() {
+      for (int i = threadIdx.x; i < nint; i += blockDim.x) {
+        if (cc) {
+          ncost[i] = cc_cost[i];
+          lz[i] = cc_size[i];
+        } else {
+          int Z;
+          ncost[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
+          lz[i] = (uint16_t)Z;
+        }
+      }
+    };
+    // The sweeping wave and the helper waves run loops of their own, which meet at the same workgroup barriers
+    // (one per sweep, one more at an evaluated level's end): wave 1's fold is a call, and in a loop of its own
+    // only the helpers' few values are live across it (in a loop shared with the sweep, every value the sweep
+    // keeps would be saved to scratch around the call at every level)
+    if (helped && wv > 0) {
+      for (int s = 0; s < nsw; s++) {
         if (s + 1 < nsw) {
           uint32_t* const nx = dbuf + (size_t)((s + 1) & 1) * 2 * nint4;
-          tsa_draw_ahead(P, nx, reinterpret_cast<float*>(nx + nint4), sw + 1u, (uint32_t)c, (int)threadIdx.x - 64,
-                         (int)blockDim.x - 64, T.exp2);
+          tsa_draw_ahead(P, nx, reinterpret_cast<float*>(nx + nint4), sweep0 + (uint32_t)s + 1u, (uint32_t)c,
+                         (int)threadIdx.x - 64, (int)blockDim.x - 64, T.exp2);
         }
         __syncthreads();
-      } else {
+        if constexpr (LVL) {
+          if (--left == 0) {  // the level's last sweep
+            const int ev = Lv.eval[lv];
+            if (ev >= 0) {
+              level_costs();
+              const int cslot = own.slot < 0 ? 0 : own.slot ^ 1;
+              if (wv == 1) {
+                tsa_level_keep(Lv, P, base, nchains, c, cslot, lane, 64);
+                if (slicing && lane < NW) s_S[lane] = S[lane];
+              }
+              __syncthreads();
+              if (wv == 1)
+                own = tsa_level_fold_arrive<W>(P, Lv, ncost, lz, slicing ? s_S : nullptr, lf, T, nchains, c, ev,
+                                               lv, own, cslot, lane);
+            }
+            if (++lv < Lv.nlev) left = Lv.niters[lv];
+          }
+        }
+      }
+    } else {
+      for (int s = 0; s < nsw; s++) {
+        const uint32_t sw = sweep0 + (uint32_t)s;
         const uint32_t* const pre_x = helped ? dbuf + (size_t)(s & 1) * 2 * nint4 : nullptr;
         const float* const pre_t = helped ? reinterpret_cast<const float*>(pre_x + nint4) : nullptr;
         if (lane == 0) wl[0] = (uint16_t)root;
@@ -826,7 +870,7 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
             // with helpers (one chain per workgroup) the staged leaf sets end where the chain's internal sets begin
             // (LDS records) and the draws are made ahead
             const TsaVisit o =
-                P.slicing ? (helped ? tsa_visit<W, MODE, true, LDS, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
+                slicing ? (helped ? tsa_visit<W, MODE, true, LDS, true>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t)
                                     : tsa_visit<W, MODE, true, false, false>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c))
                           : (helped ? tsa_visit<W, MODE, false, LDS, true, MODE == 0 && (W > 0)>(P, lab, ch, Sm, lf, s_lse, T, v, beta, sw, (uint32_t)c, pre_x, pre_t,
                                                                              cc_cost, cc_size)
@@ -847,48 +891,28 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
           sp = b0 + __popcll(b1) + __popcll(b2);
           tsa_wave_sync();
         }
-        if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
-          tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
-          tsa_wave_sync();
+        if constexpr (SLICE) {
+          if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
+            tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
+            tsa_wave_sync();
+          }
         }
         if (helped) __syncthreads();
-      }
-      if constexpr (LVL) {
-        if (--left == 0) {  // the level's last sweep
-          const int ev = Lv.eval[lv];
-          if (ev >= 0) {
-            if (helped) {
-              // the whole workgroup evaluates the node costs into pri / par (free in pre-order sweeps) and the
-              // sizes into lz, wave 1 keeps the tree and S; then wave 0 returns to its sweeps at once and wave 1
-              // folds, arrives (and selects when it is the last chain) beside them
-              // (with the cost cache: a copy of it, which the visits of the next sweep leave alone)
-              float* const ncost = reinterpret_cast<float*>(pri);
-              for (int i = threadIdx.x; i < nint; i += blockDim.x) {
-                if (cc) {
-                  ncost[i] = cc_cost[i];
-                  lz[i] = cc_size[i];
-                } else {
-                  int Z;
-                  ncost[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
-                  lz[i] = (uint16_t)Z;
-                }
+        if constexpr (LVL) {
+          if (--left == 0) {  // the level's last sweep
+            const int ev = Lv.eval[lv];
+            if (ev >= 0) {
+              if (helped) {
+                level_costs();
+                __syncthreads();
+              } else {
+                own = tsa_level_wave<W, MODE>(P, Lv, base, lab, ch, Sm, lf, T, pri, wl, nchains, c, ev, lv, own, lane);
               }
-              const int cslot = own.slot < 0 ? 0 : own.slot ^ 1;
-              if (wv == 1) {
-                tsa_level_keep(Lv, P, base, nchains, c, cslot, lane, 64);
-                if (P.slicing && lane < NW) s_S[lane] = S[lane];
-              }
-              __syncthreads();
-              if (wv == 1)
-                own = tsa_level_fold_arrive<W>(P, Lv, ncost, lz, P.slicing ? s_S : nullptr, lf, T, nchains, c, ev,
-                                               lv, own, cslot, lane);
-            } else {
-              own = tsa_level_wave<W, MODE>(P, Lv, base, lab, ch, Sm, lf, T, pri, wl, nchains, c, ev, lv, own, lane);
             }
-          }
-          if (++lv < Lv.nlev) {
-            beta = Lv.beta[lv];
-            left = Lv.niters[lv];
+            if (++lv < Lv.nlev) {
+              beta = Lv.beta[lv];
+              left = Lv.niters[lv];
+            }
           }
         }
       }
@@ -1155,7 +1179,7 @@ __global__ void k_track_init(TsaTrackState* st, unsigned long long* ticks0) {
 // ---------------------------------------------------------------------------------------------------
 // Host-side launchers
 // ---------------------------------------------------------------------------------------------------
-template <int W, int MODE, int ORDER, bool LDS, bool LVL>
+template <int W, int MODE, int ORDER, bool LDS, bool LVL, bool SLICE>
 static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
                                  const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
                                  unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st, hipEvent_t e0,
@@ -1183,7 +1207,7 @@ static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64
   }
   static size_t attr_set = 0;
   if (smem > 65536 && smem > attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_sweep<W, MODE, ORDER, LDS, LVL>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&k_sweep<W, MODE, ORDER, LDS, LVL, SLICE>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess) return e;
     attr_set = smem;
@@ -1191,17 +1215,31 @@ static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64
   if (res) {  // a query: chains resident per compute unit, no launch
     int nb = 0;
     const hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-        &nb, reinterpret_cast<const void*>(&k_sweep<W, MODE, ORDER, LDS, LVL>), threads, smem);
+        &nb, reinterpret_cast<const void*>(&k_sweep<W, MODE, ORDER, LDS, LVL, SLICE>), threads, smem);
     *res = nb * wpb;
     return e;
   }
   if (P.chain0 < 0 || P.chain0 >= nchains) return hipErrorInvalidValue;
   const int grid = (nchains - P.chain0 + wpb - 1) / wpb;
   // e0 / e1 (null: none) take the kernel's start and stop times in the dispatch itself
-  hipExtLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS, LVL>), dim3(grid), dim3(threads), (uint32_t)smem, st, e0, e1, 0u,
+  hipExtLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS, LVL, SLICE>), dim3(grid), dim3(threads), (uint32_t)smem, st, e0, e1, 0u,
                         P2, rec, leaf, fix, nchains, L.lds_words, beta, sweep0, nsweeps, stats, eo,
                         lv ? *lv : TsaLevels{});
   return hipGetLastError();
+}
+
+// the kernel without slice code when the sets are not masked (its proposals never read S and no slice step
+// runs), so that none of the slice step's calls and registers reach the sweeps that do not need them
+template <int W, int MODE, int ORDER, bool LDS, bool LVL>
+static hipError_t launch_sweep_s(const TsaLaunch& L, const TsaKParams& P, uint64_t* rec, const uint64_t* leaf,
+                                 const uint32_t* fix, int nchains, float beta, uint32_t sweep0, int nsweeps,
+                                 unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st, hipEvent_t e0,
+                                 hipEvent_t e1, const TsaLevels* lv, int* res) {
+  if (P.slicing)
+    return launch_sweep_t<W, MODE, ORDER, LDS, LVL, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats,
+                                                          eo, st, e0, e1, lv, res);
+  return launch_sweep_t<W, MODE, ORDER, LDS, LVL, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo,
+                                                         st, e0, e1, lv, res);
 }
 
 template <int W, int MODE>
@@ -1214,17 +1252,17 @@ static hipError_t launch_sweep_wm(const TsaLaunch& L, int order, const TsaKParam
       // the level loop (lv set) is a kernel of its own: its level functions are calls the plain sweep kernel
       // does not carry
       if (lv) {
-        if (order == 0) return launch_sweep_t<W, MODE, 0, true, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
-        return launch_sweep_t<W, MODE, 1, true, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+        if (order == 0) return launch_sweep_s<W, MODE, 0, true, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+        return launch_sweep_s<W, MODE, 1, true, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
       }
-      if (order == 0) return launch_sweep_t<W, MODE, 0, true, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
-      return launch_sweep_t<W, MODE, 1, true, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+      if (order == 0) return launch_sweep_s<W, MODE, 0, true, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
+      return launch_sweep_s<W, MODE, 1, true, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, lv, res);
     }
     return hipErrorInvalidValue;  // the register-width kernels exist only in the LDS variant
   } else {
     if (L.lds || lv) return hipErrorInvalidValue;  // the level loop runs on the register-width kernels only
-    if (order == 0) return launch_sweep_t<0, MODE, 0, false, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, nullptr, res);
-    return launch_sweep_t<0, MODE, 1, false, false>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, nullptr, res);
+    if (order == 0) return launch_sweep_t<0, MODE, 0, false, false, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, nullptr, res);
+    return launch_sweep_t<0, MODE, 1, false, false, true>(L, P, rec, leaf, fix, nchains, beta, sweep0, nsweeps, stats, eo, st, e0, e1, nullptr, res);
   }
 }
 
