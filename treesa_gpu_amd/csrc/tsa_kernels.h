@@ -121,6 +121,12 @@ hipError_t tsa_launch_sweeps(const TsaLaunch& L, int mode, int order, const TsaK
                              int* res = nullptr);
 // With res set nothing is launched: *res = chains of the launch's kernel (the level loop's with lv set) that
 // are resident on one compute unit at once.
+// The same for the slicing kernel variants only (tsa_sweep_sliced.hip; tsa_launch_sweeps calls it when
+// P.slicing is set).
+hipError_t tsa_launch_sweeps_sliced(const TsaLaunch& L, int mode, int order, const TsaKParams& P, uint64_t* rec,
+                                    const uint64_t* leaf, const uint32_t* fix, int nchains, float beta, uint32_t sweep0,
+                                    int nsweeps, unsigned long long* stats, const TsaEnergyOut& eo, hipStream_t st,
+                                    hipEvent_t e0, hipEvent_t e1, const TsaLevels* lv, int* res);
 hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
                              const uint32_t* fix, int nchains, float* lc, int* sc, int* ns, hipStream_t st);
 // The fold of node costs a sweep launch left in cost / z (nchains * nint4 each) into lc / sc / ns.
