@@ -44,6 +44,11 @@ struct tsa_ctx {
   int* d_sc = nullptr;
   int* d_ns = nullptr;
   uint32_t* h_en = nullptr;  // pinned host copy of the three energy arrays
+  // pinned staging of tsa_track_end's copies (tracking state, start tick, best tree, trace rows): page-locked
+  // copies are enqueued without a wait each, and the call waits once
+  char* h_tend = nullptr;
+  size_t h_tend_bytes = 0;
+  double tick_hz = 0.0;  // the device's wall-clock rate (Hz)
   uint32_t* d_hen = nullptr;  // the device's address of h_en (null: not mapped)
   bool energy_host = false;   // the last sweep launch wrote the energies of the current population into h_en
   int* d_anc = nullptr;
@@ -277,6 +282,7 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_stats) (void)hipFree(c->d_stats);
   if (c->d_lc) (void)hipFree(c->d_lc);
   if (c->h_en) (void)hipHostFree(c->h_en);
+  if (c->h_tend) (void)hipHostFree(c->h_tend);
   if (c->d_anc) (void)hipFree(c->d_anc);
   if (c->h_anc) (void)hipHostFree(c->h_anc);
   if (c->ev_anc) (void)hipEventDestroy(c->ev_anc);
@@ -922,6 +928,24 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
     TSA_HIP(ctx, hipMalloc(&ctx->d_trace, (size_t)max_levels * sizeof(TsaTraceRowD)));
   }
   ctx->track_levels = max_levels;
+  {
+    const tsa_layout_t& L = ctx->lay;
+    const size_t need = sizeof(TsaTrackState) + 16 + (size_t)(L.s_off + L.W - L.ch_off) * 8 +
+                        (size_t)max_levels * sizeof(TsaTraceRowD) + 64;
+    if (need > ctx->h_tend_bytes) {
+      if (ctx->h_tend) TSA_HIP(ctx, hipHostFree(ctx->h_tend));
+      ctx->h_tend = nullptr;
+      ctx->h_tend_bytes = 0;
+      TSA_HIP(ctx, hipHostMalloc(reinterpret_cast<void**>(&ctx->h_tend), need, hipHostMallocDefault));
+      ctx->h_tend_bytes = need;
+    }
+    if (ctx->tick_hz == 0.0) {
+      int dev = 0, khz = 0;
+      TSA_HIP(ctx, hipGetDevice(&dev));
+      TSA_HIP(ctx, hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+      ctx->tick_hz = (double)khz * 1e3;
+    }
+  }
   // timing events for the sweep launches of every level (two for a split level), created here rather than
   // inside the level loop, where their creation would hold up the host's enqueueing of short levels
   while ((int)ctx->ev.size() < 2 * (ctx->npending + 2 * max_levels)) {
@@ -958,9 +982,11 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   ctx->track_kind = 0;
   ctx->lv_reset = true;
   ctx->lv_evaluated.assign((size_t)max_levels, 0);
-  TSA_HIP(ctx, hipMemsetAsync(ctx->d_trace, 0, (size_t)max_levels * sizeof(TsaTraceRowD), ctx->st));
-  TSA_HIP(ctx, hipMemsetAsync(ctx->d_best, 0, (size_t)ctx->lay.chain_words * 8, ctx->st));
-  TSA_HIP(ctx, tsa_launch_track_init(ctx->d_track, ctx->d_ticks0, ctx->st));
+  static_assert(sizeof(TsaTraceRowD) % 8 == 0, "trace rows are whole words");
+  TSA_HIP(ctx, tsa_launch_track_init(ctx->d_track, ctx->d_ticks0, reinterpret_cast<unsigned long long*>(ctx->d_trace),
+                                     (int)((size_t)max_levels * sizeof(TsaTraceRowD) / 8),
+                                     reinterpret_cast<unsigned long long*>(ctx->d_best), ctx->lay.chain_words,
+                                     ctx->st));
   return TSA_OK;
 }
 
@@ -1017,18 +1043,28 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
   TsaTrackState h;
   unsigned long long t0 = 0;
   join_track(ctx);
-  TSA_HIP(ctx, hipMemcpyAsync(&h, ctx->d_track, sizeof h, hipMemcpyDeviceToHost, ctx->st));
-  TSA_HIP(ctx, hipMemcpyAsync(&t0, ctx->d_ticks0, sizeof t0, hipMemcpyDeviceToHost, ctx->st));
-  // the best chain's tree: children words and S (the label words of best_record are not written)
+  // every copy into the pinned staging buffer, one wait, then the caller's buffers from there
   const tsa_layout_t& L = ctx->lay;
-  TSA_HIP(ctx, hipMemcpyAsync(best_record + L.ch_off, ctx->d_best + L.ch_off, (size_t)(L.s_off + L.W - L.ch_off) * 8,
-                              hipMemcpyDeviceToHost, ctx->st));
-  TSA_HIP(ctx, hipMemcpyAsync(rows, ctx->d_trace, (size_t)ctx->track_levels * sizeof(TsaTraceRowD),
-                              hipMemcpyDeviceToHost, ctx->st));
+  const size_t cwb = (size_t)(L.s_off + L.W - L.ch_off) * 8, rowb = (size_t)ctx->track_levels * sizeof(TsaTraceRowD);
+  char* const hs = ctx->h_tend;
+  char* const h_state = hs;
+  char* const h_t0 = h_state + ((sizeof(TsaTrackState) + 15) & ~(size_t)15);
+  char* const h_werr = h_t0 + 8;
+  char* const h_tree = h_t0 + 16;
+  char* const h_rows = h_tree + ((cwb + 15) & ~(size_t)15);
+  TSA_HIP(ctx, hipMemcpyAsync(h_state, ctx->d_track, sizeof h, hipMemcpyDeviceToHost, ctx->st));
+  TSA_HIP(ctx, hipMemcpyAsync(h_t0, ctx->d_ticks0, sizeof t0, hipMemcpyDeviceToHost, ctx->st));
+  // the best chain's tree: children words and S (the label words of best_record are not written)
+  TSA_HIP(ctx, hipMemcpyAsync(h_tree, ctx->d_best + L.ch_off, cwb, hipMemcpyDeviceToHost, ctx->st));
+  TSA_HIP(ctx, hipMemcpyAsync(h_rows, ctx->d_trace, rowb, hipMemcpyDeviceToHost, ctx->st));
   uint32_t werr = 0;
-  if (ctx->wide.on)
-    TSA_HIP(ctx, hipMemcpyAsync(&werr, ctx->wsync.err, 4, hipMemcpyDeviceToHost, ctx->st));
+  if (ctx->wide.on) TSA_HIP(ctx, hipMemcpyAsync(h_werr, ctx->wsync.err, 4, hipMemcpyDeviceToHost, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  std::memcpy(&h, h_state, sizeof h);
+  std::memcpy(&t0, h_t0, sizeof t0);
+  std::memcpy(best_record + L.ch_off, h_tree, cwb);
+  std::memcpy(rows, h_rows, rowb);
+  if (ctx->wide.on) std::memcpy(&werr, h_werr, 4);
   TSA_HIP(ctx, quiesce_track(ctx));
   if (wide_error(ctx, werr) != TSA_OK) return TSA_ERR_HIP;
   if (ctx->track_kind == TRACK_ANNEAL) {
@@ -1045,21 +1081,22 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
       }
     if (h.best_chain >= 0) {
       int bs = -1;
-      TSA_HIP(ctx, hipMemcpy(&bs, ctx->d_bslot + h.best_chain, 4, hipMemcpyDeviceToHost));
+      TSA_HIP(ctx, hipMemcpyAsync(h_werr, ctx->d_bslot + h.best_chain, 4, hipMemcpyDeviceToHost, ctx->st));
+      TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+      std::memcpy(&bs, h_werr, 4);
       if (bs < 0 || bs > 1) return fail(ctx, TSA_ERR_HIP, "tsa_track_end: the best chain has no kept tree");
       const int cw = L.s_off + L.W - L.ch_off;
-      TSA_HIP(ctx, hipMemcpy(best_record + L.ch_off, ctx->d_cand + ((size_t)bs * ctx->nchains + h.best_chain) * cw,
-                             (size_t)cw * 8, hipMemcpyDeviceToHost));
+      TSA_HIP(ctx, hipMemcpyAsync(h_tree, ctx->d_cand + ((size_t)bs * ctx->nchains + h.best_chain) * cw, (size_t)cw * 8,
+                                  hipMemcpyDeviceToHost, ctx->st));
+      TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+      std::memcpy(best_record + L.ch_off, h_tree, (size_t)cw * 8);
     }
   }
-  int dev = 0, khz = 0;
-  TSA_HIP(ctx, hipGetDevice(&dev));
-  TSA_HIP(ctx, hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
   *best_chain = h.best_chain;
   *best_level = h.best_level;
   *best_score = h.best_score;
   *ticks0 = t0;
-  *tick_hz = (double)khz * 1e3;
+  *tick_hz = ctx->tick_hz;
   return TSA_OK;
 }
 

@@ -157,7 +157,8 @@ hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int n
                             const uint64_t* rec, int chain_words, int ch_off, int s_off, int W, int nint,
                             const uint32_t* ch_snap, TsaTrackState* st, TsaTraceRowD* trace, uint64_t* best_rec,
                             TsaTrackPart* part, unsigned* done, hipStream_t stream);
-hipError_t tsa_launch_track_init(TsaTrackState* st, unsigned long long* ticks0, hipStream_t stream);
+hipError_t tsa_launch_track_init(TsaTrackState* st, unsigned long long* ticks0, unsigned long long* trace,
+                                 int trace_words, unsigned long long* best, int best_words, hipStream_t stream);
 // The level loop's per-chain best (TsaLevels.own / bslot) of n chains reset: +inf, no slot.
 hipError_t tsa_launch_levels_init(double* own, int* bslot, int n, hipStream_t stream);
 hipError_t tsa_launch_copy(const uint64_t* src, uint64_t* dst, const int* anc, int nchains, int chain_words,

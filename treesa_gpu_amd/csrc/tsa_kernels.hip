@@ -185,12 +185,21 @@ __global__ void __launch_bounds__(256) k_track(const float* __restrict__ lc, con
   }
 }
 
-__global__ void k_track_init(TsaTrackState* st, unsigned long long* ticks0) {
-  st->best_score = INFINITY;
-  st->best_chain = -1;
-  st->best_level = -1;
-  st->snap = -1;
-  *ticks0 = wall_clock64();
+// A tracking session's start: the tracking state, the start tick, and the trace rows and best record cleared
+// (one launch instead of two memsets and a launch).
+__global__ void __launch_bounds__(256) k_track_init(TsaTrackState* st, unsigned long long* ticks0,
+                                                    unsigned long long* trace, int trace_words,
+                                                    unsigned long long* best, int best_words) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x, nt = gridDim.x * blockDim.x;
+  for (int i = t; i < trace_words; i += nt) trace[i] = 0ull;
+  for (int i = t; i < best_words; i += nt) best[i] = 0ull;
+  if (t == 0) {
+    st->best_score = INFINITY;
+    st->best_chain = -1;
+    st->best_level = -1;
+    st->snap = -1;
+    *ticks0 = wall_clock64();
+  }
 }
 
 // ---------------------------------------------------------------------------------------------------
@@ -246,8 +255,13 @@ hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int n
   return hipGetLastError();
 }
 
-hipError_t tsa_launch_track_init(TsaTrackState* stt, unsigned long long* ticks0, hipStream_t stream) {
-  hipLaunchKernelGGL(k_track_init, dim3(1), dim3(1), 0, stream, stt, ticks0);
+hipError_t tsa_launch_track_init(TsaTrackState* stt, unsigned long long* ticks0, unsigned long long* trace,
+                                 int trace_words, unsigned long long* best, int best_words, hipStream_t stream) {
+  const int n = trace_words > best_words ? trace_words : best_words;
+  int grid = (n + 255) / 256;
+  if (grid < 1) grid = 1;
+  if (grid > 64) grid = 64;
+  hipLaunchKernelGGL(k_track_init, dim3(grid), dim3(256), 0, stream, stt, ticks0, trace, trace_words, best, best_words);
   return hipGetLastError();
 }
 
