@@ -108,3 +108,34 @@ def test_every_unreproduced_answer_is_explained():
     reproduced = sum(fx["reproduces"] for fx in FIX.values())
     assert reproduced >= 80, reproduced
     print(f"reproduced {reproduced} of {len(FIX)}; unreproduced: {kinds}")
+
+
+def test_truncation_runs_part_where_the_cut_is_a_float_tie():
+    """Truncation ranks every chain by its float energy at every level and copies the best quarter over the
+    worst (csrc/treesa_gpu.cu:1857-1869).  In every truncation run the oracle does not reproduce:
+    * the perturbation of the energy arithmetic alone (exp2f / log2f moved by one ulp, variant 1) first changes
+      the run at a level whose ranking around the cut is a float tie -- a population margin of at most one float
+      ulp at the run's energy scale, in fact exactly zero: which of the tied chains survives is decided by the
+      energies' last bit;
+    * every other perturbation (Metropolis's expf moved by up to two ulp, variant 20) first changes the run at
+      such a tie or at or after a level whose sweeps hold a Metropolis decision within two ulp of expf.
+    So a device whose exp2f / log2f / expf round differently from this host's libm parts from this answer at a
+    tie of float energies or at a Metropolis decision on the edge, as these runs show."""
+    import numpy as np
+    rows = []
+    for cid, fx in FIX.items():
+        c = CASES[cid]
+        if c["scheme"] != "trunc" or fx["reproduces"]:
+            continue
+        ulp = float(np.spacing(np.float32(fx["oracle"]["tc"])))
+        near = fx.get("metropolis_near_levels") or []
+        moved = [p for p in fx["perturbed"] if p["answer_changes"]]
+        energy = [p for p in moved if p["variant"] == 1]
+        assert energy and all(p["pop_margin"] <= ulp for p in energy), (cid, energy)
+        for p in moved:
+            assert p["pop_margin"] <= ulp or any(L <= p["first_level"] for L in near), (cid, p, near)
+        rows.append((cid, energy[0]["first_level"], energy[0]["pop_margin"] / ulp, near[:3]))
+    assert len(rows) == 11, rows
+    for cid, first, m, near in rows:
+        print(f"{cid}: energy rounding first parts at level {first} (cut margin {m:.2f} ulp); "
+              f"Metropolis decisions within two ulp at levels {near}")
