@@ -41,8 +41,10 @@ __device__ __forceinline__ float tsa_node_eval(const TsaKParams& P, const uint64
 // group returns the result).  lf / S / NW serve the masked leaf sizes when S is set.  The lse chain of a
 // lane is serial; its operands are read TSA_FOLD_BATCH at a time ahead of it, so that no step waits on a
 // load, and the size statistics run in a loop of their own.
+// Costs are floats, or (tc mode, whose node costs are integers) 16-bit integers converted exactly.
 #define TSA_FOLD_BATCH 8
-__device__ __forceinline__ TsaEvalOut tsa_fold32(const TsaKParams& P, const float* cost, const uint16_t* z,
+template <typename CT>
+__device__ __forceinline__ TsaEvalOut tsa_fold32(const TsaKParams& P, const CT* cost, const uint16_t* z,
                                                  const uint64_t* S, const uint64_t* lf, int NW, const TsaMathTabs& T,
                                                  int l32) {
   const int nint = P.nint, m = P.m;
@@ -52,7 +54,7 @@ __device__ __forceinline__ TsaEvalOut tsa_fold32(const TsaKParams& P, const floa
 #pragma unroll
     for (int q = 0; q < TSA_FOLD_BATCH; q++) {
       const int i = i0 + 32 * q;
-      cb[q] = i < nint ? cost[i] : 0.0f;
+      cb[q] = i < nint ? (float)cost[i] : 0.0f;
     }
 #pragma unroll
     for (int q = 0; q < TSA_FOLD_BATCH; q++)

@@ -276,15 +276,45 @@ __device__ __forceinline__ float tsa_slice_energy(const TsaEvalOut& e, const Tsa
   return (float)e.ns + e.lcost + pen;
 }
 
-// Slice moves of one chain by one wave (csrc/treesa_gpu.cu:445-502).  Both 32-lane halves run the
-// reference's 32-lane algorithm on the same data; lane 0 alone writes S.
+// Whole-chain evaluation by the whole wave, tc mode: every lane computes the costs (integers, |z| + |x & y & ~z|
+// outside S) and masked sizes of internal nodes lane, lane + 64, ... into ncost / nz (node arrays the sweep has
+// finished with), then the 32-lane fold of tsa_fold32 in the reference's order: the same floats as tsa_eval32,
+// with half the node passes.
+template <int W>
+__device__ TsaEvalOut tsa_eval64_tc(const TsaKParams& P, const uint64_t* lab, const uint32_t* ch, const uint64_t* S,
+                                    const uint64_t* lf, const TsaMathTabs& T, int lane, uint16_t* ncost,
+                                    uint16_t* nz) {
+  const int NW = W > 0 ? W : P.W;
+  tsa_wave_sync();  // a previous fold's reads of ncost / nz come first
+  for (int i = lane; i < P.nint; i += 64) {
+    int Z;
+    ncost[i] = (uint16_t)tsa_node_eval<W, 0>(P, lab, ch, S, lf, T, i, Z);
+    nz[i] = (uint16_t)Z;
+  }
+  tsa_wave_sync();
+  return tsa_fold32(P, ncost, nz, S, lf, NW, T, lane & 31);
+}
+
+// Slice moves of one chain by one wave (csrc/treesa_gpu.cu:445-502); lane 0 alone writes S.  Returns the
+// evaluation of the chain as the step leaves it.  In tc mode with ncost / nz given (nint 16-bit words each, free
+// for the step) the evaluations use the whole wave (tsa_eval64_tc) and the candidate scan reads the sizes they
+// leave; otherwise both 32-lane halves run the reference's 32-lane algorithm on the same data.
 template <int W, int MODE>
-__device__ void tsa_slice_step(const TsaKParams& P, const uint64_t* lab, const uint32_t* ch, uint64_t* S,
-                               const uint64_t* lf, const TsaMathTabs& T, float beta, uint32_t sw, uint32_t chain,
-                               int lane, int& nsp, int& nsa) {
+__device__ TsaEvalOut tsa_slice_step(const TsaKParams& P, const uint64_t* lab, const uint32_t* ch, uint64_t* S,
+                                     const uint64_t* lf, const TsaMathTabs& T, float beta, uint32_t sw, uint32_t chain,
+                                     int lane, int& nsp, int& nsa, uint16_t* ncost = nullptr, uint16_t* nz = nullptr) {
   const int NW = W > 0 ? W : P.W;
   const int l32 = lane & 31;
-  TsaEvalOut cur = tsa_eval32<W, MODE>(P, lab, ch, S, lf, T, l32);
+  constexpr bool TC = MODE == 0;
+  const bool wide = TC && ncost != nullptr;
+  auto evaluate = [&]() {
+    if constexpr (TC) {
+      if (wide) return tsa_eval64_tc<W>(P, lab, ch, S, lf, T, lane, ncost, nz);
+    }
+    return tsa_eval32<W, MODE>(P, lab, ch, S, lf, T, l32);
+  };
+  TsaEvalOut cur = evaluate();
+  bool zcur = wide;  // nz holds the sizes of the current slice set
   float Ecur = tsa_slice_energy(cur, P);
   for (int j = 0; j < P.slice_moves; j++) {
     const TsaU4 r1 = tsa_philox(TsaU4{0x10000u + 2u * (uint32_t)j, sw, chain, 0u}, P.key0, P.key1);
@@ -297,18 +327,38 @@ __device__ void tsa_slice_step(const TsaKParams& P, const uint64_t* lab, const u
     if (type != 1 && cur.ncand > 0 && cur.sc_int > 0) {
       // the (r1.y % ncand)-th internal node of maximal masked size, in node-id order
       int rr = (int)(r1.y % (uint32_t)cur.ncand), node = -1;
-      for (int base = 0; base < P.nint && node < 0; base += 32) {
-        const int i = base + l32;
-        int Z = -1;
-        if (i < P.nint) {
-          Z = 0;
-          const uint64_t* z = lab + (size_t)i * NW;
-          for (int w = 0; w < NW; w++) Z += __popcll(z[w] & ~S[w]);
+      if (wide) {
+        for (int base = 0; base < P.nint && node < 0; base += 64) {
+          const int i = base + lane;
+          int Z = -1;
+          if (i < P.nint) {
+            if (zcur) {
+              Z = nz[i];
+            } else {
+              Z = 0;
+              const uint64_t* z = lab + (size_t)i * NW;
+              for (int w = 0; w < NW; w++) Z += __popcll(z[w] & ~S[w]);
+            }
+          }
+          const uint64_t b = __ballot(Z == cur.sc_int);
+          const int c = __popcll(b);
+          if (rr < c) node = base + tsa_nth_bit(b, rr);
+          else rr -= c;
         }
-        const uint32_t b = (uint32_t)(__ballot(Z == cur.sc_int) >> (lane & 32));
-        const int c = __popc(b);
-        if (rr < c) node = base + tsa_nth_bit(b, rr);
-        else rr -= c;
+      } else {
+        for (int base = 0; base < P.nint && node < 0; base += 32) {
+          const int i = base + l32;
+          int Z = -1;
+          if (i < P.nint) {
+            Z = 0;
+            const uint64_t* z = lab + (size_t)i * NW;
+            for (int w = 0; w < NW; w++) Z += __popcll(z[w] & ~S[w]);
+          }
+          const uint32_t b = (uint32_t)(__ballot(Z == cur.sc_int) >> (lane & 32));
+          const int c = __popc(b);
+          if (rr < c) node = base + tsa_nth_bit(b, rr);
+          else rr -= c;
+        }
       }
       if (node >= 0) ladd = tsa_nth_label(lab + (size_t)node * NW, S, NW, (int)(r1.z % (uint32_t)cur.sc_int));
     }
@@ -321,14 +371,16 @@ __device__ void tsa_slice_step(const TsaKParams& P, const uint64_t* lab, const u
       if (type != 0) S[lrem >> 6] &= ~(1ull << (lrem & 63));
     }
     tsa_wave_sync();
-    const TsaEvalOut nxt = tsa_eval32<W, MODE>(P, lab, ch, S, lf, T, l32);
+    const TsaEvalOut nxt = evaluate();
     const float Enew = tsa_slice_energy(nxt, P);
     nsp++;
     if (tsa_metropolis(r2.x, beta, Enew - Ecur, T.exp2)) {
       nsa++;
       cur = nxt;
       Ecur = Enew;
+      zcur = wide;
     } else {
+      zcur = false;  // nz holds the rejected set's sizes
       tsa_wave_sync();
       if (lane == 0) {
         if (type != 1) S[ladd >> 6] &= ~(1ull << (ladd & 63));
@@ -337,6 +389,7 @@ __device__ void tsa_slice_step(const TsaKParams& P, const uint64_t* lab, const u
       tsa_wave_sync();
     }
   }
+  return cur;
 }
 
 __device__ __forceinline__ long long tsa_wave_sum(long long x) {
@@ -611,6 +664,9 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
   uint16_t* const wl = par + nint4;
   uint32_t* const dw = reinterpret_cast<uint32_t*>(wl + nint4);
   int np = 0, na = 0, nst = 0, nv = 0, nsp = 0, nsa = 0, nbusy = 0;
+  // the evaluation a slice step left of the chain as it stands (valid until the next sweep changes the tree)
+  TsaEvalOut last_e{};
+  bool have_e = false;
   // the level loop (Lv.nlev > 0) or the launch's one level: sweeps in all, the current level, its sweeps left
   // and beta; the chain's best score and the candidate slot of its tree, kept by the wave that tracks the chain
   // (wave 1 with helpers, else the chain's wave)
@@ -764,8 +820,11 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
         tsa_wave_sync();
       }
       if constexpr (SLICE) {
+        have_e = false;
         if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
-          tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
+          // (pri and the work list are free until the next sweep)
+          last_e = tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa, pri, wl);
+          have_e = true;
           tsa_wave_sync();
         }
       }
@@ -898,8 +957,11 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
           tsa_wave_sync();
         }
         if constexpr (SLICE) {
+          have_e = false;
           if (P.slice_moves > 0 && (sw + 1u) % (uint32_t)P.slice_every == 0u) {
-            tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa);
+            // (pri and the work list are free in pre-order after the sweep)
+            last_e = tsa_slice_step<W, MODE>(P, lab, ch, S, lf, T, beta, sw, (uint32_t)c, lane, nsp, nsa, pri, wl);
+            have_e = true;
             tsa_wave_sync();
           }
         }
@@ -942,6 +1004,13 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
       int Z;
       gc[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
       gz[i] = (uint16_t)Z;
+    }
+  } else if (eo.lc && !helped && have_e) {
+    // the last sweep's slice step evaluated the chain as it stands: the same energy k_energy would compute
+    if (lane == 0) {
+      eo.lc[c] = last_e.lcost;
+      eo.sc[c] = last_e.sc;
+      eo.ns[c] = last_e.ns;
     }
   } else if (eo.lc) {
     // the chain's energy, as k_energy computes it: node costs into the node arrays (free after the sweeps:
