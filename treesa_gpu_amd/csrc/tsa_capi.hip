@@ -17,6 +17,12 @@
 #include "treesa_hip.h"
 #include "tsa_kernels.h"
 
+// Snapshot slots of the overlapped selection: a sweep launch takes the slot that the selection of
+// TSA_SNAP_SLOTS - 1 levels back read, so the host may enqueue that many levels ahead of the device.
+#ifndef TSA_SNAP_SLOTS
+#define TSA_SNAP_SLOTS 3
+#endif
+
 struct tsa_ctx {
   tsa_layout_t lay;
   tsa_config_t cfg;
@@ -76,8 +82,8 @@ struct tsa_ctx {
   TsaTrackPart* d_tpart = nullptr;  // selection kernel: per-workgroup results and its counter
   unsigned* d_tdone = nullptr;
   // Overlapped tracking (the wide path, and the one-wave kernels with fused energies): each sweep launch
-  // leaves a snapshot of every chain's tree and node costs (or energies) in slot `slot` (two slots,
-  // alternating), and tsa_track runs the fold and the selection of that snapshot on the second stream st2
+  // leaves a snapshot of every chain's tree and node costs (or energies) in slot `slot` (TSA_SNAP_SLOTS
+  // slots in turn), and tsa_track runs the fold and the selection of that snapshot on the second stream st2
   // while st goes on with the next level's sweep.  ev_sweep[s] marks the sweep that filled slot s,
   // ev_track[s] the selection that read it (the host waits for it before a sweep overwrites the slot).
   bool overlap = false;
@@ -90,19 +96,19 @@ struct tsa_ctx {
   // launch of the sweep that filled slot s, when split_slot[s].
   hipStream_t st3 = nullptr;
   hipEvent_t ev_fork = nullptr, ev_join = nullptr;
-  hipEvent_t ev_b[2] = {nullptr, nullptr};
-  bool split_slot[2] = {false, false};
+  hipEvent_t ev_b[TSA_SNAP_SLOTS] = {};
+  bool split_slot[TSA_SNAP_SLOTS] = {};
   bool split_pending = false;  // st3 holds work st is not yet ordered after
   long long split_levels = 0;  // sweep calls run as two launches (reported by tsa_describe)
-  hipEvent_t ev_sweep[2] = {nullptr, nullptr};  // (the stop events of those sweeps' timing pairs)
-  hipEvent_t ev_track[2] = {nullptr, nullptr};
-  bool track_pending[2] = {false, false};
+  hipEvent_t ev_sweep[TSA_SNAP_SLOTS] = {};  // (the stop events of those sweeps' timing pairs)
+  hipEvent_t ev_track[TSA_SNAP_SLOTS] = {};
+  bool track_pending[TSA_SNAP_SLOTS] = {};
   int slot = 0, last_slot = -1;  // slot of the next sweep launch / of the last one (-1: none since a reset)
-  uint32_t* d_snap_ch[2] = {nullptr, nullptr};
-  float* d_snap_cost[2] = {nullptr, nullptr};
-  uint16_t* d_snap_nz[2] = {nullptr, nullptr};
-  uint32_t* d_snap_en[2] = {nullptr, nullptr};  // energies folded by the sweep kernel: lc, sc, ns per chain
-  int snap_kind[2] = {0, 0};  // what the sweep that filled a slot left there: a SNAP_* value
+  uint32_t* d_snap_ch[TSA_SNAP_SLOTS] = {};
+  float* d_snap_cost[TSA_SNAP_SLOTS] = {};
+  uint16_t* d_snap_nz[TSA_SNAP_SLOTS] = {};
+  uint32_t* d_snap_en[TSA_SNAP_SLOTS] = {};  // energies folded by the sweep kernel: lc, sc, ns per chain
+  int snap_kind[TSA_SNAP_SLOTS] = {};  // what the sweep that filled a slot left there: a SNAP_* value
   // The level loop on the device (tsa_anneal, TsaLevels): the tracking session's kind (0: nothing tracked
   // yet, TRACK_LEVELS: tsa_track, TRACK_ANNEAL: tsa_anneal), whether the per-chain best still has to be
   // reset, the levels evaluated so far in the session, and the buffers, grown on demand.
@@ -297,11 +303,13 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_tdone) (void)hipFree(c->d_tdone);
   for (hipEvent_t e : c->ev) (void)hipEventDestroy(e);
   if (c->st3) {
-    for (hipEvent_t e : {c->ev_fork, c->ev_join, c->ev_b[0], c->ev_b[1]})
+    for (hipEvent_t e : {c->ev_fork, c->ev_join})
+      if (e) (void)hipEventDestroy(e);
+    for (hipEvent_t e : c->ev_b)
       if (e) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(c->st3);
   }
-  for (int k = 0; k < 2; k++) {
+  for (int k = 0; k < TSA_SNAP_SLOTS; k++) {
     if (c->ev_track[k]) (void)hipEventDestroy(c->ev_track[k]);
     if (c->d_snap_ch[k]) (void)hipFree(c->d_snap_ch[k]);
     if (c->d_snap_cost[k]) (void)hipFree(c->d_snap_cost[k]);
@@ -602,7 +610,7 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
 // d_sc / d_ns and write the tracking state), or wait for st2 on the host and forget the snapshots (before
 // the population is replaced).
 static void join_track(tsa_ctx* c) {
-  for (int k = 0; k < 2; k++)
+  for (int k = 0; k < TSA_SNAP_SLOTS; k++)
     if (c->track_pending[k]) (void)hipStreamWaitEvent(c->st, c->ev_track[k], 0);
 }
 
@@ -617,7 +625,7 @@ static hipError_t join_split(tsa_ctx* c) {
 static hipError_t quiesce_track(tsa_ctx* c) {
   hipError_t e = hipSuccess;
   if (c->st2) e = hipStreamSynchronize(c->st2);
-  c->track_pending[0] = c->track_pending[1] = false;
+  for (bool& p : c->track_pending) p = false;
   c->last_slot = -1;
   return e;
 }
@@ -782,7 +790,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     if (s >= 0) {
       ctx->ev_sweep[s] = e1;  // the selection of this snapshot waits for the sweep's stop event
       ctx->last_slot = s;
-      ctx->slot = s ^ 1;
+      ctx->slot = (s + 1) % TSA_SNAP_SLOTS;
     }
     ctx->energy_fresh = fold_here;
   } else {
@@ -829,7 +837,8 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
         TSA_HIP(ctx, hipStreamCreateWithFlags(&ctx->st3, hipStreamNonBlocking));
         TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_fork, hipEventDisableTiming));
         TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_join, hipEventDisableTiming));
-        for (int k = 0; k < 2; k++) TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_b[k], hipEventDisableTiming));
+        for (int k = 0; k < TSA_SNAP_SLOTS; k++)
+          TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_b[k], hipEventDisableTiming));
       }
       // the second launch's timing pair follows the first's
       hipEvent_t f0 = ctx->ev[2 * ctx->npending + 2], f1 = ctx->ev[2 * ctx->npending + 3];
@@ -860,7 +869,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
       ctx->split_slot[s] = split;
       ctx->ev_sweep[s] = e1;
       ctx->last_slot = s;
-      ctx->slot = s ^ 1;
+      ctx->slot = (s + 1) % TSA_SNAP_SLOTS;
       ctx->energy_fresh = false;  // the energies of this population exist only once tsa_track folds the slot
     } else {
       if (apart)
@@ -969,7 +978,7 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   if (want_overlap && !ctx->st2) {
     const size_t nint = (size_t)ctx->lay.nint, nint4 = (nint + 3) & ~(size_t)3;
     TSA_HIP(ctx, hipStreamCreateWithFlags(&ctx->st2, hipStreamNonBlocking));
-    for (int k = 0; k < 2; k++) {
+    for (int k = 0; k < TSA_SNAP_SLOTS; k++) {
       TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_track[k], hipEventDisableTiming));
       TSA_HIP(ctx, hipMalloc(&ctx->d_snap_ch[k], (size_t)ctx->nchains * nint * 4));
       TSA_HIP(ctx, hipMalloc(&ctx->d_snap_cost[k], (size_t)ctx->nchains * nint4 * 4));
