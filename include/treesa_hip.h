@@ -142,7 +142,7 @@ int tsa_wait(tsa_ctx* ctx);
 /* Enqueue nsweeps sweeps of every chain at inverse temperature beta, global sweep counter sweep0
  * (the RNG counter), in TSA_ORDER_*; slice moves follow every sweep s with (sweep0+s+1) % slice_every
  * == 0 when slice_moves > 0.  Asynchronous (with overlapped tracking, see track_overlap, it first waits
- * on the host for the selection of two launches back to finish); event-timed.  Replaces Runner::sweeps / sweeps_mode,
+ * on the host for the selection of three launches back to finish); event-timed.  Replaces Runner::sweeps / sweeps_mode,
  * csrc/treesa_gpu.cu:1659-1716. */
 int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0, int32_t nsweeps);
 
