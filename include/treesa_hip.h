@@ -107,6 +107,11 @@ typedef struct tsa_config_t {
    * at once, else one sweep launch and one selection per level), 1 = the level loop in one launch whenever the
    * context's kernels run it, -1 = per-level launches.  Results do not change */
   int32_t level_loop;
+  /* tsa_anneal without the one-launch level loop, on the one-wave LDS kernels whose selection overlaps the next
+   * sweep with the fold apart (more than twice the chains the device holds at once, par order, no slicing):
+   * levels per sweep launch, each evaluated level leaving its own snapshot for the fold and the selection
+   * (0 = automatic: 8, the most; 1 = one level per launch).  Results do not change */
+  int32_t level_blocks;
 } tsa_config_t;
 
 typedef struct tsa_ctx tsa_ctx;

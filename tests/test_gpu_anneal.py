@@ -142,6 +142,30 @@ def test_many_chains(level_loop, want):
     compare(s, a, b, ev)
 
 
+@pytest.mark.parametrize("blocks,want", [(0, "anneal=level_blocks8"), (3, "anneal=level_blocks3"),
+                                         (1, "anneal=level_launches")])
+def test_level_blocks(blocks, want):
+    """8192 chains with the overlapped selection and the fold apart (the benchmark's headline path): tsa_anneal
+    sweeps several levels per launch (blocks of 8 by default, here 8 + 3 levels; or of 3: 3 + 3 + 3 + 2), each
+    evaluated level leaving a snapshot of its own, whose fold and selection run as one launch each per block
+    (the selection keeping the best in level order), beside the next block's sweeps; each block is split over two
+    launches on two streams.  Sweeps per level vary and some levels are not evaluated; the records of all chains,
+    the statistics, every trace row and the best equal the per-level launches (tsa_sweeps + tsa_track, pinned to
+    the oracle's level loop by test_split_sweeps_match_oracle_level_loop)."""
+    s = Setup("sat100", "par", "tc", 8192, init="multi")
+    s.cfg.fused_energy = 1  # as the binary sets it when every level is evaluated
+    s.cfg.level_blocks = blocks
+    nlev = 11
+    betas = np.linspace(1.0, 4.0, nlev).astype(np.float32)
+    niters = [1, 2, 1, 1, 1, 1, 2, 1, 1, 1, 1]
+    ev = [1, 0, 1, 1, 1, 0, 1, 1, 1, 0, 1]
+    a = s.per_level(betas, niters, ev)
+    b = s.level_loop(betas, niters, ev)
+    assert b["desc"].endswith(want), b["desc"]
+    assert "split_levels=" in b["desc"], b["desc"]
+    compare(s, a, b, ev)
+
+
 def test_level_loop_split_over_two_calls():
     s = Setup("sat100", "preorder", "tc", 256, 1)
     betas, niters, ev = schedule(10, 2, 2)

@@ -57,7 +57,7 @@ class Config(ctypes.Structure):
                 ("wide_waves", ctypes.c_int32), ("wide_wgs", ctypes.c_int32), ("fused_energy", ctypes.c_int32),
                 ("sums", ctypes.c_int32), ("wide_lanes", ctypes.c_int32),
                 ("track_overlap", ctypes.c_int32), ("draw_waves", ctypes.c_int32), ("wide_join", ctypes.c_int32),
-                ("level_loop", ctypes.c_int32)]
+                ("level_loop", ctypes.c_int32), ("level_blocks", ctypes.c_int32)]
 
 
 _lib = None
@@ -137,7 +137,7 @@ def layout(m, nlab, wide=False):
 def make_config(mode="tc", sc_target=20.0, sc_weight=1.0, seed=1, slicing=False, slice_moves=1, slice_every=1,
                 max_slices=0, par_follow=False, par_band=0, kernel=KERNEL_AUTO, gm=DEFAULT_GM, h100=DEFAULT_H100,
                 wide_waves=0, wide_wgs=0, fused_energy=False, sums=0, wide_lanes=0, track_overlap=0, draw_waves=0, wide_join=0,
-                level_loop=0):
+                level_loop=0, level_blocks=0):
     """Config with the fields the reference's Runner derives from its options (csrc/treesa_gpu.cu:1449-1474)."""
     k = splitmix64(seed)
     c = Config()
@@ -167,6 +167,7 @@ def make_config(mode="tc", sc_target=20.0, sc_weight=1.0, seed=1, slicing=False,
     c.draw_waves = int(draw_waves)  # pre-order: 0 automatic, 1 helper waves draw ahead, -1 each visit draws
     c.wide_join = int(wide_join)  # wide kernel, K > 1: check-in polls (0 default, -1 every chain swept alone)
     c.level_loop = int(level_loop)  # tsa_anneal: 0 automatic, 1 one launch whenever possible, -1 per-level launches
+    c.level_blocks = int(level_blocks)  # tsa_anneal's per-level path: levels per sweep launch (0 automatic, 1 one)
     return c
 
 

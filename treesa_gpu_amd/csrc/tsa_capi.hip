@@ -17,11 +17,10 @@
 #include "treesa_hip.h"
 #include "tsa_kernels.h"
 
-// Snapshot slots of the overlapped selection: a sweep launch takes the slot that the selection of
-// TSA_SNAP_SLOTS - 1 levels back read, so the host may enqueue that many levels ahead of the device.
-#ifndef TSA_SNAP_SLOTS
-#define TSA_SNAP_SLOTS 3
-#endif
+// Snapshot slots of the overlapped selection: an evaluated level's sweep takes the slot that the selection of
+// nslots - 1 levels back read, so the host may enqueue that many levels ahead of the device.  Three slots for
+// one level per launch, three per level of a block of levels (tsa_anneal), at most TSA_SNAP_MAX.
+#define TSA_SNAP_MAX (3 * TSA_BLOCK_MAX)
 
 struct tsa_ctx {
   tsa_layout_t lay;
@@ -82,8 +81,8 @@ struct tsa_ctx {
   TsaTrackPart* d_tpart = nullptr;  // selection kernel: per-workgroup results and its counter
   unsigned* d_tdone = nullptr;
   // Overlapped tracking (the wide path, and the one-wave kernels with fused energies): each sweep launch
-  // leaves a snapshot of every chain's tree and node costs (or energies) in slot `slot` (TSA_SNAP_SLOTS
-  // slots in turn), and tsa_track runs the fold and the selection of that snapshot on the second stream st2
+  // leaves a snapshot of every chain's tree and node costs (or energies) in slot `slot` (nslots slots in
+  // turn), and tsa_track runs the fold and the selection of that snapshot on the second stream st2
   // while st goes on with the next level's sweep.  ev_sweep[s] marks the sweep that filled slot s,
   // ev_track[s] the selection that read it (the host waits for it before a sweep overwrites the slot).
   bool overlap = false;
@@ -96,19 +95,26 @@ struct tsa_ctx {
   // launch of the sweep that filled slot s, when split_slot[s].
   hipStream_t st3 = nullptr;
   hipEvent_t ev_fork = nullptr, ev_join = nullptr;
-  hipEvent_t ev_b[TSA_SNAP_SLOTS] = {};
-  bool split_slot[TSA_SNAP_SLOTS] = {};
+  hipEvent_t ev_b[TSA_SNAP_MAX] = {};
+  bool split_slot[TSA_SNAP_MAX] = {};
   bool split_pending = false;  // st3 holds work st is not yet ordered after
+  // st holds work other than the first launches of split levels that st3 is not yet ordered after (every call
+  // but tsa_sweeps' split launches and the overlapped tsa_track goes through join_split, which sets it): only
+  // then does the next split level's second launch wait for st (ev_fork); otherwise it follows only st3's own
+  // previous launch, so that the two halves of the population run their levels independently (the snapshot
+  // slots keep them within a few levels of each other)
+  bool fork_needed = true;
   long long split_levels = 0;  // sweep calls run as two launches (reported by tsa_describe)
-  hipEvent_t ev_sweep[TSA_SNAP_SLOTS] = {};  // (the stop events of those sweeps' timing pairs)
-  hipEvent_t ev_track[TSA_SNAP_SLOTS] = {};
-  bool track_pending[TSA_SNAP_SLOTS] = {};
+  hipEvent_t ev_sweep[TSA_SNAP_MAX] = {};  // (the stop events of those sweeps' timing pairs)
+  hipEvent_t ev_track[TSA_SNAP_MAX] = {};
+  bool track_pending[TSA_SNAP_MAX] = {};
   int slot = 0, last_slot = -1;  // slot of the next sweep launch / of the last one (-1: none since a reset)
-  uint32_t* d_snap_ch[TSA_SNAP_SLOTS] = {};
-  float* d_snap_cost[TSA_SNAP_SLOTS] = {};
-  uint16_t* d_snap_nz[TSA_SNAP_SLOTS] = {};
-  uint32_t* d_snap_en[TSA_SNAP_SLOTS] = {};  // energies folded by the sweep kernel: lc, sc, ns per chain
-  int snap_kind[TSA_SNAP_SLOTS] = {};  // what the sweep that filled a slot left there: a SNAP_* value
+  int nslots = 0;                // slots allocated (their buffers), the ones in turn
+  uint32_t* d_snap_ch[TSA_SNAP_MAX] = {};
+  float* d_snap_cost[TSA_SNAP_MAX] = {};
+  uint16_t* d_snap_nz[TSA_SNAP_MAX] = {};
+  uint32_t* d_snap_en[TSA_SNAP_MAX] = {};  // energies folded by the sweep kernel: lc, sc, ns per chain
+  int snap_kind[TSA_SNAP_MAX] = {};  // what the sweep that filled a slot left there: a SNAP_* value
   // The level loop on the device (tsa_anneal, TsaLevels): the tracking session's kind (0: nothing tracked
   // yet, TRACK_LEVELS: tsa_track, TRACK_ANNEAL: tsa_anneal), whether the per-chain best still has to be
   // reset, the levels evaluated so far in the session, and the buffers, grown on demand.
@@ -119,6 +125,7 @@ struct tsa_ctx {
   int track_kind = 0;
   bool lv_reset = false;
   int lv_resident[6] = {-1, -1, -1, -1, -1, -1};  // level-loop chains resident per compute unit, per mode and order
+  int blocks_k = 0;   // levels per launch of tsa_anneal's last block path (reported by tsa_describe)
   int lv_used = -1;                               // whether the last tsa_anneal ran the level loop (-1: none yet)
   std::vector<char> lv_evaluated;
   int lv_cap_levels = 0, lv_cap_evals = 0;
@@ -309,7 +316,7 @@ static void free_ctx(tsa_ctx* c) {
       if (e) (void)hipEventDestroy(e);
     (void)hipStreamDestroy(c->st3);
   }
-  for (int k = 0; k < TSA_SNAP_SLOTS; k++) {
+  for (int k = 0; k < TSA_SNAP_MAX; k++) {
     if (c->ev_track[k]) (void)hipEventDestroy(c->ev_track[k]);
     if (c->d_snap_ch[k]) (void)hipFree(c->d_snap_ch[k]);
     if (c->d_snap_cost[k]) (void)hipFree(c->d_snap_cost[k]);
@@ -610,11 +617,12 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
 // d_sc / d_ns and write the tracking state), or wait for st2 on the host and forget the snapshots (before
 // the population is replaced).
 static void join_track(tsa_ctx* c) {
-  for (int k = 0; k < TSA_SNAP_SLOTS; k++)
+  for (int k = 0; k < TSA_SNAP_MAX; k++)
     if (c->track_pending[k]) (void)hipStreamWaitEvent(c->st, c->ev_track[k], 0);
 }
 
 static hipError_t join_split(tsa_ctx* c) {
+  c->fork_needed = true;  // the caller enqueues work on st
   if (!c->split_pending) return hipSuccess;
   c->split_pending = false;
   hipError_t e = hipEventRecord(c->ev_join, c->st3);
@@ -628,6 +636,20 @@ static hipError_t quiesce_track(tsa_ctx* c) {
   for (bool& p : c->track_pending) p = false;
   c->last_slot = -1;
   return e;
+}
+
+// Snapshot slots 0 .. n - 1 allocated (the slots in turn become n; the rotation goes on from where it is).
+static int ensure_slots(tsa_ctx* ctx, int n) {
+  if (n > TSA_SNAP_MAX) return fail(ctx, TSA_ERR_ARG, "snapshot slots: more than TSA_SNAP_MAX");
+  const size_t nint = (size_t)ctx->lay.nint, nint4 = (nint + 3) & ~(size_t)3;
+  for (int k = ctx->nslots; k < n; k++) {
+    TSA_HIP(ctx, hipMalloc(&ctx->d_snap_ch[k], (size_t)ctx->nchains * nint * 4));
+    TSA_HIP(ctx, hipMalloc(&ctx->d_snap_cost[k], (size_t)ctx->nchains * nint4 * 4));
+    TSA_HIP(ctx, hipMalloc(&ctx->d_snap_nz[k], (size_t)ctx->nchains * nint4 * 2));
+    TSA_HIP(ctx, hipMalloc(&ctx->d_snap_en[k], (size_t)ctx->nchains * 12));
+    ctx->nslots = k + 1;
+  }
+  return TSA_OK;
 }
 
 // Before a sweep overwrites snapshot slot s, the selection that last read it must be done.  The host waits
@@ -728,7 +750,11 @@ extern "C" int tsa_wait(tsa_ctx* ctx) {
   return TSA_OK;
 }
 
-extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0, int32_t nsweeps) {
+// tsa_sweeps, or with blk set (tsa_anneal; the one-wave kernels with the overlapped selection and the fold
+// apart) one launch (one split pair) of a block of levels, nsweeps = blk->total: every level with blk_ev[i] set
+// takes a snapshot slot of its own, returned in blk_slots[i] (-1: none), for tsa_track.
+static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0, int32_t nsweeps, const TsaBlock* blk,
+                       const uint8_t* blk_ev, int* blk_slots) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps: null context");
   if (order != TSA_ORDER_PAR && order != TSA_ORDER_PREORDER) return fail(ctx, TSA_ERR_ARG, "--order par|preorder");
   if (nsweeps < 0) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps: nsweeps < 0");
@@ -746,6 +772,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
   ctx->host_waited = false;
   hipEvent_t d0 = markers ? nullptr : e0, d1 = markers ? nullptr : e1;
   ctx->energy_fresh = ctx->energy_host = false;
+  if (blk && ctx->wide.on) return fail(ctx, TSA_ERR_ARG, "block of levels: not on the wide path");
   if (ctx->wide.on && order == TSA_ORDER_PAR) {
     TSA_HIP(ctx, join_split(ctx));
     // energies stay a separate fold of the node-cost cache: every chain ends its sweep at about the same
@@ -790,7 +817,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     if (s >= 0) {
       ctx->ev_sweep[s] = e1;  // the selection of this snapshot waits for the sweep's stop event
       ctx->last_slot = s;
-      ctx->slot = (s + 1) % TSA_SNAP_SLOTS;
+      ctx->slot = (s + 1) % ctx->nslots;
     }
     ctx->energy_fresh = fold_here;
   } else {
@@ -803,9 +830,32 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
     const bool split = ctx->overlap && apart && h > 0 && h < ctx->nchains;
     if (!split) TSA_HIP(ctx, join_split(ctx));
     TsaEnergyOut eo{fuse && !apart ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns, apart ? ctx->d_ncost : nullptr,
-                    apart ? ctx->d_nz : nullptr, nullptr};
+                    apart ? ctx->d_nz : nullptr, nullptr, TsaBlock{}};
     int s = -1;
-    if (ctx->overlap && fuse) {
+    if (blk) {
+      if (!ctx->overlap || !apart || order != TSA_ORDER_PAR || blk->n < 1 || blk->n > TSA_BLOCK_MAX ||
+          blk->total != nsweeps)
+        return fail(ctx, TSA_ERR_ARG, "block of levels: needs the overlapped selection with the fold apart, par order");
+      // the block's evaluated levels leave their snapshots in slots of their own, folded and selected on st2
+      eo.cost = nullptr;
+      eo.z = nullptr;
+      eo.blk = *blk;
+      for (int i = 0; i < blk->n; i++) {
+        blk_slots[i] = -1;
+        eo.blk.cost[i] = nullptr;
+        eo.blk.z[i] = nullptr;
+        eo.blk.ch[i] = nullptr;
+        if (!blk_ev[i]) continue;
+        const int t = ctx->slot;
+        TSA_HIP(ctx, claim_slot(ctx, t));
+        ctx->snap_kind[t] = SNAP_COSTS;
+        eo.blk.cost[i] = ctx->d_snap_cost[t];
+        eo.blk.z[i] = ctx->d_snap_nz[t];
+        eo.blk.ch[i] = ctx->d_snap_ch[t];
+        blk_slots[i] = t;
+        ctx->slot = (t + 1) % ctx->nslots;
+      }
+    } else if (ctx->overlap && fuse) {
       // node costs (or, folded in the kernel, energies) and children words go to snapshot slot s, folded and
       // selected on st2 by tsa_track
       s = ctx->slot;
@@ -837,13 +887,16 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
         TSA_HIP(ctx, hipStreamCreateWithFlags(&ctx->st3, hipStreamNonBlocking));
         TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_fork, hipEventDisableTiming));
         TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_join, hipEventDisableTiming));
-        for (int k = 0; k < TSA_SNAP_SLOTS; k++)
+        for (int k = 0; k < TSA_SNAP_MAX; k++)
           TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_b[k], hipEventDisableTiming));
       }
       // the second launch's timing pair follows the first's
       hipEvent_t f0 = ctx->ev[2 * ctx->npending + 2], f1 = ctx->ev[2 * ctx->npending + 3];
-      TSA_HIP(ctx, hipEventRecord(ctx->ev_fork, ctx->st));
-      TSA_HIP(ctx, hipStreamWaitEvent(ctx->st3, ctx->ev_fork, 0));
+      if (ctx->fork_needed) {
+        TSA_HIP(ctx, hipEventRecord(ctx->ev_fork, ctx->st));
+        TSA_HIP(ctx, hipStreamWaitEvent(ctx->st3, ctx->ev_fork, 0));
+        ctx->fork_needed = false;
+      }
       if (markers) TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
       TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, h, beta,
                                      sweep0, nsweeps, ctx->d_stats, eo, ctx->st, d0, d1));
@@ -855,7 +908,12 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
                                      ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st3,
                                      markers ? nullptr : f0, markers ? nullptr : f1));
       if (markers) TSA_HIP(ctx, hipEventRecord(f1, ctx->st3));
-      TSA_HIP(ctx, hipEventRecord(ctx->ev_b[s], ctx->st3));
+      if (blk) {
+        for (int i = 0; i < blk->n; i++)
+          if (blk_slots[i] >= 0) TSA_HIP(ctx, hipEventRecord(ctx->ev_b[blk_slots[i]], ctx->st3));
+      } else {
+        TSA_HIP(ctx, hipEventRecord(ctx->ev_b[s], ctx->st3));
+      }
       ctx->split_pending = true;
       ctx->split_levels++;
       ctx->npending++;  // (the first launch's pair is counted below)
@@ -865,11 +923,20 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
                                      ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st, d0, d1));
       if (markers) TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
     }
-    if (s >= 0) {
+    if (blk) {
+      for (int i = 0; i < blk->n; i++) {
+        const int t = blk_slots[i];
+        if (t < 0) continue;
+        ctx->split_slot[t] = split;
+        ctx->ev_sweep[t] = e1;
+        ctx->last_slot = t;
+      }
+      ctx->energy_fresh = false;
+    } else if (s >= 0) {
       ctx->split_slot[s] = split;
       ctx->ev_sweep[s] = e1;
       ctx->last_slot = s;
-      ctx->slot = (s + 1) % TSA_SNAP_SLOTS;
+      ctx->slot = (s + 1) % ctx->nslots;
       ctx->energy_fresh = false;  // the energies of this population exist only once tsa_track folds the slot
     } else {
       if (apart)
@@ -880,6 +947,10 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
   }
   ctx->npending++;
   return TSA_OK;
+}
+
+extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0, int32_t nsweeps) {
+  return sweeps_impl(ctx, order, beta, sweep0, nsweeps, nullptr, nullptr, nullptr);
 }
 
 extern "C" int tsa_sweeps_ms(tsa_ctx* ctx, double* ms) {
@@ -927,9 +998,12 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   if (!ctx->d_ticks0) TSA_HIP(ctx, hipMalloc(&ctx->d_ticks0, sizeof(unsigned long long)));
   if (!ctx->d_best) TSA_HIP(ctx, hipMalloc(&ctx->d_best, (size_t)ctx->lay.chain_words * 8));
   if (!ctx->d_tpart) {
-    TSA_HIP(ctx, hipMalloc(&ctx->d_tpart, (size_t)((ctx->nchains + 255) / 256) * sizeof(TsaTrackPart)));
-    TSA_HIP(ctx, hipMalloc(&ctx->d_tdone, sizeof(unsigned)));
-    TSA_HIP(ctx, hipMemsetAsync(ctx->d_tdone, 0, sizeof(unsigned), ctx->st));
+    // (room for a selection launch of TSA_BLOCK_MAX levels: per level its groups' results and counter, then
+    // each level's best and the launch's counter)
+    TSA_HIP(ctx, hipMalloc(&ctx->d_tpart,
+                           (size_t)(TSA_BLOCK_MAX + 1) * ((ctx->nchains + 255) / 256) * sizeof(TsaTrackPart)));
+    TSA_HIP(ctx, hipMalloc(&ctx->d_tdone, (TSA_BLOCK_MAX + 1) * sizeof(unsigned)));
+    TSA_HIP(ctx, hipMemsetAsync(ctx->d_tdone, 0, (TSA_BLOCK_MAX + 1) * sizeof(unsigned), ctx->st));
   }
   if (max_levels > ctx->track_levels) {
     if (ctx->d_trace) TSA_HIP(ctx, hipFree(ctx->d_trace));
@@ -976,16 +1050,11 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
       ((ctx->wide.on && ctx->wide.K == 1 && ctx->nchains < ctx->ncu) ||
        (!ctx->wide.on && ctx->cfg.fused_energy != 0 && !ctx->cfg.slicing));
   if (want_overlap && !ctx->st2) {
-    const size_t nint = (size_t)ctx->lay.nint, nint4 = (nint + 3) & ~(size_t)3;
     TSA_HIP(ctx, hipStreamCreateWithFlags(&ctx->st2, hipStreamNonBlocking));
-    for (int k = 0; k < TSA_SNAP_SLOTS; k++) {
+    for (int k = 0; k < TSA_SNAP_MAX; k++)
       TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_track[k], hipEventDisableTiming));
-      TSA_HIP(ctx, hipMalloc(&ctx->d_snap_ch[k], (size_t)ctx->nchains * nint * 4));
-      TSA_HIP(ctx, hipMalloc(&ctx->d_snap_cost[k], (size_t)ctx->nchains * nint4 * 4));
-      TSA_HIP(ctx, hipMalloc(&ctx->d_snap_nz[k], (size_t)ctx->nchains * nint4 * 2));
-      TSA_HIP(ctx, hipMalloc(&ctx->d_snap_en[k], (size_t)ctx->nchains * 12));
-    }
   }
+  if (want_overlap && ensure_slots(ctx, 3) != TSA_OK) return TSA_ERR_HIP;
   ctx->overlap = want_overlap;
   ctx->slot = 0;
   ctx->track_kind = 0;
@@ -996,6 +1065,49 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
                                      (int)((size_t)max_levels * sizeof(TsaTraceRowD) / 8),
                                      reinterpret_cast<unsigned long long*>(ctx->d_best), ctx->lay.chain_words,
                                      ctx->st));
+  return TSA_OK;
+}
+
+// The fold and the selection of the evaluated levels of one block of levels (tsa_anneal), on st2 beside the next
+// block's sweeps: one fold launch for all of their snapshots (each level's energies into its own slot) and one
+// selection launch that writes their trace rows and keeps the best in level order.
+static int track_block(tsa_ctx* ctx, const int* slots, const int* levels, int n) {
+  if (n == 0) return TSA_OK;
+  ctx->track_kind = TRACK_LEVELS;
+  TsaSelect S = ctx->sel;
+  S.mode = ctx->mode;
+  const tsa_layout_t& L = ctx->lay;
+  TsaFoldLevels F{};
+  TsaTrackLevels T{};
+  F.n = T.n = n;
+  for (int i = 0; i < n; i++) {
+    const int s = slots[i];
+    if (i == 0 || ctx->ev_sweep[s] != ctx->ev_sweep[slots[i - 1]]) {
+      TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_sweep[s], 0));
+      if (ctx->split_slot[s]) TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_b[s], 0));
+    }
+    float* lc = reinterpret_cast<float*>(ctx->d_snap_en[s]);
+    int* sc = reinterpret_cast<int*>(ctx->d_snap_en[s]) + ctx->nchains;
+    int* ns = reinterpret_cast<int*>(ctx->d_snap_en[s]) + 2 * (size_t)ctx->nchains;
+    F.cost[i] = ctx->d_snap_cost[s];
+    F.z[i] = ctx->d_snap_nz[s];
+    F.lc[i] = lc;
+    F.sc[i] = sc;
+    F.ns[i] = ns;
+    T.lev[i] = levels[i];
+    T.lc[i] = lc;
+    T.sc[i] = sc;
+    T.ns[i] = ns;
+    T.ch[i] = ctx->d_snap_ch[s];
+  }
+  TSA_HIP(ctx, tsa_launch_fold_levels(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, F, ctx->nchains, ctx->st2));
+  TSA_HIP(ctx, tsa_launch_track_levels(T, ctx->nchains, S, ctx->d_rec, L.chain_words, L.ch_off, L.s_off, L.W, L.nint,
+                                       ctx->d_track, ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2));
+  for (int i = 0; i < n; i++) {
+    TSA_HIP(ctx, hipEventRecord(ctx->ev_track[slots[i]], ctx->st2));
+    ctx->track_pending[slots[i]] = true;
+  }
+  ctx->energy_fresh = false;
   return TSA_OK;
 }
 
@@ -1184,6 +1296,45 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
     }
   }
   ctx->lv_used = loop ? 1 : 0;
+  // Several levels per sweep launch (the one-wave LDS kernels with the overlapped selection and the fold apart,
+  // where the population is more than twice what the device holds at once): a launch ends with a tail in which
+  // fewer and fewer chains are left to run, and a level of one sweep per chain is short next to it; a block of
+  // levels has one tail for all of them.  Each evaluated level of a block leaves its snapshot in a slot of its
+  // own, whose fold and selection tsa_track runs as for one level.
+  if (ctx->cfg.level_blocks < 0 || ctx->cfg.level_blocks > TSA_BLOCK_MAX)
+    return fail(ctx, TSA_ERR_ARG, "tsa_config_t.level_blocks: 0 (automatic) or 1..8");
+  const int K = ctx->cfg.level_blocks > 0 ? ctx->cfg.level_blocks : TSA_BLOCK_MAX;
+  if (!loop && K > 1 && ctx->overlap && !ctx->wide.on && ctx->L.lds && ctx->cfg.fused_energy != 0 &&
+      ctx->fold_apart && !ctx->cfg.slicing && order == TSA_ORDER_PAR) {
+    ctx->lv_used = 2;
+    ctx->blocks_k = K;
+    if (ensure_slots(ctx, 3 * K) != TSA_OK) return TSA_ERR_HIP;
+    uint32_t sw = sweep0;
+    for (int l = 0; l < nlevels; l += K) {
+      TsaBlock blk{};
+      uint8_t bev[TSA_BLOCK_MAX];
+      int slots[TSA_BLOCK_MAX];
+      blk.n = nlevels - l < K ? nlevels - l : K;
+      for (int i = 0; i < blk.n; i++) {
+        blk.beta[i] = betas[l + i];
+        blk.niters[i] = niters[l + i];
+        blk.total += niters[l + i];
+        bev[i] = evaluated[l + i] != 0;
+      }
+      int rc = sweeps_impl(ctx, order, blk.beta[0], sw, blk.total, &blk, bev, slots);
+      if (rc != TSA_OK) return rc;
+      sw += (uint32_t)blk.total;
+      int es[TSA_BLOCK_MAX], el[TSA_BLOCK_MAX], ne = 0;
+      for (int i = 0; i < blk.n; i++) {
+        if (slots[i] < 0) continue;
+        es[ne] = slots[i];
+        el[ne++] = level0 + l + i;
+      }
+      rc = track_block(ctx, es, el, ne);
+      if (rc != TSA_OK) return rc;
+    }
+    return TSA_OK;
+  }
   if (!loop) {  // one sweep launch per level, a selection at each evaluated one
     uint32_t sw = sweep0;
     for (int l = 0; l < nlevels; l++) {
@@ -1338,8 +1489,10 @@ extern "C" int tsa_describe(tsa_ctx* ctx, char* buf, int32_t len) {
   if (!ctx || !buf || len < 1) return fail(ctx, TSA_ERR_ARG, "tsa_describe: null argument");
   char sp[48] = "";
   if (ctx->split_levels > 0) snprintf(sp, sizeof sp, " split_levels=%lld", ctx->split_levels);
-  snprintf(buf, (size_t)len, "%s%s%s", ctx->kname.c_str(), sp,
-           ctx->lv_used < 0 ? "" : (ctx->lv_used ? " anneal=level_loop" : " anneal=level_launches"));
+  char an[40] = "";
+  if (ctx->lv_used == 2) snprintf(an, sizeof an, " anneal=level_blocks%d", ctx->blocks_k);
+  else if (ctx->lv_used >= 0) snprintf(an, sizeof an, "%s", ctx->lv_used ? " anneal=level_loop" : " anneal=level_launches");
+  snprintf(buf, (size_t)len, "%s%s%s", ctx->kname.c_str(), sp, an);
   return TSA_OK;
 }
 

@@ -55,6 +55,20 @@ static inline int tsa_draw_words(int nint) { return 2 * ((nint + 3) & ~3); }
 // or, with cost set, only every node's cost and masked size (cost / z + chain * nint4; k_fold folds them);
 // with ch set, also a copy of every chain's children words (ch + chain * nint): a snapshot of the trees those
 // energies describe, which the selection reads while the next sweep rewrites the records.
+// Several levels in one par sweep launch (n > 0; not the level loop): level i has niters[i] sweeps at beta[i]
+// (total sweeps in all), and after its last sweep every chain leaves its node costs, masked sizes and children
+// words in cost[i] / z[i] / ch[i] (+ chain * nint4, nint4, nint; the snapshot slot that the level's fold and
+// selection read; null: the level is not evaluated).  The chain stays staged from its first level to its last.
+#define TSA_BLOCK_MAX 8
+struct TsaBlock {
+  int n, total;
+  float beta[TSA_BLOCK_MAX];
+  int niters[TSA_BLOCK_MAX];
+  float* cost[TSA_BLOCK_MAX];
+  uint16_t* z[TSA_BLOCK_MAX];
+  uint32_t* ch[TSA_BLOCK_MAX];
+};
+
 struct TsaEnergyOut {
   float* lc;
   int* sc;
@@ -62,6 +76,7 @@ struct TsaEnergyOut {
   float* cost;
   uint16_t* z;
   uint32_t* ch;
+  TsaBlock blk;  // (blk.n == 0: the launch is one level of nsweeps sweeps at beta)
 };
 
 struct TsaTrackPart;
@@ -133,6 +148,17 @@ hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64
 hipError_t tsa_launch_fold(const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf, const uint32_t* fix,
                            const float* cost, const uint16_t* z, int nchains, float* lc, int* sc, int* ns,
                            hipStream_t st);
+// The same for several levels' snapshots in one launch: level i folds cost[i] / z[i] into lc[i] / sc[i] / ns[i].
+struct TsaFoldLevels {
+  int n;
+  const float* cost[TSA_BLOCK_MAX];
+  const uint16_t* z[TSA_BLOCK_MAX];
+  float* lc[TSA_BLOCK_MAX];
+  int* sc[TSA_BLOCK_MAX];
+  int* ns[TSA_BLOCK_MAX];
+};
+hipError_t tsa_launch_fold_levels(const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf, const uint32_t* fix,
+                                  const TsaFoldLevels& F, int nchains, hipStream_t st);
 struct TsaTrackState {
   double best_score;
   int best_chain, best_level;
@@ -149,10 +175,24 @@ struct TsaTrackPart {
   double score, sumE, sumNs;
   int idx;
 };
-// part: ceil(nchains / 256) entries; done: one zeroed counter (left zero after every launch).  When a level
-// improves the best score, the chain's tree is copied into best_rec: its children words (from ch_snap,
-// nint words per chain, when not null, else from rec) and its S words (from rec); label words are left as
-// they are.
+// Levels of one selection launch, in level order: level i writes trace row lev[i] from the energies lc[i] /
+// sc[i] / ns[i] of the trees whose children words are ch[i] (nint words per chain; null: the records' own).
+struct TsaTrackLevels {
+  int n;
+  int lev[TSA_BLOCK_MAX];
+  const float* lc[TSA_BLOCK_MAX];
+  const int* sc[TSA_BLOCK_MAX];
+  const int* ns[TSA_BLOCK_MAX];
+  const uint32_t* ch[TSA_BLOCK_MAX];
+};
+// part: (L.n + 1) * ceil(nchains / 256) entries; done: L.n + 1 zeroed counters (left zero after every launch).
+// When a level improves the best score, the chain's tree is copied into best_rec: its children words (from
+// L.ch, when not null, else from rec) and its S words (from rec); label words are left as they are.
+hipError_t tsa_launch_track_levels(const TsaTrackLevels& L, int nchains, const TsaSelect& S, const uint64_t* rec,
+                                   int chain_words, int ch_off, int s_off, int W, int nint, TsaTrackState* st,
+                                   TsaTraceRowD* trace, uint64_t* best_rec, TsaTrackPart* part, unsigned* done,
+                                   hipStream_t stream);
+// One level: lc / sc / ns, trace row `level`, children words ch_snap.
 hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int nchains, const TsaSelect& S, int level,
                             const uint64_t* rec, int chain_words, int ch_off, int s_off, int W, int nint,
                             const uint32_t* ch_snap, TsaTrackState* st, TsaTraceRowD* trace, uint64_t* best_rec,

@@ -4,12 +4,17 @@
 
 // Per-chain energy from node costs a sweep launch left (TsaEnergyOut.cost / z), one 32-lane half-wave per
 // chain: the reference's fold (csrc/treesa_gpu.cu:386-434) of every chain at once, instead of at the end of
-// each chain's sweep, where the serial lse chain is paid once per round of resident chains.
+// each chain's sweep, where the serial lse chain is paid once per round of resident chains.  blockIdx.y: the
+// level (several levels' snapshots fold in one launch).
 __global__ void __launch_bounds__(256) k_fold(TsaKParams P, const uint64_t* __restrict__ rec,
                                               const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
-                                              const float* __restrict__ cost, const uint16_t* __restrict__ z,
-                                              int nchains, float* __restrict__ lc, int* __restrict__ sc,
-                                              int* __restrict__ ns) {
+                                              TsaFoldLevels F, int nchains) {
+  const int li = (int)blockIdx.y;
+  const float* __restrict__ cost = F.cost[li];
+  const uint16_t* __restrict__ z = F.z[li];
+  float* __restrict__ lc = F.lc[li];
+  int* __restrict__ sc = F.sc[li];
+  int* __restrict__ ns = F.ns[li];
   __shared__ uint64_t s_exp2[32];
   if (threadIdx.x < 32) s_exp2[threadIdx.x] = tsa_exp2_tab_d[threadIdx.x];
   __syncthreads();
@@ -30,8 +35,21 @@ __global__ void __launch_bounds__(256) k_fold(TsaKParams P, const uint64_t* __re
 hipError_t tsa_launch_fold(const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf, const uint32_t* fix,
                            const float* cost, const uint16_t* z, int nchains, float* lc, int* sc, int* ns,
                            hipStream_t st) {
+  TsaFoldLevels F{};
+  F.n = 1;
+  F.cost[0] = cost;
+  F.z[0] = z;
+  F.lc[0] = lc;
+  F.sc[0] = sc;
+  F.ns[0] = ns;
+  return tsa_launch_fold_levels(P, rec, leaf, fix, F, nchains, st);
+}
+
+hipError_t tsa_launch_fold_levels(const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf, const uint32_t* fix,
+                                  const TsaFoldLevels& F, int nchains, hipStream_t st) {
+  if (F.n < 1 || F.n > TSA_BLOCK_MAX) return hipErrorInvalidValue;
   const int threads = 256, grid = (nchains * 32 + threads - 1) / threads;
-  hipLaunchKernelGGL(k_fold, dim3(grid), dim3(threads), 0, st, P, rec, leaf, fix, cost, z, nchains, lc, sc, ns);
+  hipLaunchKernelGGL(k_fold, dim3(grid, F.n), dim3(threads), 0, st, P, rec, leaf, fix, F, nchains);
   return hipGetLastError();
 }
 
@@ -67,121 +85,135 @@ __global__ void __launch_bounds__(256) k_copy(const uint4* __restrict__ src, uin
   for (int i = threadIdx.x; i < n4; i += blockDim.x) d[i] = s[i];
 }
 
-// Best tracking of one level (csrc/treesa_gpu.cu:1810-1832): every chain scored by its own thread, argmin
-// with the lowest index on ties and the population sums reduced per workgroup of 256 in a fixed tree order,
-// then the last workgroup to finish reduces the per-workgroup results in index order, writes the trace
-// row, keeps the best so far and snapshots it when it improves.  Sums are therefore deterministic.
-__global__ void __launch_bounds__(256) k_track(const float* __restrict__ lc, const int* __restrict__ sc,
-                                               const int* __restrict__ ns, int n, TsaSelect S, int level,
-                                               const uint64_t* __restrict__ rec, int chain_words, int ch_off,
-                                               int s_off, int W, int nint, const uint32_t* __restrict__ ch_snap,
-                                               TsaTrackState* __restrict__ st, TsaTraceRowD* __restrict__ trace,
-                                               uint64_t* __restrict__ best_rec, TsaTrackPart* __restrict__ part,
-                                               unsigned* __restrict__ done) {
-  __shared__ double s_s[256], s_e[256], s_n[256];
-  __shared__ int s_i[256];
-  __shared__ int s_last, s_copy, s_bi;
-  const int t = threadIdx.x, c = blockIdx.x * 256 + t;
-  double bs = INFINITY, se = 0.0, sn = 0.0;
-  int bi = n;
-  if (c < n) {
-    bs = tsa_score(lc[c], sc[c], ns[c], S);
-    bi = bs < INFINITY ? c : n;
-    se = tsa_energyE(lc[c], sc[c], ns[c], S);
-    sn = (double)ns[c];
+// One entry of the selection's reduction: best score and its chain, sums of E and |S|.
+struct TsaTrackAcc {
+  double s, e, n;
+  int i;
+};
+
+// a (lower position) combined with b: the lower score, the lower chain on ties; the sums added.
+__device__ __forceinline__ void tsa_track_comb(TsaTrackAcc& a, const TsaTrackAcc& b) {
+  if (b.s < a.s || (b.s == a.s && b.i < a.i)) {
+    a.s = b.s;
+    a.i = b.i;
   }
-  s_s[t] = bs;
-  s_i[t] = bi;
-  s_e[t] = se;
-  s_n[t] = sn;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (t < o) {
-      const double a = s_s[t], b = s_s[t + o];
-      const int ia = s_i[t], ib = s_i[t + o];
-      if (b < a || (b == a && ib < ia)) {
-        s_s[t] = b;
-        s_i[t] = ib;
-      }
-      s_e[t] += s_e[t + o];
-      s_n[t] += s_n[t + o];
+  a.e += b.e;
+  a.n += b.n;
+}
+
+// 256 entries (entry t = lane + 64 j in v[j]) reduced in the order of a halving tree over 256 positions
+// (position t takes t + 128, then t + 64, then 32, 16, ..., 1) by one wave: lane 0 returns the result.
+__device__ __forceinline__ TsaTrackAcc tsa_track_tree(TsaTrackAcc (&v)[4], int lane) {
+  tsa_track_comb(v[0], v[2]);
+  tsa_track_comb(v[1], v[3]);
+  tsa_track_comb(v[0], v[1]);
+  for (int o = 32; o > 0; o >>= 1) {
+    TsaTrackAcc b;
+    b.s = __shfl_down(v[0].s, o);
+    b.e = __shfl_down(v[0].e, o);
+    b.n = __shfl_down(v[0].n, o);
+    b.i = __shfl_down(v[0].i, o);
+    if (lane < o) tsa_track_comb(v[0], b);
+  }
+  return v[0];
+}
+
+// Best tracking of L.n levels (csrc/treesa_gpu.cu:1810-1832), one wave per group of 256 chains and level
+// (blockIdx.y): every chain scored, argmin with the lowest index on ties and the population sums reduced per
+// group in a fixed tree order; the last group of a level to finish reduces the groups' results in index order
+// and writes the level's trace row; the last level to finish keeps the best over the launch's levels in level
+// order (the lowest score; the first level on ties, as one launch per level would) and copies the new best
+// chain's tree.  No LDS, so that the selection's waves fit beside sweep workgroups that fill a compute unit's
+// LDS.  Sums are deterministic.
+__global__ void __launch_bounds__(64) k_track(TsaTrackLevels L, int n, TsaSelect S, const uint64_t* __restrict__ rec,
+                                              int chain_words, int ch_off, int s_off, int W, int nint,
+                                              TsaTrackState* __restrict__ st, TsaTraceRowD* __restrict__ trace,
+                                              uint64_t* __restrict__ best_rec, TsaTrackPart* __restrict__ part,
+                                              unsigned* __restrict__ done) {
+  const int lane = (int)threadIdx.x, g = (int)blockIdx.x, li = (int)blockIdx.y, G = (int)gridDim.x;
+  const float* __restrict__ lc = L.lc[li];
+  const int* __restrict__ sc = L.sc[li];
+  const int* __restrict__ ns = L.ns[li];
+  TsaTrackAcc v[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int c = g * 256 + lane + 64 * j;
+    v[j] = TsaTrackAcc{INFINITY, 0.0, 0.0, n};
+    if (c < n) {
+      const double s = tsa_score(lc[c], sc[c], ns[c], S);
+      v[j].s = s;
+      v[j].i = s < INFINITY ? c : n;
+      v[j].e = tsa_energyE(lc[c], sc[c], ns[c], S);
+      v[j].n = (double)ns[c];
     }
-    __syncthreads();
   }
-  if (t == 0) {
-    part[blockIdx.x] = TsaTrackPart{s_s[0], s_e[0], s_n[0], s_i[0]};
+  const TsaTrackAcc r = tsa_track_tree(v, lane);
+  int last = 0;
+  if (lane == 0) {
+    part[li * G + g] = TsaTrackPart{r.s, r.e, r.n, r.i};
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    const unsigned old = __hip_atomic_fetch_add(done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int last = old == gridDim.x - 1;
-    if (last) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      __hip_atomic_store(done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    s_last = last;
+    const unsigned old = __hip_atomic_fetch_add(done + li, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last = old == (unsigned)G - 1u;
+    if (last) __hip_atomic_store(done + li, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();
-  if (!s_last) return;
-  // the per-workgroup results, in workgroup order: thread t folds workgroups t, t+256, ... then a tree
-  bs = INFINITY;
-  bi = n;
-  se = 0.0;
-  sn = 0.0;
-  for (int k = t; k < (int)gridDim.x; k += 256) {
-    const TsaTrackPart q = part[k];
-    if (q.score < bs || (q.score == bs && q.idx < bi)) {
-      bs = q.score;
-      bi = q.idx;
+  if (!__shfl(last, 0)) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // the level's group results, in group order: position t (= lane + 64 j) folds groups t, t + 256, ... then the
+  // same tree
+  TsaTrackAcc w[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    w[j] = TsaTrackAcc{INFINITY, 0.0, 0.0, n};
+    for (int k = lane + 64 * j; k < G; k += 256) {
+      const TsaTrackPart q = part[li * G + k];
+      tsa_track_comb(w[j], TsaTrackAcc{q.score, q.sumE, q.sumNs, q.idx});
     }
-    se += q.sumE;
-    sn += q.sumNs;
   }
-  s_s[t] = bs;
-  s_i[t] = bi;
-  s_e[t] = se;
-  s_n[t] = sn;
-  __syncthreads();
-  for (int o = 128; o > 0; o >>= 1) {
-    if (t < o) {
-      const double a = s_s[t], b = s_s[t + o];
-      const int ia = s_i[t], ib = s_i[t + o];
-      if (b < a || (b == a && ib < ia)) {
-        s_s[t] = b;
-        s_i[t] = ib;
-      }
-      s_e[t] += s_e[t + o];
-      s_n[t] += s_n[t + o];
-    }
-    __syncthreads();
-  }
-  if (t == 0) {
-    const int b = s_i[0];
+  const TsaTrackAcc a = tsa_track_tree(w, lane);
+  int blast = 0;
+  if (lane == 0) {
+    const int b = a.i;
     TsaTraceRowD row;
     row.chain = b < n ? b : -1;
     row.lc = b < n ? lc[b] : 0.0f;
     row.sc = b < n ? sc[b] : 0;
     row.ns = b < n ? ns[b] : 0;
-    row.score = s_s[0];
-    row.meanE = s_e[0] / n;
-    row.meanNs = s_n[0] / n;
+    row.score = a.s;
+    row.meanE = a.e / n;
+    row.meanNs = a.n / n;
     row.ticks = wall_clock64();
-    trace[level] = row;
-    const bool better = b < n && s_s[0] < st->best_score;
-    if (better) {
-      st->best_score = s_s[0];
-      st->best_chain = b;
-      st->best_level = level;
-    }
-    st->snap = better ? b : -1;
-    s_copy = better ? 1 : 0;
-    s_bi = b;
+    trace[L.lev[li]] = row;
+    part[L.n * G + li] = TsaTrackPart{a.s, 0.0, 0.0, b};  // the level's best, for the launch's last level
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+    const unsigned old = __hip_atomic_fetch_add(done + L.n, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    blast = old == (unsigned)L.n - 1u;
+    if (blast) __hip_atomic_store(done + L.n, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  __syncthreads();
-  if (s_copy) {  // the new best chain's tree: children words and S (label words follow from the tree)
-    const uint64_t* src = rec + (size_t)s_bi * chain_words;
-    const uint32_t* chs = ch_snap ? ch_snap + (size_t)s_bi * nint : reinterpret_cast<const uint32_t*>(src + ch_off);
+  if (!__shfl(blast, 0)) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  int win = -1, wc = 0;
+  if (lane == 0) {
+    for (int i = 0; i < L.n; i++) {
+      const TsaTrackPart q = part[L.n * G + i];
+      const bool better = q.idx < n && q.score < st->best_score;
+      if (better) {
+        st->best_score = q.score;
+        st->best_chain = q.idx;
+        st->best_level = L.lev[i];
+        win = i;
+        wc = q.idx;
+      }
+      st->snap = better ? q.idx : -1;
+    }
+  }
+  win = __shfl(win, 0);
+  wc = __shfl(wc, 0);
+  if (win >= 0) {  // the new best chain's tree: children words and S (label words follow from the tree)
+    const uint64_t* src = rec + (size_t)wc * chain_words;
+    const uint32_t* chs = L.ch[win] ? L.ch[win] + (size_t)wc * nint : reinterpret_cast<const uint32_t*>(src + ch_off);
     uint32_t* chd = reinterpret_cast<uint32_t*>(best_rec + ch_off);
-    for (int i = t; i < nint; i += 256) chd[i] = chs[i];
-    for (int w = t; w < W; w += 256) best_rec[s_off + w] = src[s_off + w];
+    for (int i = lane; i < nint; i += 64) chd[i] = chs[i];
+    for (int x = lane; x < W; x += 64) best_rec[s_off + x] = src[s_off + x];
   }
 }
 
@@ -246,13 +278,29 @@ hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64
   }
 }
 
+hipError_t tsa_launch_track_levels(const TsaTrackLevels& L, int nchains, const TsaSelect& S, const uint64_t* rec,
+                                   int chain_words, int ch_off, int s_off, int W, int nint, TsaTrackState* stt,
+                                   TsaTraceRowD* trace, uint64_t* best_rec, TsaTrackPart* part, unsigned* done,
+                                   hipStream_t stream) {
+  if (L.n < 1 || L.n > TSA_BLOCK_MAX || nchains < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_track, dim3((nchains + 255) / 256, L.n), dim3(64), 0, stream, L, nchains, S, rec, chain_words,
+                     ch_off, s_off, W, nint, stt, trace, best_rec, part, done);
+  return hipGetLastError();
+}
+
 hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int nchains, const TsaSelect& S, int level,
                             const uint64_t* rec, int chain_words, int ch_off, int s_off, int W, int nint,
                             const uint32_t* ch_snap, TsaTrackState* stt, TsaTraceRowD* trace, uint64_t* best_rec,
                             TsaTrackPart* part, unsigned* done, hipStream_t stream) {
-  hipLaunchKernelGGL(k_track, dim3((nchains + 255) / 256), dim3(256), 0, stream, lc, sc, ns, nchains, S, level, rec,
-                     chain_words, ch_off, s_off, W, nint, ch_snap, stt, trace, best_rec, part, done);
-  return hipGetLastError();
+  TsaTrackLevels L{};
+  L.n = 1;
+  L.lev[0] = level;
+  L.lc[0] = lc;
+  L.sc[0] = sc;
+  L.ns[0] = ns;
+  L.ch[0] = ch_snap;
+  return tsa_launch_track_levels(L, nchains, S, rec, chain_words, ch_off, s_off, W, nint, stt, trace, best_rec, part,
+                                 done, stream);
 }
 
 hipError_t tsa_launch_track_init(TsaTrackState* stt, unsigned long long* ticks0, unsigned long long* trace,

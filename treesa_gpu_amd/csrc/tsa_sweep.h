@@ -670,9 +670,11 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
   // the level loop (Lv.nlev > 0) or the launch's one level: sweeps in all, the current level, its sweeps left
   // and beta; the chain's best score and the candidate slot of its tree, kept by the wave that tracks the chain
   // (wave 1 with helpers, else the chain's wave)
-  const int nsw = LVL ? Lv.total : nsweeps;
-  int lv = 0, left = LVL ? Lv.niters[0] : nsweeps;
-  float beta = LVL ? Lv.beta[0] : beta1;
+  // (or a block of levels, eo.blk: their sweeps in all, the current level, its sweeps left and its beta)
+  const bool blocked = !LVL && ORDER == 0 && eo.blk.n > 0;
+  const int nsw = LVL ? Lv.total : (blocked ? eo.blk.total : nsweeps);
+  int lv = 0, left = LVL ? Lv.niters[0] : (blocked ? eo.blk.niters[0] : nsweeps);
+  float beta = LVL ? Lv.beta[0] : (blocked ? eo.blk.beta[0] : beta1);
   const bool tracker = LVL && (!helped || wv == 1);
   TsaOwn own{INFINITY, -1};
   if (tracker) own = TsaOwn{Lv.own[c], Lv.bslot[c]};
@@ -841,6 +843,24 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
             left = Lv.niters[lv];
           }
         }
+      } else {
+        if (blocked && --left == 0) {  // a block's level ends: its snapshot (node costs, sizes, children words)
+          if (eo.blk.cost[lv]) {
+            float* const gc = eo.blk.cost[lv] + (size_t)c * nint4;
+            uint16_t* const gz = eo.blk.z[lv] + (size_t)c * nint4;
+            uint32_t* const gch = eo.blk.ch[lv] + (size_t)c * nint;
+            for (int i = lane; i < nint; i += 64) {
+              int Z;
+              gc[i] = tsa_node_eval<W, MODE>(P, lab, ch, Sm, lf, T, i, Z);
+              gz[i] = (uint16_t)Z;
+              gch[i] = ch[i];
+            }
+          }
+          if (++lv < eo.blk.n) {
+            beta = eo.blk.beta[lv];
+            left = eo.blk.niters[lv];
+          }
+        }
       }
     }
   } else {
@@ -993,6 +1013,7 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
     }
   }
 
+
   // with helper waves the whole workgroup evaluates the node costs, then the helpers write the snapshot and
   // the record back while wave 0 folds the energy
   const int e0 = helped ? (int)threadIdx.x : lane, es = helped ? (int)blockDim.x : 64;
@@ -1102,6 +1123,8 @@ static hipError_t launch_sweep_t(const TsaLaunch& L, const TsaKParams& P, uint64
   }
   if (P.chain0 < 0 || P.chain0 >= nchains) return hipErrorInvalidValue;
   const int grid = (nchains - P.chain0 + wpb - 1) / wpb;
+  if (eo.blk.n > 0 && (ORDER != 0 || LVL || eo.blk.n > TSA_BLOCK_MAX || eo.blk.total != nsweeps))
+    return hipErrorInvalidValue;  // a block of levels: par sweeps of one launch's total sweeps
   // e0 / e1 (null: none) take the kernel's start and stop times in the dispatch itself
   hipExtLaunchKernelGGL((k_sweep<W, MODE, ORDER, LDS, LVL, SLICE>), dim3(grid), dim3(threads), (uint32_t)smem, st, e0, e1, 0u,
                         P2, rec, leaf, fix, nchains, L.lds_words, beta, sweep0, nsweeps, stats, eo,

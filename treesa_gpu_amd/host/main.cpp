@@ -254,6 +254,7 @@ void Run::resolve_kernel() {
     throw InputError("slice moves need the warp kernels with --lpc 32");
   if (O_.nchains < 1) throw InputError("--nchains must be at least 1");
   if (O_.eval_every < 1) throw InputError("--eval-every must be at least 1");
+  if (O_.level_blocks < 0 || O_.level_blocks > 8) throw InputError("--level-blocks K: 0 (automatic) or 1..8");
   if (O_.scheme != "indep" && O_.scheme != "pa" && O_.scheme != "trunc") throw InputError("--scheme indep|pa|trunc");
 }
 
@@ -298,6 +299,7 @@ void Run::fill_config() {
   cfg_.track_overlap = O_.no_overlap ? -1 : 0;
   cfg_.draw_waves = O_.draw_waves;
   cfg_.level_loop = O_.level_loop ? 1 : 0;
+  cfg_.level_blocks = O_.level_blocks;
 }
 
 const std::vector<std::vector<uint32_t>>& Run::start_trees() {

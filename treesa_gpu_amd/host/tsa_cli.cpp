@@ -156,6 +156,8 @@ const std::vector<Flag>& flags() {
        "in one launch", SWITCH(level_launches, true)},
       {"--level-loop", nullptr, "scheme indep: the level loop in one launch also with more chains than are resident "
        "at once", SWITCH(level_loop, true)},
+      {"--level-blocks", "K", "scheme indep, par order, more than twice the chains the device holds at once: levels "
+       "per sweep launch (0: automatic, 1: one)", INT_FIELD(level_blocks)},
       {"--level-log", "FILE", "one JSON line per evaluated level: best chain, score, energies, ancestors",
        TEXT_FIELD(level_log)},
   };

@@ -46,6 +46,7 @@ struct Options {
   // diagnostics of this build
   bool quiet = false, host_select = false, no_overlap = false, level_launches = false, level_loop = false;
   int bench_warmup = 0;
+  int level_blocks = 0;  // tsa_config_t.level_blocks
   std::string level_log, dump_population;
 };
 
