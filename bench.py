@@ -20,7 +20,10 @@ event-timed sweep kernels only.
 
 roofline: of the sweep kernel, per launch, with the resource that bounds it.  Where the binary runs the level
 loop in one launch (scheme indep with every chain resident at once: c1) a launch is the whole schedule
-(levels_per_launch), else one level.  Chains staged in LDS (c1-c3):
+(levels_per_launch); where it sweeps blocks of K levels per launch (scheme indep with more than twice the chains
+the device holds at once: c2, "anneal=level_blocksK") a launch is K levels (the schedule's last block may be
+shorter: the figures are averages over the run's launches, and the HBM traffic is the committed summary's per
+level times the levels per launch); else one level.  Chains staged in LDS (c1-c3):
 bound "lds", achieved = the algorithmic bytes of the proposals (5 label sets of W words + 8 B of children per
 proposal, W words + 8 B written per accept, 4 B per visit without a rule, plus the slice steps' tree passes;
 from the kernel's own counters), all served from LDS, over the average event-timed launch, against the LDS read
@@ -56,6 +59,7 @@ import argparse
 import json
 import os
 import platform
+import re
 import subprocess
 import sys
 import tempfile
@@ -172,9 +176,10 @@ def label_path(desc):
     return "sums" if desc.startswith("wide") and " sums=0 " not in desc else "dense"
 
 
-def measured_traffic(cfgname, path="dense"):
+def measured_traffic(cfgname, path="dense", levels_per_launch=1.0):
     """HBM bytes per sweep-kernel dispatch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary of the
-    same workload and path (None when there is none)."""
+    same workload and path (None when there is none): its traffic_bytes_per_launch, or its
+    traffic_bytes_per_level times the levels of a launch."""
     f = PROFILES.get((cfgname, path))
     if not f or not os.path.exists(os.path.join(ROOT, "profiles", f)):
         return None
@@ -182,7 +187,21 @@ def measured_traffic(cfgname, path="dense"):
         for line in fh:
             if line.strip().startswith("traffic_bytes_per_launch:"):
                 return float(line.split(":")[1])
+            if line.strip().startswith("traffic_bytes_per_level:"):
+                return float(line.split(":")[1]) * levels_per_launch
     return None
+
+
+def launch_count(desc, steps):
+    """Sweep launches of a run of `steps` levels, from the binary's kernel description: one for the level loop in
+    one launch, one per block of K levels for "anneal=level_blocksK", else one per level."""
+    if desc.endswith("anneal=level_loop"):
+        return 1
+    m = re.search(r"anneal=level_blocks(\d+)$", desc)
+    if m:
+        k = int(m.group(1))
+        return (steps + k - 1) // k
+    return steps
 
 
 def profile_value(cfgname, key, path="dense"):
@@ -401,6 +420,9 @@ def kernel_label(desc, order):
         how = "nonzero 16-byte chunks only (chunk summaries)" if " sums=0 " not in desc else "dense streaming"
         return f"k_wide par, label sets in HBM, {how}, " + desc.split(" ", 1)[1]
     loop = ", the whole level loop in one launch" if desc.endswith("anneal=level_loop") else ""
+    m = re.search(r"anneal=level_blocks(\d+)$", desc)
+    if m:
+        loop = f", blocks of {m.group(1)} levels per launch"
     return f"k_sweep {o}, " + ("chain in LDS" if desc.startswith("lds") else "chain in HBM") + loop
 
 
@@ -591,13 +613,13 @@ def main():
         st = [r["proposals"], r["accepts"], r["warp_steps"], r["node_visits"], r["slice_proposals"]]
         slice_steps = steps * C["niters"] * nchains if C["slicing"] else 0
         desc = r.get("hip_kernel") or ""
-        # the level loop in one launch runs every level of the schedule; else one sweep launch per level
-        launches = 1 if desc.endswith("anneal=level_loop") else steps
+        # the level loop in one launch runs every level of the schedule, a block K levels; else one level
+        launches = launch_count(desc, steps)
         B = algorithmic_bytes(st, lay.W, inst.m - 1, C["slicing"], slice_steps) / launches
         dur = r["kernel_s"] / launches
         path = label_path(desc)
-        traffic = measured_traffic(a.config, path)
-        roof = {"kernel": kernel_label(desc, order), "levels_per_launch": steps // launches,
+        traffic = measured_traffic(a.config, path, steps / launches)
+        roof = {"kernel": kernel_label(desc, order), "levels_per_launch": steps / launches,
                 "algorithmic_bytes_per_launch": B, "avg_launch_ms": dur * 1e3, "traffic": traffic}
         if desc.startswith("lds"):
             # label sets served from LDS: the LDS read peak of this GPU bounds the proposals' reads; HBM carries

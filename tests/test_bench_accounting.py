@@ -48,3 +48,16 @@ def test_summary_path_bytes():
     full = bench.loaded_bytes([prop, 0, 0, prop, 0], (prop * W // 2, 0))
     alg = bench.algorithmic_bytes([prop, 0, 0, prop, 0], W, nint=4095)
     assert full == alg * 4 // 5 - prop * 8 * 4 // 5 + prop * (8 + 10)
+
+
+def test_launch_count_follows_the_kernel_description():
+    """Levels per sweep launch, from the binary's kernel description: the level loop in one launch, blocks of K
+    levels (the schedule's last block shorter), or one launch per level."""
+    d = "lds W=2 waves/block=4 lds_bytes/wave=11104 fold=apart split_levels=6"
+    assert bench.launch_count(d + " anneal=level_blocks8", 20) == 3  # 8 + 8 + 4
+    assert bench.launch_count(d + " anneal=level_blocks8", 16) == 2
+    assert bench.launch_count(d + " anneal=level_blocks3", 200) == 67
+    assert bench.launch_count("lds W=2 waves/block=1 anneal=level_loop", 100) == 1
+    assert bench.launch_count(d + " anneal=level_launches", 20) == 20
+    assert bench.launch_count("wide W=48 G=8 anneal=level_launches", 100) == 100
+    assert "blocks of 8 levels" in bench.kernel_label(d + " anneal=level_blocks8", 0)

@@ -107,6 +107,7 @@ struct tsa_ctx {
   long long split_levels = 0;  // sweep calls run as two launches (reported by tsa_describe)
   hipEvent_t ev_sweep[TSA_SNAP_MAX] = {};  // (the stop events of those sweeps' timing pairs)
   hipEvent_t ev_track[TSA_SNAP_MAX] = {};
+  int last_track = -1;  // the slot whose ev_track was recorded last (st2 runs the selections in order)
   bool track_pending[TSA_SNAP_MAX] = {};
   int slot = 0, last_slot = -1;  // slot of the next sweep launch / of the last one (-1: none since a reset)
   int nslots = 0;                // slots allocated (their buffers), the ones in turn
@@ -617,8 +618,10 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
 // d_sc / d_ns and write the tracking state), or wait for st2 on the host and forget the snapshots (before
 // the population is replaced).
 static void join_track(tsa_ctx* c) {
-  for (int k = 0; k < TSA_SNAP_MAX; k++)
-    if (c->track_pending[k]) (void)hipStreamWaitEvent(c->st, c->ev_track[k], 0);
+  // st2 runs the selections in the order they were enqueued, so the last one's event covers every pending one
+  // (one wait in the queue: each costs the device a few microseconds even when already satisfied)
+  if (c->last_track >= 0 && c->track_pending[c->last_track])
+    (void)hipStreamWaitEvent(c->st, c->ev_track[c->last_track], 0);
 }
 
 static hipError_t join_split(tsa_ctx* c) {
@@ -750,6 +753,11 @@ extern "C" int tsa_wait(tsa_ctx* ctx) {
   return TSA_OK;
 }
 
+// The first chain of a split level's second launch: half the chains, in whole workgroups.
+static int split_point(const tsa_ctx* ctx) {
+  return (ctx->nchains / 2 + ctx->L.wpb - 1) / ctx->L.wpb * ctx->L.wpb;
+}
+
 // tsa_sweeps, or with blk set (tsa_anneal; the one-wave kernels with the overlapped selection and the fold
 // apart) one launch (one split pair) of a block of levels, nsweeps = blk->total: every level with blk_ev[i] set
 // takes a snapshot slot of its own, returned in blk_slots[i] (-1: none), for tsa_track.
@@ -826,7 +834,7 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
     const bool fuse = ctx->cfg.fused_energy != 0;
     const bool apart = fuse && ctx->fold_apart;
     // a split level: chains [0, h) on st, [h, nchains) on st3 (h in whole workgroups)
-    const int h = (ctx->nchains / 2 + ctx->L.wpb - 1) / ctx->L.wpb * ctx->L.wpb;
+    const int h = split_point(ctx);
     const bool split = ctx->overlap && apart && h > 0 && h < ctx->nchains;
     if (!split) TSA_HIP(ctx, join_split(ctx));
     TsaEnergyOut eo{fuse && !apart ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns, apart ? ctx->d_ncost : nullptr,
@@ -1069,8 +1077,10 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
 }
 
 // The fold and the selection of the evaluated levels of one block of levels (tsa_anneal), on st2 beside the next
-// block's sweeps: one fold launch for all of their snapshots (each level's energies into its own slot) and one
-// selection launch that writes their trace rows and keeps the best in level order.
+// block's sweeps: one fold launch for all of their snapshots (each level's energies into its own slot; with the
+// block split over two launches, one fold per part, each after its own part, so that only the second part's fold
+// follows the block's last sweep) and one selection launch that writes their trace rows and keeps the best in
+// level order.
 static int track_block(tsa_ctx* ctx, const int* slots, const int* levels, int n) {
   if (n == 0) return TSA_OK;
   ctx->track_kind = TRACK_LEVELS;
@@ -1082,10 +1092,6 @@ static int track_block(tsa_ctx* ctx, const int* slots, const int* levels, int n)
   F.n = T.n = n;
   for (int i = 0; i < n; i++) {
     const int s = slots[i];
-    if (i == 0 || ctx->ev_sweep[s] != ctx->ev_sweep[slots[i - 1]]) {
-      TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_sweep[s], 0));
-      if (ctx->split_slot[s]) TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_b[s], 0));
-    }
     float* lc = reinterpret_cast<float*>(ctx->d_snap_en[s]);
     int* sc = reinterpret_cast<int*>(ctx->d_snap_en[s]) + ctx->nchains;
     int* ns = reinterpret_cast<int*>(ctx->d_snap_en[s]) + 2 * (size_t)ctx->nchains;
@@ -1100,12 +1106,23 @@ static int track_block(tsa_ctx* ctx, const int* slots, const int* levels, int n)
     T.ns[i] = ns;
     T.ch[i] = ctx->d_snap_ch[s];
   }
-  TSA_HIP(ctx, tsa_launch_fold_levels(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, F, ctx->nchains, ctx->st2));
+  // (every slot of the block has the same sweep events)
+  const int s0 = slots[0];
+  TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_sweep[s0], 0));
+  if (ctx->split_slot[s0]) {
+    const int h = split_point(ctx);
+    TSA_HIP(ctx, tsa_launch_fold_levels(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, F, 0, h, ctx->st2));
+    TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_b[s0], 0));
+    TSA_HIP(ctx, tsa_launch_fold_levels(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, F, h, ctx->nchains, ctx->st2));
+  } else {
+    TSA_HIP(ctx, tsa_launch_fold_levels(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, F, 0, ctx->nchains, ctx->st2));
+  }
   TSA_HIP(ctx, tsa_launch_track_levels(T, ctx->nchains, S, ctx->d_rec, L.chain_words, L.ch_off, L.s_off, L.W, L.nint,
                                        ctx->d_track, ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2));
   for (int i = 0; i < n; i++) {
     TSA_HIP(ctx, hipEventRecord(ctx->ev_track[slots[i]], ctx->st2));
     ctx->track_pending[slots[i]] = true;
+    ctx->last_track = slots[i];
   }
   ctx->energy_fresh = false;
   return TSA_OK;
@@ -1143,6 +1160,7 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
                                   ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2));
     TSA_HIP(ctx, hipEventRecord(ctx->ev_track[s], ctx->st2));
     ctx->track_pending[s] = true;
+    ctx->last_track = s;
     ctx->energy_fresh = false;  // d_lc / d_sc / d_ns now hold the snapshot's energies
     return TSA_OK;
   }

@@ -148,7 +148,8 @@ hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64
 hipError_t tsa_launch_fold(const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf, const uint32_t* fix,
                            const float* cost, const uint16_t* z, int nchains, float* lc, int* sc, int* ns,
                            hipStream_t st);
-// The same for several levels' snapshots in one launch: level i folds cost[i] / z[i] into lc[i] / sc[i] / ns[i].
+// The same for several levels' snapshots in one launch, chains chain0 .. nchains - 1: level i folds cost[i] / z[i]
+// into lc[i] / sc[i] / ns[i].
 struct TsaFoldLevels {
   int n;
   const float* cost[TSA_BLOCK_MAX];
@@ -158,7 +159,7 @@ struct TsaFoldLevels {
   int* ns[TSA_BLOCK_MAX];
 };
 hipError_t tsa_launch_fold_levels(const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf, const uint32_t* fix,
-                                  const TsaFoldLevels& F, int nchains, hipStream_t st);
+                                  const TsaFoldLevels& F, int chain0, int nchains, hipStream_t st);
 struct TsaTrackState {
   double best_score;
   int best_chain, best_level;

@@ -8,7 +8,7 @@
 // level (several levels' snapshots fold in one launch).
 __global__ void __launch_bounds__(256) k_fold(TsaKParams P, const uint64_t* __restrict__ rec,
                                               const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
-                                              TsaFoldLevels F, int nchains) {
+                                              TsaFoldLevels F, int chain0, int nchains) {
   const int li = (int)blockIdx.y;
   const float* __restrict__ cost = F.cost[li];
   const uint16_t* __restrict__ z = F.z[li];
@@ -20,7 +20,7 @@ __global__ void __launch_bounds__(256) k_fold(TsaKParams P, const uint64_t* __re
   __syncthreads();
   const TsaMathTabs T{s_exp2, fix, fix + TSA_LOG2FIX_WORDS, tsa_log2_tab_d};
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  const int c = t >> 5, l32 = threadIdx.x & 31;
+  const int c = chain0 + (t >> 5), l32 = threadIdx.x & 31;
   const int cc = c < nchains ? c : nchains - 1;  // a half-wave past the end duplicates the last chain
   const size_t nint4 = (size_t)((P.nint + 3) & ~3);
   const uint64_t* S = P.slicing ? rec + (size_t)cc * P.chain_words + P.s_off : nullptr;
@@ -42,14 +42,14 @@ hipError_t tsa_launch_fold(const TsaKParams& P, const uint64_t* rec, const uint6
   F.lc[0] = lc;
   F.sc[0] = sc;
   F.ns[0] = ns;
-  return tsa_launch_fold_levels(P, rec, leaf, fix, F, nchains, st);
+  return tsa_launch_fold_levels(P, rec, leaf, fix, F, 0, nchains, st);
 }
 
 hipError_t tsa_launch_fold_levels(const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf, const uint32_t* fix,
-                                  const TsaFoldLevels& F, int nchains, hipStream_t st) {
-  if (F.n < 1 || F.n > TSA_BLOCK_MAX) return hipErrorInvalidValue;
-  const int threads = 256, grid = (nchains * 32 + threads - 1) / threads;
-  hipLaunchKernelGGL(k_fold, dim3(grid, F.n), dim3(threads), 0, st, P, rec, leaf, fix, F, nchains);
+                                  const TsaFoldLevels& F, int chain0, int nchains, hipStream_t st) {
+  if (F.n < 1 || F.n > TSA_BLOCK_MAX || chain0 < 0 || chain0 >= nchains) return hipErrorInvalidValue;
+  const int threads = 256, grid = ((nchains - chain0) * 32 + threads - 1) / threads;
+  hipLaunchKernelGGL(k_fold, dim3(grid, F.n), dim3(threads), 0, st, P, rec, leaf, fix, F, chain0, nchains);
   return hipGetLastError();
 }
 

@@ -454,13 +454,15 @@ int Run::loop_on_device(PinnedWords& best, double t0) {
       if (evaluated[lev]) dev_->ok(tsa_track(c, lev));
     }
   }
-  kernel_ms_ += dev_->take_kernel_ms();
+  // the best and the trace rows first: their copies are enqueued behind the device's work while it still runs,
+  // and the call returns when it ends; the kernel time after that finds every timing event complete
   std::vector<tsa_trace_row_t> rows(n);
   int32_t best_chain = -1, best_level = -1;
   double best_score = 0, hz = 1;
   uint64_t tk0 = 0;
   dev_->ok(tsa_track_end(c, &best_chain, &best_level, &best_score, best.p, rows.data(), &tk0, &hz));
   const double wall = wall_seconds() - t0;
+  kernel_ms_ += dev_->take_kernel_ms();
   const double span = std::max(1.0, (double)(rows[n - 1].ticks - tk0));
   for (int lev = 0; lev < n; lev++) {
     if (!evaluated[lev]) continue;
