@@ -130,6 +130,7 @@ struct tsa_ctx {
   int lv_used = -1;                               // whether the last tsa_anneal ran the level loop (-1: none yet)
   std::vector<char> lv_evaluated;
   int lv_cap_levels = 0, lv_cap_evals = 0;
+  bool lv_cnt_fresh = false;  // the arrival counters were (re)allocated and are not yet cleared
   int* d_lv = nullptr;               // per level: beta (as bits), sweeps, evaluated index (-1: not evaluated)
   int* h_lv = nullptr;               // pinned staging of d_lv
   hipEvent_t ev_lv = nullptr;        // recorded after the upload that read h_lv last
@@ -1207,29 +1208,18 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
   TSA_HIP(ctx, quiesce_track(ctx));
   if (wide_error(ctx, werr) != TSA_OK) return TSA_ERR_HIP;
   if (ctx->track_kind == TRACK_ANNEAL) {
-    // the device level loop wrote the rows; the best is the lowest score over the evaluated levels' rows
-    // (first level on ties, as k_track keeps it), and that chain's tree is the one its best slot holds: a chain
-    // whose score equals the lowest at an earlier level would have been chosen at that level
-    h.best_score = INFINITY;
-    h.best_chain = h.best_level = -1;
+    // the device kept the best after each level-loop launch (the lowest score over the evaluated levels' rows,
+    // the first level on ties) and copied that chain's kept tree; the rows must agree
+    double s = INFINITY;
+    int bc = -1, bl = -1;
     for (int l = 0; l < ctx->track_levels; l++)
-      if (ctx->lv_evaluated[l] && rows[l].chain >= 0 && rows[l].score < h.best_score) {
-        h.best_score = rows[l].score;
-        h.best_chain = rows[l].chain;
-        h.best_level = l;
+      if (ctx->lv_evaluated[l] && rows[l].chain >= 0 && rows[l].score < s) {
+        s = rows[l].score;
+        bc = rows[l].chain;
+        bl = l;
       }
-    if (h.best_chain >= 0) {
-      int bs = -1;
-      TSA_HIP(ctx, hipMemcpyAsync(h_werr, ctx->d_bslot + h.best_chain, 4, hipMemcpyDeviceToHost, ctx->st));
-      TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
-      std::memcpy(&bs, h_werr, 4);
-      if (bs < 0 || bs > 1) return fail(ctx, TSA_ERR_HIP, "tsa_track_end: the best chain has no kept tree");
-      const int cw = L.s_off + L.W - L.ch_off;
-      TSA_HIP(ctx, hipMemcpyAsync(h_tree, ctx->d_cand + ((size_t)bs * ctx->nchains + h.best_chain) * cw, (size_t)cw * 8,
-                                  hipMemcpyDeviceToHost, ctx->st));
-      TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
-      std::memcpy(best_record + L.ch_off, h_tree, (size_t)cw * 8);
-    }
+    if (bc != h.best_chain || bl != h.best_level || (bc >= 0 && s != h.best_score))
+      return fail(ctx, TSA_ERR_HIP, "tsa_track_end: the level loop's best disagrees with its trace rows");
   }
   *best_chain = h.best_chain;
   *best_level = h.best_level;
@@ -1271,6 +1261,7 @@ static int levels_alloc(tsa_ctx* ctx, int nlev, int nev) {
     ctx->d_lv_part = nullptr;
     TSA_HIP(ctx, hipMalloc(&ctx->d_lv_en, (size_t)nev * n * 3 * 4));
     TSA_HIP(ctx, hipMalloc(&ctx->d_lv_cnt, ((size_t)nev * (ng + 1) + 1) / 2 * 8));  // cleared as 64-bit words
+    ctx->lv_cnt_fresh = true;
     TSA_HIP(ctx, hipMalloc(&ctx->d_lv_part, (size_t)nev * ng * sizeof(TsaTrackPart)));
     ctx->lv_cap_evals = nev;
   }
@@ -1386,10 +1377,13 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
     TSA_HIP(ctx, tsa_launch_levels_init(ctx->d_own, ctx->d_bslot, n, ctx->st));
     ctx->lv_reset = false;
   }
-  // the arrival counters start at zero (each launch also leaves them so, unless it was cut short)
-  const size_t cnt_words = (size_t)(nev > 0 ? nev : 1) * (ng + 1);
-  TSA_HIP(ctx, tsa_launch_zero(reinterpret_cast<unsigned long long*>(ctx->d_lv_cnt), (int)((cnt_words + 1) / 2),
-                               ctx->st));
+  // the arrival counters start at zero: cleared once when allocated, and every launch leaves them so
+  if (ctx->lv_cnt_fresh) {
+    const size_t cnt_words = (size_t)ctx->lv_cap_evals * (ng + 1);
+    TSA_HIP(ctx, tsa_launch_zero(reinterpret_cast<unsigned long long*>(ctx->d_lv_cnt), (int)((cnt_words + 1) / 2),
+                                 ctx->st));
+    ctx->lv_cnt_fresh = false;
+  }
   while ((int)ctx->ev.size() < 2 * (ctx->npending + 1)) {
     hipEvent_t e;
     TSA_HIP(ctx, hipEventCreate(&e));
@@ -1419,6 +1413,10 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
   TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, n, 0.0f,
                                  sweep0, 0, ctx->d_stats, eo, ctx->st, e0, e1, &lv));
   ctx->npending++;
+  // the session's best over the launch's levels and its tree, on the device (tsa_track_end then copies it with
+  // the trace rows instead of asking for the chain's kept tree after reading them)
+  if (nev > 0)
+    TSA_HIP(ctx, tsa_launch_level_best(lv, n, ctx->d_track, ctx->d_best, ctx->lay.ch_off, ctx->st));
   return TSA_OK;
 }
 

@@ -81,6 +81,7 @@ struct TsaEnergyOut {
 
 struct TsaTrackPart;
 struct TsaTraceRowD;
+struct TsaTrackState;
 
 // The level loop of independent chains run by one sweep launch (nlev > 0; nlev == 0: the launch's single
 // beta and nsweeps).  Level l sweeps niters[l] >= 1 times at beta[l], the sweep counter running on across
@@ -198,6 +199,12 @@ hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int n
                             const uint64_t* rec, int chain_words, int ch_off, int s_off, int W, int nint,
                             const uint32_t* ch_snap, TsaTrackState* st, TsaTraceRowD* trace, uint64_t* best_rec,
                             TsaTrackPart* part, unsigned* done, hipStream_t stream);
+// After a level-loop launch (Lv: its levels, trace rows, candidate slots and the chains' own / bslot as the
+// launch left them): the best over the launch's evaluated levels in level order (the lowest score, the first
+// level on ties) against the session's best in st, which it replaces, and the best chain's kept tree (its
+// slot's words: children words and S) into best_rec + ch_off.  One wave.
+hipError_t tsa_launch_level_best(const TsaLevels& Lv, int nchains, TsaTrackState* st, uint64_t* best_rec, int ch_off,
+                                 hipStream_t stream);
 hipError_t tsa_launch_track_init(TsaTrackState* st, unsigned long long* ticks0, unsigned long long* trace,
                                  int trace_words, unsigned long long* best, int best_words, hipStream_t stream);
 // The level loop's per-chain best (TsaLevels.own / bslot) of n chains reset: +inf, no slot.

@@ -303,6 +303,59 @@ hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int n
                                  done, stream);
 }
 
+// The session's best after a level-loop launch (tsa_launch_level_best): lane l takes the launch's levels l,
+// l + 64, ... (all trace rows read at once), the wave reduces their lowest (score, level), and lane 0 keeps it
+// when it beats st's; the wave then copies that chain's kept tree.  The chains' bslot are the launch's final
+// values (the launch has ended).
+__global__ void __launch_bounds__(64) k_level_best(TsaLevels Lv, int n, TsaTrackState* __restrict__ st,
+                                                   uint64_t* __restrict__ best_rec, int ch_off) {
+  const int lane = (int)threadIdx.x;
+  double bs = INFINITY;
+  int bl = -1, bc = -1;
+  for (int l = lane; l < Lv.nlev; l += 64) {
+    if (Lv.eval[l] < 0) continue;
+    const TsaTraceRowD q = Lv.trace[Lv.level0 + l];
+    if (q.chain >= 0 && q.score < bs) {  // (a lane's levels rise, so the first of equal scores stays)
+      bs = q.score;
+      bc = q.chain;
+      bl = Lv.level0 + l;
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const double s2 = __shfl_down(bs, o, 64);
+    const int l2 = __shfl_down(bl, o, 64), c2 = __shfl_down(bc, o, 64);
+    if (lane + o < 64 && l2 >= 0 && (s2 < bs || (s2 == bs && (bl < 0 || l2 < bl)))) {
+      bs = s2;
+      bl = l2;
+      bc = c2;
+    }
+  }
+  int slot = -1;
+  if (lane == 0) {
+    if (bc >= 0 && bs < st->best_score) {
+      slot = Lv.bslot[bc];
+      if (slot == 0 || slot == 1) {  // (a chain with a finite score has kept a tree)
+        st->best_score = bs;
+        st->best_chain = bc;
+        st->best_level = bl;
+        st->snap = bc;
+      }
+    }
+  }
+  slot = __shfl(slot, 0, 64);
+  bc = __shfl(bc, 0, 64);
+  if (slot == 0 || slot == 1) {
+    const uint64_t* const src = Lv.cand + ((size_t)slot * n + bc) * Lv.cand_words;
+    for (int i = lane; i < Lv.cand_words; i += 64) best_rec[ch_off + i] = src[i];
+  }
+}
+
+hipError_t tsa_launch_level_best(const TsaLevels& Lv, int nchains, TsaTrackState* stt, uint64_t* best_rec, int ch_off,
+                                 hipStream_t stream) {
+  hipLaunchKernelGGL(k_level_best, dim3(1), dim3(64), 0, stream, Lv, nchains, stt, best_rec, ch_off);
+  return hipGetLastError();
+}
+
 hipError_t tsa_launch_track_init(TsaTrackState* stt, unsigned long long* ticks0, unsigned long long* trace,
                                  int trace_words, unsigned long long* best, int best_words, hipStream_t stream) {
   const int n = trace_words > best_words ? trace_words : best_words;
