@@ -53,6 +53,10 @@ struct tsa_ctx {
   // copies are enqueued without a wait each, and the call waits once
   char* h_tend = nullptr;
   size_t h_tend_bytes = 0;
+  char* d_tend = nullptr;  // the device's address of h_tend (null: not mapped, the results go by copies)
+  // tsa_track_begin leaves the session's start (k_track_init) to the next call, which enqueues it before
+  // anything else (the same place in the stream's order), or to the level loop's set-up launch, which does it
+  bool track_init_pending = false;
   double tick_hz = 0.0;  // the device's wall-clock rate (Hz)
   uint32_t* d_hen = nullptr;  // the device's address of h_en (null: not mapped)
   bool energy_host = false;   // the last sweep launch wrote the energies of the current population into h_en
@@ -108,6 +112,9 @@ struct tsa_ctx {
   hipEvent_t ev_sweep[TSA_SNAP_MAX] = {};  // (the stop events of those sweeps' timing pairs)
   hipEvent_t ev_track[TSA_SNAP_MAX] = {};
   int last_track = -1;  // the slot whose ev_track was recorded last (st2 runs the selections in order)
+  // the session's start was enqueued on st2 (behind the first sweeps) and st has not yet waited for it
+  hipEvent_t ev_tinit = nullptr;
+  bool tinit_pending = false;
   bool track_pending[TSA_SNAP_MAX] = {};
   int slot = 0, last_slot = -1;  // slot of the next sweep launch / of the last one (-1: none since a reset)
   int nslots = 0;                // slots allocated (their buffers), the ones in turn
@@ -132,9 +139,13 @@ struct tsa_ctx {
   int lv_cap_levels = 0, lv_cap_evals = 0;
   bool lv_cnt_fresh = false;  // the arrival counters were (re)allocated and are not yet cleared
   int* d_lv = nullptr;               // per level: beta (as bits), sweeps, evaluated index (-1: not evaluated)
-  int* h_lv = nullptr;               // pinned staging of d_lv
-  hipEvent_t ev_lv = nullptr;        // recorded after the upload that read h_lv last
-  bool lv_pending = false;
+  // pinned staging of d_lv in two halves of lv_cap_levels * 3 words, used in turn: the set-up launch reads
+  // one while the host fills the other; ev_lv[h] is recorded after the launches that read half h
+  int* h_lv = nullptr;
+  int* d_hlv = nullptr;  // the device's address of h_lv (null: not mapped, the table goes by a copy)
+  hipEvent_t ev_lv[2] = {nullptr, nullptr};
+  bool lv_pending[2] = {false, false};
+  int lv_half = 0;
   uint32_t* d_lv_en = nullptr;       // lc | sc | ns per evaluated level and chain
   unsigned* d_lv_cnt = nullptr;      // arrival counters, (ngroups + 1) per evaluated level
   TsaTrackPart* d_lv_part = nullptr; // group results, ngroups per evaluated level
@@ -325,6 +336,7 @@ static void free_ctx(tsa_ctx* c) {
     if (c->d_snap_nz[k]) (void)hipFree(c->d_snap_nz[k]);
     if (c->d_snap_en[k]) (void)hipFree(c->d_snap_en[k]);
   }
+  if (c->ev_tinit) (void)hipEventDestroy(c->ev_tinit);
   if (c->st2) (void)hipStreamDestroy(c->st2);
   if (c->d_track) (void)hipFree(c->d_track);
   if (c->d_trace) (void)hipFree(c->d_trace);
@@ -332,7 +344,8 @@ static void free_ctx(tsa_ctx* c) {
   if (c->d_ticks0) (void)hipFree(c->d_ticks0);
   if (c->d_lv) (void)hipFree(c->d_lv);
   if (c->h_lv) (void)hipHostFree(c->h_lv);
-  if (c->ev_lv) (void)hipEventDestroy(c->ev_lv);
+  for (hipEvent_t e : c->ev_lv)
+    if (e) (void)hipEventDestroy(e);
   if (c->d_lv_en) (void)hipFree(c->d_lv_en);
   if (c->d_lv_cnt) (void)hipFree(c->d_lv_cnt);
   if (c->d_lv_part) (void)hipFree(c->d_lv_part);
@@ -623,6 +636,9 @@ static void join_track(tsa_ctx* c) {
   // (one wait in the queue: each costs the device a few microseconds even when already satisfied)
   if (c->last_track >= 0 && c->track_pending[c->last_track])
     (void)hipStreamWaitEvent(c->st, c->ev_track[c->last_track], 0);
+  else if (c->tinit_pending)
+    (void)hipStreamWaitEvent(c->st, c->ev_tinit, 0);
+  c->tinit_pending = false;
 }
 
 static hipError_t join_split(tsa_ctx* c) {
@@ -634,10 +650,26 @@ static hipError_t join_split(tsa_ctx* c) {
   return e;
 }
 
+static hipError_t flush_track_init(tsa_ctx* c, bool on_st2 = false) {
+  if (!c->track_init_pending) return hipSuccess;
+  c->track_init_pending = false;
+  hipError_t e = tsa_launch_track_init(c->d_track, c->d_ticks0, reinterpret_cast<unsigned long long*>(c->d_trace),
+                                       (int)((size_t)c->track_levels * sizeof(TsaTraceRowD) / 8),
+                                       reinterpret_cast<unsigned long long*>(c->d_best), c->lay.chain_words,
+                                       on_st2 ? c->st2 : c->st);
+  if (on_st2) {
+    if (e == hipSuccess && !c->ev_tinit) e = hipEventCreateWithFlags(&c->ev_tinit, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(c->ev_tinit, c->st2);
+    c->tinit_pending = e == hipSuccess;
+  }
+  return e;
+}
+
 static hipError_t quiesce_track(tsa_ctx* c) {
   hipError_t e = hipSuccess;
   if (c->st2) e = hipStreamSynchronize(c->st2);
   for (bool& p : c->track_pending) p = false;
+  c->tinit_pending = false;
   c->last_slot = -1;
   return e;
 }
@@ -705,6 +737,7 @@ static int wide_error(tsa_ctx* c, uint32_t word) {
 extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
   if (!ctx || !population) return fail(ctx, TSA_ERR_ARG, "tsa_upload: null argument");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_track_init(ctx));
   const tsa_layout_t& L = ctx->lay;
   std::vector<char> seen;
   std::vector<int> st;
@@ -720,12 +753,14 @@ extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
   TSA_HIP(ctx, hipMemcpyAsync(ctx->d_rec, population, (size_t)ctx->nchains * L.chain_words * 8,
                               hipMemcpyHostToDevice, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  ctx->host_waited = true;
   return TSA_OK;
 }
 
 extern "C" int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* out) {
   if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_download: null argument");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_track_init(ctx));
   if (c0 < 0 || count < 0 || c0 + count > ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_download: range");
   const size_t cw = ctx->lay.chain_words;
   TSA_HIP(ctx, hipMemcpyAsync(out, ctx->d_rec + (size_t)c0 * cw, (size_t)count * cw * 8, hipMemcpyDeviceToHost,
@@ -738,6 +773,7 @@ extern "C" int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* o
 extern "C" int tsa_download_async(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* out) {
   if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_download_async: null argument");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_track_init(ctx));
   if (c0 < 0 || count < 0 || c0 + count > ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_download_async: range");
   const size_t cw = ctx->lay.chain_words;
   TSA_HIP(ctx, hipMemcpyAsync(out, ctx->d_rec + (size_t)c0 * cw, (size_t)count * cw * 8, hipMemcpyDeviceToHost,
@@ -748,6 +784,7 @@ extern "C" int tsa_download_async(tsa_ctx* ctx, int32_t c0, int32_t count, uint6
 extern "C" int tsa_wait(tsa_ctx* ctx) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_wait: null context");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_track_init(ctx));
   if (ctx->st2) TSA_HIP(ctx, hipStreamSynchronize(ctx->st2));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
   ctx->host_waited = true;
@@ -768,6 +805,11 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
   if (order != TSA_ORDER_PAR && order != TSA_ORDER_PREORDER) return fail(ctx, TSA_ERR_ARG, "--order par|preorder");
   if (nsweeps < 0) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps: nsweeps < 0");
   if (nsweeps == 0) return TSA_OK;
+  // the session's start (tsa_track_begin): with the selection on st2, enqueued there after this call's sweeps,
+  // so that the host issues the sweeps first (st2's folds and selections come after it in st2's order, and st
+  // waits for it in join_track); otherwise on st before them
+  const bool init_on_st2 = ctx->track_init_pending && ctx->overlap && ctx->st2 != nullptr;
+  if (!init_on_st2) TSA_HIP(ctx, flush_track_init(ctx));
   while ((int)ctx->ev.size() < 2 * (ctx->npending + 2)) {
     hipEvent_t e;
     TSA_HIP(ctx, hipEventCreate(&e));
@@ -955,6 +997,7 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
     }
   }
   ctx->npending++;
+  if (init_on_st2) TSA_HIP(ctx, flush_track_init(ctx, true));
   return TSA_OK;
 }
 
@@ -965,6 +1008,7 @@ extern "C" int tsa_sweeps(tsa_ctx* ctx, int32_t order, float beta, uint32_t swee
 extern "C" int tsa_sweeps_ms(tsa_ctx* ctx, double* ms) {
   if (!ctx || !ms) return fail(ctx, TSA_ERR_ARG, "tsa_sweeps_ms: null argument");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_track_init(ctx));
   *ms = 0.0;
   if (ctx->npending == 0) return TSA_OK;
   // the union of the launches' intervals (the two launches of a split level run at the same time), each in ms
@@ -1030,6 +1074,10 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
       ctx->h_tend_bytes = 0;
       TSA_HIP(ctx, hipHostMalloc(reinterpret_cast<void**>(&ctx->h_tend), need, hipHostMallocDefault));
       ctx->h_tend_bytes = need;
+      if (hipHostGetDevicePointer(reinterpret_cast<void**>(&ctx->d_tend), ctx->h_tend, 0) != hipSuccess) {
+        (void)hipGetLastError();  // not mapped: the copies
+        ctx->d_tend = nullptr;
+      }
     }
     if (ctx->tick_hz == 0.0) {
       int dev = 0, khz = 0;
@@ -1070,10 +1118,7 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   ctx->lv_reset = true;
   ctx->lv_evaluated.assign((size_t)max_levels, 0);
   static_assert(sizeof(TsaTraceRowD) % 8 == 0, "trace rows are whole words");
-  TSA_HIP(ctx, tsa_launch_track_init(ctx->d_track, ctx->d_ticks0, reinterpret_cast<unsigned long long*>(ctx->d_trace),
-                                     (int)((size_t)max_levels * sizeof(TsaTraceRowD) / 8),
-                                     reinterpret_cast<unsigned long long*>(ctx->d_best), ctx->lay.chain_words,
-                                     ctx->st));
+  ctx->track_init_pending = true;
   return TSA_OK;
 }
 
@@ -1132,6 +1177,7 @@ static int track_block(tsa_ctx* ctx, const int* slots, const int* levels, int n)
 extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_track: null context");
   if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_track: no tsa_track_begin");
+  TSA_HIP(ctx, flush_track_init(ctx));
   if (level < 0 || level >= ctx->track_levels) return fail(ctx, TSA_ERR_ARG, "tsa_track: level out of range");
   if (ctx->track_kind == TRACK_ANNEAL)
     return fail(ctx, TSA_ERR_ARG, "tsa_track: this tracking session runs its levels with tsa_anneal");
@@ -1178,11 +1224,18 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
   if (!ctx || !best_chain || !best_level || !best_score || !best_record || !rows || !ticks0 || !tick_hz)
     return fail(ctx, TSA_ERR_ARG, "tsa_track_end: null argument");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_track_init(ctx));
   if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_track_end: no tsa_track_begin");
   static_assert(sizeof(TsaTraceRowD) == sizeof(tsa_trace_row_t), "trace row layout");
   TsaTrackState h;
   unsigned long long t0 = 0;
-  join_track(ctx);
+  // The results are written by the selections on st2 when they run there (the wide path's error word, which
+  // its sweeps write, aside): then the results' launch follows them on st2 and the host waits for both
+  // streams, instead of a wait of st for st2 in the queue (about 10 us on the device)
+  const bool on2 = ctx->st2 && !ctx->wide.on && ctx->d_tend &&
+                   ((ctx->last_track >= 0 && ctx->track_pending[ctx->last_track]) || ctx->tinit_pending);
+  hipStream_t so = on2 ? ctx->st2 : ctx->st;
+  if (!on2) join_track(ctx);
   // every copy into the pinned staging buffer, one wait, then the caller's buffers from there
   const tsa_layout_t& L = ctx->lay;
   const size_t cwb = (size_t)(L.s_off + L.W - L.ch_off) * 8, rowb = (size_t)ctx->track_levels * sizeof(TsaTraceRowD);
@@ -1192,14 +1245,31 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
   char* const h_werr = h_t0 + 8;
   char* const h_tree = h_t0 + 16;
   char* const h_rows = h_tree + ((cwb + 15) & ~(size_t)15);
-  TSA_HIP(ctx, hipMemcpyAsync(h_state, ctx->d_track, sizeof h, hipMemcpyDeviceToHost, ctx->st));
-  TSA_HIP(ctx, hipMemcpyAsync(h_t0, ctx->d_ticks0, sizeof t0, hipMemcpyDeviceToHost, ctx->st));
   // the best chain's tree: children words and S (the label words of best_record are not written)
-  TSA_HIP(ctx, hipMemcpyAsync(h_tree, ctx->d_best + L.ch_off, cwb, hipMemcpyDeviceToHost, ctx->st));
-  TSA_HIP(ctx, hipMemcpyAsync(h_rows, ctx->d_trace, rowb, hipMemcpyDeviceToHost, ctx->st));
+  static_assert(sizeof(TsaTrackState) % 8 == 0, "the tracking state is whole words");
   uint32_t werr = 0;
-  if (ctx->wide.on) TSA_HIP(ctx, hipMemcpyAsync(h_werr, ctx->wsync.err, 4, hipMemcpyDeviceToHost, ctx->st));
+  if (ctx->d_tend) {
+    // one launch writes them all into the mapped staging buffer (four or five copies cost about 5 us each)
+    char* const d = ctx->d_tend;
+    TSA_HIP(ctx, tsa_launch_track_out(
+                     reinterpret_cast<const unsigned long long*>(ctx->d_track), (int)(sizeof h / 8), ctx->d_ticks0,
+                     reinterpret_cast<const unsigned long long*>(ctx->d_best + L.ch_off), (int)(cwb / 8),
+                     reinterpret_cast<const unsigned long long*>(ctx->d_trace), (int)(rowb / 8),
+                     ctx->wide.on ? ctx->wsync.err : nullptr, reinterpret_cast<unsigned long long*>(d + (h_state - hs)),
+                     reinterpret_cast<unsigned long long*>(d + (h_t0 - hs)),
+                     reinterpret_cast<unsigned long long*>(d + (h_tree - hs)),
+                     reinterpret_cast<unsigned long long*>(d + (h_rows - hs)),
+                     reinterpret_cast<unsigned*>(d + (h_werr - hs)), so));
+  } else {
+    TSA_HIP(ctx, hipMemcpyAsync(h_state, ctx->d_track, sizeof h, hipMemcpyDeviceToHost, ctx->st));
+    TSA_HIP(ctx, hipMemcpyAsync(h_t0, ctx->d_ticks0, sizeof t0, hipMemcpyDeviceToHost, ctx->st));
+    TSA_HIP(ctx, hipMemcpyAsync(h_tree, ctx->d_best + L.ch_off, cwb, hipMemcpyDeviceToHost, ctx->st));
+    TSA_HIP(ctx, hipMemcpyAsync(h_rows, ctx->d_trace, rowb, hipMemcpyDeviceToHost, ctx->st));
+    if (ctx->wide.on) TSA_HIP(ctx, hipMemcpyAsync(h_werr, ctx->wsync.err, 4, hipMemcpyDeviceToHost, ctx->st));
+  }
+  if (on2) TSA_HIP(ctx, hipStreamSynchronize(ctx->st2));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  ctx->host_waited = true;
   std::memcpy(&h, h_state, sizeof h);
   std::memcpy(&t0, h_t0, sizeof t0);
   std::memcpy(best_record + L.ch_off, h_tree, cwb);
@@ -1238,17 +1308,24 @@ static int levels_alloc(tsa_ctx* ctx, int nlev, int nev) {
     TSA_HIP(ctx, hipMalloc(&ctx->d_cand, 2 * (size_t)n * cw * 8));
     TSA_HIP(ctx, hipMalloc(&ctx->d_own, (size_t)n * 8));
     TSA_HIP(ctx, hipMalloc(&ctx->d_bslot, (size_t)n * 4));
-    TSA_HIP(ctx, hipEventCreateWithFlags(&ctx->ev_lv, hipEventDisableTiming));
+    for (hipEvent_t& e : ctx->ev_lv) TSA_HIP(ctx, hipEventCreateWithFlags(&e, hipEventDisableTiming));
   }
   if (nlev > ctx->lv_cap_levels) {
-    if (ctx->lv_pending) TSA_HIP(ctx, hipEventSynchronize(ctx->ev_lv));
-    ctx->lv_pending = false;
+    for (int k = 0; k < 2; k++) {
+      if (ctx->lv_pending[k]) TSA_HIP(ctx, hipEventSynchronize(ctx->ev_lv[k]));
+      ctx->lv_pending[k] = false;
+    }
     if (ctx->d_lv) TSA_HIP(ctx, hipFree(ctx->d_lv));
     if (ctx->h_lv) TSA_HIP(ctx, hipHostFree(ctx->h_lv));
     ctx->d_lv = nullptr;
     ctx->h_lv = nullptr;
+    ctx->d_hlv = nullptr;
     TSA_HIP(ctx, hipMalloc(&ctx->d_lv, (size_t)nlev * 3 * 4));
-    TSA_HIP(ctx, hipHostMalloc(&ctx->h_lv, (size_t)nlev * 3 * 4, hipHostMallocDefault));
+    TSA_HIP(ctx, hipHostMalloc(&ctx->h_lv, 2 * (size_t)nlev * 3 * 4, hipHostMallocDefault));
+    if (hipHostGetDevicePointer(reinterpret_cast<void**>(&ctx->d_hlv), ctx->h_lv, 0) != hipSuccess) {
+      (void)hipGetLastError();  // not mapped: the table goes by a copy
+      ctx->d_hlv = nullptr;
+    }
     ctx->lv_cap_levels = nlev;
   }
   if (nev > ctx->lv_cap_evals) {
@@ -1305,6 +1382,7 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
     }
   }
   ctx->lv_used = loop ? 1 : 0;
+  if (!loop) TSA_HIP(ctx, flush_track_init(ctx));  // (the level loop's set-up launch does it)
   // Several levels per sweep launch (the one-wave LDS kernels with the overlapped selection and the fold apart,
   // where the population is more than twice what the device holds at once): a launch ends with a tail in which
   // fewer and fewer chains are left to run, and a level of one sweep per chain is short next to it; a block of
@@ -1357,9 +1435,13 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
   if (levels_alloc(ctx, nlevels, nev > 0 ? nev : 1) != TSA_OK) return TSA_ERR_HIP;
   ctx->track_kind = TRACK_ANNEAL;
   const int n = ctx->nchains, ng = (n + 255) / 256;
-  // the schedule, through pinned staging the previous call's upload has finished reading
-  if (ctx->lv_pending) TSA_HIP(ctx, hipEventSynchronize(ctx->ev_lv));
-  int* h = ctx->h_lv;
+  // the schedule, through the half of the pinned staging that the call before the previous one read
+  const int half = ctx->lv_half;
+  ctx->lv_half ^= 1;
+  if (ctx->lv_pending[half]) TSA_HIP(ctx, hipEventSynchronize(ctx->ev_lv[half]));
+  ctx->lv_pending[half] = false;
+  const size_t hoff = (size_t)half * 3 * ctx->lv_cap_levels;
+  int* h = ctx->h_lv + hoff;
   for (int l = 0, e = 0; l < nlevels; l++) {
     memcpy(&h[l], &betas[l], 4);
     h[nlevels + l] = niters[l];
@@ -1370,26 +1452,50 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
   ctx->last_slot = -1;
   ctx->energy_fresh = ctx->energy_host = false;
   ctx->costs_valid = ctx->sums_valid = false;
-  TSA_HIP(ctx, hipMemcpyAsync(ctx->d_lv, h, (size_t)nlevels * 3 * 4, hipMemcpyHostToDevice, ctx->st));
-  TSA_HIP(ctx, hipEventRecord(ctx->ev_lv, ctx->st));
-  ctx->lv_pending = true;
+  // the set-up in one launch: the session's start (when this is its first call), the chains' best reset, the
+  // table from the pinned staging and the arrival counters zeroed (they start at zero: cleared once when
+  // allocated, and every launch leaves them so)
+  TsaAnnealInit A{};
+  if (ctx->track_init_pending) {
+    ctx->track_init_pending = false;
+    A.track = ctx->d_track;
+    A.ticks0 = ctx->d_ticks0;
+    A.trace = reinterpret_cast<unsigned long long*>(ctx->d_trace);
+    A.trace_words = (int)((size_t)ctx->track_levels * sizeof(TsaTraceRowD) / 8);
+    A.best = reinterpret_cast<unsigned long long*>(ctx->d_best);
+    A.best_words = ctx->lay.chain_words;
+  }
   if (ctx->lv_reset) {
-    TSA_HIP(ctx, tsa_launch_levels_init(ctx->d_own, ctx->d_bslot, n, ctx->st));
+    A.own = ctx->d_own;
+    A.bslot = ctx->d_bslot;
+    A.nchains = n;
     ctx->lv_reset = false;
   }
-  // the arrival counters start at zero: cleared once when allocated, and every launch leaves them so
+  if (ctx->d_hlv) {
+    A.tab_src = ctx->d_hlv + hoff;
+    A.tab_dst = ctx->d_lv;
+    A.tab_words = 3 * nlevels;
+  } else {
+    TSA_HIP(ctx, hipMemcpyAsync(ctx->d_lv, h, (size_t)nlevels * 3 * 4, hipMemcpyHostToDevice, ctx->st));
+  }
   if (ctx->lv_cnt_fresh) {
     const size_t cnt_words = (size_t)ctx->lv_cap_evals * (ng + 1);
-    TSA_HIP(ctx, tsa_launch_zero(reinterpret_cast<unsigned long long*>(ctx->d_lv_cnt), (int)((cnt_words + 1) / 2),
-                                 ctx->st));
+    A.cnt = reinterpret_cast<unsigned long long*>(ctx->d_lv_cnt);
+    A.cnt_words = (int)((cnt_words + 1) / 2);
     ctx->lv_cnt_fresh = false;
   }
+  if (A.track || A.own || A.tab_src || A.cnt) TSA_HIP(ctx, tsa_launch_anneal_init(A, ctx->st));
   while ((int)ctx->ev.size() < 2 * (ctx->npending + 1)) {
     hipEvent_t e;
     TSA_HIP(ctx, hipEventCreate(&e));
     ctx->ev.push_back(e);
   }
   hipEvent_t e0 = ctx->ev[2 * ctx->npending], e1 = ctx->ev[2 * ctx->npending + 1];
+  // the timing events as markers around a plain dispatch, which costs the host less time before the kernel
+  // starts than events recorded by the dispatch (about 6 against 20 us); a launch of whole levels is long
+  // next to the gap a marker may leave before the kernel
+  const bool markers = true;
+  ctx->host_waited = false;
   TsaLevels lv{};
   lv.beta = reinterpret_cast<const float*>(ctx->d_lv);
   lv.niters = ctx->d_lv + nlevels;
@@ -1410,19 +1516,25 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
   lv.S = ctx->sel;
   lv.S.mode = ctx->mode;
   const TsaEnergyOut eo{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
+  if (markers) TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
   TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, n, 0.0f,
-                                 sweep0, 0, ctx->d_stats, eo, ctx->st, e0, e1, &lv));
+                                 sweep0, 0, ctx->d_stats, eo, ctx->st, markers ? nullptr : e0,
+                                 markers ? nullptr : e1, &lv));
+  if (markers) TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
   ctx->npending++;
   // the session's best over the launch's levels and its tree, on the device (tsa_track_end then copies it with
   // the trace rows instead of asking for the chain's kept tree after reading them)
   if (nev > 0)
     TSA_HIP(ctx, tsa_launch_level_best(lv, n, ctx->d_track, ctx->d_best, ctx->lay.ch_off, ctx->st));
+  TSA_HIP(ctx, hipEventRecord(ctx->ev_lv[half], ctx->st));
+  ctx->lv_pending[half] = true;
   return TSA_OK;
 }
 
 extern "C" int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns) {
   if (!ctx || !lc || !sc || !ns) return fail(ctx, TSA_ERR_ARG, "tsa_energy: null argument");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_track_init(ctx));
   const size_t b = (size_t)ctx->nchains * 4;
   if (ctx->energy_host) {  // the last sweep launch wrote them into h_en
     TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
@@ -1442,6 +1554,7 @@ extern "C" int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns) {
 extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
   if (!ctx || !anc) return fail(ctx, TSA_ERR_ARG, "tsa_resample: null argument");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_track_init(ctx));
   for (int c = 0; c < ctx->nchains; c++)
     if (anc[c] < 0 || anc[c] >= ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_resample: ancestor out of range");
   if (!ctx->d_rec2) TSA_HIP(ctx, hipMalloc(&ctx->d_rec2, (size_t)ctx->nchains * ctx->lay.chain_words * 8));
@@ -1465,6 +1578,7 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
 extern "C" int tsa_set_mode(tsa_ctx* ctx, int32_t mode) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: null context");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_track_init(ctx));
   if (mode < 0 || mode > 2) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: mode must be 0, 1 or 2");
   if (mode != ctx->mode) {
     TSA_HIP(ctx, quiesce_track(ctx));
@@ -1477,6 +1591,7 @@ extern "C" int tsa_set_mode(tsa_ctx* ctx, int32_t mode) {
 extern "C" int tsa_stats(tsa_ctx* ctx, uint64_t out[7]) {
   if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_stats: null argument");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_track_init(ctx));
   unsigned long long s[TSA_NSTAT * TSA_STAT_SLOTS];
   TSA_HIP(ctx, hipMemcpyAsync(s, ctx->d_stats, sizeof s, hipMemcpyDeviceToHost, ctx->st));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
@@ -1490,6 +1605,7 @@ extern "C" int tsa_stats(tsa_ctx* ctx, uint64_t out[7]) {
 extern "C" int tsa_chunk_stats(tsa_ctx* ctx, uint64_t out[2]) {
   if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_chunk_stats: null argument");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_track_init(ctx));
   unsigned long long s[2 * TSA_STAT_SLOTS];
   TSA_HIP(ctx, hipMemcpyAsync(s, ctx->d_stats + TSA_ST_CHUNKS * TSA_STAT_SLOTS, sizeof s, hipMemcpyDeviceToHost,
                               ctx->st));

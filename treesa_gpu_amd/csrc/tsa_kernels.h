@@ -207,8 +207,36 @@ hipError_t tsa_launch_level_best(const TsaLevels& Lv, int nchains, TsaTrackState
                                  hipStream_t stream);
 hipError_t tsa_launch_track_init(TsaTrackState* st, unsigned long long* ticks0, unsigned long long* trace,
                                  int trace_words, unsigned long long* best, int best_words, hipStream_t stream);
-// The level loop's per-chain best (TsaLevels.own / bslot) of n chains reset: +inf, no slot.
-hipError_t tsa_launch_levels_init(double* own, int* bslot, int n, hipStream_t stream);
+// The set-up of a level-loop launch in one launch, each part optional: a tracking session's start (as
+// k_track_init: track != nullptr), the chains' best (TsaLevels.own / bslot) reset to +inf and no candidate
+// slot (own != nullptr), the level table copied from
+// page-locked host memory (tab_src != nullptr: tab_words 32-bit words into tab_dst) and the arrival counters
+// zeroed (cnt != nullptr: cnt_words 64-bit words).
+struct TsaAnnealInit {
+  TsaTrackState* track;
+  unsigned long long* ticks0;
+  unsigned long long* trace;
+  int trace_words;
+  unsigned long long* best;
+  int best_words;
+  double* own;
+  int* bslot;
+  int nchains;
+  const int* tab_src;
+  int* tab_dst;
+  int tab_words;
+  unsigned long long* cnt;
+  int cnt_words;
+};
+hipError_t tsa_launch_anneal_init(const TsaAnnealInit& A, hipStream_t stream);
+// A tracking session's results into page-locked host memory in one launch (instead of one copy each): the
+// tracking state (st_words 64-bit words), the start tick, the best record's tree (tree_words words from tree)
+// and the trace rows (row_words words), and, when werr is not null, the wide path's error word.
+hipError_t tsa_launch_track_out(const unsigned long long* st, int st_words, const unsigned long long* ticks0,
+                                const unsigned long long* tree, int tree_words, const unsigned long long* rows,
+                                int row_words, const unsigned* werr, unsigned long long* h_st,
+                                unsigned long long* h_t0, unsigned long long* h_tree, unsigned long long* h_rows,
+                                unsigned* h_werr, hipStream_t stream);
 hipError_t tsa_launch_copy(const uint64_t* src, uint64_t* dst, const int* anc, int nchains, int chain_words,
                            hipStream_t st);
 // n zeroed 64-bit words, by a kernel.

@@ -366,17 +366,68 @@ hipError_t tsa_launch_track_init(TsaTrackState* stt, unsigned long long* ticks0,
   return hipGetLastError();
 }
 
-// The level loop's per-chain best: score +inf, no candidate slot.
-__global__ void k_levels_init(double* __restrict__ own, int* __restrict__ bslot, int n) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i < n) {
-    own[i] = INFINITY;
-    bslot[i] = -1;
+__global__ void __launch_bounds__(256) k_anneal_init(TsaAnnealInit A) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x, nt = gridDim.x * blockDim.x;
+  if (A.track) {
+    for (int i = t; i < A.trace_words; i += nt) A.trace[i] = 0ull;
+    for (int i = t; i < A.best_words; i += nt) A.best[i] = 0ull;
+    if (t == 0) {
+      A.track->best_score = INFINITY;
+      A.track->best_chain = -1;
+      A.track->best_level = -1;
+      A.track->snap = -1;
+      *A.ticks0 = wall_clock64();
+    }
   }
+  if (A.own)
+    for (int i = t; i < A.nchains; i += nt) {
+      A.own[i] = INFINITY;
+      A.bslot[i] = -1;
+    }
+  if (A.tab_src)
+    for (int i = t; i < A.tab_words; i += nt) A.tab_dst[i] = A.tab_src[i];
+  if (A.cnt)
+    for (int i = t; i < A.cnt_words; i += nt) A.cnt[i] = 0ull;
 }
 
-hipError_t tsa_launch_levels_init(double* own, int* bslot, int n, hipStream_t stream) {
-  hipLaunchKernelGGL(k_levels_init, dim3((n + 255) / 256), dim3(256), 0, stream, own, bslot, n);
+hipError_t tsa_launch_anneal_init(const TsaAnnealInit& A, hipStream_t stream) {
+  int n = A.track ? (A.trace_words > A.best_words ? A.trace_words : A.best_words) : 1;
+  if (A.own && A.nchains > n) n = A.nchains;
+  if (A.tab_src && A.tab_words > n) n = A.tab_words;
+  if (A.cnt && A.cnt_words > n) n = A.cnt_words;
+  int grid = (n + 255) / 256;
+  if (grid > 64) grid = 64;
+  hipLaunchKernelGGL(k_anneal_init, dim3(grid), dim3(256), 0, stream, A);
+  return hipGetLastError();
+}
+
+__global__ void __launch_bounds__(256) k_track_out(const unsigned long long* __restrict__ st, int st_words,
+                                                   const unsigned long long* __restrict__ ticks0,
+                                                   const unsigned long long* __restrict__ tree, int tree_words,
+                                                   const unsigned long long* __restrict__ rows, int row_words,
+                                                   const unsigned* __restrict__ werr, unsigned long long* h_st,
+                                                   unsigned long long* h_t0, unsigned long long* h_tree,
+                                                   unsigned long long* h_rows, unsigned* h_werr) {
+  const int t = blockIdx.x * blockDim.x + threadIdx.x, nt = gridDim.x * blockDim.x;
+  for (int i = t; i < row_words; i += nt) h_rows[i] = rows[i];
+  for (int i = t; i < tree_words; i += nt) h_tree[i] = tree[i];
+  if (t < st_words) h_st[t] = st[t];
+  if (t == 0) *h_t0 = *ticks0;
+  if (t == 0 && werr) *h_werr = *werr;
+}
+
+hipError_t tsa_launch_track_out(const unsigned long long* st, int st_words, const unsigned long long* ticks0,
+                                const unsigned long long* tree, int tree_words, const unsigned long long* rows,
+                                int row_words, const unsigned* werr, unsigned long long* h_st,
+                                unsigned long long* h_t0, unsigned long long* h_tree, unsigned long long* h_rows,
+                                unsigned* h_werr, hipStream_t stream) {
+  int n = row_words > tree_words ? row_words : tree_words;
+  if (st_words > n) n = st_words;
+  int grid = (n + 255) / 256;
+  if (grid < 1) grid = 1;
+  if (grid > 16) grid = 16;
+  hipLaunchKernelGGL(k_track_out, dim3(grid), dim3(256), 0, stream, st, st_words, ticks0, tree, tree_words, rows,
+                     row_words, werr, h_st, h_t0, h_tree, h_rows, h_werr);
   return hipGetLastError();
 }
 

@@ -22,6 +22,7 @@
 
 #include "treesa_hip.h"
 #include "tsa_cli.h"
+#include "tsa_fmt.h"
 #include "tsa_host.h"
 
 using namespace tsa;
@@ -349,11 +350,31 @@ void Run::build_schedule() {
       sched_.push_back({x, O_.stage2_mode, O_.stage2_niters > 0 ? O_.stage2_niters : O_.niters});
 }
 
+// One trace row, the characters of "%s[%.4f,%d,%.4f,%.6f,%d,%.6f,%d,%d,%d,%.3f]" (tsa_fmt.h)
 void Run::add_trace(double t, int lev, float lc, int sc, double meanE, int families, int ns, double meanNs) {
-  char b[320];
-  snprintf(b, sizeof b, "%s[%.4f,%d,%.4f,%.6f,%d,%.6f,%d,%d,%d,%.3f]", trace_.empty() ? "" : ",", t, lev,
-           (double)sched_[lev].beta, (double)lc, sc, meanE, families, mode_, ns, meanNs);
-  trace_ += b;
+  char b[1600];
+  int n = 0;
+  if (!trace_.empty()) b[n++] = ',';
+  b[n++] = '[';
+  n += fmt_fixed(b + n, t, 4);
+  b[n++] = ',';
+  n += fmt_int(b + n, lev);
+  b[n++] = ',';
+  n += fmt_fixed(b + n, (double)sched_[lev].beta, 4);
+  b[n++] = ',';
+  n += fmt_fixed(b + n, (double)lc, 6);
+  b[n++] = ',';
+  n += fmt_int(b + n, sc);
+  b[n++] = ',';
+  n += fmt_fixed(b + n, meanE, 6);
+  for (int v : {families, mode_, ns}) {
+    b[n++] = ',';
+    n += fmt_int(b + n, v);
+  }
+  b[n++] = ',';
+  n += fmt_fixed(b + n, meanNs, 3);
+  b[n++] = ']';
+  trace_.append(b, (size_t)n);
 }
 
 void Run::progress(int lev, float lc, int sc, int ns, double meanE, double meanNs, int families, double t) const {
