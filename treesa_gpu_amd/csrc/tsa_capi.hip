@@ -111,6 +111,10 @@ struct tsa_ctx {
   long long split_levels = 0;  // sweep calls run as two launches (reported by tsa_describe)
   hipEvent_t ev_sweep[TSA_SNAP_MAX] = {};  // (the stop events of those sweeps' timing pairs)
   hipEvent_t ev_track[TSA_SNAP_MAX] = {};
+  // the slot whose ev_track covers slot s (the slots of one block of levels share the event recorded after
+  // their one selection launch: every event recorded on a busy stream is a packet the device processes, about
+  // 5 us each)
+  int track_ev[TSA_SNAP_MAX] = {};
   int last_track = -1;  // the slot whose ev_track was recorded last (st2 runs the selections in order)
   // the session's start was enqueued on st2 (behind the first sweeps) and st has not yet waited for it
   hipEvent_t ev_tinit = nullptr;
@@ -694,7 +698,7 @@ static int ensure_slots(tsa_ctx* ctx, int n) {
 // even when it is already satisfied, and the host is normally many levels ahead of the device.
 static hipError_t claim_slot(tsa_ctx* c, int s) {
   hipError_t e = hipSuccess;
-  if (c->track_pending[s]) e = hipEventSynchronize(c->ev_track[s]);
+  if (c->track_pending[s]) e = hipEventSynchronize(c->ev_track[c->track_ev[s]]);
   c->track_pending[s] = false;
   return e;
 }
@@ -961,7 +965,11 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
       if (markers) TSA_HIP(ctx, hipEventRecord(f1, ctx->st3));
       if (blk) {
         for (int i = 0; i < blk->n; i++)
-          if (blk_slots[i] >= 0) TSA_HIP(ctx, hipEventRecord(ctx->ev_b[blk_slots[i]], ctx->st3));
+          if (blk_slots[i] >= 0) {  // (one event for the block: the first evaluated level's, which its
+                                    // selection launch waits for)
+            TSA_HIP(ctx, hipEventRecord(ctx->ev_b[blk_slots[i]], ctx->st3));
+            break;
+          }
       } else {
         TSA_HIP(ctx, hipEventRecord(ctx->ev_b[s], ctx->st3));
       }
@@ -1165,11 +1173,13 @@ static int track_block(tsa_ctx* ctx, const int* slots, const int* levels, int n)
   }
   TSA_HIP(ctx, tsa_launch_track_levels(T, ctx->nchains, S, ctx->d_rec, L.chain_words, L.ch_off, L.s_off, L.W, L.nint,
                                        ctx->d_track, ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2));
+  const int sl = slots[n - 1];
+  TSA_HIP(ctx, hipEventRecord(ctx->ev_track[sl], ctx->st2));
   for (int i = 0; i < n; i++) {
-    TSA_HIP(ctx, hipEventRecord(ctx->ev_track[slots[i]], ctx->st2));
     ctx->track_pending[slots[i]] = true;
-    ctx->last_track = slots[i];
+    ctx->track_ev[slots[i]] = sl;
   }
+  ctx->last_track = sl;
   ctx->energy_fresh = false;
   return TSA_OK;
 }
@@ -1206,6 +1216,7 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
                                   L.chain_words, L.ch_off, L.s_off, L.W, L.nint, ctx->d_snap_ch[s], ctx->d_track,
                                   ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2));
     TSA_HIP(ctx, hipEventRecord(ctx->ev_track[s], ctx->st2));
+    ctx->track_ev[s] = s;
     ctx->track_pending[s] = true;
     ctx->last_track = s;
     ctx->energy_fresh = false;  // d_lc / d_sc / d_ns now hold the snapshot's energies
@@ -1382,7 +1393,7 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
     }
   }
   ctx->lv_used = loop ? 1 : 0;
-  if (!loop) TSA_HIP(ctx, flush_track_init(ctx));  // (the level loop's set-up launch does it)
+  // (a pending session start: the first sweeps enqueue it, or the level loop's set-up launch does it)
   // Several levels per sweep launch (the one-wave LDS kernels with the overlapped selection and the fold apart,
   // where the population is more than twice what the device holds at once): a launch ends with a tail in which
   // fewer and fewer chains are left to run, and a level of one sweep per chain is short next to it; a block of
