@@ -214,7 +214,8 @@ int tsa_track(tsa_ctx* ctx, int32_t level);
 /* Wait and return the best over the tracked levels (best_chain -1 if none), its tree in best_record (a
  * chain_words record of which the children words and S are written; its label words are a function of the
  * tree and are left as they were), max_levels trace rows (rows of untracked levels are zero) and the device
- * wall-clock rate in Hz; ticks0 = device wall clock at tsa_track_begin. */
+ * wall-clock rate in Hz; ticks0 = device wall clock when the session started on the device (the session's
+ * start is enqueued with its first launch after tsa_track_begin). */
 int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_level, double* best_score, uint64_t* best_record,
                   tsa_trace_row_t* rows, uint64_t* ticks0, double* tick_hz);
 

@@ -62,7 +62,8 @@ struct tsa_ctx {
   bool energy_host = false;   // the last sweep launch wrote the energies of the current population into h_en
   int* d_anc = nullptr;
   int* h_anc = nullptr;            // pinned staging of the ancestor list
-  hipEvent_t ev_anc = nullptr;     // recorded after the ancestor upload that read h_anc last
+  int* d_hanc = nullptr;           // the device's address of h_anc (null: not mapped, the list goes by a copy)
+  hipEvent_t ev_anc = nullptr;     // recorded after the launch that read h_anc last
   bool anc_pending = false;
   TsaWide wide{};              // wide path plan (wide.on: par sweeps and energies run tsa_wide.hip)
   TsaWideSync wsync{};         // chain barrier words (one allocation) and visit outcomes
@@ -625,6 +626,10 @@ extern "C" int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t
   }
   TSA_CREATE_HIP(hipMalloc(&c->d_anc, (size_t)nchains * 4));
   TSA_CREATE_HIP(hipHostMalloc(&c->h_anc, (size_t)nchains * 4, hipHostMallocDefault));
+  if (hipHostGetDevicePointer(reinterpret_cast<void**>(&c->d_hanc), c->h_anc, 0) != hipSuccess) {
+    (void)hipGetLastError();  // not mapped: the list goes by a copy
+    c->d_hanc = nullptr;
+  }
   TSA_CREATE_HIP(hipEventCreateWithFlags(&c->ev_anc, hipEventDisableTiming));
   TSA_CREATE_HIP(hipStreamSynchronize(c->st));
 #undef TSA_CREATE_HIP
@@ -1172,7 +1177,8 @@ static int track_block(tsa_ctx* ctx, const int* slots, const int* levels, int n)
     TSA_HIP(ctx, tsa_launch_fold_levels(ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, F, 0, ctx->nchains, ctx->st2));
   }
   TSA_HIP(ctx, tsa_launch_track_levels(T, ctx->nchains, S, ctx->d_rec, L.chain_words, L.ch_off, L.s_off, L.W, L.nint,
-                                       ctx->d_track, ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2));
+                                       ctx->d_track, ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2,
+                                       false));
   const int sl = slots[n - 1];
   TSA_HIP(ctx, hipEventRecord(ctx->ev_track[sl], ctx->st2));
   for (int i = 0; i < n; i++) {
@@ -1214,7 +1220,7 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
     const int* ns = folded ? reinterpret_cast<const int*>(ctx->d_snap_en[s]) + 2 * (size_t)ctx->nchains : ctx->d_ns;
     TSA_HIP(ctx, tsa_launch_track(lc, sc, ns, ctx->nchains, S, level, ctx->d_rec,
                                   L.chain_words, L.ch_off, L.s_off, L.W, L.nint, ctx->d_snap_ch[s], ctx->d_track,
-                                  ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2));
+                                  ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2, false));
     TSA_HIP(ctx, hipEventRecord(ctx->ev_track[s], ctx->st2));
     ctx->track_ev[s] = s;
     ctx->track_pending[s] = true;
@@ -1226,7 +1232,7 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
   TSA_HIP(ctx, launch_energy(ctx));  // (orders st after any selection pending on st2)
   TSA_HIP(ctx, tsa_launch_track(ctx->d_lc, ctx->d_sc, ctx->d_ns, ctx->nchains, S, level, ctx->d_rec, L.chain_words,
                                 L.ch_off, L.s_off, L.W, L.nint, nullptr, ctx->d_track, ctx->d_trace, ctx->d_best,
-                                ctx->d_tpart, ctx->d_tdone, ctx->st));
+                                ctx->d_tpart, ctx->d_tdone, ctx->st, true));
   return TSA_OK;
 }
 
@@ -1570,18 +1576,20 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
     if (anc[c] < 0 || anc[c] >= ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_resample: ancestor out of range");
   if (!ctx->d_rec2) TSA_HIP(ctx, hipMalloc(&ctx->d_rec2, (size_t)ctx->nchains * ctx->lay.chain_words * 8));
   TSA_HIP(ctx, quiesce_track(ctx));
-  // the ancestors go through the pinned staging buffer (an asynchronous copy); the last upload from it must
-  // have been read before it is overwritten
+  // the ancestors go through the pinned staging buffer, which the copy kernel reads where it is mapped (else
+  // an asynchronous copy to d_anc); the last launch that read it must be done before it is overwritten
   if (ctx->anc_pending) TSA_HIP(ctx, hipEventSynchronize(ctx->ev_anc));
   memcpy(ctx->h_anc, anc, (size_t)ctx->nchains * 4);
-  TSA_HIP(ctx, hipMemcpyAsync(ctx->d_anc, ctx->h_anc, (size_t)ctx->nchains * 4, hipMemcpyHostToDevice, ctx->st));
-  TSA_HIP(ctx, hipEventRecord(ctx->ev_anc, ctx->st));
-  ctx->anc_pending = true;
+  if (!ctx->d_hanc)
+    TSA_HIP(ctx, hipMemcpyAsync(ctx->d_anc, ctx->h_anc, (size_t)ctx->nchains * 4, hipMemcpyHostToDevice, ctx->st));
   ctx->costs_valid = false;
   ctx->energy_fresh = ctx->energy_host = false;
   ctx->sums_valid = false;
   // the copy and everything after it run in stream order: no wait here
-  TSA_HIP(ctx, tsa_launch_copy(ctx->d_rec, ctx->d_rec2, ctx->d_anc, ctx->nchains, ctx->lay.chain_words, ctx->st));
+  TSA_HIP(ctx, tsa_launch_copy(ctx->d_rec, ctx->d_rec2, ctx->d_hanc ? ctx->d_hanc : ctx->d_anc, ctx->nchains,
+                               ctx->lay.chain_words, ctx->st));
+  TSA_HIP(ctx, hipEventRecord(ctx->ev_anc, ctx->st));
+  ctx->anc_pending = true;
   std::swap(ctx->d_rec, ctx->d_rec2);
   return TSA_OK;
 }

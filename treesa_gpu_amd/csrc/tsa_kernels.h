@@ -189,16 +189,18 @@ struct TsaTrackLevels {
 };
 // part: (L.n + 1) * ceil(nchains / 256) entries; done: L.n + 1 zeroed counters (left zero after every launch).
 // When a level improves the best score, the chain's tree is copied into best_rec: its children words (from
-// L.ch, when not null, else from rec) and its S words (from rec); label words are left as they are.
+// L.ch, when not null, else from rec) and its S words (from rec); label words are left as they are.  alone: the
+// selection runs by itself between sweeps (workgroups of four waves that score a chain per lane at once) rather
+// than beside a sweep (one wave per group, no LDS); the results are the same.
 hipError_t tsa_launch_track_levels(const TsaTrackLevels& L, int nchains, const TsaSelect& S, const uint64_t* rec,
                                    int chain_words, int ch_off, int s_off, int W, int nint, TsaTrackState* st,
                                    TsaTraceRowD* trace, uint64_t* best_rec, TsaTrackPart* part, unsigned* done,
-                                   hipStream_t stream);
+                                   hipStream_t stream, bool alone);
 // One level: lc / sc / ns, trace row `level`, children words ch_snap.
 hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int nchains, const TsaSelect& S, int level,
                             const uint64_t* rec, int chain_words, int ch_off, int s_off, int W, int nint,
                             const uint32_t* ch_snap, TsaTrackState* st, TsaTraceRowD* trace, uint64_t* best_rec,
-                            TsaTrackPart* part, unsigned* done, hipStream_t stream);
+                            TsaTrackPart* part, unsigned* done, hipStream_t stream, bool alone);
 // After a level-loop launch (Lv: its levels, trace rows, candidate slots and the chains' own / bslot as the
 // launch left them): the best over the launch's evaluated levels in level order (the lowest score, the first
 // level on ties) against the session's best in st, which it replaces, and the best chain's kept tree (its

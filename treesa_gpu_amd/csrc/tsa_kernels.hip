@@ -123,29 +123,47 @@ __device__ __forceinline__ TsaTrackAcc tsa_track_tree(TsaTrackAcc (&v)[4], int l
 // group in a fixed tree order; the last group of a level to finish reduces the groups' results in index order
 // and writes the level's trace row; the last level to finish keeps the best over the launch's levels in level
 // order (the lowest score; the first level on ties, as one launch per level would) and copies the new best
-// chain's tree.  No LDS, so that the selection's waves fit beside sweep workgroups that fill a compute unit's
-// LDS.  Sums are deterministic.
-__global__ void __launch_bounds__(64) k_track(TsaTrackLevels L, int n, TsaSelect S, const uint64_t* __restrict__ rec,
-                                              int chain_words, int ch_off, int s_off, int W, int nint,
-                                              TsaTrackState* __restrict__ st, TsaTraceRowD* __restrict__ trace,
-                                              uint64_t* __restrict__ best_rec, TsaTrackPart* __restrict__ part,
-                                              unsigned* __restrict__ done) {
-  const int lane = (int)threadIdx.x, g = (int)blockIdx.x, li = (int)blockIdx.y, G = (int)gridDim.x;
+// chain's tree.  Sums are deterministic.  WAVES = 1: no LDS, so that the selection's waves fit beside sweep
+// workgroups that fill a compute unit's LDS (each lane scores four chains in turn); WAVES = 4, for a selection
+// that runs alone between sweeps: the four waves score a chain per lane at once and hand the entries to wave 0
+// through LDS, which reduces them in the same order.
+__device__ __forceinline__ TsaTrackAcc tsa_track_entry(int c, int n, const float* __restrict__ lc,
+                                                       const int* __restrict__ sc, const int* __restrict__ ns,
+                                                       const TsaSelect& S) {
+  TsaTrackAcc v{INFINITY, 0.0, 0.0, n};
+  if (c < n) {
+    const double s = tsa_score(lc[c], sc[c], ns[c], S);
+    v.s = s;
+    v.i = s < INFINITY ? c : n;
+    v.e = tsa_energyE(lc[c], sc[c], ns[c], S);
+    v.n = (double)ns[c];
+  }
+  return v;
+}
+
+template <int WAVES>
+__global__ void __launch_bounds__(64 * WAVES) k_track(TsaTrackLevels L, int n, TsaSelect S,
+                                                      const uint64_t* __restrict__ rec, int chain_words, int ch_off,
+                                                      int s_off, int W, int nint, TsaTrackState* __restrict__ st,
+                                                      TsaTraceRowD* __restrict__ trace, uint64_t* __restrict__ best_rec,
+                                                      TsaTrackPart* __restrict__ part, unsigned* __restrict__ done) {
+  const int lane = (int)threadIdx.x & 63, g = (int)blockIdx.x, li = (int)blockIdx.y, G = (int)gridDim.x;
   const float* __restrict__ lc = L.lc[li];
   const int* __restrict__ sc = L.sc[li];
   const int* __restrict__ ns = L.ns[li];
   TsaTrackAcc v[4];
+  if constexpr (WAVES == 1) {
 #pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int c = g * 256 + lane + 64 * j;
-    v[j] = TsaTrackAcc{INFINITY, 0.0, 0.0, n};
-    if (c < n) {
-      const double s = tsa_score(lc[c], sc[c], ns[c], S);
-      v[j].s = s;
-      v[j].i = s < INFINITY ? c : n;
-      v[j].e = tsa_energyE(lc[c], sc[c], ns[c], S);
-      v[j].n = (double)ns[c];
-    }
+    for (int j = 0; j < 4; j++) v[j] = tsa_track_entry(g * 256 + lane + 64 * j, n, lc, sc, ns, S);
+  } else {
+    static_assert(WAVES == 4, "one wave, or four waves of 64 chains each");
+    __shared__ TsaTrackAcc sh[256];
+    const int w = (int)threadIdx.x >> 6;
+    sh[threadIdx.x] = tsa_track_entry(g * 256 + lane + 64 * w, n, lc, sc, ns, S);
+    __syncthreads();
+    if (w != 0) return;
+#pragma unroll
+    for (int j = 0; j < 4; j++) v[j] = sh[lane + 64 * j];
   }
   const TsaTrackAcc r = tsa_track_tree(v, lane);
   int last = 0;
@@ -281,17 +299,22 @@ hipError_t tsa_launch_energy(int Wt, int mode, const TsaKParams& P, const uint64
 hipError_t tsa_launch_track_levels(const TsaTrackLevels& L, int nchains, const TsaSelect& S, const uint64_t* rec,
                                    int chain_words, int ch_off, int s_off, int W, int nint, TsaTrackState* stt,
                                    TsaTraceRowD* trace, uint64_t* best_rec, TsaTrackPart* part, unsigned* done,
-                                   hipStream_t stream) {
+                                   hipStream_t stream, bool alone) {
   if (L.n < 1 || L.n > TSA_BLOCK_MAX || nchains < 1) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_track, dim3((nchains + 255) / 256, L.n), dim3(64), 0, stream, L, nchains, S, rec, chain_words,
-                     ch_off, s_off, W, nint, stt, trace, best_rec, part, done);
+  const dim3 grid((nchains + 255) / 256, L.n);
+  if (alone)
+    hipLaunchKernelGGL(k_track<4>, grid, dim3(256), 0, stream, L, nchains, S, rec, chain_words, ch_off, s_off, W, nint,
+                       stt, trace, best_rec, part, done);
+  else
+    hipLaunchKernelGGL(k_track<1>, grid, dim3(64), 0, stream, L, nchains, S, rec, chain_words, ch_off, s_off, W, nint,
+                       stt, trace, best_rec, part, done);
   return hipGetLastError();
 }
 
 hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int nchains, const TsaSelect& S, int level,
                             const uint64_t* rec, int chain_words, int ch_off, int s_off, int W, int nint,
                             const uint32_t* ch_snap, TsaTrackState* stt, TsaTraceRowD* trace, uint64_t* best_rec,
-                            TsaTrackPart* part, unsigned* done, hipStream_t stream) {
+                            TsaTrackPart* part, unsigned* done, hipStream_t stream, bool alone) {
   TsaTrackLevels L{};
   L.n = 1;
   L.lev[0] = level;
@@ -300,7 +323,7 @@ hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int n
   L.ns[0] = ns;
   L.ch[0] = ch_snap;
   return tsa_launch_track_levels(L, nchains, S, rec, chain_words, ch_off, s_off, W, nint, stt, trace, best_rec, part,
-                                 done, stream);
+                                 done, stream, alone);
 }
 
 // The session's best after a level-loop launch (tsa_launch_level_best): lane l takes the launch's levels l,
