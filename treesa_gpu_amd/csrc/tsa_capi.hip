@@ -674,6 +674,13 @@ static hipError_t flush_track_init(tsa_ctx* c, bool on_st2 = false) {
   return e;
 }
 
+// The wide path's overlapped selection with the fold in the sweep launch: dense plans of one workgroup per chain
+// with more chains than compute units (with fewer, the fold of the node-cost snapshot runs beside the next
+// sweep as well).
+static bool wide_fold_snap(const tsa_ctx* c) {
+  return c->wide.on && c->wide.K == 1 && c->wide.nsw == 0 && c->nchains >= c->ncu && !c->cfg.slicing;
+}
+
 static hipError_t quiesce_track(tsa_ctx* c) {
   hipError_t e = hipSuccess;
   if (c->st2) e = hipStreamSynchronize(c->st2);
@@ -852,9 +859,11 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
                                           ctx->d_ns, 1, ctx->st, wide_sums(ctx)));
       ctx->costs_valid = true;
     }
-    // without the overlap, a dense plan of one workgroup per chain folds the energies at the end of the sweep
-    // (the sweep kernel has every chain's cost cache at hand; a fold launch after it would find the device idle
-    // but for its one lane group per chain)
+    // a dense plan of one workgroup per chain folds the energies at the end of the sweep (the sweep kernel has
+    // every chain's cost cache at hand; a fold launch after it would find the device idle but for its one lane
+    // group per chain): without the overlap into d_lc / d_sc / d_ns, with it into the snapshot slot, whose tree
+    // the selection beside the next sweep reads
+    const bool snap_fold = ctx->overlap && wide_fold_snap(ctx) && ctx->costs_valid;
     const bool fold_here = !ctx->overlap && ctx->wide.K == 1 && ctx->wide.nsw == 0 && ctx->costs_valid;
     if (fold_here) {
       join_track(ctx);  // a selection still pending on st2 reads d_lc / d_sc / d_ns
@@ -866,9 +875,16 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
       s = ctx->slot;
       TSA_HIP(ctx, claim_slot(ctx, s));
       sy.snap_ch = ctx->d_snap_ch[s];
-      sy.snap_cost = ctx->d_snap_cost[s];
-      sy.snap_nz = ctx->d_snap_nz[s];
-      ctx->snap_kind[s] = SNAP_WIDE;
+      if (snap_fold) {
+        sy.flc = reinterpret_cast<float*>(ctx->d_snap_en[s]);
+        sy.fsc = reinterpret_cast<int*>(ctx->d_snap_en[s]) + ctx->nchains;
+        sy.fns = reinterpret_cast<int*>(ctx->d_snap_en[s]) + 2 * (size_t)ctx->nchains;
+        ctx->snap_kind[s] = SNAP_ENERGIES;
+      } else {
+        sy.snap_cost = ctx->d_snap_cost[s];
+        sy.snap_nz = ctx->d_snap_nz[s];
+        ctx->snap_kind[s] = SNAP_WIDE;
+      }
     }
     if (markers) TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
     TSA_HIP(ctx, tsa_launch_wide(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, ctx->nchains, beta,
@@ -1111,13 +1127,15 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   // left: on the wide path with one workgroup per chain (a chain barrier, K > 1, needs all of the sweep's
   // workgroups resident at once, so nothing may take their place) and fewer chains than compute units (with
   // more, the fold's workgroups, which stage 64 KB of tables in LDS, take the places of sweep workgroups:
-  // C4's sweep 265 -> 353 us), and on the one-wave kernels with fused energies.  The fold and the selection are serial chains of dependent operations: beside a sweep they
-  // fill issue slots and compute units the sweep leaves idle (its last round of workgroups, its waves'
-  // memory or LDS waits) instead of adding their latency to every level.  Slice moves rewrite S, which the
-  // fold and the selection read from the records, so they keep the serial order.
+  // C4's sweep 265 -> 353 us; there a dense plan folds in the sweep launch itself and only the selection, one
+  // wave per 256 chains, runs beside the next sweep), and on the one-wave kernels with fused energies.  The
+  // fold and the selection are serial chains of dependent operations: beside a sweep they fill issue slots and
+  // compute units the sweep leaves idle (its last round of workgroups, its waves' memory or LDS waits) instead
+  // of adding their latency to every level.  Slice moves rewrite S, which the fold and the selection read from
+  // the records, so they keep the serial order.
   const bool want_overlap =
       ctx->cfg.track_overlap >= 0 &&
-      ((ctx->wide.on && ctx->wide.K == 1 && ctx->nchains < ctx->ncu) ||
+      ((ctx->wide.on && ctx->wide.K == 1 && ctx->nchains < ctx->ncu) || wide_fold_snap(ctx) ||
        (!ctx->wide.on && ctx->cfg.fused_energy != 0 && !ctx->cfg.slicing));
   if (want_overlap && !ctx->st2) {
     TSA_HIP(ctx, hipStreamCreateWithFlags(&ctx->st2, hipStreamNonBlocking));

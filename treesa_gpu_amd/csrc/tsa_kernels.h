@@ -298,7 +298,8 @@ struct TsaWideSync {
   int lsum_lds;  // 1: the sweep kernel stages leafsum in LDS (when it fits beside the node arrays)
   // Snapshot of every chain's tree and node-cost cache at the end of the launch (null: none), so that the
   // energy fold and the selection of this level can run beside the next level's sweep:
-  // snap_ch[nchains][nint], snap_cost / snap_nz [nchains][nint4].
+  // snap_ch[nchains][nint], snap_cost / snap_nz [nchains][nint4] (snap_cost null: the tree alone, for a launch
+  // that folds the energies itself).
   uint32_t* snap_ch;
   float* snap_cost;
   uint16_t* snap_nz;

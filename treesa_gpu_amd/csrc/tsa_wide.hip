@@ -747,9 +747,11 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
     if (sy.snap_ch) {  // the level's snapshot: tree from LDS, node costs (final after the last barrier)
       uint32_t* const sch = sy.snap_ch + (size_t)c * nint;
       for (int i = threadIdx.x; i < nint; i += NT) sch[i] = ch[i];
-      const size_t cb = (size_t)c * nint4;
-      tsa_copy_inflight<float, 8>(sy.snap_cost + cb, sy.ncost + cb, nint, threadIdx.x, NT);
-      tsa_copy_inflight<uint16_t, 8>(sy.snap_nz + cb, sy.nz + cb, nint, threadIdx.x, NT);
+      if (sy.snap_cost) {
+        const size_t cb = (size_t)c * nint4;
+        tsa_copy_inflight<float, 8>(sy.snap_cost + cb, sy.ncost + cb, nint, threadIdx.x, NT);
+        tsa_copy_inflight<uint16_t, 8>(sy.snap_nz + cb, sy.nz + cb, nint, threadIdx.x, NT);
+      }
     }
   }
   if constexpr (!COOP && !SUMS) {
