@@ -80,6 +80,25 @@ def test_overlapped_selection(nchains, order, tmp_path):
     assert max(abs(x[5] - y[5]) for x, y in zip(ta, tc)) < 1e-9
 
 
+# The wide path with one workgroup per chain and more chains than compute units (MI355X: 256): the sweep launch
+# folds the energies into the level's snapshot slot beside the tree, and the selection runs on a second stream
+# beside the next sweep.  The result equals the same run with the selection after each sweep on its stream and
+# the host-side level loop.
+def test_wide_selection_beside_the_sweep(tmp_path):
+    args = ["-i", common.inst_path("sq46"), "--nchains", "320", "--niters", "1", "--betas", "0.5:0.5:4",
+            "--sc-target", "30", "--order", "par", "--seed", "4", "--no-sum", "--wide-wgs", "1"]
+    a = run(args, tmp_path, "a.json")
+    b = run(args + ["--no-overlap"], tmp_path, "b.json")
+    c = run(args + ["--host-select"], tmp_path, "c.json")
+    for k in ("tc", "sc", "best_chain", "tree", "proposals", "accepts", "node_visits", "valid", "labels_ok"):
+        assert a[k] == b[k] == c[k], k
+    assert a["valid"] and a["labels_ok"]
+    ta, tb, tc = ([list(r) for r in x["trace"]] for x in (a, b, c))
+    assert [r[1:] for r in ta] == [r[1:] for r in tb]
+    assert [r[1:5] + r[6:] for r in ta] == [r[1:5] + r[6:] for r in tc]
+    assert max(abs(x[5] - y[5]) for x, y in zip(ta, tc)) < 1e-9
+
+
 @pytest.mark.parametrize("inst,extra", [("sat100", ["--kernel", "par"]), ("sat100", ["--order", "preorder"]),
                                         ("reg3_250", ["--mode", "h100"]), ("grid24", ["--mode", "gpu"]),
                                         ("sat60", ["--random-slices", "8"]), ("sq46", ["--kernel", "par"]),

@@ -57,6 +57,9 @@ struct tsa_ctx {
   // tsa_track_begin leaves the session's start (k_track_init) to the next call, which enqueues it before
   // anything else (the same place in the stream's order), or to the level loop's set-up launch, which does it
   bool track_init_pending = false;
+  // the last level-loop launch's k_level_best wrote the session's results into h_tend (tsa_track_end then
+  // only waits)
+  bool tend_staged = false;
   double tick_hz = 0.0;  // the device's wall-clock rate (Hz)
   uint32_t* d_hen = nullptr;  // the device's address of h_en (null: not mapped)
   bool energy_host = false;   // the last sweep launch wrote the energies of the current population into h_en
@@ -674,6 +677,25 @@ static hipError_t flush_track_init(tsa_ctx* c, bool on_st2 = false) {
   return e;
 }
 
+// Where tsa_track_end's results sit in the page-locked staging buffer h_tend (byte offsets): the tracking
+// state, the start tick, the wide path's error word, the best tree (children words and S: tree bytes) and the
+// trace rows (row bytes).
+struct TendLayout {
+  size_t st, t0, werr, tree, rows, tree_bytes, row_bytes;
+};
+static TendLayout tend_layout(const tsa_ctx* c) {
+  const tsa_layout_t& L = c->lay;
+  TendLayout o;
+  o.tree_bytes = (size_t)(L.s_off + L.W - L.ch_off) * 8;
+  o.row_bytes = (size_t)c->track_levels * sizeof(TsaTraceRowD);
+  o.st = 0;
+  o.t0 = (sizeof(TsaTrackState) + 15) & ~(size_t)15;
+  o.werr = o.t0 + 8;
+  o.tree = o.t0 + 16;
+  o.rows = o.tree + ((o.tree_bytes + 15) & ~(size_t)15);
+  return o;
+}
+
 // The wide path's overlapped selection with the fold in the sweep launch: dense plans of one workgroup per chain
 // with more chains than compute units (with fewer, the fold of the node-cost snapshot runs beside the next
 // sweep as well).
@@ -1098,6 +1120,8 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
     const size_t need = sizeof(TsaTrackState) + 16 + (size_t)(L.s_off + L.W - L.ch_off) * 8 +
                         (size_t)max_levels * sizeof(TsaTraceRowD) + 64;
     if (need > ctx->h_tend_bytes) {
+      // (a level-loop launch of an unfinished session may still write its results there)
+      if (ctx->h_tend) TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
       if (ctx->h_tend) TSA_HIP(ctx, hipHostFree(ctx->h_tend));
       ctx->h_tend = nullptr;
       ctx->h_tend_bytes = 0;
@@ -1150,6 +1174,7 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
   ctx->lv_evaluated.assign((size_t)max_levels, 0);
   static_assert(sizeof(TsaTraceRowD) % 8 == 0, "trace rows are whole words");
   ctx->track_init_pending = true;
+  ctx->tend_staged = false;
   return TSA_OK;
 }
 
@@ -1161,6 +1186,7 @@ extern "C" int tsa_track_begin(tsa_ctx* ctx, const tsa_select_t* sel, int32_t ma
 static int track_block(tsa_ctx* ctx, const int* slots, const int* levels, int n) {
   if (n == 0) return TSA_OK;
   ctx->track_kind = TRACK_LEVELS;
+  ctx->tend_staged = false;
   TsaSelect S = ctx->sel;
   S.mode = ctx->mode;
   const tsa_layout_t& L = ctx->lay;
@@ -1216,6 +1242,7 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
   if (ctx->track_kind == TRACK_ANNEAL)
     return fail(ctx, TSA_ERR_ARG, "tsa_track: this tracking session runs its levels with tsa_anneal");
   ctx->track_kind = TRACK_LEVELS;
+  ctx->tend_staged = false;
   TsaSelect S = ctx->sel;
   S.mode = ctx->mode;
   const tsa_layout_t& L = ctx->lay;
@@ -1273,17 +1300,20 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
   if (!on2) join_track(ctx);
   // every copy into the pinned staging buffer, one wait, then the caller's buffers from there
   const tsa_layout_t& L = ctx->lay;
-  const size_t cwb = (size_t)(L.s_off + L.W - L.ch_off) * 8, rowb = (size_t)ctx->track_levels * sizeof(TsaTraceRowD);
+  const TendLayout tl = tend_layout(ctx);
+  const size_t cwb = tl.tree_bytes, rowb = tl.row_bytes;
   char* const hs = ctx->h_tend;
-  char* const h_state = hs;
-  char* const h_t0 = h_state + ((sizeof(TsaTrackState) + 15) & ~(size_t)15);
-  char* const h_werr = h_t0 + 8;
-  char* const h_tree = h_t0 + 16;
-  char* const h_rows = h_tree + ((cwb + 15) & ~(size_t)15);
+  char* const h_state = hs + tl.st;
+  char* const h_t0 = hs + tl.t0;
+  char* const h_werr = hs + tl.werr;
+  char* const h_tree = hs + tl.tree;
+  char* const h_rows = hs + tl.rows;
   // the best chain's tree: children words and S (the label words of best_record are not written)
   static_assert(sizeof(TsaTrackState) % 8 == 0, "the tracking state is whole words");
   uint32_t werr = 0;
-  if (ctx->d_tend) {
+  if (ctx->tend_staged && ctx->d_tend) {
+    // the last level-loop launch's selection of the best wrote them (behind it on st)
+  } else if (ctx->d_tend) {
     // one launch writes them all into the mapped staging buffer (four or five copies cost about 5 us each)
     char* const d = ctx->d_tend;
     TSA_HIP(ctx, tsa_launch_track_out(
@@ -1305,6 +1335,7 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
   if (on2) TSA_HIP(ctx, hipStreamSynchronize(ctx->st2));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
   ctx->host_waited = true;
+  ctx->tend_staged = false;
   std::memcpy(&h, h_state, sizeof h);
   std::memcpy(&t0, h_t0, sizeof t0);
   std::memcpy(best_record + L.ch_off, h_tree, cwb);
@@ -1559,8 +1590,21 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
   ctx->npending++;
   // the session's best over the launch's levels and its tree, on the device (tsa_track_end then copies it with
   // the trace rows instead of asking for the chain's kept tree after reading them)
-  if (nev > 0)
-    TSA_HIP(ctx, tsa_launch_level_best(lv, n, ctx->d_track, ctx->d_best, ctx->lay.ch_off, ctx->st));
+  if (nev > 0) {
+    // (and the session's results into the staging buffer, so that tsa_track_end only waits)
+    TsaTrackOut O{};
+    if (ctx->d_tend) {
+      const TendLayout tl = tend_layout(ctx);
+      O.h_st = reinterpret_cast<unsigned long long*>(ctx->d_tend + tl.st);
+      O.h_t0 = reinterpret_cast<unsigned long long*>(ctx->d_tend + tl.t0);
+      O.h_tree = reinterpret_cast<unsigned long long*>(ctx->d_tend + tl.tree);
+      O.h_rows = reinterpret_cast<unsigned long long*>(ctx->d_tend + tl.rows);
+      O.ticks0 = ctx->d_ticks0;
+      O.row_words = (int)(tl.row_bytes / 8);
+    }
+    TSA_HIP(ctx, tsa_launch_level_best(lv, n, ctx->d_track, ctx->d_best, ctx->lay.ch_off, O, ctx->st));
+    ctx->tend_staged = ctx->d_tend != nullptr;
+  }
   TSA_HIP(ctx, hipEventRecord(ctx->ev_lv[half], ctx->st));
   ctx->lv_pending[half] = true;
   return TSA_OK;

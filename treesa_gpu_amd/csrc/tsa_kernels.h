@@ -204,9 +204,19 @@ hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int n
 // After a level-loop launch (Lv: its levels, trace rows, candidate slots and the chains' own / bslot as the
 // launch left them): the best over the launch's evaluated levels in level order (the lowest score, the first
 // level on ties) against the session's best in st, which it replaces, and the best chain's kept tree (its
-// slot's words: children words and S) into best_rec + ch_off.  One wave.
+// slot's words: children words and S) into best_rec + ch_off.  One wave.  With O.h_st set it then writes the
+// session's results as k_track_out does (the state, the start tick, the best tree and all O.row_words words of
+// trace rows into mapped page-locked memory), so that the session's end needs no launch of its own.
+struct TsaTrackOut {
+  unsigned long long* h_st;  // null: no results written
+  unsigned long long* h_t0;
+  unsigned long long* h_tree;
+  unsigned long long* h_rows;
+  const unsigned long long* ticks0;
+  int row_words;
+};
 hipError_t tsa_launch_level_best(const TsaLevels& Lv, int nchains, TsaTrackState* st, uint64_t* best_rec, int ch_off,
-                                 hipStream_t stream);
+                                 const TsaTrackOut& O, hipStream_t stream);
 hipError_t tsa_launch_track_init(TsaTrackState* st, unsigned long long* ticks0, unsigned long long* trace,
                                  int trace_words, unsigned long long* best, int best_words, hipStream_t stream);
 // The set-up of a level-loop launch in one launch, each part optional: a tracking session's start (as

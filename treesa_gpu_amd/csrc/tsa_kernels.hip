@@ -331,7 +331,7 @@ hipError_t tsa_launch_track(const float* lc, const int* sc, const int* ns, int n
 // when it beats st's; the wave then copies that chain's kept tree.  The chains' bslot are the launch's final
 // values (the launch has ended).
 __global__ void __launch_bounds__(64) k_level_best(TsaLevels Lv, int n, TsaTrackState* __restrict__ st,
-                                                   uint64_t* __restrict__ best_rec, int ch_off) {
+                                                   uint64_t* __restrict__ best_rec, int ch_off, TsaTrackOut O) {
   const int lane = (int)threadIdx.x;
   double bs = INFINITY;
   int bl = -1, bc = -1;
@@ -367,15 +367,25 @@ __global__ void __launch_bounds__(64) k_level_best(TsaLevels Lv, int n, TsaTrack
   }
   slot = __shfl(slot, 0, 64);
   bc = __shfl(bc, 0, 64);
-  if (slot == 0 || slot == 1) {
-    const uint64_t* const src = Lv.cand + ((size_t)slot * n + bc) * Lv.cand_words;
+  const bool kept = slot == 0 || slot == 1;
+  const uint64_t* const src = kept ? Lv.cand + ((size_t)slot * n + bc) * Lv.cand_words : nullptr;
+  if (kept)
     for (int i = lane; i < Lv.cand_words; i += 64) best_rec[ch_off + i] = src[i];
+  if (!O.h_st) return;
+  // the session's results: the best tree from the words just copied (their source) or, unchanged by this launch,
+  // from best_rec; the state as lane 0 left it; every trace row (the earlier launches' too)
+  for (int i = lane; i < Lv.cand_words; i += 64) O.h_tree[i] = kept ? src[i] : best_rec[ch_off + i];
+  for (int i = lane; i < O.row_words; i += 64) O.h_rows[i] = reinterpret_cast<const unsigned long long*>(Lv.trace)[i];
+  if (lane == 0) {
+    const unsigned long long* const sw = reinterpret_cast<const unsigned long long*>(st);
+    for (int i = 0; i < (int)(sizeof(TsaTrackState) / 8); i++) O.h_st[i] = sw[i];
+    *O.h_t0 = *O.ticks0;
   }
 }
 
 hipError_t tsa_launch_level_best(const TsaLevels& Lv, int nchains, TsaTrackState* stt, uint64_t* best_rec, int ch_off,
-                                 hipStream_t stream) {
-  hipLaunchKernelGGL(k_level_best, dim3(1), dim3(64), 0, stream, Lv, nchains, stt, best_rec, ch_off);
+                                 const TsaTrackOut& O, hipStream_t stream) {
+  hipLaunchKernelGGL(k_level_best, dim3(1), dim3(64), 0, stream, Lv, nchains, stt, best_rec, ch_off, O);
   return hipGetLastError();
 }
 
