@@ -68,6 +68,10 @@ struct tsa_ctx {
   int* d_hanc = nullptr;           // the device's address of h_anc (null: not mapped, the list goes by a copy)
   hipEvent_t ev_anc = nullptr;     // recorded after the launch that read h_anc last
   bool anc_pending = false;
+  // tsa_resample's copy of the ancestors' records not made yet: the next sweep launch of the LDS kernels reads
+  // each chain's record from its ancestor's in d_rec and writes the population into d_rec2 (then the two swap);
+  // any other call makes the copy first (flush_resample)
+  bool anc_pend = false;
   TsaWide wide{};              // wide path plan (wide.on: par sweeps and energies run tsa_wide.hip)
   TsaWideSync wsync{};         // chain barrier words (one allocation) and visit outcomes
   unsigned* d_wsync = nullptr;
@@ -662,6 +666,17 @@ static hipError_t join_split(tsa_ctx* c) {
   return e;
 }
 
+static hipError_t flush_resample(tsa_ctx* c) {
+  if (!c->anc_pend) return hipSuccess;
+  c->anc_pend = false;
+  hipError_t e = tsa_launch_copy(c->d_rec, c->d_rec2, c->d_hanc ? c->d_hanc : c->d_anc, c->nchains,
+                                 c->lay.chain_words, c->st);
+  if (e == hipSuccess) e = hipEventRecord(c->ev_anc, c->st);
+  c->anc_pending = e == hipSuccess;
+  std::swap(c->d_rec, c->d_rec2);
+  return e;
+}
+
 static hipError_t flush_track_init(tsa_ctx* c, bool on_st2 = false) {
   if (!c->track_init_pending) return hipSuccess;
   c->track_init_pending = false;
@@ -785,6 +800,7 @@ extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
       return fail(ctx, TSA_ERR_ARG, "tsa_upload: chain " + std::to_string(c) + " is not a valid tree");
   }
   TSA_HIP(ctx, quiesce_track(ctx));
+  ctx->anc_pend = false;  // (a resampling not yet made applies to the population this replaces)
   ctx->costs_valid = false;
   ctx->energy_fresh = ctx->energy_host = false;
   ctx->sums_valid = false;
@@ -799,6 +815,7 @@ extern "C" int tsa_download(tsa_ctx* ctx, int32_t c0, int32_t count, uint64_t* o
   if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_download: null argument");
   TSA_HIP(ctx, join_split(ctx));
   TSA_HIP(ctx, flush_track_init(ctx));
+  TSA_HIP(ctx, flush_resample(ctx));
   if (c0 < 0 || count < 0 || c0 + count > ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_download: range");
   const size_t cw = ctx->lay.chain_words;
   TSA_HIP(ctx, hipMemcpyAsync(out, ctx->d_rec + (size_t)c0 * cw, (size_t)count * cw * 8, hipMemcpyDeviceToHost,
@@ -812,6 +829,7 @@ extern "C" int tsa_download_async(tsa_ctx* ctx, int32_t c0, int32_t count, uint6
   if (!ctx || !out) return fail(ctx, TSA_ERR_ARG, "tsa_download_async: null argument");
   TSA_HIP(ctx, join_split(ctx));
   TSA_HIP(ctx, flush_track_init(ctx));
+  TSA_HIP(ctx, flush_resample(ctx));
   if (c0 < 0 || count < 0 || c0 + count > ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_download_async: range");
   const size_t cw = ctx->lay.chain_words;
   TSA_HIP(ctx, hipMemcpyAsync(out, ctx->d_rec + (size_t)c0 * cw, (size_t)count * cw * 8, hipMemcpyDeviceToHost,
@@ -823,6 +841,7 @@ extern "C" int tsa_wait(tsa_ctx* ctx) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_wait: null context");
   TSA_HIP(ctx, join_split(ctx));
   TSA_HIP(ctx, flush_track_init(ctx));
+  TSA_HIP(ctx, flush_resample(ctx));
   if (ctx->st2) TSA_HIP(ctx, hipStreamSynchronize(ctx->st2));
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
   ctx->host_waited = true;
@@ -864,6 +883,7 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
   if (blk && ctx->wide.on) return fail(ctx, TSA_ERR_ARG, "block of levels: not on the wide path");
   if (ctx->wide.on && order == TSA_ORDER_PAR) {
     TSA_HIP(ctx, join_split(ctx));
+    TSA_HIP(ctx, flush_resample(ctx));
     // energies stay a separate fold of the node-cost cache: every chain ends its sweep at about the same
     // time, so folding inside the sweep kernel would only lengthen it
     if (ctx->wide.nsw && !ctx->sums_valid) {
@@ -927,6 +947,10 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
     const int h = split_point(ctx);
     const bool split = ctx->overlap && apart && h > 0 && h < ctx->nchains;
     if (!split) TSA_HIP(ctx, join_split(ctx));
+    // a resampling not yet made: this launch's kernel stages each chain from its ancestor's record (the chain
+    // in LDS, one launch), else the copy first
+    const bool gather = ctx->anc_pend && ctx->L.lds && !split && !blk;
+    if (!gather) TSA_HIP(ctx, flush_resample(ctx));
     TsaEnergyOut eo{fuse && !apart ? ctx->d_lc : nullptr, ctx->d_sc, ctx->d_ns, apart ? ctx->d_ncost : nullptr,
                     apart ? ctx->d_nz : nullptr, nullptr, TsaBlock{}};
     int s = -1;
@@ -1020,10 +1044,23 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
       ctx->split_levels++;
       ctx->npending++;  // (the first launch's pair is counted below)
     } else {
+      TsaKParams Pg = ctx->P;
+      uint64_t* out = ctx->d_rec;
+      if (gather) {
+        Pg.gsrc = ctx->d_rec;
+        Pg.ganc = ctx->d_hanc ? ctx->d_hanc : ctx->d_anc;
+        out = ctx->d_rec2;
+      }
       if (markers) TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
-      TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
-                                     ctx->nchains, beta, sweep0, nsweeps, ctx->d_stats, eo, ctx->st, d0, d1));
+      TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, Pg, out, ctx->d_leaf, ctx->d_fix, ctx->nchains, beta,
+                                     sweep0, nsweeps, ctx->d_stats, eo, ctx->st, d0, d1));
       if (markers) TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
+      if (gather) {  // the resampled population, swept, is now in the other buffer
+        TSA_HIP(ctx, hipEventRecord(ctx->ev_anc, ctx->st));
+        ctx->anc_pending = true;
+        ctx->anc_pend = false;
+        std::swap(ctx->d_rec, ctx->d_rec2);
+      }
     }
     if (blk) {
       for (int i = 0; i < blk->n; i++) {
@@ -1238,6 +1275,7 @@ extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_track: null context");
   if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_track: no tsa_track_begin");
   TSA_HIP(ctx, flush_track_init(ctx));
+  TSA_HIP(ctx, flush_resample(ctx));
   if (level < 0 || level >= ctx->track_levels) return fail(ctx, TSA_ERR_ARG, "tsa_track: level out of range");
   if (ctx->track_kind == TRACK_ANNEAL)
     return fail(ctx, TSA_ERR_ARG, "tsa_track: this tracking session runs its levels with tsa_anneal");
@@ -1287,6 +1325,7 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
     return fail(ctx, TSA_ERR_ARG, "tsa_track_end: null argument");
   TSA_HIP(ctx, join_split(ctx));
   TSA_HIP(ctx, flush_track_init(ctx));
+  TSA_HIP(ctx, flush_resample(ctx));
   if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_track_end: no tsa_track_begin");
   static_assert(sizeof(TsaTraceRowD) == sizeof(tsa_trace_row_t), "trace row layout");
   TsaTrackState h;
@@ -1415,6 +1454,7 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
                           const int32_t* niters, const uint8_t* evaluated, uint32_t sweep0) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_anneal: null context");
   TSA_HIP(ctx, join_split(ctx));
+  TSA_HIP(ctx, flush_resample(ctx));
   if (order != TSA_ORDER_PAR && order != TSA_ORDER_PREORDER) return fail(ctx, TSA_ERR_ARG, "--order par|preorder");
   if (!betas || !niters || !evaluated || nlevels < 1) return fail(ctx, TSA_ERR_ARG, "tsa_anneal: no levels");
   if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_anneal: no tsa_track_begin");
@@ -1614,6 +1654,7 @@ extern "C" int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns) {
   if (!ctx || !lc || !sc || !ns) return fail(ctx, TSA_ERR_ARG, "tsa_energy: null argument");
   TSA_HIP(ctx, join_split(ctx));
   TSA_HIP(ctx, flush_track_init(ctx));
+  TSA_HIP(ctx, flush_resample(ctx));
   const size_t b = (size_t)ctx->nchains * 4;
   if (ctx->energy_host) {  // the last sweep launch wrote them into h_en
     TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
@@ -1634,25 +1675,24 @@ extern "C" int tsa_resample(tsa_ctx* ctx, const int32_t* anc) {
   if (!ctx || !anc) return fail(ctx, TSA_ERR_ARG, "tsa_resample: null argument");
   TSA_HIP(ctx, join_split(ctx));
   TSA_HIP(ctx, flush_track_init(ctx));
+  TSA_HIP(ctx, flush_resample(ctx));  // (the previous one, if not made yet)
   for (int c = 0; c < ctx->nchains; c++)
     if (anc[c] < 0 || anc[c] >= ctx->nchains) return fail(ctx, TSA_ERR_ARG, "tsa_resample: ancestor out of range");
   if (!ctx->d_rec2) TSA_HIP(ctx, hipMalloc(&ctx->d_rec2, (size_t)ctx->nchains * ctx->lay.chain_words * 8));
   TSA_HIP(ctx, quiesce_track(ctx));
-  // the ancestors go through the pinned staging buffer, which the copy kernel reads where it is mapped (else
-  // an asynchronous copy to d_anc); the last launch that read it must be done before it is overwritten
+  // the ancestors go through the pinned staging buffer, which the kernels read where it is mapped (else an
+  // asynchronous copy to d_anc); the last launch that read it must be done before it is overwritten
   if (ctx->anc_pending) TSA_HIP(ctx, hipEventSynchronize(ctx->ev_anc));
+  ctx->anc_pending = false;
   memcpy(ctx->h_anc, anc, (size_t)ctx->nchains * 4);
   if (!ctx->d_hanc)
     TSA_HIP(ctx, hipMemcpyAsync(ctx->d_anc, ctx->h_anc, (size_t)ctx->nchains * 4, hipMemcpyHostToDevice, ctx->st));
   ctx->costs_valid = false;
   ctx->energy_fresh = ctx->energy_host = false;
   ctx->sums_valid = false;
-  // the copy and everything after it run in stream order: no wait here
-  TSA_HIP(ctx, tsa_launch_copy(ctx->d_rec, ctx->d_rec2, ctx->d_hanc ? ctx->d_hanc : ctx->d_anc, ctx->nchains,
-                               ctx->lay.chain_words, ctx->st));
-  TSA_HIP(ctx, hipEventRecord(ctx->ev_anc, ctx->st));
-  ctx->anc_pending = true;
-  std::swap(ctx->d_rec, ctx->d_rec2);
+  // the copy itself is left to the next sweep launch (its kernel stages each chain from its ancestor's record)
+  // or to the next other call (flush_resample), in stream order: no wait here
+  ctx->anc_pend = true;
   return TSA_OK;
 }
 
@@ -1660,6 +1700,7 @@ extern "C" int tsa_set_mode(tsa_ctx* ctx, int32_t mode) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: null context");
   TSA_HIP(ctx, join_split(ctx));
   TSA_HIP(ctx, flush_track_init(ctx));
+  TSA_HIP(ctx, flush_resample(ctx));
   if (mode < 0 || mode > 2) return fail(ctx, TSA_ERR_ARG, "tsa_set_mode: mode must be 0, 1 or 2");
   if (mode != ctx->mode) {
     TSA_HIP(ctx, quiesce_track(ctx));

@@ -20,6 +20,11 @@ struct TsaKParams {
   uint32_t key0, key1;
   TsaModel model;
   float lse[64];               // lse[d] = (float)log2(1 + 2^-d), 0 for d >= 53
+  // k_sweep with the chain staged in LDS: when ganc is set, chain c starts from the record of chain ganc[c] in
+  // gsrc (a resampled population, read from the previous population's buffer; the launch's rec is the other
+  // buffer, which receives the swept records)
+  const uint64_t* gsrc;
+  const int* ganc;
 };
 
 // Statistic slots (the reference's d_stats order, csrc/treesa_gpu.cu:713-721).

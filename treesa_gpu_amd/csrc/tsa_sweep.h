@@ -636,7 +636,7 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
   if constexpr (LDS) {
     base = wbase;
     if (!helped || wv == 0) {  // with helpers wave 0 copies while the others draw the first sweep's numbers
-      const uint4* src = reinterpret_cast<const uint4*>(g);
+      const uint4* src = reinterpret_cast<const uint4*>(P.ganc ? P.gsrc + (size_t)P.ganc[c] * P.chain_words : g);
       uint4* dst = reinterpret_cast<uint4*>(base);
       const int n16 = P.chain_words / 2;
       int i = lane;
