@@ -399,15 +399,16 @@ def cpu_baseline(cfgname, C, inst, lay, trees, betas, nsample, dump=None, gpu=No
 
 
 def copy_calibration(cfgname, reps=10):
-    """reps population copies with identity ancestors through the C ABI (tsa_resample, kernel k_copy): every
-    launch reads and writes exactly nchains * chain_words * 8 bytes once, the reference point for the
-    FETCH_SIZE / WRITE_SIZE counters."""
+    """reps population copies with identity ancestors through the C ABI (tsa_resample, then tsa_wait, whose
+    copy kernel k_copy makes the resampling no sweep takes over): every launch reads and writes exactly
+    nchains * chain_words * 8 bytes once, the reference point for the FETCH_SIZE / WRITE_SIZE counters."""
     C, inst, lay, trees, pop, cfg, betas, order = setup(cfgname)
     with capi.Context(lay, inst.leaf(lay.W), inst.leaf_sc, cfg, C["nchains"]) as ctx:
         ctx.upload(pop)
         anc = np.arange(C["nchains"], dtype=np.int32)
         for _ in range(reps):
             ctx.resample(anc)
+            ctx.wait()
     print(json.dumps({"config": cfgname, "kernel": "k_copy", "launches": reps,
                       "bytes_read_per_launch": C["nchains"] * lay.chain_words * 8,
                       "bytes_written_per_launch": C["nchains"] * lay.chain_words * 8}))

@@ -162,8 +162,10 @@ int tsa_sweeps_ms(tsa_ctx* ctx, double* ms);
 int tsa_energy(tsa_ctx* ctx, float* lc, int32_t* sc, int32_t* ns);
 
 /* Population step: chain c <- chain anc[c] for every c.  Asynchronous (anc is copied before the call
- * returns); later calls on the context see the new population.  Replaces Runner::resample + k_copy,
- * csrc/treesa_gpu.cu:1016-1022, 1925-1933. */
+ * returns); later calls on the context see the new population.  The copy itself is made by the next sweep
+ * launch of the kernels that stage a chain in LDS (each chain starts from its ancestor's record) or, before
+ * any other call's work, by a copy kernel.  Replaces Runner::resample + k_copy, csrc/treesa_gpu.cu:1016-1022,
+ * 1925-1933. */
 int tsa_resample(tsa_ctx* ctx, const int32_t* anc);
 
 /* Switch the energy mode (stage 2 of a two-stage run, csrc/treesa_gpu.cu:1790-1798). */

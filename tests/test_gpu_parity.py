@@ -379,6 +379,42 @@ def test_resample_copies_ancestors():
     assert np.array_equal(after, before[anc])
 
 
+# tsa_resample's copy is made by the next sweep launch of the LDS kernels (each chain staged from its ancestor's
+# record in the previous population buffer) or by a copy kernel before any other call: a resampling followed by
+# sweeps, two resamplings in a row, and one followed by an energy call all give the oracle's records and
+# energies, for both orders (pre-order with and without helper waves) and with slice moves.
+@pytest.mark.parametrize("order,kw", [("par", {}), ("preorder", {}), ("preorder", {"draw_waves": -1}),
+                                      ("par", {"slicing": True})])
+def test_resample_taken_over_by_the_next_sweep(order, kw):
+    case = Case("sat40", order, "tc", nchains=96, **kw)
+    rng = np.random.default_rng(8)
+    a1, a2, a3 = (rng.integers(0, case.nchains, case.nchains).astype(np.int32) for _ in range(3))
+    opop = case.pop0.copy()
+    print(f"[gpu] resample taken over by the next sweep sat40 {order} {kw}", flush=True)
+    with capi.Context(case.lay, case.leaf, case.leaf_sc, case.cfg, case.nchains) as ctx:
+        ctx.upload(case.pop0)
+        ctx.sweeps(case.ord, 1.0, 0, 2)
+        case.O.sweeps(case.P, case.lay, opop, case.ord, 1.0, 0, 2)
+        ctx.resample(a1)  # taken over by the sweep launch
+        opop = opop[a1].copy()
+        ctx.sweeps(case.ord, 2.0, 2, 1)
+        case.O.sweeps(case.P, case.lay, opop, case.ord, 2.0, 2, 1)
+        assert np.array_equal(ctx.download(), opop), "a resampling, then sweeps"
+        ctx.resample(a2)  # two in a row: the first copied before the second is staged
+        ctx.resample(a3)
+        opop = opop[a2][a3].copy()
+        ctx.sweeps(case.ord, 3.0, 3, 2)
+        case.O.sweeps(case.P, case.lay, opop, case.ord, 3.0, 3, 2)
+        assert np.array_equal(ctx.download(), opop), "two resamplings, then sweeps"
+        ctx.resample(a1)  # an energy call makes the copy
+        opop = opop[a1].copy()
+        glc, gsc, gns = ctx.energy()
+        olc, osc, ons = case.O.energy(case.P, case.lay, opop)
+        assert np.array_equal(glc.view(np.uint32), olc.view(np.uint32)) and np.array_equal(gsc, osc)
+        assert np.array_equal(gns, ons)
+        assert np.array_equal(ctx.download(), opop), "a resampling, then an energy call"
+
+
 def test_upload_rejects_invalid_tree():
     case = Case("sat40", "par", "tc", nchains=4)
     bad = case.pop0.copy()

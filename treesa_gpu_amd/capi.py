@@ -219,6 +219,9 @@ class Context:
         anc = np.ascontiguousarray(anc, dtype=np.int32)
         self._check(self.lib.tsa_resample(self.h, anc.ctypes.data))
 
+    def wait(self):
+        self._check(self.lib.tsa_wait(self.h))
+
     def set_mode(self, mode):
         self._check(self.lib.tsa_set_mode(self.h, MODES[mode] if isinstance(mode, str) else int(mode)))
 
