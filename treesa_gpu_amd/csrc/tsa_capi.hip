@@ -806,6 +806,22 @@ extern "C" int tsa_upload(tsa_ctx* ctx, const uint64_t* population) {
   ctx->sums_valid = false;
   TSA_HIP(ctx, hipMemcpyAsync(ctx->d_rec, population, (size_t)ctx->nchains * L.chain_words * 8,
                               hipMemcpyHostToDevice, ctx->st));
+  // the population's derived data on the wide path, made with it as the reference's start builds the chunk
+  // summaries with the labels (csrc/treesa_gpu.cu:1604-1612): the summaries and, in tc mode, the node-cost
+  // cache that the visits read (with the energies, which that pass folds)
+  if (ctx->wide.on) {
+    if (ctx->wide.nsw) {
+      TSA_HIP(ctx, tsa_launch_wsum(ctx->wide, ctx->P, ctx->d_rec, ctx->nchains, ctx->d_sum, ctx->st));
+      ctx->sums_valid = true;
+    }
+    if (ctx->mode == 0) {
+      TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
+                                          ctx->nchains, ctx->d_ncost, ctx->d_nz, ctx->d_fcnt, ctx->d_lc, ctx->d_sc,
+                                          ctx->d_ns, 1, ctx->st, wide_sums(ctx)));
+      ctx->costs_valid = true;
+      ctx->energy_fresh = true;
+    }
+  }
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
   ctx->host_waited = true;
   return TSA_OK;
