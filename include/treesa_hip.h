@@ -127,8 +127,10 @@ int tsa_layout(int32_t m, int32_t nlab, int32_t wide, tsa_layout_t* out);
 int tsa_create(const tsa_layout_t* lay, const uint64_t* leaf, int32_t leaf_sc, const tsa_config_t* cfg,
                int32_t nchains, tsa_ctx** out);
 
-/* Upload the whole population (nchains * chain_words words).  Replaces the H2D copy of init_chains,
- * csrc/treesa_gpu.cu:1629. */
+/* Upload the whole population (nchains * chain_words words).  Synchronous.  On the wide path it also builds
+ * the population's derived data before it returns: the chunk summaries (as init_chains builds them with the
+ * labels, csrc/treesa_gpu.cu:1604-1612) and, in tc mode, the node-cost cache and the energies.  Replaces the
+ * H2D copy of init_chains, csrc/treesa_gpu.cu:1629. */
 int tsa_upload(tsa_ctx* ctx, const uint64_t* population);
 
 /* Download count chain records starting at chain c0.  Replaces the best-chain and --check copies,
