@@ -99,6 +99,25 @@ def test_wide_selection_beside_the_sweep(tmp_path):
     assert max(abs(x[5] - y[5]) for x, y in zip(ta, tc)) < 1e-9
 
 
+# The wide path with chunk summaries and one workgroup per chain sweeps blocks of up to 8 levels per launch,
+# each evaluated level leaving its node-cost snapshot for the fold and selection beside the next block: the
+# same result as one level per launch and as the host-side level loop.
+def test_wide_blocks_of_levels(tmp_path):
+    args = ["-i", common.inst_path("sq46"), "--nchains", "72", "--niters", "1", "--betas", "0.5:0.5:6",
+            "--sc-target", "30", "--order", "par", "--seed", "6", "--wide-wgs", "1"]
+    a = run(args, tmp_path, "a.json")
+    assert "anneal=level_blocks8" in a["hip_kernel"] and " sums=1 " in a["hip_kernel"], a["hip_kernel"]
+    b = run(args + ["--level-blocks", "1"], tmp_path, "b.json")
+    assert "anneal=level_blocks" not in b["hip_kernel"], b["hip_kernel"]
+    c = run(args + ["--host-select"], tmp_path, "c.json")
+    for k in ("tc", "sc", "best_chain", "tree", "proposals", "accepts", "node_visits", "valid", "labels_ok"):
+        assert a[k] == b[k] == c[k], k
+    ta, tb, tc = ([list(r) for r in x["trace"]] for x in (a, b, c))
+    assert [r[1:] for r in ta] == [r[1:] for r in tb]
+    assert [r[1:5] + r[6:] for r in ta] == [r[1:5] + r[6:] for r in tc]
+    assert max(abs(x[5] - y[5]) for x, y in zip(ta, tc)) < 1e-9
+
+
 @pytest.mark.parametrize("inst,extra", [("sat100", ["--kernel", "par"]), ("sat100", ["--order", "preorder"]),
                                         ("reg3_250", ["--mode", "h100"]), ("grid24", ["--mode", "gpu"]),
                                         ("sat60", ["--random-slices", "8"]), ("sq46", ["--kernel", "par"]),

@@ -718,6 +718,14 @@ static bool wide_fold_snap(const tsa_ctx* c) {
   return c->wide.on && c->wide.K == 1 && c->wide.nsw == 0 && c->nchains >= c->ncu && !c->cfg.slicing;
 }
 
+// Blocks of levels on the wide path (tsa_anneal): one workgroup per chain (no chain barrier between levels)
+// with chunk summaries, the overlapped selection with the node-cost snapshots folded apart, the node-cost
+// cache of tc mode.
+static bool wide_blocks_ok(const tsa_ctx* c, int order) {
+  return c->wide.on && c->wide.K == 1 && c->wide.nsw > 0 && c->overlap && !wide_fold_snap(c) && c->mode == 0 &&
+         !c->cfg.slicing && order == TSA_ORDER_PAR;
+}
+
 static hipError_t quiesce_track(tsa_ctx* c) {
   hipError_t e = hipSuccess;
   if (c->st2) e = hipStreamSynchronize(c->st2);
@@ -896,7 +904,9 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
   ctx->host_waited = false;
   hipEvent_t d0 = markers ? nullptr : e0, d1 = markers ? nullptr : e1;
   ctx->energy_fresh = ctx->energy_host = false;
-  if (blk && ctx->wide.on) return fail(ctx, TSA_ERR_ARG, "block of levels: not on the wide path");
+  if (blk && ctx->wide.on && !wide_blocks_ok(ctx, order))
+    return fail(ctx, TSA_ERR_ARG, "block of levels on the wide path: one workgroup per chain, the overlapped "
+                                  "selection with the fold apart, tc mode, par order");
   if (ctx->wide.on && order == TSA_ORDER_PAR) {
     TSA_HIP(ctx, join_split(ctx));
     TSA_HIP(ctx, flush_resample(ctx));
@@ -929,7 +939,24 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
       sy.fsc = ctx->d_sc;
       sy.fns = ctx->d_ns;
     }
-    if (ctx->overlap) {
+    if (blk) {
+      // the block's evaluated levels leave their snapshots in slots of their own, folded and selected on st2
+      sy.blk_n = blk->n;
+      for (int i = 0; i < blk->n; i++) {
+        sy.blk_beta[i] = blk->beta[i];
+        sy.blk_niters[i] = blk->niters[i];
+        blk_slots[i] = -1;
+        if (!blk_ev[i]) continue;
+        const int t = ctx->slot;
+        TSA_HIP(ctx, claim_slot(ctx, t));
+        ctx->snap_kind[t] = SNAP_WIDE;
+        sy.blk_ch[i] = ctx->d_snap_ch[t];
+        sy.blk_cost[i] = ctx->d_snap_cost[t];
+        sy.blk_nz[i] = ctx->d_snap_nz[t];
+        blk_slots[i] = t;
+        ctx->slot = (t + 1) % ctx->nslots;
+      }
+    } else if (ctx->overlap) {
       s = ctx->slot;
       TSA_HIP(ctx, claim_slot(ctx, s));
       sy.snap_ch = ctx->d_snap_ch[s];
@@ -950,9 +977,17 @@ static int sweeps_impl(tsa_ctx* ctx, int32_t order, float beta, uint32_t sweep0,
     if (markers) TSA_HIP(ctx, hipEventRecord(e1, ctx->st));
     if (s >= 0) {
       ctx->ev_sweep[s] = e1;  // the selection of this snapshot waits for the sweep's stop event
+      ctx->split_slot[s] = false;
       ctx->last_slot = s;
       ctx->slot = (s + 1) % ctx->nslots;
     }
+    if (blk)
+      for (int i = 0; i < blk->n; i++)
+        if (blk_slots[i] >= 0) {
+          ctx->ev_sweep[blk_slots[i]] = e1;
+          ctx->split_slot[blk_slots[i]] = false;
+          ctx->last_slot = blk_slots[i];
+        }
     ctx->energy_fresh = fold_here;
   } else {
     ctx->costs_valid = false;
@@ -1287,6 +1322,46 @@ static int track_block(tsa_ctx* ctx, const int* slots, const int* levels, int n)
   return TSA_OK;
 }
 
+// The same for a block of levels on the wide path: a fold of each evaluated level's node-cost snapshot into
+// the slot's energies, then one selection launch for them all.
+static int track_wide_block(tsa_ctx* ctx, const int* slots, const int* levels, int n) {
+  if (n == 0) return TSA_OK;
+  ctx->track_kind = TRACK_LEVELS;
+  ctx->tend_staged = false;
+  TsaSelect S = ctx->sel;
+  S.mode = ctx->mode;
+  const tsa_layout_t& L = ctx->lay;
+  TsaTrackLevels T{};
+  T.n = n;
+  TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_sweep[slots[0]], 0));  // (one sweep launch for the block)
+  for (int i = 0; i < n; i++) {
+    const int s = slots[i];
+    float* lc = reinterpret_cast<float*>(ctx->d_snap_en[s]);
+    int* sc = reinterpret_cast<int*>(ctx->d_snap_en[s]) + ctx->nchains;
+    int* ns = reinterpret_cast<int*>(ctx->d_snap_en[s]) + 2 * (size_t)ctx->nchains;
+    TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
+                                        ctx->nchains, ctx->d_snap_cost[s], ctx->d_snap_nz[s], ctx->d_fcnt, lc, sc, ns,
+                                        0, ctx->st2));
+    T.lev[i] = levels[i];
+    T.lc[i] = lc;
+    T.sc[i] = sc;
+    T.ns[i] = ns;
+    T.ch[i] = ctx->d_snap_ch[s];
+  }
+  TSA_HIP(ctx, tsa_launch_track_levels(T, ctx->nchains, S, ctx->d_rec, L.chain_words, L.ch_off, L.s_off, L.W, L.nint,
+                                       ctx->d_track, ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2,
+                                       false));
+  const int sl = slots[n - 1];
+  TSA_HIP(ctx, hipEventRecord(ctx->ev_track[sl], ctx->st2));
+  for (int i = 0; i < n; i++) {
+    ctx->track_pending[slots[i]] = true;
+    ctx->track_ev[slots[i]] = sl;
+  }
+  ctx->last_track = sl;
+  ctx->energy_fresh = false;
+  return TSA_OK;
+}
+
 extern "C" int tsa_track(tsa_ctx* ctx, int32_t level) {
   if (!ctx) return fail(ctx, TSA_ERR_ARG, "tsa_track: null context");
   if (ctx->track_levels == 0) return fail(ctx, TSA_ERR_ARG, "tsa_track: no tsa_track_begin");
@@ -1513,8 +1588,9 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
   if (ctx->cfg.level_blocks < 0 || ctx->cfg.level_blocks > TSA_BLOCK_MAX)
     return fail(ctx, TSA_ERR_ARG, "tsa_config_t.level_blocks: 0 (automatic) or 1..8");
   const int K = ctx->cfg.level_blocks > 0 ? ctx->cfg.level_blocks : TSA_BLOCK_MAX;
-  if (!loop && K > 1 && ctx->overlap && !ctx->wide.on && ctx->L.lds && ctx->cfg.fused_energy != 0 &&
-      ctx->fold_apart && !ctx->cfg.slicing && order == TSA_ORDER_PAR) {
+  const bool wide_blocks = !loop && K > 1 && wide_blocks_ok(ctx, order);
+  if (wide_blocks || (!loop && K > 1 && ctx->overlap && !ctx->wide.on && ctx->L.lds && ctx->cfg.fused_energy != 0 &&
+                      ctx->fold_apart && !ctx->cfg.slicing && order == TSA_ORDER_PAR)) {
     ctx->lv_used = 2;
     ctx->blocks_k = K;
     if (ensure_slots(ctx, 3 * K) != TSA_OK) return TSA_ERR_HIP;
@@ -1539,7 +1615,7 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
         es[ne] = slots[i];
         el[ne++] = level0 + l + i;
       }
-      rc = track_block(ctx, es, el, ne);
+      rc = wide_blocks ? track_wide_block(ctx, es, el, ne) : track_block(ctx, es, el, ne);
       if (rc != TSA_OK) return rc;
     }
     return TSA_OK;

@@ -324,6 +324,15 @@ struct TsaWideSync {
   float* flc;
   int* fsc;
   int* fns;
+  // A block of blk_n > 0 levels in one launch (one workgroup per chain, chunk summaries): level i sweeps
+  // blk_niters[i] times at blk_beta[i] (the launch's nsweeps is their sum) and, when blk_ch[i] is set, leaves
+  // its snapshot (tree and node-cost cache, as snap_ch / snap_cost / snap_nz) there at its end.
+  int blk_n;
+  float blk_beta[TSA_BLOCK_MAX];
+  int blk_niters[TSA_BLOCK_MAX];
+  uint32_t* blk_ch[TSA_BLOCK_MAX];
+  float* blk_cost[TSA_BLOCK_MAX];
+  uint16_t* blk_nz[TSA_BLOCK_MAX];
 };
 
 // LDS byte offsets of k_wide (same function on host and device).

@@ -263,7 +263,7 @@ __device__ __forceinline__ void wide_fold(const TsaKParams& P, int c, const floa
 template <int G, int MODE, bool COOP, bool SUMS>
 __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64_t* __restrict__ rec,
                                                const uint64_t* __restrict__ leaf, const uint32_t* __restrict__ fix,
-                                               int nchains, int K, float beta, uint32_t sweep0, int nsweeps,
+                                               int nchains, int K, float beta0, uint32_t sweep0, int nsweeps,
                                                unsigned long long* __restrict__ stats, TsaWideSync sy) {
   extern __shared__ __align__(16) unsigned char tsa_wsm[];
   __shared__ float s_lse[64];
@@ -344,6 +344,11 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
   int np = 0, na = 0, nv = 0, nst = 0, nck = 0, nxk = 0;
   unsigned nb = 0;
   bool ok = true;
+  // a block of levels (one workgroup per chain, chunk summaries): the current level, its beta and its sweeps
+  // left
+  const bool blocked = SUMS && !COOP && sy.blk_n > 0;
+  int lv = 0, left = blocked ? sy.blk_niters[0] : nsweeps;
+  float beta = blocked ? sy.blk_beta[0] : beta0;
 
   for (int s = 0; s < nsweeps && ok; s++) {
     const uint32_t sw = sweep0 + (uint32_t)s;
@@ -739,6 +744,22 @@ __global__ void __launch_bounds__(SUMS ? 512 : 1024) k_wide(TsaKParams P, uint64
         pri[v - m] = 0;
       }
       __syncthreads();
+    }
+    if (blocked && --left == 0) {
+      // the level's end: its snapshot, the tree from LDS and the node-cost cache (final after the sweep's last
+      // barrier), read by all before the next level's first accept rewrites the cache
+      if (sy.blk_ch[lv]) {
+        uint32_t* const sch = sy.blk_ch[lv] + (size_t)c * nint;
+        for (int i = threadIdx.x; i < nint; i += NT) sch[i] = ch[i];
+        const size_t cb = (size_t)c * nint4;
+        tsa_copy_inflight<float, 8>(sy.blk_cost[lv] + cb, sy.ncost + cb, nint, threadIdx.x, NT);
+        tsa_copy_inflight<uint16_t, 8>(sy.blk_nz[lv] + cb, sy.nz + cb, nint, threadIdx.x, NT);
+        __syncthreads();
+      }
+      if (++lv < sy.blk_n) {
+        left = sy.blk_niters[lv];
+        beta = sy.blk_beta[lv];
+      }
     }
   }
 
