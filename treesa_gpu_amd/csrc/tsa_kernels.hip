@@ -230,8 +230,10 @@ __global__ void __launch_bounds__(64 * WAVES) k_track(TsaTrackLevels L, int n, T
     const uint64_t* src = rec + (size_t)wc * chain_words;
     const uint32_t* chs = L.ch[win] ? L.ch[win] + (size_t)wc * nint : reinterpret_cast<const uint32_t*>(src + ch_off);
     uint32_t* chd = reinterpret_cast<uint32_t*>(best_rec + ch_off);
-    for (int i = lane; i < nint; i += 64) chd[i] = chs[i];
-    for (int x = lane; x < W; x += 64) best_rec[s_off + x] = src[s_off + x];
+    // (eight loads in flight per lane: a copy that stores each word before loading the next waits a cache
+    // latency per 64 words, about 20 us for a tree of 4 095 nodes)
+    tsa_copy_inflight<uint32_t, 8>(chd, chs, nint, lane, 64);
+    tsa_copy_inflight<uint64_t, 8>(best_rec + s_off, src + s_off, W, lane, 64);
   }
 }
 
@@ -369,13 +371,14 @@ __global__ void __launch_bounds__(64) k_level_best(TsaLevels Lv, int n, TsaTrack
   bc = __shfl(bc, 0, 64);
   const bool kept = slot == 0 || slot == 1;
   const uint64_t* const src = kept ? Lv.cand + ((size_t)slot * n + bc) * Lv.cand_words : nullptr;
-  if (kept)
-    for (int i = lane; i < Lv.cand_words; i += 64) best_rec[ch_off + i] = src[i];
+  if (kept) tsa_copy_inflight<uint64_t, 8>(best_rec + ch_off, src, Lv.cand_words, lane, 64);
   if (!O.h_st) return;
   // the session's results: the best tree from the words just copied (their source) or, unchanged by this launch,
   // from best_rec; the state as lane 0 left it; every trace row (the earlier launches' too)
-  for (int i = lane; i < Lv.cand_words; i += 64) O.h_tree[i] = kept ? src[i] : best_rec[ch_off + i];
-  for (int i = lane; i < O.row_words; i += 64) O.h_rows[i] = reinterpret_cast<const unsigned long long*>(Lv.trace)[i];
+  tsa_copy_inflight<unsigned long long, 8>(O.h_tree, reinterpret_cast<const unsigned long long*>(kept ? src : best_rec + ch_off),
+                                           Lv.cand_words, lane, 64);
+  tsa_copy_inflight<unsigned long long, 8>(O.h_rows, reinterpret_cast<const unsigned long long*>(Lv.trace),
+                                           O.row_words, lane, 64);
   if (lane == 0) {
     const unsigned long long* const sw = reinterpret_cast<const unsigned long long*>(st);
     for (int i = 0; i < (int)(sizeof(TsaTrackState) / 8); i++) O.h_st[i] = sw[i];
@@ -442,8 +445,8 @@ __global__ void __launch_bounds__(256) k_track_out(const unsigned long long* __r
                                                    unsigned long long* h_t0, unsigned long long* h_tree,
                                                    unsigned long long* h_rows, unsigned* h_werr) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x, nt = gridDim.x * blockDim.x;
-  for (int i = t; i < row_words; i += nt) h_rows[i] = rows[i];
-  for (int i = t; i < tree_words; i += nt) h_tree[i] = tree[i];
+  tsa_copy_inflight<unsigned long long, 4>(h_rows, rows, row_words, t, nt);
+  tsa_copy_inflight<unsigned long long, 4>(h_tree, tree, tree_words, t, nt);
   if (t < st_words) h_st[t] = st[t];
   if (t == 0) *h_t0 = *ticks0;
   if (t == 0 && werr) *h_werr = *werr;
