@@ -82,7 +82,7 @@ __global__ void __launch_bounds__(256) k_copy(const uint4* __restrict__ src, uin
                                               const int* __restrict__ anc, int n4) {
   const uint4* s = src + (size_t)anc[blockIdx.x] * n4;
   uint4* d = dst + (size_t)blockIdx.x * n4;
-  for (int i = threadIdx.x; i < n4; i += blockDim.x) d[i] = s[i];
+  tsa_copy_inflight<uint4, 4>(d, s, n4, (int)threadIdx.x, (int)blockDim.x);
 }
 
 // One entry of the selection's reduction: best score and its chain, sums of E and |S|.
