@@ -155,6 +155,7 @@ struct tsa_ctx {
   // one while the host fills the other; ev_lv[h] is recorded after the launches that read half h
   int* h_lv = nullptr;
   int* d_hlv = nullptr;  // the device's address of h_lv (null: not mapped, the table goes by a copy)
+  std::vector<int> lv_tab;  // the table d_lv holds (empty: unknown)
   hipEvent_t ev_lv[2] = {nullptr, nullptr};
   bool lv_pending[2] = {false, false};
   int lv_half = 0;
@@ -1517,6 +1518,7 @@ static int levels_alloc(tsa_ctx* ctx, int nlev, int nev) {
     ctx->h_lv = nullptr;
     ctx->d_hlv = nullptr;
     TSA_HIP(ctx, hipMalloc(&ctx->d_lv, (size_t)nlev * 3 * 4));
+    ctx->lv_tab.clear();
     TSA_HIP(ctx, hipHostMalloc(&ctx->h_lv, 2 * (size_t)nlev * 3 * 4, hipHostMallocDefault));
     if (hipHostGetDevicePointer(reinterpret_cast<void**>(&ctx->d_hlv), ctx->h_lv, 0) != hipSuccess) {
       (void)hipGetLastError();  // not mapped: the table goes by a copy
@@ -1650,31 +1652,24 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
   ctx->last_slot = -1;
   ctx->energy_fresh = ctx->energy_host = false;
   ctx->costs_valid = ctx->sums_valid = false;
-  // the set-up in one launch: the session's start (when this is its first call), the chains' best reset, the
-  // table from the pinned staging and the arrival counters zeroed (they start at zero: cleared once when
-  // allocated, and every launch leaves them so)
+  // The session's start (when this is its first call) and the chains' best reset are made by the level-loop
+  // kernel itself; a set-up launch copies the table from the pinned staging when d_lv does not hold it already
+  // (the previous call's table) and zeroes freshly allocated arrival counters (every launch leaves them at zero)
+  const bool tinit = ctx->track_init_pending, reset = ctx->lv_reset;
+  ctx->track_init_pending = false;
+  ctx->lv_reset = false;
   TsaAnnealInit A{};
-  if (ctx->track_init_pending) {
-    ctx->track_init_pending = false;
-    A.track = ctx->d_track;
-    A.ticks0 = ctx->d_ticks0;
-    A.trace = reinterpret_cast<unsigned long long*>(ctx->d_trace);
-    A.trace_words = (int)((size_t)ctx->track_levels * sizeof(TsaTraceRowD) / 8);
-    A.best = reinterpret_cast<unsigned long long*>(ctx->d_best);
-    A.best_words = ctx->lay.chain_words;
-  }
-  if (ctx->lv_reset) {
-    A.own = ctx->d_own;
-    A.bslot = ctx->d_bslot;
-    A.nchains = n;
-    ctx->lv_reset = false;
-  }
-  if (ctx->d_hlv) {
-    A.tab_src = ctx->d_hlv + hoff;
-    A.tab_dst = ctx->d_lv;
-    A.tab_words = 3 * nlevels;
-  } else {
-    TSA_HIP(ctx, hipMemcpyAsync(ctx->d_lv, h, (size_t)nlevels * 3 * 4, hipMemcpyHostToDevice, ctx->st));
+  const bool same_tab = ctx->lv_tab.size() == (size_t)3 * nlevels &&
+                        std::memcmp(ctx->lv_tab.data(), h, (size_t)3 * nlevels * 4) == 0;
+  if (!same_tab) {
+    if (ctx->d_hlv) {
+      A.tab_src = ctx->d_hlv + hoff;
+      A.tab_dst = ctx->d_lv;
+      A.tab_words = 3 * nlevels;
+    } else {
+      TSA_HIP(ctx, hipMemcpyAsync(ctx->d_lv, h, (size_t)nlevels * 3 * 4, hipMemcpyHostToDevice, ctx->st));
+    }
+    ctx->lv_tab.assign(h, h + 3 * (size_t)nlevels);
   }
   if (ctx->lv_cnt_fresh) {
     const size_t cnt_words = (size_t)ctx->lv_cap_evals * (ng + 1);
@@ -1682,7 +1677,7 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
     A.cnt_words = (int)((cnt_words + 1) / 2);
     ctx->lv_cnt_fresh = false;
   }
-  if (A.track || A.own || A.tab_src || A.cnt) TSA_HIP(ctx, tsa_launch_anneal_init(A, ctx->st));
+  if (A.tab_src || A.cnt) TSA_HIP(ctx, tsa_launch_anneal_init(A, ctx->st));
   while ((int)ctx->ev.size() < 2 * (ctx->npending + 1)) {
     hipEvent_t e;
     TSA_HIP(ctx, hipEventCreate(&e));
@@ -1713,6 +1708,14 @@ extern "C" int tsa_anneal(tsa_ctx* ctx, int32_t order, int32_t level0, int32_t n
   lv.trace = ctx->d_trace;
   lv.S = ctx->sel;
   lv.S.mode = ctx->mode;
+  lv.reset = reset ? 1 : 0;
+  if (tinit) {
+    lv.tinit = ctx->d_track;
+    lv.ticks0 = ctx->d_ticks0;
+    lv.trace_words = (int)((size_t)ctx->track_levels * sizeof(TsaTraceRowD) / 8);
+    lv.best = ctx->d_best;
+    lv.best_words = ctx->lay.chain_words;
+  }
   const TsaEnergyOut eo{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr};
   if (markers) TSA_HIP(ctx, hipEventRecord(e0, ctx->st));
   TSA_HIP(ctx, tsa_launch_sweeps(ctx->L, ctx->mode, order, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix, n, 0.0f,

@@ -113,6 +113,15 @@ struct TsaLevels {
   int* bslot;
   TsaTraceRowD* trace;
   TsaSelect S;
+  int reset;  // 1: every chain starts with no best (own +inf, no slot) instead of reading own / bslot
+  // a tracking session's start, made by chain 0's tracking wave before its first arrival (null: none): the
+  // tracking state, the start tick, trace_words words of trace rows and best_words words of the best record
+  // cleared
+  TsaTrackState* tinit;
+  unsigned long long* ticks0;
+  int trace_words;
+  uint64_t* best;
+  int best_words;
 };
 
 // Copy n elements with nthr threads (this one is tid), U loads per thread in flight at once: a loop that
@@ -224,21 +233,10 @@ hipError_t tsa_launch_level_best(const TsaLevels& Lv, int nchains, TsaTrackState
                                  const TsaTrackOut& O, hipStream_t stream);
 hipError_t tsa_launch_track_init(TsaTrackState* st, unsigned long long* ticks0, unsigned long long* trace,
                                  int trace_words, unsigned long long* best, int best_words, hipStream_t stream);
-// The set-up of a level-loop launch in one launch, each part optional: a tracking session's start (as
-// k_track_init: track != nullptr), the chains' best (TsaLevels.own / bslot) reset to +inf and no candidate
-// slot (own != nullptr), the level table copied from
-// page-locked host memory (tab_src != nullptr: tab_words 32-bit words into tab_dst) and the arrival counters
-// zeroed (cnt != nullptr: cnt_words 64-bit words).
+// The set-up of a level-loop launch in one launch, each part optional: the level table copied from page-locked
+// host memory (tab_src != nullptr: tab_words 32-bit words into tab_dst) and the arrival counters zeroed
+// (cnt != nullptr: cnt_words 64-bit words).
 struct TsaAnnealInit {
-  TsaTrackState* track;
-  unsigned long long* ticks0;
-  unsigned long long* trace;
-  int trace_words;
-  unsigned long long* best;
-  int best_words;
-  double* own;
-  int* bslot;
-  int nchains;
   const int* tab_src;
   int* tab_dst;
   int tab_words;

@@ -404,22 +404,6 @@ hipError_t tsa_launch_track_init(TsaTrackState* stt, unsigned long long* ticks0,
 
 __global__ void __launch_bounds__(256) k_anneal_init(TsaAnnealInit A) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x, nt = gridDim.x * blockDim.x;
-  if (A.track) {
-    for (int i = t; i < A.trace_words; i += nt) A.trace[i] = 0ull;
-    for (int i = t; i < A.best_words; i += nt) A.best[i] = 0ull;
-    if (t == 0) {
-      A.track->best_score = INFINITY;
-      A.track->best_chain = -1;
-      A.track->best_level = -1;
-      A.track->snap = -1;
-      *A.ticks0 = wall_clock64();
-    }
-  }
-  if (A.own)
-    for (int i = t; i < A.nchains; i += nt) {
-      A.own[i] = INFINITY;
-      A.bslot[i] = -1;
-    }
   if (A.tab_src)
     for (int i = t; i < A.tab_words; i += nt) A.tab_dst[i] = A.tab_src[i];
   if (A.cnt)
@@ -427,8 +411,7 @@ __global__ void __launch_bounds__(256) k_anneal_init(TsaAnnealInit A) {
 }
 
 hipError_t tsa_launch_anneal_init(const TsaAnnealInit& A, hipStream_t stream) {
-  int n = A.track ? (A.trace_words > A.best_words ? A.trace_words : A.best_words) : 1;
-  if (A.own && A.nchains > n) n = A.nchains;
+  int n = 1;
   if (A.tab_src && A.tab_words > n) n = A.tab_words;
   if (A.cnt && A.cnt_words > n) n = A.cnt_words;
   int grid = (n + 255) / 256;

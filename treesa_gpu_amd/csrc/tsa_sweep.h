@@ -677,7 +677,21 @@ __global__ void __launch_bounds__(256, (LVL && ORDER == 0 && MODE == 0) ? 3 : 1)
   float beta = LVL ? Lv.beta[0] : (blocked ? eo.blk.beta[0] : beta1);
   const bool tracker = LVL && (!helped || wv == 1);
   TsaOwn own{INFINITY, -1};
-  if (tracker) own = TsaOwn{Lv.own[c], Lv.bslot[c]};
+  if (tracker && !Lv.reset) own = TsaOwn{Lv.own[c], Lv.bslot[c]};
+  if (tracker && Lv.tinit && c == 0) {
+    // the session's start: its stores precede this chain's first arrival (release), which every trace row's
+    // writer waits for (acquire)
+    unsigned long long* const tr = reinterpret_cast<unsigned long long*>(Lv.trace);
+    for (int i = lane; i < Lv.trace_words; i += 64) tr[i] = 0ull;
+    for (int i = lane; i < Lv.best_words; i += 64) Lv.best[i] = 0ull;
+    if (lane == 0) {
+      Lv.tinit->best_score = INFINITY;
+      Lv.tinit->best_chain = -1;
+      Lv.tinit->best_level = -1;
+      Lv.tinit->snap = -1;
+      *Lv.ticks0 = wall_clock64();
+    }
+  }
   tsa_wave_sync();
 
   if constexpr (ORDER == 0) {
