@@ -1323,8 +1323,9 @@ static int track_block(tsa_ctx* ctx, const int* slots, const int* levels, int n)
   return TSA_OK;
 }
 
-// The same for a block of levels on the wide path: a fold of each evaluated level's node-cost snapshot into
-// the slot's energies, then one selection launch for them all.
+// The same for a block of levels on the wide path: one launch folds every evaluated level's node-cost
+// snapshot into the slot's energies (the folds of the levels side by side: one level's is a serial lse chain
+// of some 50 us on C5's trees), then one selection launch for them all.
 static int track_wide_block(tsa_ctx* ctx, const int* slots, const int* levels, int n) {
   if (n == 0) return TSA_OK;
   ctx->track_kind = TRACK_LEVELS;
@@ -1333,22 +1334,27 @@ static int track_wide_block(tsa_ctx* ctx, const int* slots, const int* levels, i
   S.mode = ctx->mode;
   const tsa_layout_t& L = ctx->lay;
   TsaTrackLevels T{};
-  T.n = n;
+  TsaFoldLevels F{};
+  T.n = F.n = n;
   TSA_HIP(ctx, hipStreamWaitEvent(ctx->st2, ctx->ev_sweep[slots[0]], 0));  // (one sweep launch for the block)
   for (int i = 0; i < n; i++) {
     const int s = slots[i];
     float* lc = reinterpret_cast<float*>(ctx->d_snap_en[s]);
     int* sc = reinterpret_cast<int*>(ctx->d_snap_en[s]) + ctx->nchains;
     int* ns = reinterpret_cast<int*>(ctx->d_snap_en[s]) + 2 * (size_t)ctx->nchains;
-    TSA_HIP(ctx, tsa_launch_wide_energy(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
-                                        ctx->nchains, ctx->d_snap_cost[s], ctx->d_snap_nz[s], ctx->d_fcnt, lc, sc, ns,
-                                        0, ctx->st2));
+    F.cost[i] = ctx->d_snap_cost[s];
+    F.z[i] = ctx->d_snap_nz[s];
+    F.lc[i] = lc;
+    F.sc[i] = sc;
+    F.ns[i] = ns;
     T.lev[i] = levels[i];
     T.lc[i] = lc;
     T.sc[i] = sc;
     T.ns[i] = ns;
     T.ch[i] = ctx->d_snap_ch[s];
   }
+  TSA_HIP(ctx, tsa_launch_wide_fold_levels(ctx->wide, ctx->mode, ctx->P, ctx->d_rec, ctx->d_leaf, ctx->d_fix,
+                                           ctx->nchains, F, ctx->st2));
   TSA_HIP(ctx, tsa_launch_track_levels(T, ctx->nchains, S, ctx->d_rec, L.chain_words, L.ch_off, L.s_off, L.W, L.nint,
                                        ctx->d_track, ctx->d_trace, ctx->d_best, ctx->d_tpart, ctx->d_tdone, ctx->st2,
                                        false));

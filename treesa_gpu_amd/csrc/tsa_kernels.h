@@ -386,3 +386,8 @@ hipError_t tsa_launch_wide_energy(const TsaWide& X, int mode, const TsaKParams& 
                                   const uint64_t* leaf, const uint32_t* fix, int nchains, float* ncost,
                                   uint16_t* nz, unsigned* fcnt, float* lc, int* sc, int* ns, int nodes,
                                   hipStream_t st, TsaSums sums = TsaSums{nullptr, nullptr, 0});
+// The folds of F.n levels' cached costs (F.cost / F.z, nchains * nint4 each) into F.lc / F.sc / F.ns in one
+// launch (blockIdx.y: the level), as tsa_launch_wide_energy with nodes = 0 does for one.
+hipError_t tsa_launch_wide_fold_levels(const TsaWide& X, int mode, const TsaKParams& P, const uint64_t* rec,
+                                       const uint64_t* leaf, const uint32_t* fix, int nchains,
+                                       const TsaFoldLevels& F, hipStream_t st);

@@ -818,7 +818,7 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
                                                int nchains, int K2, int nodes, int stage, float* __restrict__ ncost,
                                                uint16_t* __restrict__ nz, unsigned* __restrict__ fcnt,
                                                float* __restrict__ lc, int* __restrict__ sc, int* __restrict__ ns,
-                                               TsaSums sums) {
+                                               TsaSums sums, TsaFoldLevels FL) {
   // LDS (stage != 0): the chain's node costs f32[nint4] and sizes u16[nint4], then (stage == 2) the log2f
   // summary bitmap at the next 16-byte boundary
   extern __shared__ __align__(16) unsigned char s_dyn[];
@@ -832,6 +832,12 @@ __global__ void __launch_bounds__(256) k_wcost(TsaKParams P, const uint64_t* __r
   const int m = P.m, nint = P.nint, nint4 = (nint + 3) & ~3, NW = P.W, nch = NW >> 1;
   const uint64_t* const lab = rec + (size_t)c * P.chain_words;
   const uint64_t* const S = P.slicing ? lab + P.s_off : nullptr;
+  if (FL.n > 0) {  // several levels' folds (nodes = 0): this workgroup's level is blockIdx.y
+    const int li = (int)blockIdx.y;
+    wide_fold(P, c, FL.cost[li] + (size_t)c * nint4, FL.z[li] + (size_t)c * nint4, S, leaf, fix, s_mt, stage, s_dyn,
+              FL.lc[li], FL.sc[li], FL.ns[li]);
+    return;
+  }
   float* const cst = ncost + (size_t)c * nint4;
   uint16_t* const zz = nz + (size_t)c * nint4;
 
@@ -965,7 +971,17 @@ hipError_t launch_wcost_gm(const TsaWide& X, const TsaKParams& P, const uint64_t
   const int stage = nodes ? (X.fold_smem > 0 ? 1 : 0) : X.fold_stage;
   const size_t smem = stage == 2 ? (size_t)X.fold_smem_map : stage == 1 ? (size_t)X.fold_smem : 0;
   hipLaunchKernelGGL((k_wcost<G, MODE>), dim3(nchains * K2), dim3(256), smem, st, P, rec, leaf, fix, nchains, K2, nodes,
-                     stage, ncost, nz, fcnt, lc, sc, ns, sums);
+                     stage, ncost, nz, fcnt, lc, sc, ns, sums, TsaFoldLevels{});
+  return hipGetLastError();
+}
+
+template <int G, int MODE>
+hipError_t launch_wfold_levels_gm(const TsaWide& X, const TsaKParams& P, const uint64_t* rec, const uint64_t* leaf,
+                                  const uint32_t* fix, int nchains, const TsaFoldLevels& F, hipStream_t st) {
+  const int stage = X.fold_stage;
+  const size_t smem = stage == 2 ? (size_t)X.fold_smem_map : stage == 1 ? (size_t)X.fold_smem : 0;
+  hipLaunchKernelGGL((k_wcost<G, MODE>), dim3(nchains, F.n), dim3(256), smem, st, P, rec, leaf, fix, nchains, 1, 0,
+                     stage, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, TsaSums{nullptr, nullptr, 0}, F);
   return hipGetLastError();
 }
 
@@ -1196,4 +1212,23 @@ hipError_t tsa_launch_wide_energy(const TsaWide& X, int mode, const TsaKParams& 
     case 64: return launch_wcost_g<64>(X, mode, P, rec, leaf, fix, nchains, ncost, nz, fcnt, lc, sc, ns, nodes, st, sums);
     default: return hipErrorInvalidValue;
   }
+}
+
+hipError_t tsa_launch_wide_fold_levels(const TsaWide& X, int mode, const TsaKParams& P, const uint64_t* rec,
+                                       const uint64_t* leaf, const uint32_t* fix, int nchains,
+                                       const TsaFoldLevels& F, hipStream_t st) {
+  if (F.n < 1 || F.n > TSA_BLOCK_MAX) return hipErrorInvalidValue;
+#define TSA_WFL(G)                                                                             \
+  return mode == 0 ? launch_wfold_levels_gm<G, 0>(X, P, rec, leaf, fix, nchains, F, st)        \
+         : mode == 1 ? launch_wfold_levels_gm<G, 1>(X, P, rec, leaf, fix, nchains, F, st)      \
+                     : launch_wfold_levels_gm<G, 2>(X, P, rec, leaf, fix, nchains, F, st)
+  switch (X.eG) {
+    case 4: TSA_WFL(4);
+    case 8: TSA_WFL(8);
+    case 16: TSA_WFL(16);
+    case 32: TSA_WFL(32);
+    case 64: TSA_WFL(64);
+    default: return hipErrorInvalidValue;
+  }
+#undef TSA_WFL
 }
