@@ -61,13 +61,22 @@ __device__ __forceinline__ TsaEvalOut tsa_fold32(const TsaKParams& P, const CT* 
       if (i0 + 32 * q < nint) acc = tsa_lse_f(acc, cb[q], T);
   }
   int scl = 0, cntl = 0;
-  for (int i = l32; i < nint; i += 32) {
-    const int Z = z[i];
-    if (Z > scl) {
-      scl = Z;
-      cntl = 1;
-    } else if (Z == scl) {
-      cntl++;
+  for (int i0 = l32; i0 < nint; i0 += 32 * TSA_FOLD_BATCH) {  // (the sizes read ahead too)
+    int zb[TSA_FOLD_BATCH];
+#pragma unroll
+    for (int q = 0; q < TSA_FOLD_BATCH; q++) {
+      const int i = i0 + 32 * q;
+      zb[q] = i < nint ? (int)z[i] : -1;
+    }
+#pragma unroll
+    for (int q = 0; q < TSA_FOLD_BATCH; q++) {
+      const int Z = zb[q];
+      if (Z > scl) {
+        scl = Z;
+        cntl = 1;
+      } else if (Z == scl) {
+        cntl++;
+      }
     }
   }
   int scmax = scl;
