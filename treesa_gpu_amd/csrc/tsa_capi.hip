@@ -1469,8 +1469,10 @@ extern "C" int tsa_track_end(tsa_ctx* ctx, int32_t* best_chain, int32_t* best_le
     TSA_HIP(ctx, hipMemcpyAsync(h_rows, ctx->d_trace, rowb, hipMemcpyDeviceToHost, ctx->st));
     if (ctx->wide.on) TSA_HIP(ctx, hipMemcpyAsync(h_werr, ctx->wsync.err, 4, hipMemcpyDeviceToHost, ctx->st));
   }
-  if (on2) TSA_HIP(ctx, hipStreamSynchronize(ctx->st2));
+  // (st first: its sweeps ended before the selections on st2 that follow them, so its wait -- the wait for
+  // the join of the third stream included -- passes while st2 still runs, instead of after it)
   TSA_HIP(ctx, hipStreamSynchronize(ctx->st));
+  if (on2) TSA_HIP(ctx, hipStreamSynchronize(ctx->st2));
   ctx->host_waited = true;
   ctx->tend_staged = false;
   std::memcpy(&h, h_state, sizeof h);
